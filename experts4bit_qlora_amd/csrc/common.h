@@ -1,0 +1,136 @@
+// Shared device helpers for the gfx950 frozen-expert MoE kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/e4b_amd.h"
+
+#define E4B_DEV __device__ __forceinline__
+
+namespace e4b {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------------- dtypes
+// Activations travel as raw 16-bit patterns; DT selects bf16 (0) or fp16 (1).
+template <int DT>
+E4B_DEV float to_f(uint16_t v);
+template <>
+E4B_DEV float to_f<E4B_BF16>(uint16_t v) {
+  return __uint_as_float(static_cast<uint32_t>(v) << 16);
+}
+template <>
+E4B_DEV float to_f<E4B_FP16>(uint16_t v) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, v));
+}
+
+// fp32 -> 16-bit, round to nearest even (the rounding torch's .to(dtype) performs).
+template <int DT>
+E4B_DEV uint16_t from_f(float f);
+template <>
+E4B_DEV uint16_t from_f<E4B_BF16>(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+template <>
+E4B_DEV uint16_t from_f<E4B_FP16>(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+template <int DT>
+E4B_DEV float rnd(float f) {
+  return to_f<DT>(from_f<DT>(f));
+}
+
+// Low / high 16-bit halves of a packed pair of activations as fp32.
+template <int DT>
+E4B_DEV float lo_f(uint32_t p) {
+  return to_f<DT>(static_cast<uint16_t>(p & 0xffffu));
+}
+template <int DT>
+E4B_DEV float hi_f(uint32_t p) {
+  return to_f<DT>(static_cast<uint16_t>(p >> 16));
+}
+template <>
+E4B_DEV float lo_f<E4B_BF16>(uint32_t p) {
+  return __uint_as_float(p << 16);
+}
+template <>
+E4B_DEV float hi_f<E4B_BF16>(uint32_t p) {
+  return __uint_as_float(p & 0xffff0000u);
+}
+
+E4B_DEV uint32_t pack2(uint16_t lo, uint16_t hi) {
+  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+}
+
+// ------------------------------------------------------------------------------ epilogues
+E4B_DEV float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+E4B_DEV float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// Gated activation of one (gate, up) pair. Inputs are fp32 GEMM sums; the result is the
+// activation value already rounded to DT. Rounding points follow the reference:
+//   SWIGLU        lora.py:125-127       bf16 ops: rnd(rnd(silu(g)) * u)
+//   CLAMP_SWIGLU  deepseek_v4.py:190-195 fp32 GLU, one rounding
+//   GPTOSS        hot_residency.py:72-80 bias add then five rounded bf16 ops
+template <int DT>
+E4B_DEV float gated(int epi, float g, float u, float alpha, float limit, float bg, float bu) {
+  g = rnd<DT>(g);
+  u = rnd<DT>(u);
+  if (epi == E4B_EPI_GPTOSS) {
+    g = rnd<DT>(g + bg);
+    u = rnd<DT>(u + bu);
+    g = fminf(g, limit);
+    u = fminf(fmaxf(u, -limit), limit);
+    const float t = rnd<DT>(g * alpha);
+    const float sg = rnd<DT>(sigmoid_f32(t));
+    const float gs = rnd<DT>(g * sg);
+    const float u1 = rnd<DT>(u + 1.0f);
+    return rnd<DT>(u1 * gs);
+  }
+  if (epi == E4B_EPI_CLAMP_SWIGLU) {
+    if (limit > 0.0f) {
+      g = fminf(g, limit);
+      u = fminf(fmaxf(u, -limit), limit);
+    }
+    return rnd<DT>(silu_f32(g) * u);
+  }
+  // E4B_EPI_SWIGLU
+  return rnd<DT>(rnd<DT>(silu_f32(g)) * u);
+}
+
+// Single-output epilogue: NONE (optionally + bias, gpt-oss down_proj) or ACT.
+template <int DT>
+E4B_DEV float single(int epi, float p, float b, bool has_bias) {
+  p = rnd<DT>(p);
+  if (has_bias) p = rnd<DT>(p + b);
+  if (epi == E4B_EPI_ACT) return rnd<DT>(silu_f32(p));
+  return p;
+}
+
+E4B_DEV bool is_gated(int epi) {
+  return epi == E4B_EPI_SWIGLU || epi == E4B_EPI_CLAMP_SWIGLU || epi == E4B_EPI_GPTOSS;
+}
+
+// ------------------------------------------------------------------------------ weights
+// Per-(expert, row, 64-element block) scale of the NF4 formats.
+template <int FMT>
+E4B_DEV float nf4_block_scale(const e4b_qweight& w, int e, int64_t block) {
+  const int64_t nb = w.n * (w.k / 64);
+  if constexpr (FMT == E4B_FMT_NF4) {
+    return static_cast<const float*>(w.absmax)[e * nb + block];
+  } else {
+    const uint8_t q = static_cast<const uint8_t*>(w.absmax)[e * nb + block];
+    const int64_t nb2 = (nb + 255) / 256;
+    // fp32(fp32(code2[q] * absmax2) + offset): two separately rounded operations.
+    const float p = __fmul_rn(w.code2[q], w.absmax2[e * nb2 + block / 256]);
+    return __fadd_rn(p, w.offset[e]);
+  }
+}
+
+// 2^(s - 127) for an e8m0 byte, exact (s = 0 is the subnormal 2^-127, s = 255 is +inf).
+E4B_DEV float e8m0_to_f32(uint32_t s) {
+  return s == 0 ? __uint_as_float(0x00400000u) : __uint_as_float(s << 23);
+}
+
+}  // namespace e4b

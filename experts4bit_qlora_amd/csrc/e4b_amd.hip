@@ -1,0 +1,359 @@
+// C-ABI entry points of libe4b_amd.so (declared in include/e4b_amd.h).
+//
+// Host code only validates, picks a kernel instantiation and launches on the caller's stream.
+// No device memory is allocated here and no call synchronises the device.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "common.h"
+#include "dequant.h"
+#include "gemm.h"
+#include "gemv.h"
+#include "route.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(E4B_ELAUNCH, "%s: %s", what, hipGetErrorString(err));
+  return E4B_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+bool act_dtype_ok(int dt) { return dt == E4B_BF16 || dt == E4B_FP16; }
+bool any_dtype_ok(int dt) { return dt == E4B_BF16 || dt == E4B_FP16 || dt == E4B_FP32; }
+
+int check_weight(const e4b_qweight* w) {
+  if (!w) return fail(E4B_EINVAL, "weight descriptor is NULL");
+  if (w->num_experts <= 0 || w->n <= 0 || w->k <= 0)
+    return fail(E4B_EINVAL, "weight dims must be positive (E=%d n=%lld k=%lld)", w->num_experts,
+                (long long)w->n, (long long)w->k);
+  if (w->k % 64) return fail(E4B_EUNSUPPORTED, "k=%lld is not a multiple of 64", (long long)w->k);
+  if (!w->packed || !w->absmax) return fail(E4B_EINVAL, "packed/absmax pointer is NULL");
+  if (!aligned16(w->packed)) return fail(E4B_EINVAL, "packed weights must be 16-byte aligned");
+  switch (w->format) {
+    case E4B_FMT_NF4:
+      if (!w->code) return fail(E4B_EINVAL, "NF4 needs the 16-entry code table");
+      break;
+    case E4B_FMT_NF4_DQ:
+      if (!w->code || !w->code2 || !w->absmax2 || !w->offset)
+        return fail(E4B_EINVAL, "double-quant NF4 needs code, code2, absmax2 and offset");
+      break;
+    case E4B_FMT_MXFP4:
+      break;
+    default:
+      return fail(E4B_EINVAL, "unknown weight format %d", w->format);
+  }
+  return E4B_OK;
+}
+
+int check_routing(const e4b_routing* rt, int64_t M) {
+  if (!rt) return fail(E4B_EINVAL, "routing descriptor is NULL");
+  if (!rt->sorted_flat || !rt->inv || !rt->offsets || !rt->active || !rt->tiles || !rt->meta)
+    return fail(E4B_EINVAL, "routing buffers must all be non-NULL");
+  if (rt->tile_m <= 0) return fail(E4B_EINVAL, "tile_m must be positive");
+  if (M > 0 && rt->max_tiles <= 0) return fail(E4B_EINVAL, "max_tiles must be positive");
+  return E4B_OK;
+}
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+template <int FMT>
+int launch_dequant_fmt(const e4b_qweight& w, int eb, int ec, int od, void* out, hipStream_t s) {
+  const int64_t words = int64_t(ec) * w.n * w.k / 8;
+  const int grid = static_cast<int>(std::min<int64_t>(cdiv(words, 256), 16384));
+  switch (od) {
+    case E4B_FP32:
+      hipLaunchKernelGGL((e4b::dequant_kernel<FMT, E4B_FP32>), dim3(grid), dim3(256), 0, s, w, eb, words, out);
+      break;
+    case E4B_BF16:
+      hipLaunchKernelGGL((e4b::dequant_kernel<FMT, E4B_BF16>), dim3(grid), dim3(256), 0, s, w, eb, words, out);
+      break;
+    default:
+      hipLaunchKernelGGL((e4b::dequant_kernel<FMT, E4B_FP16>), dim3(grid), dim3(256), 0, s, w, eb, words, out);
+      break;
+  }
+  return check_launch("dequant_kernel");
+}
+
+// GEMV lanes per weight row: about four 16-byte chunks per lane.
+int gemv_group(int64_t k) {
+  const int64_t chunks = k / 32;
+  int g = 2;
+  while (g < 64 && chunks / (2 * g) >= 4) g *= 2;
+  return g;
+}
+
+template <int DT, int FMT, int G>
+void launch_gemv_g(const e4b::GemmArgs& a, int64_t max_active, hipStream_t s) {
+  constexpr int slots = e4b::kWave / G;
+  const int64_t cols_per_block = (e4b::kGemvThreads / e4b::kWave) * slots;
+  dim3 grid(static_cast<unsigned>(cdiv(a.n_out, cols_per_block)), static_cast<unsigned>(max_active));
+  hipLaunchKernelGGL((e4b::gemv_kernel<DT, FMT, G>), grid, dim3(e4b::kGemvThreads), 0, s, a);
+}
+
+template <int DT, int FMT>
+void launch_gemv_fmt(const e4b::GemmArgs& a, int64_t max_active, hipStream_t s) {
+  switch (gemv_group(a.w.k)) {
+    case 2: launch_gemv_g<DT, FMT, 2>(a, max_active, s); break;
+    case 4: launch_gemv_g<DT, FMT, 4>(a, max_active, s); break;
+    case 8: launch_gemv_g<DT, FMT, 8>(a, max_active, s); break;
+    case 16: launch_gemv_g<DT, FMT, 16>(a, max_active, s); break;
+    case 32: launch_gemv_g<DT, FMT, 32>(a, max_active, s); break;
+    default: launch_gemv_g<DT, FMT, 64>(a, max_active, s); break;
+  }
+}
+
+template <int DT, int FMT>
+void launch_mfma_fmt(const e4b::GemmArgs& a, hipStream_t s) {
+  const bool pair = a.epi == E4B_EPI_SWIGLU || a.epi == E4B_EPI_CLAMP_SWIGLU || a.epi == E4B_EPI_GPTOSS;
+  const int64_t cols = pair ? e4b::kTileNW / 2 : e4b::kTileNW;
+  dim3 grid(static_cast<unsigned>(a.rt.max_tiles), static_cast<unsigned>(cdiv(a.n_out, cols)));
+  hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT>), grid, dim3(e4b::kGemmThreads), 0, s, a);
+}
+
+template <int DT>
+int launch_gemm_dt(const e4b::GemmArgs& a, bool gemv, int64_t max_active, hipStream_t s) {
+  switch (a.w.format) {
+    case E4B_FMT_NF4:
+      gemv ? launch_gemv_fmt<DT, E4B_FMT_NF4>(a, max_active, s) : launch_mfma_fmt<DT, E4B_FMT_NF4>(a, s);
+      break;
+    case E4B_FMT_NF4_DQ:
+      gemv ? launch_gemv_fmt<DT, E4B_FMT_NF4_DQ>(a, max_active, s) : launch_mfma_fmt<DT, E4B_FMT_NF4_DQ>(a, s);
+      break;
+    default:
+      gemv ? launch_gemv_fmt<DT, E4B_FMT_MXFP4>(a, max_active, s) : launch_mfma_fmt<DT, E4B_FMT_MXFP4>(a, s);
+      break;
+  }
+  return check_launch(gemv ? "gemv_kernel" : "gemm_mfma_kernel");
+}
+
+template <int DT, int WDT>
+void launch_combine_w(const uint16_t* down, const int32_t* inv, const void* w, int64_t T, int k, int64_t H,
+                      void* out, int od, hipStream_t s) {
+  const int64_t work = T * ((H % 8) == 0 ? H / 8 : H);
+  const int grid = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(cdiv(work, 256), 16384)));
+  switch (od) {
+    case E4B_FP32:
+      hipLaunchKernelGGL((e4b::combine_kernel<DT, WDT, E4B_FP32>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
+      break;
+    case E4B_BF16:
+      hipLaunchKernelGGL((e4b::combine_kernel<DT, WDT, E4B_BF16>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
+      break;
+    default:
+      hipLaunchKernelGGL((e4b::combine_kernel<DT, WDT, E4B_FP16>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
+      break;
+  }
+}
+
+template <int DT>
+void launch_combine_dt(const uint16_t* down, const int32_t* inv, const void* w, int wd, int64_t T, int k,
+                       int64_t H, void* out, int od, hipStream_t s) {
+  switch (wd) {
+    case E4B_FP32: launch_combine_w<DT, E4B_FP32>(down, inv, w, T, k, H, out, od, s); break;
+    case E4B_BF16: launch_combine_w<DT, E4B_BF16>(down, inv, w, T, k, H, out, od, s); break;
+    default: launch_combine_w<DT, E4B_FP16>(down, inv, w, T, k, H, out, od, s); break;
+  }
+}
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+int64_t max_tiles_for(int64_t M, int E, int tile_m) { return cdiv(M, tile_m) + std::min<int64_t>(E, M); }
+
+bool is_gated_epi(int epi) {
+  return epi == E4B_EPI_SWIGLU || epi == E4B_EPI_CLAMP_SWIGLU || epi == E4B_EPI_GPTOSS;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* e4b_version(void) { return "e4b_amd 0.1.0 (gfx950)"; }
+
+const char* e4b_last_error(void) { return g_last_error.c_str(); }
+
+int32_t e4b_mfma_tile_m(void) { return e4b::kTileM; }
+
+int e4b_dequant(const e4b_qweight* w, int32_t expert_begin, int32_t expert_count, int32_t out_dtype, void* out,
+                hipStream_t stream) {
+  int rc = check_weight(w);
+  if (rc) return rc;
+  if (!out) return fail(E4B_EINVAL, "out is NULL");
+  if (!any_dtype_ok(out_dtype)) return fail(E4B_EINVAL, "bad out_dtype %d", out_dtype);
+  if (expert_begin < 0 || expert_count < 0 || expert_begin + expert_count > w->num_experts)
+    return fail(E4B_EINVAL, "expert range [%d, %d) outside [0, %d)", expert_begin, expert_begin + expert_count,
+                w->num_experts);
+  if (!aligned16(out)) return fail(E4B_EINVAL, "out must be 16-byte aligned");
+  if (expert_count == 0) return E4B_OK;
+  switch (w->format) {
+    case E4B_FMT_NF4: return launch_dequant_fmt<E4B_FMT_NF4>(*w, expert_begin, expert_count, out_dtype, out, stream);
+    case E4B_FMT_NF4_DQ:
+      return launch_dequant_fmt<E4B_FMT_NF4_DQ>(*w, expert_begin, expert_count, out_dtype, out, stream);
+    default: return launch_dequant_fmt<E4B_FMT_MXFP4>(*w, expert_begin, expert_count, out_dtype, out, stream);
+  }
+}
+
+int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t num_experts, const e4b_routing* rt,
+              hipStream_t stream) {
+  if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "tokens must be >= 0 and top_k > 0");
+  const int64_t M = tokens * top_k;
+  if (M > 0x7fffffffLL) return fail(E4B_EUNSUPPORTED, "tokens*top_k=%lld exceeds int32", (long long)M);
+  if (num_experts <= 0 || num_experts > e4b::kRouteMaxExperts)
+    return fail(E4B_EUNSUPPORTED, "num_experts=%d outside [1, %d]", num_experts, e4b::kRouteMaxExperts);
+  int rc = check_routing(rt, M);
+  if (rc) return rc;
+  if (M > 0 && !top_k_index) return fail(E4B_EINVAL, "top_k_index is NULL");
+  if (M > 0 && rt->max_tiles < max_tiles_for(M, num_experts, rt->tile_m))
+    return fail(E4B_ESPACE, "max_tiles=%d < %lld needed", rt->max_tiles,
+                (long long)max_tiles_for(M, num_experts, rt->tile_m));
+  hipLaunchKernelGGL(e4b::route_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, top_k_index, M, num_experts,
+                     *rt);
+  return check_launch("route_kernel");
+}
+
+int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e4b_qweight* w, const e4b_routing* rt,
+                     int64_t tokens, int64_t M, int32_t epilogue, float alpha, float limit, int32_t flags, void* out,
+                     hipStream_t stream) {
+  int rc = check_weight(w);
+  if (rc) return rc;
+  rc = check_routing(rt, M);
+  if (rc) return rc;
+  if (!act_dtype_ok(act_dtype)) return fail(E4B_EINVAL, "act_dtype must be bf16 or fp16 (got %d)", act_dtype);
+  if (epilogue < E4B_EPI_NONE || epilogue > E4B_EPI_GPTOSS) return fail(E4B_EINVAL, "bad epilogue %d", epilogue);
+  const bool pair = is_gated_epi(epilogue);
+  if (pair && (w->n % 2)) return fail(E4B_EINVAL, "gated epilogue needs an even n (got %lld)", (long long)w->n);
+  if (epilogue == E4B_EPI_GPTOSS && !w->bias) return fail(E4B_EINVAL, "gpt-oss epilogue needs the gate_up bias");
+  if (M < 0 || tokens < 0) return fail(E4B_EINVAL, "negative sizes");
+  if (M == 0) return E4B_OK;
+  if (!a || !out) return fail(E4B_EINVAL, "a/out is NULL");
+  if (!aligned16(a)) return fail(E4B_EINVAL, "activations must be 16-byte aligned");
+  if (gather_k < 0) return fail(E4B_EINVAL, "gather_k must be >= 0");
+  bool gemv;
+  if (flags == E4B_PATH_GEMV) gemv = true;
+  else if (flags == E4B_PATH_MFMA) gemv = false;
+  else if (flags == E4B_PATH_AUTO) gemv = tokens <= 4;
+  else return fail(E4B_EINVAL, "bad flags %d", flags);
+  if (!gemv && rt->tile_m != e4b::kTileM)
+    return fail(E4B_EINVAL, "routing tile_m=%d but the MFMA GEMM needs %d", rt->tile_m, e4b::kTileM);
+
+  e4b::GemmArgs args;
+  args.a = static_cast<const uint16_t*>(a);
+  args.gather_k = gather_k;
+  args.w = *w;
+  args.rt = *rt;
+  args.M = M;
+  args.epi = epilogue;
+  args.alpha = alpha;
+  args.limit = limit;
+  args.out = static_cast<uint16_t*>(out);
+  args.n_out = pair ? w->n / 2 : w->n;
+  const int64_t max_active = std::min<int64_t>(w->num_experts, M);
+  return act_dtype == E4B_BF16 ? launch_gemm_dt<E4B_BF16>(args, gemv, max_active, stream)
+                               : launch_gemm_dt<E4B_FP16>(args, gemv, max_active, stream);
+}
+
+int e4b_combine(const void* down, int32_t act_dtype, const int32_t* inv, const void* top_k_weights,
+                int32_t weight_dtype, int64_t tokens, int32_t top_k, int64_t hidden, void* out, int32_t out_dtype,
+                hipStream_t stream) {
+  if (!act_dtype_ok(act_dtype)) return fail(E4B_EINVAL, "act_dtype must be bf16 or fp16");
+  if (!any_dtype_ok(weight_dtype) || !any_dtype_ok(out_dtype)) return fail(E4B_EINVAL, "bad weight/out dtype");
+  if (tokens < 0 || top_k <= 0 || hidden <= 0) return fail(E4B_EINVAL, "bad sizes");
+  if (tokens == 0) return E4B_OK;
+  if (!down || !inv || !top_k_weights || !out) return fail(E4B_EINVAL, "NULL pointer");
+  if (hidden % 8 == 0 && !aligned16(down)) return fail(E4B_EINVAL, "down must be 16-byte aligned");
+  const uint16_t* d = static_cast<const uint16_t*>(down);
+  if (act_dtype == E4B_BF16)
+    launch_combine_dt<E4B_BF16>(d, inv, top_k_weights, weight_dtype, tokens, top_k, hidden, out, out_dtype, stream);
+  else
+    launch_combine_dt<E4B_FP16>(d, inv, top_k_weights, weight_dtype, tokens, top_k, hidden, out, out_dtype, stream);
+  return check_launch("combine_kernel");
+}
+
+size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts, int64_t n1, int64_t n2,
+                               int32_t epilogue, int32_t act_dtype) {
+  (void)act_dtype;
+  const int64_t M = tokens * top_k;
+  const int64_t h_cols = is_gated_epi(epilogue) ? n1 / 2 : n1;
+  size_t b = 0;
+  b += align256(sizeof(int32_t) * M);                                  // sorted_flat
+  b += align256(sizeof(int32_t) * M);                                  // inv
+  b += align256(sizeof(int32_t) * (num_experts + 1));                  // offsets
+  b += align256(sizeof(int32_t) * num_experts);                        // active
+  b += align256(sizeof(int32_t) * 2 * max_tiles_for(M, num_experts, e4b::kTileM));  // tiles
+  b += align256(sizeof(int32_t) * 4);                                  // meta
+  b += align256(sizeof(uint16_t) * M * h_cols);                        // h
+  b += align256(sizeof(uint16_t) * M * n2);                            // down
+  return b;
+}
+
+int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                    const void* top_k_weights, int32_t weight_dtype, int32_t top_k, const e4b_qweight* w1,
+                    const e4b_qweight* w2, int32_t epilogue, float alpha, float limit, int32_t flags, void* workspace,
+                    size_t workspace_bytes, void* out, int32_t out_dtype, hipStream_t stream) {
+  int rc = check_weight(w1);
+  if (rc) return rc;
+  rc = check_weight(w2);
+  if (rc) return rc;
+  if (w1->num_experts != w2->num_experts) return fail(E4B_EINVAL, "w1/w2 expert counts differ");
+  const bool pair = is_gated_epi(epilogue);
+  const int64_t h_cols = pair ? w1->n / 2 : w1->n;
+  if (h_cols != w2->k)
+    return fail(E4B_EINVAL, "gate_up output (%lld) does not match down k (%lld)", (long long)h_cols,
+                (long long)w2->k);
+  if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "bad tokens/top_k");
+  if (tokens == 0) return E4B_OK;
+  const int E = w1->num_experts;
+  const int64_t M = tokens * top_k;
+  const size_t need = e4b_moe_workspace_bytes(tokens, top_k, E, w1->n, w2->n, epilogue, act_dtype);
+  if (!workspace || workspace_bytes < need)
+    return fail(E4B_ESPACE, "workspace %zu bytes < %zu needed", workspace_bytes, need);
+  if (!aligned16(workspace)) return fail(E4B_EINVAL, "workspace must be 16-byte aligned");
+
+  char* p = static_cast<char*>(workspace);
+  auto take = [&](size_t bytes) {
+    char* q = p;
+    p += align256(bytes);
+    return q;
+  };
+  e4b_routing rt;
+  rt.sorted_flat = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));
+  rt.inv = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));
+  rt.offsets = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (E + 1)));
+  rt.active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
+  rt.max_tiles = static_cast<int32_t>(max_tiles_for(M, E, e4b::kTileM));
+  rt.tile_m = e4b::kTileM;
+  rt.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rt.max_tiles));
+  rt.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
+  void* h = take(sizeof(uint16_t) * M * h_cols);
+  void* down = take(sizeof(uint16_t) * M * w2->n);
+
+  rc = e4b_route(top_k_index, tokens, top_k, E, &rt, stream);
+  if (rc) return rc;
+  rc = e4b_grouped_gemm(hidden, act_dtype, top_k, w1, &rt, tokens, M, epilogue, alpha, limit, flags, h, stream);
+  if (rc) return rc;
+  rc = e4b_grouped_gemm(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, stream);
+  if (rc) return rc;
+  return e4b_combine(down, act_dtype, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
+                     stream);
+}
+
+}  // extern "C"

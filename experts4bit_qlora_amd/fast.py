@@ -1,0 +1,319 @@
+"""``enable_fast``: route frozen expert modules through the gfx950 kernels.
+
+Same entry points, eligibility rules, markers, return counts and fallbacks as the reference
+(``experts4bit_qlora/engines/fast.py:66-423``):
+
+* ``fast_available()`` -- the HIP library loads and a device is up.
+* ``enable_fast(model, verbose=False) -> int`` patches every eligible ``ExpertsLoRA`` wrapper
+  (skipping its wrapped base) and every eligible bare ``ExpertsNbit``; it sets
+  ``mod._e4b_fast_ref = mod.forward`` and binds the fused forward; idempotent; mutually
+  exclusive with the other engines' markers; warns in training mode.
+* ``disable_fast(model) -> int`` restores the saved forwards.
+
+The fused forwards keep the reference's positional signature ``(mod, hidden_states,
+top_k_index, top_k_weights)`` (the offload pre-hook reads ``args[1]``) and fall back to the saved
+reference forward when grad is required, in training mode (wrapper), for a non-bf16/fp16
+compute dtype, or for an evicted (0-element) store.
+
+Beyond the reference: ``GptOssExpertsMxfp4`` modules (MXFP4 + biases + clamped GLU) are fused
+too, and NF4 with double-quantized absmax is eligible. Where the reference issues ~15 torch
+launches and a device->host sync per layer (``fast.py:125-160``), the bare fused forward here is
+ONE library call (route, gate_up + epilogue, down, combine) with no host sync.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import _native as N
+from . import ops
+from .arch.deepseek_v4 import _DeepseekV4ForwardMixin
+from .arch.gptoss import GptOssExpertsMxfp4
+from .experts import Experts4bit, ExpertsNbit
+from .lora import ExpertsLoRA, _epilogue
+
+_PATH = {"auto": N.PATH_AUTO, "gemv": N.PATH_GEMV, "mfma": N.PATH_MFMA}
+_kernel_path = N.PATH_AUTO
+
+
+def set_kernel_path(path: str) -> None:
+    """Force the grouped-GEMM kernel family ("auto" | "gemv" | "mfma"); for tests and benchmarks."""
+    global _kernel_path
+    _kernel_path = _PATH[path]
+
+
+def fast_available() -> bool:
+    """True iff the MI355X kernel library loads and a HIP device is up (``fast.py:66-72``)."""
+    return N.available() and torch.cuda.is_available()
+
+
+def _eligible(mod) -> Optional[str]:
+    """None if ``mod`` can take the fast path, else the reason not (``fast.py:75-97``)."""
+    if getattr(mod, "_e4b_mxfp4_arena", False):
+        return ("storage is MXFP4 (arena), which the NF4 grouped kernel cannot read -- "
+                "the MXFP4 forward is wired by nvme_experts and needs no patch here")
+    if getattr(mod, "bits", None) != 4 or getattr(mod, "quant_type", None) != "nf4":
+        return "storage is not nf4-4bit"
+    if getattr(mod, "blocksize", None) != 64:
+        return f"blocksize {getattr(mod, 'blocksize', None)} != 64"
+    n1, k1 = mod._gate_up_shape
+    n2, k2 = mod._down_shape
+    if k1 % 64 or k2 % 64:
+        return "K not divisible by 64"
+    if not mod.gate_up_proj.is_cuda:
+        return "storage not on CUDA"
+    return None
+
+
+def _eligible_mxfp4(mod) -> Optional[str]:
+    n1, k1 = mod._gate_up_shape
+    n2, k2 = mod._down_shape
+    if k1 % 64 or k2 % 64:
+        return "K not divisible by 64"
+    if not mod.gate_up_proj.is_cuda:
+        return "storage not on CUDA"
+    return None
+
+
+# ------------------------------------------------------------------- kernel descriptors
+
+
+def _qweights(mod):
+    """(gate_up, down) kernel descriptors of an NF4 ``ExpertsNbit`` (fp32 or double-quant absmax)."""
+    E = mod.num_experts
+    n1, k1 = mod._gate_up_shape
+    n2, k2 = mod._down_shape
+    if getattr(mod, "compress_statistics", False):
+        w1 = ops.nf4_dq_qweight(mod.gate_up_proj, mod.gate_up_absmax, mod.gate_up_absmax2, mod.gate_up_absmax_offset,
+                                mod.code, mod.code2, n1, k1, num_experts=E)
+        w2 = ops.nf4_dq_qweight(mod.down_proj, mod.down_absmax, mod.down_absmax2, mod.down_absmax_offset,
+                                mod.code, mod.code2, n2, k2, num_experts=E)
+    else:
+        w1 = ops.nf4_qweight(mod.gate_up_proj, mod.gate_up_absmax, mod.code, n1, k1, num_experts=E)
+        w2 = ops.nf4_qweight(mod.down_proj, mod.down_absmax, mod.code, n2, k2, num_experts=E)
+    return w1, w2
+
+
+def _fused_epilogue(base):
+    """(epilogue code, limit) the kernel can apply for this base, or None when only the base's own
+    Python epilogue reproduces it (a custom ``_apply_gate`` or activation)."""
+    hook = getattr(base, "_apply_gate", None)
+    if hook is not None:
+        if isinstance(base, _DeepseekV4ForwardMixin) and type(base)._apply_gate is _DeepseekV4ForwardMixin._apply_gate:
+            return N.EPI_CLAMP_SWIGLU, float(base.limit)
+        return None
+    if base.act_fn is not F.silu:
+        return None
+    return (N.EPI_SWIGLU if base.has_gate else N.EPI_ACT), 0.0
+
+
+def _wants_reference(mod, hidden_states) -> bool:
+    return torch.is_grad_enabled() and (hidden_states.requires_grad or any(p.requires_grad for p in mod.parameters()))
+
+
+# ------------------------------------------------------------------------ fused forwards
+
+
+def fused_experts_forward(mod, hidden_states, top_k_index, top_k_weights):
+    """Fused inference forward of a bare ``ExpertsNbit`` (``fast.py:100-160``)."""
+    if _wants_reference(mod, hidden_states):
+        return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+    compute_dtype = mod.compute_dtype if mod.compute_dtype is not None else hidden_states.dtype
+    if compute_dtype not in (torch.bfloat16, torch.float16):
+        return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+    if mod.gate_up_proj.numel() == 0 or mod.down_proj.numel() == 0:
+        return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+
+    input_dtype = hidden_states.dtype
+    x = hidden_states.to(compute_dtype)
+    tokens = x.shape[0]
+    k = top_k_index.shape[1]
+    hidden = mod._down_shape[0]
+    if tokens == 0:
+        return torch.zeros(0, hidden, dtype=input_dtype, device=x.device)
+    w1, w2 = _qweights(mod)
+    epi = _fused_epilogue(mod)
+    if epi is not None:
+        code, limit = epi
+        return ops.moe_forward(x, top_k_index, top_k_weights, w1, w2, code, input_dtype, limit=limit,
+                               path=_kernel_path)
+    # custom epilogue: unfused GEMMs around the base's own Python epilogue
+    M = tokens * k
+    rb = ops.route(top_k_index, mod.num_experts)
+    up = ops.grouped_gemm(x, w1, rb, tokens, M, N.EPI_NONE, gather_k=k, path=_kernel_path)
+    h = _epilogue(mod, up).to(compute_dtype).contiguous()
+    down = ops.grouped_gemm(h, w2, rb, tokens, M, N.EPI_NONE, path=_kernel_path)
+    return ops.combine(down, rb, top_k_weights, tokens, k, input_dtype)
+
+
+def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
+    """Fused inference forward of an ``ExpertsLoRA`` (``fast.py:163-257``): grouped GEMMs over the
+    expert-sorted rows with the low-rank delta added per expert group before the base's
+    epilogue. The group sizes come to the host once (as in the reference) to slice the groups."""
+    base = mod.base
+    if _wants_reference(mod, hidden_states):
+        return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+    if mod.training:
+        return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+    compute_dtype = base.compute_dtype if base.compute_dtype is not None else hidden_states.dtype
+    if compute_dtype not in (torch.bfloat16, torch.float16):
+        return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+    if base.gate_up_proj.numel() == 0 or base.down_proj.numel() == 0:
+        return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+
+    input_dtype = hidden_states.dtype
+    x = hidden_states.to(compute_dtype)
+    tokens = x.shape[0]
+    k = top_k_index.shape[1]
+    hidden = base._down_shape[0]
+    if tokens == 0:
+        return torch.zeros(0, hidden, dtype=input_dtype, device=x.device)
+    E = base.num_experts
+    M = tokens * k
+    w1, w2 = _qweights(base)
+    rb = ops.route(top_k_index, E)
+    offsets = rb.offsets.tolist()
+    a_cat = x.index_select(0, (rb.sorted_flat[:M] // k).long())
+    up = ops.grouped_gemm(x, w1, rb, tokens, M, N.EPI_NONE, gather_k=k, path=_kernel_path)
+    active = [e for e in range(E) if offsets[e + 1] > offsets[e]]
+    for e in active:
+        s, t = offsets[e], offsets[e + 1]
+        up[s:t] += mod._lora(a_cat[s:t], mod.gate_up_lora_A[e], mod.gate_up_lora_B[e])
+    h = _epilogue(base, up).to(compute_dtype).contiguous()
+    down = ops.grouped_gemm(h, w2, rb, tokens, M, N.EPI_NONE, path=_kernel_path)
+    for e in active:
+        s, t = offsets[e], offsets[e + 1]
+        down[s:t] += mod._lora(h[s:t], mod.down_lora_A[e], mod.down_lora_B[e])
+    return ops.combine(down, rb, top_k_weights, tokens, k, input_dtype)
+
+
+def fused_mxfp4_forward(mod, hidden_states, top_k_index, top_k_weights):
+    """Fused inference forward of a ``GptOssExpertsMxfp4``: MXFP4 decode in both GEMMs, gate_up
+    bias + clamped GLU fused into the first, down bias into the second, the deterministic
+    combine (the grouped path of ``hot_residency.py:72-80`` / ``nvme_experts.py:805-868``)."""
+    if _wants_reference(mod, hidden_states):
+        return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+    cd = mod.compute_dtype if mod.compute_dtype is not None else hidden_states.dtype
+    if cd not in (torch.bfloat16, torch.float16) or mod.gate_up_proj.numel() == 0:
+        return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+    input_dtype = hidden_states.dtype
+    x = hidden_states.to(cd)
+    if x.shape[0] == 0:
+        return torch.zeros(0, mod.hidden_dim, dtype=input_dtype, device=x.device)
+    E = mod.num_experts
+    n1, k1 = mod._gate_up_shape
+    n2, k2 = mod._down_shape
+    w1 = ops.mxfp4_qweight(mod.gate_up_proj, mod.gate_up_absmax, n1, k1, num_experts=E,
+                           bias=mod.gate_up_bias.to(cd))
+    w2 = ops.mxfp4_qweight(mod.down_proj, mod.down_absmax, n2, k2, num_experts=E, bias=mod.down_bias.to(cd))
+    return ops.moe_forward(x, top_k_index, top_k_weights, w1, w2, N.EPI_GPTOSS, input_dtype, alpha=mod.alpha,
+                           limit=mod.limit, path=_kernel_path)
+
+
+# ------------------------------------------------------------------------- patching
+
+
+def enable_fast(model, verbose: bool = False) -> int:
+    """Patch every eligible expert module under ``model`` (or ``model`` itself); returns the count
+    (``fast.py:281-411``)."""
+    stock_forwards = {ExpertsNbit.forward, Experts4bit.forward}
+    mods = list(model.modules()) if hasattr(model, "modules") else [model]
+    patched = 0
+
+    wrapped_bases = {id(m.base) for m in mods if isinstance(m, ExpertsLoRA)}
+    for mod in mods:
+        if not isinstance(mod, ExpertsLoRA):
+            continue
+        if type(mod).forward is not ExpertsLoRA.forward:
+            if verbose:
+                print(f"[e4b.fast] skip {type(mod).__name__}: custom forward")
+            continue
+        if not isinstance(mod.base, ExpertsNbit):
+            if verbose:
+                print(f"[e4b.fast] skip {type(mod).__name__}: base {type(mod.base).__name__} is not an ExpertsNbit")
+            continue
+        reason = _eligible(mod.base)
+        if reason is not None:
+            if verbose:
+                print(f"[e4b.fast] skip {type(mod).__name__}: {reason}")
+            continue
+        if type(mod.base).forward not in stock_forwards and not hasattr(mod.base, "_apply_gate"):
+            if verbose:
+                print(f"[e4b.fast] skip {type(mod).__name__}: base {type(mod.base).__name__} has a custom forward")
+            continue
+        if hasattr(mod, "_e4b_fast_ref"):
+            continue
+        mod._e4b_fast_ref = mod.forward
+        mod.forward = fused_experts_lora_forward.__get__(mod)
+        patched += 1
+
+    for mod in mods:
+        if isinstance(mod, GptOssExpertsMxfp4):
+            if id(mod) in wrapped_bases:
+                continue
+            reason = _eligible_mxfp4(mod)
+            if reason is not None:
+                if verbose:
+                    print(f"[e4b.fast] skip {type(mod).__name__}: {reason}")
+                continue
+            if hasattr(mod, "_e4b_fast_ref"):
+                continue
+            mod._e4b_fast_ref = mod.forward
+            mod.forward = fused_mxfp4_forward.__get__(mod)
+            patched += 1
+            continue
+        if not isinstance(mod, ExpertsNbit):
+            continue
+        if id(mod) in wrapped_bases:
+            if verbose:
+                print(f"[e4b.fast] skip {type(mod).__name__}: wrapped by a patched ExpertsLoRA "
+                      "(its forward is never called)")
+            continue
+        if type(mod).forward not in stock_forwards and not hasattr(mod, "_apply_gate"):
+            if verbose:
+                print(f"[e4b.fast] skip {type(mod).__name__}: custom forward")
+            continue
+        reason = _eligible(mod)
+        if reason is not None:
+            if verbose:
+                print(f"[e4b.fast] skip {type(mod).__name__}: {reason}")
+            continue
+        skip = None
+        for attr, what in (("_hot_residency", "hot_residency"), ("_e4b_cold_ref", "cold engine"),
+                           ("_e4b_pipe_ref", "pipelined residency"), ("_e4b_mxfp4_ref", "mxfp4 NVMe residency")):
+            if hasattr(mod, attr):
+                skip = what
+                break
+        if skip is not None:
+            if verbose:
+                print(f"[e4b.fast] skip {type(mod).__name__}: {skip} enabled -- disable it first")
+            continue
+        if hasattr(mod, "_e4b_fast_ref"):
+            continue
+        mod._e4b_fast_ref = mod.forward
+        mod.forward = fused_experts_forward.__get__(mod)
+        patched += 1
+
+    if patched and getattr(model, "training", False):
+        import warnings
+
+        warnings.warn(
+            f"[e4b.fast] model is in TRAINING mode: fused_experts_lora_forward falls back to the reference "
+            f"path while `training` is set, so all {patched} patch(es) will be bypassed and the fused kernel "
+            "will not run. Call model.eval() before inference.",
+            RuntimeWarning, stacklevel=2)
+    return patched
+
+
+def disable_fast(model) -> int:
+    """Undo :func:`enable_fast`; returns the number of modules restored (``fast.py:414-423``)."""
+    mods = model.modules() if hasattr(model, "modules") else [model]
+    restored = 0
+    for mod in mods:
+        if hasattr(mod, "_e4b_fast_ref"):
+            mod.forward = mod._e4b_fast_ref
+            del mod._e4b_fast_ref
+            restored += 1
+    return restored

@@ -1,0 +1,293 @@
+"""torch-tensor wrappers over the C ABI (``include/e4b_amd.h``).
+
+Tensors are handed to the library as raw device pointers, the stream is torch's current HIP
+stream, and every output / workspace is allocated by torch's caching allocator. No function
+here synchronises the device, and none computes anything itself: a missing library raises
+(:class:`experts4bit_qlora_amd._native.NativeUnavailable`).
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _native as N
+
+_DT = {torch.bfloat16: N.BF16, torch.float16: N.FP16, torch.float32: N.FP32}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DT[dt]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dt}") from None
+
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("the MI355X kernels need tensors on the HIP device")
+
+
+@dataclass
+class QW:
+    """A 4-bit weight stack as the kernels see it (tensors kept alive alongside the struct)."""
+
+    fmt: int
+    num_experts: int
+    n: int
+    k: int
+    packed: torch.Tensor
+    absmax: torch.Tensor
+    absmax2: torch.Tensor | None = None
+    offset: torch.Tensor | None = None
+    code: torch.Tensor | None = None
+    code2: torch.Tensor | None = None
+    bias: torch.Tensor | None = None
+
+    def struct(self) -> N.QWeight:
+        s = N.QWeight()
+        s.format = self.fmt
+        s.num_experts = self.num_experts
+        s.n = self.n
+        s.k = self.k
+        s.packed = _ptr(self.packed)
+        s.absmax = _ptr(self.absmax)
+        s.absmax2 = _ptr(self.absmax2)
+        s.offset = _ptr(self.offset)
+        s.code = _ptr(self.code)
+        s.code2 = _ptr(self.code2)
+        s.bias = _ptr(self.bias)
+        return s
+
+
+def nf4_qweight(packed, absmax, code, n, k, num_experts=None, bias=None) -> QW:
+    """NF4 stack: ``packed`` u8 (any shape, ``E*n*k/2`` bytes), ``absmax`` fp32 ``E*n*k/64``."""
+    E = num_experts if num_experts is not None else packed.shape[0]
+    return QW(N.FMT_NF4, E, n, k, packed.contiguous(), absmax.contiguous().float(), code=code.contiguous().float(),
+              bias=None if bias is None else bias.contiguous())
+
+
+def nf4_dq_qweight(packed, qabsmax, absmax2, offset, code, code2, n, k, num_experts=None, bias=None) -> QW:
+    E = num_experts if num_experts is not None else packed.shape[0]
+    return QW(N.FMT_NF4_DQ, E, n, k, packed.contiguous(), qabsmax.contiguous(), absmax2.contiguous().float(),
+              offset.contiguous().float(), code.contiguous().float(), code2.contiguous().float(),
+              None if bias is None else bias.contiguous())
+
+
+def mxfp4_qweight(blocks, scales, n, k, num_experts=None, bias=None) -> QW:
+    E = num_experts if num_experts is not None else blocks.shape[0]
+
+    def u8(t):
+        return t if t.dtype == torch.uint8 else t.view(torch.uint8)
+
+    return QW(N.FMT_MXFP4, E, n, k, u8(blocks).contiguous(), u8(scales).contiguous(),
+              bias=None if bias is None else bias.contiguous())
+
+
+# ------------------------------------------------------------------------------ dequant
+
+
+def dequant(qw: QW, expert_begin: int = 0, expert_count: int | None = None, dtype=torch.float32) -> torch.Tensor:
+    """Bit-exact dense ``[count, n, k]`` decode of experts ``[begin, begin+count)``."""
+    _require_cuda(qw.packed)
+    L = N.lib()
+    count = qw.num_experts - expert_begin if expert_count is None else expert_count
+    out = torch.empty(count, qw.n, qw.k, dtype=dtype, device=qw.packed.device)
+    s = qw.struct()
+    N.check("e4b_dequant", L.e4b_dequant(ctypes.byref(s), expert_begin, count, dtype_code(dtype), out.data_ptr(),
+                                         _stream(out.device)))
+    return out
+
+
+# ------------------------------------------------------------------------------ routing
+
+
+@dataclass
+class RoutingBuffers:
+    """Device routing (``e4b_routing``) for ``M = tokens * top_k`` rows."""
+
+    sorted_flat: torch.Tensor
+    inv: torch.Tensor
+    offsets: torch.Tensor
+    active: torch.Tensor
+    tiles: torch.Tensor
+    meta: torch.Tensor
+    max_tiles: int
+    tile_m: int
+
+    def struct(self) -> N.Routing:
+        r = N.Routing()
+        r.sorted_flat = self.sorted_flat.data_ptr()
+        r.inv = self.inv.data_ptr()
+        r.offsets = self.offsets.data_ptr()
+        r.active = self.active.data_ptr()
+        r.tiles = self.tiles.data_ptr()
+        r.meta = self.meta.data_ptr()
+        r.max_tiles = self.max_tiles
+        r.tile_m = self.tile_m
+        return r
+
+
+def mfma_tile_m() -> int:
+    return int(N.lib().e4b_mfma_tile_m())
+
+
+def route(top_k_index: torch.Tensor, num_experts: int, tile_m: int | None = None) -> RoutingBuffers:
+    """Stable token->expert permutation on the device (no host sync)."""
+    _require_cuda(top_k_index)
+    L = N.lib()
+    idx = top_k_index.to(torch.int64).contiguous()
+    T, k = idx.shape
+    M = T * k
+    tm = tile_m or mfma_tile_m()
+    max_tiles = max(1, -(-M // tm) + min(num_experts, M))
+    dev = idx.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    rb = RoutingBuffers(
+        sorted_flat=torch.empty(max(M, 1), **i32),
+        inv=torch.empty(max(M, 1), **i32),
+        offsets=torch.empty(num_experts + 1, **i32),
+        active=torch.empty(num_experts, **i32),
+        tiles=torch.empty(2 * max_tiles, **i32),
+        meta=torch.empty(4, **i32),
+        max_tiles=max_tiles,
+        tile_m=tm,
+    )
+    rs = rb.struct()
+    N.check("e4b_route", L.e4b_route(idx.data_ptr(), T, k, num_experts, ctypes.byref(rs), _stream(dev)))
+    return rb
+
+
+# -------------------------------------------------------------------------------- GEMMs
+
+
+def grouped_gemm(a: torch.Tensor, qw: QW, rb: RoutingBuffers, tokens: int, M: int, epilogue: int = N.EPI_NONE,
+                 gather_k: int = 0, alpha: float = 1.702, limit: float = 7.0, path: int = N.PATH_AUTO) -> torch.Tensor:
+    """Grouped GEMM over expert-sorted rows with an optional fused epilogue; ``[M, n_out]``."""
+    _require_cuda(a, qw.packed)
+    L = N.lib()
+    a = a.contiguous()
+    gated = epilogue in (N.EPI_SWIGLU, N.EPI_CLAMP_SWIGLU, N.EPI_GPTOSS)
+    n_out = qw.n // 2 if gated else qw.n
+    out = torch.empty(M, n_out, dtype=a.dtype, device=a.device)
+    s = qw.struct()
+    rs = rb.struct()
+    N.check("e4b_grouped_gemm",
+            L.e4b_grouped_gemm(a.data_ptr(), dtype_code(a.dtype), gather_k, ctypes.byref(s), ctypes.byref(rs),
+                               tokens, M, epilogue, float(alpha), float(limit), path, out.data_ptr(),
+                               _stream(a.device)))
+    return out
+
+
+def combine(down: torch.Tensor, rb: RoutingBuffers, top_k_weights: torch.Tensor, tokens: int, top_k: int,
+            out_dtype: torch.dtype) -> torch.Tensor:
+    """Deterministic weighted k-sum back to token order (``[tokens, hidden]`` in ``out_dtype``)."""
+    _require_cuda(down, top_k_weights)
+    L = N.lib()
+    H = down.shape[1]
+    w = top_k_weights.contiguous()
+    out = torch.empty(tokens, H, dtype=out_dtype, device=down.device)
+    N.check("e4b_combine",
+            L.e4b_combine(down.data_ptr(), dtype_code(down.dtype), rb.inv.data_ptr(), w.data_ptr(),
+                          dtype_code(w.dtype), tokens, top_k, H, out.data_ptr(), dtype_code(out_dtype),
+                          _stream(down.device)))
+    return out
+
+
+def moe_forward(hidden: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: torch.Tensor, w1: QW, w2: QW,
+                epilogue: int, out_dtype: torch.dtype, alpha: float = 1.702, limit: float = 7.0,
+                path: int = N.PATH_AUTO) -> torch.Tensor:
+    """The whole fused expert forward in one C-ABI call (route, gate_up+epilogue, down, combine)."""
+    _require_cuda(hidden, top_k_index, top_k_weights, w1.packed, w2.packed)
+    L = N.lib()
+    x = hidden.contiguous()
+    idx = top_k_index.to(torch.int64).contiguous()
+    w = top_k_weights.contiguous()
+    T, k = idx.shape
+    ws_bytes = int(L.e4b_moe_workspace_bytes(T, k, w1.num_experts, w1.n, w2.n, epilogue, dtype_code(x.dtype)))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    out = torch.empty(T, w2.n, dtype=out_dtype, device=x.device)
+    s1, s2 = w1.struct(), w2.struct()
+    N.check("e4b_moe_forward",
+            L.e4b_moe_forward(x.data_ptr(), dtype_code(x.dtype), T, idx.data_ptr(), w.data_ptr(), dtype_code(w.dtype),
+                              k, ctypes.byref(s1), ctypes.byref(s2), epilogue, float(alpha), float(limit), path,
+                              ws.data_ptr(), ws_bytes, out.data_ptr(), dtype_code(out_dtype), _stream(x.device)))
+    return out
+
+
+# ------------------------------------------------- the nf4_grouped / mxfp4_grouped API shape
+
+
+def _routing_from_sizes(sizes, expert_ids, num_experts: int, device) -> tuple[RoutingBuffers, int]:
+    """Host-described groups (the reference's ``sizes`` / ``expert_ids`` lists) -> device routing."""
+    sizes = [int(s) for s in sizes]
+    ids = [int(e) for e in (expert_ids.tolist() if torch.is_tensor(expert_ids) else expert_ids)]
+    if len(sizes) != len(ids):
+        raise ValueError("sizes and expert_ids differ in length")
+    if any(s < 0 for s in sizes) or any(not 0 <= e < num_experts for e in ids):
+        raise ValueError("bad group sizes / expert ids")
+    if len(set(ids)) != len(ids) or ids != sorted(ids):
+        raise ValueError("expert_ids must be strictly ascending (one group per expert)")
+    M = sum(sizes)
+    tm = mfma_tile_m()
+    counts = [0] * num_experts
+    for e, s in zip(ids, sizes):
+        counts[e] = s
+    offsets = [0]
+    for c in counts:
+        offsets.append(offsets[-1] + c)
+    active = [e for e in range(num_experts) if counts[e] > 0]
+    tiles = []
+    for e in active:
+        for t in range(-(-counts[e] // tm)):
+            tiles += [e, offsets[e] + t * tm]
+    max_tiles = max(1, len(tiles) // 2)
+    i32 = dict(dtype=torch.int32, device=device)
+    ar = torch.arange(max(M, 1), **i32)
+    rb = RoutingBuffers(
+        sorted_flat=ar, inv=ar,
+        offsets=torch.tensor(offsets, **i32),
+        active=torch.tensor(active + [0] * (num_experts - len(active)), **i32),
+        tiles=torch.tensor(tiles or [0, 0], **i32),
+        meta=torch.tensor([len(tiles) // 2, len(active), 0, tm], **i32),
+        max_tiles=max_tiles, tile_m=tm,
+    )
+    return rb, M
+
+
+def gemm_4bit_grouped(a: torch.Tensor, w: torch.Tensor, absmax: torch.Tensor, sizes, expert_ids,
+                      code: torch.Tensor | None = None) -> torch.Tensor:
+    """Drop-in for ``nf4_grouped.gemm_4bit_grouped(a, w[E,N,K/2], absmax[E,N,K/64], sizes, ids)``
+    (the call shape at engines/fast.py:137-156): ``[M, N]`` in ``a``'s dtype."""
+    from .quant import code_4bit
+
+    E, n, kh = w.shape
+    c = code if code is not None else code_4bit("nf4", device=w.device)
+    rb, M = _routing_from_sizes(sizes, expert_ids, E, w.device)
+    if a.shape[0] != M:
+        raise ValueError(f"a has {a.shape[0]} rows but sizes sum to {M}")
+    qw = nf4_qweight(w, absmax, c, n, kh * 2, num_experts=E)
+    tokens = max(sizes) if len(sizes) else 0
+    return grouped_gemm(a, qw, rb, tokens, M)
+
+
+def gemm_mxfp4_grouped(a: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, sizes, expert_ids) -> torch.Tensor:
+    """Drop-in for ``mxfp4_grouped.gemm_mxfp4_grouped(a, blocks[E,N,K/2], scales[E,N,K/32], sizes, ids)``
+    (engines/nvme_experts.py:852-865)."""
+    E, n, kh = blocks.shape
+    rb, M = _routing_from_sizes(sizes, expert_ids, E, blocks.device)
+    if a.shape[0] != M:
+        raise ValueError(f"a has {a.shape[0]} rows but sizes sum to {M}")
+    qw = mxfp4_qweight(blocks, scales, n, kh * 2, num_experts=E)
+    tokens = max(sizes) if len(sizes) else 0
+    return grouped_gemm(a, qw, rb, tokens, M)

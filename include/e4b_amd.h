@@ -1,0 +1,143 @@
+/* e4b_amd.h -- C ABI of the MI355X (gfx950) frozen-expert MoE forward.
+ *
+ * The drop-in boundary for the hot path that experts4bit-qlora's `enable_fast(model)` routes
+ * `ExpertsNbit` / `Experts4bit` modules through (pjordanandrsn/experts4bit-qlora v0.19.1).
+ * Plain pointers and sizes only: every device pointer is HIP device memory, every call is
+ * asynchronous on `stream`, nothing allocates device memory (callers pass outputs and any
+ * workspace), and no C++ exception crosses the ABI. Each function returns E4B_OK (0) or a
+ * negative status; `e4b_last_error()` then describes the failure (per host thread).
+ *
+ * Weight layouts (per expert, row = one output feature, `k` input features contiguous):
+ *   NF4      packed u8 [E, n, k/2], FIRST element of a pair in the HIGH nibble;
+ *            absmax fp32 [E, n*k/64]  (one scale per 64 consecutive elements of a row).
+ *   NF4_DQ   as NF4, but absmax is u8 codes [E, n*k/64] into `code2` (256 fp32), with
+ *            absmax2 fp32 [E, ceil(n*k/64/256)] and offset fp32 [E]:
+ *            absmax[b] = fp32(fp32(code2[q[b]] * absmax2[b/256]) + offset).
+ *   MXFP4    packed u8 [E, n, k/2], FIRST element in the LOW nibble (e2m1);
+ *            absmax = e8m0 u8 [E, n, k/32] (value * 2^(s-127)).
+ * Activations are bf16 or fp16 (the module's compute dtype); every GEMM accumulates in fp32.
+ */
+#ifndef E4B_AMD_H
+#define E4B_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum e4b_status {
+  E4B_OK = 0,
+  E4B_EINVAL = -1,       /* bad argument (null pointer, shape, alignment, enum) */
+  E4B_EUNSUPPORTED = -2, /* valid but not implemented (e.g. k not a multiple of 64) */
+  E4B_ELAUNCH = -3,      /* a kernel launch failed (see e4b_last_error) */
+  E4B_ESPACE = -4        /* workspace too small */
+};
+
+enum e4b_format { E4B_FMT_NF4 = 0, E4B_FMT_NF4_DQ = 1, E4B_FMT_MXFP4 = 2 };
+enum e4b_dtype { E4B_BF16 = 0, E4B_FP16 = 1, E4B_FP32 = 2 };
+
+/* Activation applied between the two projections (fused into the gate_up GEMM). */
+enum e4b_epilogue {
+  E4B_EPI_NONE = 0,         /* plain GEMM output (the reference's `gemm_4bit_grouped`) */
+  E4B_EPI_SWIGLU = 1,       /* silu(gate) * up, gate = rows [0, n/2), up = rows [n/2, n) */
+  E4B_EPI_ACT = 2,          /* silu(proj)  (has_gate = False) */
+  E4B_EPI_CLAMP_SWIGLU = 3, /* silu(min(gate, L)) * clamp(up, -L, L) in fp32 (L <= 0: no clamp) */
+  E4B_EPI_GPTOSS = 4        /* (clamp(up,-L,L) + 1) * (g * sigmoid(alpha * g)), g = min(gate, L),
+                               after adding the per-expert gate_up bias */
+};
+
+/* Kernel-path selection flags for the grouped GEMMs (0 = automatic by token count). */
+enum e4b_flags { E4B_PATH_AUTO = 0, E4B_PATH_GEMV = 1, E4B_PATH_MFMA = 2 };
+
+typedef struct e4b_qweight {
+  int32_t format;        /* e4b_format */
+  int32_t num_experts;   /* E */
+  int64_t n;             /* output features per expert */
+  int64_t k;             /* input features per expert (multiple of 64) */
+  const uint8_t* packed; /* [E, n, k/2] */
+  const void* absmax;    /* NF4: fp32 [E, n*k/64]; NF4_DQ: u8 [E, n*k/64]; MXFP4: u8 [E, n, k/32] */
+  const float* absmax2;  /* NF4_DQ only: fp32 [E, ceil(n*k/64/256)] */
+  const float* offset;   /* NF4_DQ only: fp32 [E] */
+  const float* code;     /* NF4 / NF4_DQ: fp32 [16] 4-bit code (the module's `code` buffer) */
+  const float* code2;    /* NF4_DQ only: fp32 [256] second-level code */
+  const void* bias;      /* optional [E, n] in the activation dtype (gpt-oss), else NULL */
+} e4b_qweight;
+
+/* Device-side routing of M = tokens * top_k (token, slot) assignments. */
+typedef struct e4b_routing {
+  int32_t* sorted_flat; /* [M]     flat index (token*k + slot) of each expert-sorted row */
+  int32_t* inv;         /* [M]     sorted row of each flat index (-1: dropped, id out of range) */
+  int32_t* offsets;     /* [E + 1] exclusive prefix of per-expert row counts */
+  int32_t* active;      /* [E]     ascending ids of experts with >= 1 row */
+  int32_t* tiles;       /* [2 * max_tiles] (expert, first sorted row) of each tile_m-row tile */
+  int32_t* meta;        /* [4]     num_tiles, num_active, num_dropped, tile_m */
+  int32_t max_tiles;    /* capacity of `tiles`: >= ceil(M / tile_m) + min(E, M) */
+  int32_t tile_m;       /* rows per tile (the MFMA path uses 64) */
+} e4b_routing;
+
+/* Library version string and the last error message of the calling host thread. */
+const char* e4b_version(void);
+const char* e4b_last_error(void);
+
+/* Rows per tile the grouped MFMA GEMM expects in e4b_routing.tile_m. */
+int32_t e4b_mfma_tile_m(void);
+
+/* Dequantize experts [expert_begin, expert_begin + expert_count) to a dense row-major
+ * [count, n, k] tensor in out_dtype (E4B_BF16 / E4B_FP16 / E4B_FP32). Bit-exact: one fp32
+ * product code[nib] * absmax, one round-to-nearest-even into out_dtype.
+ * Replaces: ExpertsNbit._dequantize_expert (experts4bit_qlora/_vendor/experts.py:428-457,
+ * bitsandbytes dequantize_4bit; pure-torch form engines/cold_engine.py:104-115) and, for
+ * MXFP4, formats/mxfp4.py:35-105 dequantize_mxfp4 before its final transpose. */
+int e4b_dequant(const e4b_qweight* w, int32_t expert_begin, int32_t expert_count, int32_t out_dtype,
+                void* out, hipStream_t stream);
+
+/* Token -> expert permutation, bit-exact to a stable argsort of top_k_index.reshape(-1).
+ * Replaces: engines/fast.py:125-133 (argsort(stable), //k, %k, bincount, nonzero, .tolist());
+ * nothing is copied to the host. Ids outside [0, E) are dropped (counted in meta[2]). */
+int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t num_experts,
+              const e4b_routing* rt, hipStream_t stream);
+
+/* Grouped GEMM over the expert-sorted rows: out[r, :] = epilogue(a_row(r) @ deq(W[e(r)]).T).
+ * a_row(r) = a[sorted_flat[r] / gather_k] when gather_k > 0 (the gather of fast.py:135 fused
+ * into the A loads), else a[r]. out is [M, n] (E4B_EPI_NONE) or [M, n/2] (gated epilogues) or
+ * [M, n] (E4B_EPI_ACT), in act_dtype. The per-expert bias (w->bias) is added to the rounded
+ * projection before the epilogue, as gpt-oss does.
+ * Replaces: nf4_grouped.gemm_4bit_grouped (engines/fast.py:137-143, 150-156, 220-226, 242-248)
+ * and mxfp4_grouped.gemm_mxfp4_grouped (engines/nvme_experts.py:852-865), plus the epilogue
+ * of lora.py:102-128 / hot_residency.py:72-80 fused into the same launch. */
+int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e4b_qweight* w,
+                     const e4b_routing* rt, int64_t tokens, int64_t M, int32_t epilogue, float alpha,
+                     float limit, int32_t flags, void* out, hipStream_t stream);
+
+/* Deterministic weighted combine back to token order:
+ * out[t, :] = out_dtype( sum_{s<k} float(down[inv[t*k+s], :]) * float(top_k_weights[t, s]) ),
+ * the slots summed in slot order in fp32 -- unique writes + a fixed-axis sum, never atomics.
+ * Replaces: engines/fast.py:158 and _scatter_combine at fast.py:260-278. */
+int e4b_combine(const void* down, int32_t act_dtype, const int32_t* inv, const void* top_k_weights,
+                int32_t weight_dtype, int64_t tokens, int32_t top_k, int64_t hidden, void* out,
+                int32_t out_dtype, hipStream_t stream);
+
+/* Bytes of workspace e4b_moe_forward needs for these sizes. */
+size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts, int64_t n1,
+                               int64_t n2, int32_t epilogue, int32_t act_dtype);
+
+/* The whole frozen-expert forward: route -> gate_up (+epilogue) -> down (+bias) -> combine.
+ * hidden [tokens, w1->k] in act_dtype; top_k_index [tokens, top_k] int64; top_k_weights
+ * [tokens, top_k] in weight_dtype; out [tokens, w2->n] in out_dtype.
+ * Replaces: engines/fast.py:100-160 fused_experts_forward (the bare-module forward that
+ * enable_fast binds, fast.py:371-372), with no device->host synchronisation. */
+int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                    const void* top_k_weights, int32_t weight_dtype, int32_t top_k, const e4b_qweight* w1,
+                    const e4b_qweight* w2, int32_t epilogue, float alpha, float limit, int32_t flags,
+                    void* workspace, size_t workspace_bytes, void* out, int32_t out_dtype,
+                    hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* E4B_AMD_H */

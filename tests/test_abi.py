@@ -1,0 +1,157 @@
+"""The C-ABI library: it loads, exports every symbol ``include/e4b_amd.h`` declares, and its host
+logic rejects bad arguments with a status and a message -- all without touching a GPU (every
+call below returns before any HIP launch)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from experts4bit_qlora_amd import _native as N
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "e4b_amd.h")
+
+
+def _declared():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(e4b_[a-z_0-9]+)\s*\(", src)))
+
+
+def test_library_is_built_and_loads():
+    assert N.available(), N._load_error
+    assert N.lib().e4b_version().startswith(b"e4b_amd")
+
+
+def test_exports_every_declared_symbol():
+    declared = _declared()
+    assert declared, "no declarations parsed from the header"
+    assert sorted(N.EXPORTS) == declared
+    raw = ctypes.CDLL(N.LIB_PATH)
+    for name in declared:
+        assert hasattr(raw, name), f"{name} declared in include/e4b_amd.h but not exported"
+
+
+def test_enums_match_header():
+    src = open(HEADER).read()
+    for name, val in (("E4B_FMT_NF4", N.FMT_NF4), ("E4B_FMT_NF4_DQ", N.FMT_NF4_DQ), ("E4B_FMT_MXFP4", N.FMT_MXFP4),
+                      ("E4B_BF16", N.BF16), ("E4B_FP16", N.FP16), ("E4B_FP32", N.FP32),
+                      ("E4B_EPI_NONE", N.EPI_NONE), ("E4B_EPI_SWIGLU", N.EPI_SWIGLU), ("E4B_EPI_ACT", N.EPI_ACT),
+                      ("E4B_EPI_CLAMP_SWIGLU", N.EPI_CLAMP_SWIGLU), ("E4B_EPI_GPTOSS", N.EPI_GPTOSS),
+                      ("E4B_PATH_AUTO", N.PATH_AUTO), ("E4B_PATH_GEMV", N.PATH_GEMV),
+                      ("E4B_PATH_MFMA", N.PATH_MFMA)):
+        m = re.search(rf"\b{name}\s*=\s*(-?\d+)", src)
+        assert m and int(m.group(1)) == val, name
+
+
+def test_struct_layouts():
+    assert ctypes.sizeof(N.QWeight) == 4 + 4 + 8 + 8 + 7 * 8
+    assert ctypes.sizeof(N.Routing) == 6 * 8 + 4 + 4
+
+
+def _qw(**kw):
+    s = N.QWeight()
+    s.format, s.num_experts, s.n, s.k = kw.get("format", N.FMT_NF4), kw.get("E", 2), kw.get("n", 64), kw.get("k", 64)
+    s.packed = kw.get("packed", 4096)
+    s.absmax = kw.get("absmax", 8192)
+    s.code = kw.get("code", 16384)
+    return s
+
+
+def _err():
+    return N.lib().e4b_last_error().decode()
+
+
+def test_dequant_rejects_bad_arguments():
+    L = N.lib()
+    assert L.e4b_dequant(None, 0, 1, N.FP32, 4096, None) == -1
+    assert "NULL" in _err()
+    s = _qw(k=96)
+    assert L.e4b_dequant(ctypes.byref(s), 0, 1, N.FP32, 4096, None) == -2
+    assert "multiple of 64" in _err()
+    s = _qw()
+    assert L.e4b_dequant(ctypes.byref(s), 1, 2, N.FP32, 4096, None) == -1
+    assert "expert range" in _err()
+    assert L.e4b_dequant(ctypes.byref(s), 0, 1, 7, 4096, None) == -1
+    s = _qw(format=N.FMT_NF4_DQ)
+    assert L.e4b_dequant(ctypes.byref(s), 0, 1, N.FP32, 4096, None) == -1
+    assert "double-quant" in _err()
+    s = _qw(packed=4097)
+    assert L.e4b_dequant(ctypes.byref(s), 0, 1, N.FP32, 4096, None) == -1
+    assert "aligned" in _err()
+    # an empty range is a valid no-op
+    s = _qw()
+    assert L.e4b_dequant(ctypes.byref(s), 0, 0, N.FP32, 4096, None) == 0
+
+
+def _rt(max_tiles=8, tile_m=64):
+    r = N.Routing()
+    r.sorted_flat = r.inv = r.offsets = r.active = r.tiles = r.meta = 4096
+    r.max_tiles, r.tile_m = max_tiles, tile_m
+    return r
+
+
+def test_route_rejects_bad_arguments():
+    L = N.lib()
+    r = _rt()
+    assert L.e4b_route(4096, 4, 2, 0, ctypes.byref(r), None) == -2
+    assert L.e4b_route(4096, 4, 2, 4096, ctypes.byref(r), None) == -2
+    assert L.e4b_route(4096, -1, 2, 8, ctypes.byref(r), None) == -1
+    small = _rt(max_tiles=1)
+    assert L.e4b_route(4096, 100, 8, 64, ctypes.byref(small), None) == -4
+    assert "max_tiles" in _err()
+    bad = _rt()
+    bad.meta = None
+    assert L.e4b_route(4096, 4, 2, 8, ctypes.byref(bad), None) == -1
+
+
+def test_grouped_gemm_rejects_bad_arguments():
+    L = N.lib()
+    s, r = _qw(n=63), _rt()
+    assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r), 1, 2, N.EPI_SWIGLU, 1.0, 7.0, 0,
+                              8192, None) == -1
+    assert "even n" in _err()
+    s = _qw()
+    assert L.e4b_grouped_gemm(4096, N.FP32, 0, ctypes.byref(s), ctypes.byref(r), 1, 2, N.EPI_NONE, 1.0, 7.0, 0,
+                              8192, None) == -1
+    assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r), 1, 2, N.EPI_GPTOSS, 1.0, 7.0, 0,
+                              8192, None) == -1
+    assert "bias" in _err()
+    r32 = _rt(tile_m=32)
+    assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r32), 64, 128, N.EPI_NONE, 1.0, 7.0,
+                              N.PATH_MFMA, 8192, None) == -1
+    assert "tile_m" in _err()
+    # M == 0 is a valid no-op
+    assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r), 0, 0, N.EPI_NONE, 1.0, 7.0, 0,
+                              8192, None) == 0
+
+
+def test_moe_forward_checks_shapes_and_workspace():
+    L = N.lib()
+    w1, w2 = _qw(n=128, k=64), _qw(n=64, k=128)  # gate_up out 128 -> h 64, but down k 128
+    assert L.e4b_moe_forward(4096, N.BF16, 2, 4096, 4096, N.BF16, 2, ctypes.byref(w1), ctypes.byref(w2),
+                             N.EPI_SWIGLU, 1.0, 7.0, 0, 4096, 1 << 20, 8192, N.BF16, None) == -1
+    assert "does not match" in _err()
+    w2 = _qw(n=64, k=64)
+    need = L.e4b_moe_workspace_bytes(2, 2, 2, 128, 64, N.EPI_SWIGLU, N.BF16)
+    assert need > 0
+    assert L.e4b_moe_forward(4096, N.BF16, 2, 4096, 4096, N.BF16, 2, ctypes.byref(w1), ctypes.byref(w2),
+                             N.EPI_SWIGLU, 1.0, 7.0, 0, 4096, need - 1, 8192, N.BF16, None) == -4
+    assert "workspace" in _err()
+    # tokens == 0 is a valid no-op
+    assert L.e4b_moe_forward(4096, N.BF16, 0, 4096, 4096, N.BF16, 2, ctypes.byref(w1), ctypes.byref(w2),
+                             N.EPI_SWIGLU, 1.0, 7.0, 0, 4096, 0, 8192, N.BF16, None) == 0
+
+
+def test_workspace_grows_with_tokens():
+    L = N.lib()
+    a = L.e4b_moe_workspace_bytes(1, 8, 64, 2048, 2048, N.EPI_SWIGLU, N.BF16)
+    b = L.e4b_moe_workspace_bytes(4096, 8, 64, 2048, 2048, N.EPI_SWIGLU, N.BF16)
+    assert b > a and b >= 4096 * 8 * (1024 + 2048) * 2
+
+
+def test_native_error_raises_with_message():
+    with pytest.raises(N.NativeError, match="status -1"):
+        N.lib().e4b_dequant(None, 0, 1, N.FP32, 4096, None)
+        N.check("e4b_dequant", -1)

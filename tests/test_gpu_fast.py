@@ -1,0 +1,517 @@
+"""GPU parity of the drop-in ``enable_fast`` path, mirroring the reference's own tests
+(``tests/test_fast.py``, ``test_fast_lora.py``, ``test_fast_v4.py``,
+``test_fast_expertslora_delegation.py``, ``test_deterministic_scatter.py``) plus the BASELINE
+configurations at their real shapes.
+
+Accuracy bars: against the fp32 oracle over the same dequantized weights, rel-Frobenius <= 1e-2
+and max-abs <= 2e-2 on oracle-RMS-normalised outputs, and no worse than
+``max(2 * reference-loop error, 5e-3)`` (the reference's own ordering rule, test_fast.py:82-87).
+"""
+import numpy as np
+import pytest
+import torch
+
+import experts4bit_qlora_amd as e4b
+from experts4bit_qlora_amd import _native as N
+from experts4bit_qlora_amd import fast as F
+from experts4bit_qlora_amd import ops
+from oracle import moe
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _announce(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.fixture(autouse=True)
+def _auto_path():
+    F.set_kernel_path("auto")
+    yield
+    F.set_kernel_path("auto")
+
+
+def _b_rel(a, b):
+    return ((a.float() - b.float()).abs().max() / b.float().abs().max().clamp_min(1e-6)).item()
+
+
+def _make(E=4, H=128, inter=64, k=2, tokens=16, seed=0, has_gate=True, scale=1.0, dq=False):
+    torch.manual_seed(seed)
+    gate_up = torch.randn(E, 2 * inter if has_gate else inter, H) * scale
+    down = torch.randn(E, H, inter) * scale
+    mod = e4b.Experts4bit.from_float(gate_up.to(DEV), down.to(DEV), compute_dtype=torch.bfloat16, has_gate=has_gate,
+                                     compress_statistics=dq)
+    hs = torch.randn(tokens, H, dtype=torch.bfloat16, device=DEV)
+    logits = torch.randn(tokens, E, device=DEV)
+    top_w, top_i = torch.topk(torch.softmax(logits, -1), k=k, dim=-1)
+    return mod, hs, top_i, top_w.to(torch.bfloat16)
+
+
+def _oracle(mod, hs, top_i, top_w):
+    """fp32 forward over the same dequantized NF4 values (test_fast.py:49-68), CPU oracle."""
+    E = mod.num_experts
+    w1 = np.stack([mod._dequantize_expert(mod.gate_up_proj, mod.gate_up_absmax, mod._gate_up_shape, e,
+                                          torch.float32).cpu().numpy() for e in range(E)])
+    w2 = np.stack([mod._dequantize_expert(mod.down_proj, mod.down_absmax, mod._down_shape, e,
+                                          torch.float32).cpu().numpy() for e in range(E)])
+    epi = "swiglu" if mod.has_gate else "act"
+    return moe.forward_fp32(hs.float().cpu().numpy(), top_i.cpu().numpy(), top_w.float().cpu().numpy(), w1, w2, epi)
+
+
+def _assert_fidelity(fast, ref, oracle, label=""):
+    fro, maxabs, _ = moe.rel_errors(fast.float().cpu().numpy(), oracle)
+    fro_ref, _, _ = moe.rel_errors(ref.float().cpu().numpy(), oracle)
+    assert fro <= 1e-2 and maxabs <= 2e-2, (label, fro, maxabs)
+    assert fro <= max(2 * fro_ref, 5e-3), (label, fro, fro_ref)
+
+
+# ------------------------------------------------------------- test_fast.py equivalents
+
+
+@pytest.mark.parametrize("path", ["auto", "gemv", "mfma"])
+def test_fused_matches_reference(path):
+    _announce(f"fused vs reference path={path}")
+    F.set_kernel_path(path)
+    mod, hs, top_i, top_w = _make()
+    with torch.no_grad():
+        ref = mod(hs, top_i, top_w)
+    assert e4b.enable_fast(mod) == 1
+    with torch.no_grad():
+        fast = mod(hs, top_i, top_w)
+    oracle = _oracle(mod, hs, top_i, top_w)
+    assert fast.shape == ref.shape and fast.dtype == ref.dtype
+    assert _b_rel(fast, ref) < 1.5e-2
+    err_ref = _b_rel(ref, torch.from_numpy(oracle))
+    err_fast = _b_rel(fast, torch.from_numpy(oracle))
+    assert err_fast <= max(2 * err_ref, 5e-3), (err_fast, err_ref)
+    assert e4b.disable_fast(mod) == 1
+    with torch.no_grad():
+        back = mod(hs, top_i, top_w)
+    assert torch.equal(back, ref)
+
+
+def test_training_path_falls_back_and_backprops():
+    _announce("training fallback")
+    mod, hs, top_i, top_w = _make()
+    e4b.enable_fast(mod)
+    x = hs.clone().requires_grad_(True)
+    out = mod(x, top_i, top_w)
+    out.float().sum().backward()
+    assert x.grad is not None and torch.isfinite(x.grad).all()
+    e4b.disable_fast(mod)
+
+
+def test_skips_ineligible_blocksize():
+    mod, *_ = _make()
+    mod.blocksize = 128
+    assert e4b.enable_fast(mod) == 0
+
+
+def test_uneven_routing_and_empty_experts():
+    _announce("uneven routing")
+    mod, hs, top_i, top_w = _make(E=4, k=2, tokens=8, seed=3)
+    top_i = torch.stack([torch.zeros(8, dtype=torch.long), torch.ones(8, dtype=torch.long)], 1).to(DEV)
+    with torch.no_grad():
+        ref = mod(hs, top_i, top_w)
+    e4b.enable_fast(mod)
+    with torch.no_grad():
+        fast = mod(hs, top_i, top_w)
+    assert _b_rel(fast, ref) < 1.5e-2
+    e4b.disable_fast(mod)
+
+
+def test_plain_up_projection_has_gate_false():
+    _announce("has_gate=False")
+    mod, hs, top_i, top_w = _make(has_gate=False, seed=4)
+    with torch.no_grad():
+        ref = mod(hs, top_i, top_w)
+        e4b.enable_fast(mod)
+        fast = mod(hs, top_i, top_w)
+    _assert_fidelity(fast, ref, _oracle(mod, hs, top_i, top_w))
+
+
+def test_custom_activation_runs_unfused_epilogue():
+    _announce("custom activation")
+    mod, hs, top_i, top_w = _make(seed=5)
+    mod.act_fn = torch.nn.functional.gelu
+    with torch.no_grad():
+        ref = mod(hs, top_i, top_w)
+        assert e4b.enable_fast(mod) == 1
+        fast = mod(hs, top_i, top_w)
+    assert _b_rel(fast, ref) < 1.5e-2
+
+
+def test_fp32_input_dtype_round_trips():
+    _announce("fp32 input")
+    mod, hs, top_i, top_w = _make(seed=6)
+    x = hs.float()
+    with torch.no_grad():
+        ref = mod(x, top_i, top_w.float())
+        e4b.enable_fast(mod)
+        fast = mod(x, top_i, top_w.float())
+    assert fast.dtype == torch.float32 and _b_rel(fast, ref) < 1.5e-2
+
+
+def test_fp16_compute_dtype():
+    _announce("fp16 compute")
+    torch.manual_seed(7)
+    gate_up, down = torch.randn(4, 128, 128) * 0.1, torch.randn(4, 128, 64) * 0.1
+    mod = e4b.Experts4bit.from_float(gate_up.to(DEV), down.to(DEV), compute_dtype=torch.float16)
+    hs = torch.randn(10, 128, dtype=torch.float16, device=DEV)
+    top_w, top_i = torch.topk(torch.softmax(torch.randn(10, 4, device=DEV), -1), 2)
+    with torch.no_grad():
+        ref = mod(hs, top_i, top_w.half())
+        e4b.enable_fast(mod)
+        fast = mod(hs, top_i, top_w.half())
+    assert fast.dtype == torch.float16 and _b_rel(fast, ref) < 1.5e-2
+
+
+def test_empty_batch():
+    mod, hs, top_i, top_w = _make()
+    e4b.enable_fast(mod)
+    with torch.no_grad():
+        out = mod(hs[:0], top_i[:0], top_w[:0])
+    assert out.shape == (0, 128)
+
+
+# --------------------------------------------------------------- determinism & sync-free
+
+
+def test_forward_is_bit_stable_across_runs():
+    _announce("bit-stable x25")
+    mod, hs, top_i, top_w = _make(E=8, tokens=64, k=2, seed=8)
+    e4b.enable_fast(mod)
+    with torch.no_grad():
+        first = mod(hs, top_i, top_w)
+        for _ in range(25):
+            assert torch.equal(first, mod(hs, top_i, top_w))
+
+
+def test_bare_fused_forward_never_syncs():
+    _announce("sync-free decode")
+    mod, hs, top_i, top_w = _make(E=8, tokens=1, k=2, seed=9)
+    e4b.enable_fast(mod)
+    with torch.no_grad():
+        mod(hs, top_i, top_w)  # warm the caching allocator
+        torch.cuda.synchronize()
+        torch.cuda.set_sync_debug_mode("error")
+        try:
+            mod(hs, top_i, top_w)
+        finally:
+            torch.cuda.set_sync_debug_mode("default")
+
+
+# ----------------------------------------------------------------------- ExpertsLoRA
+
+
+def _lora(seed=0, E=8, H=128, inter=192):
+    torch.manual_seed(seed)
+    base = e4b.Experts4bit.from_float((torch.randn(E, 2 * inter, H) * 0.1).to(DEV),
+                                      (torch.randn(E, H, inter) * 0.1).to(DEV), compute_dtype=torch.bfloat16)
+    mod = e4b.ExpertsLoRA(base, r=8, alpha=16, dtype=torch.float32).to(DEV)
+    with torch.no_grad():
+        for p in (mod.gate_up_lora_B, mod.down_lora_B):
+            p.normal_(0, 0.02)
+    return mod.eval()
+
+
+def _lora_inputs(n_tok, E=8, H=128, seed=1):
+    torch.manual_seed(seed)
+    hs = torch.randn(n_tok, H, dtype=torch.bfloat16, device=DEV)
+    idx = torch.randint(0, E, (n_tok, 2), device=DEV)
+    wts = torch.rand(n_tok, 2, dtype=torch.bfloat16, device=DEV)
+    return hs, idx, wts
+
+
+def test_lora_patches_wrapper_and_skips_wrapped_base():
+    mod = _lora()
+    assert e4b.enable_fast(mod) == 1
+    assert hasattr(mod, "_e4b_fast_ref") and not hasattr(mod.base, "_e4b_fast_ref")
+    assert e4b.disable_fast(mod) == 1
+
+
+@pytest.mark.parametrize("n_tok", [1, 12])
+def test_lora_fused_matches_reference(n_tok):
+    _announce(f"lora n_tok={n_tok}")
+    mod = _lora()
+    hs, idx, wts = _lora_inputs(n_tok)
+    with torch.no_grad():
+        ref = mod(hs, idx, wts)
+    assert e4b.enable_fast(mod) == 1
+    with torch.no_grad():
+        got = mod(hs, idx, wts)
+    rel = ((got.float() - ref.float()).norm() / ref.float().norm().clamp_min(1e-12)).item()
+    assert got.dtype == ref.dtype and rel < 2e-2, rel
+
+
+def test_lora_training_and_grad_fall_back_exactly():
+    _announce("lora fallback")
+    mod = _lora()
+    hs, idx, wts = _lora_inputs(12)
+    mod.train()
+    with torch.no_grad():
+        ref_train = mod(hs, idx, wts)
+    mod.eval()
+    e4b.enable_fast(mod)
+    mod.train()
+    with torch.no_grad():
+        got = mod(hs, idx, wts)
+    assert torch.equal(got, ref_train)
+    mod.eval()
+    hs_g = hs.clone().requires_grad_(True)
+    out = mod(hs_g, idx, wts)
+    assert out.requires_grad
+    out.float().sum().backward()
+    assert hs_g.grad is not None
+
+
+def test_lora_evicted_placeholder_falls_back_and_raises():
+    mod = _lora()
+    e4b.enable_fast(mod)
+    hs, idx, wts = _lora_inputs(4)
+    real = mod.base.gate_up_proj
+    try:
+        mod.base.gate_up_proj = torch.nn.Parameter(torch.empty(0, dtype=real.dtype, device=real.device),
+                                                   requires_grad=False)
+        with pytest.raises(Exception):
+            with torch.no_grad():
+                mod(hs, idx, wts)
+    finally:
+        mod.base.gate_up_proj = real
+
+
+def test_zero_adapter_delegates_to_patched_base():
+    _announce("lora delegation")
+    torch.manual_seed(0)
+    base = e4b.Experts4bit.from_float(torch.randn(4, 128, 128).to(DEV), torch.randn(4, 128, 64).to(DEV),
+                                      compute_dtype=torch.bfloat16)
+    mod = e4b.ExpertsLoRA(base, r=4, alpha=8).to(DEV).eval()
+    x, idx, w = _lora_inputs(8, E=4)
+    with torch.no_grad():
+        ref = mod(x, idx, w).float().cpu()
+    calls = {"n": 0}
+    orig = F.fused_experts_forward
+
+    def counting(*a, **kw):
+        calls["n"] += 1
+        return orig(*a, **kw)
+
+    F.fused_experts_forward = counting
+    try:
+        assert e4b.enable_fast(mod.base) == 1
+        with torch.no_grad():
+            got = mod(x, idx, w).float().cpu()
+        assert calls["n"] > 0
+        assert not torch.equal(ref, got)
+        assert ((ref - got).abs().max() / got.abs().max().clamp_min(1e-3)) < 5e-2
+    finally:
+        F.fused_experts_forward = orig
+        e4b.disable_fast(mod.base)
+
+
+# ---------------------------------------------------------------- DeepSeek-V4 clamps
+
+
+def _v4(limit, seed, lora=False):
+    from experts4bit_qlora_amd.arch.deepseek_v4 import _DeepseekV4ForwardMixin
+
+    g = torch.Generator().manual_seed(seed)
+    E, H, INTER, K, T = 8, 128, 64, 3, 24
+    base = _DeepseekV4ForwardMixin.from_deepseek_v4(torch.randn(E, 2 * INTER, H, generator=g) * 0.35,
+                                                    torch.randn(E, H, INTER, generator=g) * 0.35, limit=limit,
+                                                    compute_dtype=torch.bfloat16).to(DEV).eval()
+    mod = e4b.ExpertsLoRA(base, r=8, alpha=16, dtype=torch.bfloat16).to(DEV).eval() if lora else base
+    x = (torch.randn(T, H, generator=g) * 1.5).to(torch.bfloat16).to(DEV)
+    val, idx = torch.topk(torch.randn(T, E, generator=g), K, dim=-1)
+    return mod, x, idx.to(DEV), torch.softmax(val, dim=-1).to(torch.bfloat16).to(DEV)
+
+
+@pytest.mark.parametrize("lora", [False, True])
+def test_v4_fused_keeps_the_clamps(lora):
+    _announce(f"v4 clamps lora={lora}")
+    TOL = 1.5e-2
+    mod, x, idx, w = _v4(2.0, seed=6, lora=lora)
+    unclamped, *_ = _v4(0.0, seed=6, lora=lora)
+    with torch.no_grad():
+        ref = mod(x, idx, w)
+        ref_noclamp = unclamped(x, idx, w)
+        assert _b_rel(ref, ref_noclamp) > 10 * TOL
+        assert e4b.enable_fast(mod) == 1
+        got = mod(x, idx, w)
+    assert _b_rel(got, ref) < TOL, _b_rel(got, ref)
+    assert _b_rel(got, ref_noclamp) > 10 * TOL
+    e4b.disable_fast(mod)
+
+
+def test_gptoss_nf4_stays_skipped():
+    from experts4bit_qlora_amd.arch.gptoss import GptOssExperts4bit
+
+    g = torch.Generator().manual_seed(3)
+    E, H, INTER = 8, 128, 64
+    base = GptOssExperts4bit.from_gptoss(torch.randn(E, H, 2 * INTER, generator=g) * 0.1,
+                                         torch.randn(E, 2 * INTER, generator=g) * 0.05,
+                                         torch.randn(E, INTER, H, generator=g) * 0.1,
+                                         torch.randn(E, H, generator=g) * 0.05).to(DEV)
+    assert e4b.enable_fast(base) == 0
+    mod = e4b.ExpertsLoRA(base, r=8, alpha=16, dtype=torch.bfloat16).to(DEV).eval()
+    assert e4b.enable_fast(mod) == 0
+
+
+# ---------------------------------------------------------------------- gpt-oss MXFP4
+
+
+@pytest.mark.parametrize("T", [1, 7, 80])
+def test_gptoss_mxfp4_fused_matches_reference_and_oracle(T):
+    _announce(f"gpt-oss mxfp4 T={T}")
+    g = torch.Generator().manual_seed(T)
+    E, H, I, k = 8, 256, 128, 4
+    gu = torch.randn(E, 2 * I, H, generator=g) * 0.05
+    dn = torch.randn(E, H, I, generator=g) * 0.05
+    b1 = torch.randn(E, 2 * I, generator=g) * 0.05
+    b2 = torch.randn(E, H, generator=g) * 0.05
+    mod = e4b.GptOssExpertsMxfp4.from_float(gu.to(DEV), b1.to(DEV), dn.to(DEV), b2.to(DEV)).eval()
+    x = (torch.randn(T, H, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    val, idx = torch.topk(torch.randn(T, E, generator=g), k, dim=-1)
+    w = torch.softmax(val, -1).to(torch.bfloat16).to(DEV)
+    idx = idx.to(DEV)
+    with torch.no_grad():
+        ref = mod(x, idx, w)
+        assert e4b.enable_fast(mod) == 1
+        got = mod(x, idx, w)
+    w1 = np.stack([mod._dequantize_expert("gate_up", e, torch.float32).cpu().numpy() for e in range(E)])
+    w2 = np.stack([mod._dequantize_expert("down", e, torch.float32).cpu().numpy() for e in range(E)])
+    oracle = moe.forward_fp32(x.float().cpu().numpy(), idx.cpu().numpy(), w.float().cpu().numpy(), w1, w2,
+                              ("gptoss", 1.702, 7.0), b1=mod.gate_up_bias.float().cpu().numpy(),
+                              b2=mod.down_bias.float().cpu().numpy())
+    _assert_fidelity(got, ref, oracle, f"gptoss T={T}")
+
+
+def test_mxfp4_checkpoint_layout_is_deinterleaved_losslessly():
+    g = torch.Generator().manual_seed(0)
+    E, H, I = 2, 64, 64
+    gb = torch.randint(0, 256, (E, 2 * I, H // 32, 16), generator=g, dtype=torch.uint8)
+    gs = torch.randint(110, 140, (E, 2 * I, H // 32), generator=g, dtype=torch.uint8)
+    db = torch.randint(0, 256, (E, H, I // 32, 16), generator=g, dtype=torch.uint8)
+    ds = torch.randint(110, 140, (E, H, I // 32), generator=g, dtype=torch.uint8)
+    b1, b2 = torch.randn(E, 2 * I, generator=g), torch.randn(E, H, generator=g)
+    mod = e4b.GptOssExpertsMxfp4.from_gptoss_mxfp4(gb.to(DEV), gs.to(DEV), b1.to(DEV), db.to(DEV), ds.to(DEV),
+                                                   b2.to(DEV))
+    dense = e4b.dequantize_mxfp4(gb.to(DEV), gs.to(DEV), dtype=torch.float32)  # [E, H, 2I] interleaved
+    for e in range(E):
+        w = mod._dequantize_expert("gate_up", e, torch.float32)
+        assert torch.equal(w[:I], dense[e].T[0::2]) and torch.equal(w[I:], dense[e].T[1::2])
+
+
+# ---------------------------------------------------------- BASELINE-shaped parity
+
+
+def _cfg_module(E, H, I, seed, dq):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    gu = torch.randn(E, 2 * I, H, generator=g, device=DEV) * 0.02
+    dn = torch.randn(E, H, I, generator=g, device=DEV) * 0.02
+    return e4b.Experts4bit.from_float(gu, dn, compute_dtype=torch.bfloat16, compress_statistics=dq).eval()
+
+
+def _cfg_inputs(T, E, H, k, seed, renorm):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn(T, H, generator=g, device=DEV).to(torch.bfloat16)
+    logits = torch.randn(T, E, generator=g, device=DEV)
+    w, idx = torch.topk(torch.softmax(logits, -1), k, dim=-1)
+    if renorm:
+        w = w / w.sum(-1, keepdim=True)
+    return x, idx, w.to(torch.bfloat16)
+
+
+def _oracle_rows(mod, x, idx, w, rows):
+    """CPU fp64 oracle on a subset of tokens (only the experts those tokens hit are decoded)."""
+    sub_idx = idx[rows].cpu().numpy()
+    hit = sorted(set(sub_idx.reshape(-1).tolist()))
+    E = mod.num_experts
+    w1 = np.zeros((E,) + mod._gate_up_shape, np.float32)
+    w2 = np.zeros((E,) + mod._down_shape, np.float32)
+    for e in hit:
+        w1[e] = mod._dequantize_expert(mod.gate_up_proj, mod.gate_up_absmax, mod._gate_up_shape, e,
+                                       torch.float32).cpu().numpy()
+        w2[e] = mod._dequantize_expert(mod.down_proj, mod.down_absmax, mod._down_shape, e, torch.float32).cpu().numpy()
+    return moe.forward_fp32(x[rows].float().cpu().numpy(), sub_idx, w[rows].float().cpu().numpy(), w1, w2)
+
+
+@pytest.mark.parametrize("cfg,T", [("olmoe", 1), ("olmoe", 8), ("olmoe", 64), ("qwen3_dq", 1), ("qwen3_dq", 32),
+                                   ("qwen3_dq", 256)])
+def test_baseline_configs_decode(cfg, T):
+    _announce(f"baseline config {cfg} T={T}")
+    if cfg == "olmoe":
+        E, H, I, k, dq, renorm = 64, 2048, 1024, 8, False, False
+    else:
+        E, H, I, k, dq, renorm = 128, 2048, 768, 8, True, True
+    mod = _cfg_module(E, H, I, seed=1000 + T, dq=dq)
+    x, idx, w = _cfg_inputs(T, E, H, k, seed=2000 + T, renorm=renorm)
+    with torch.no_grad():
+        ref = mod(x, idx, w)
+        assert e4b.enable_fast(mod) == 1
+        got = mod(x, idx, w)
+    rows = list(range(min(T, 8)))
+    oracle = _oracle_rows(mod, x, idx, w, rows)
+    _assert_fidelity(got[rows], ref[rows], oracle, f"{cfg} T={T}")
+
+
+def test_qwen3_zipf_prefill_4096():
+    _announce("qwen3 zipf prefill 4096")
+    E, H, I, k, T = 128, 2048, 768, 8, 4096
+    mod = _cfg_module(E, H, I, seed=3000, dq=True)
+    g = torch.Generator(device=DEV).manual_seed(3001)
+    x = torch.randn(T, H, generator=g, device=DEV).to(torch.bfloat16)
+    rank = torch.randperm(E, generator=torch.Generator().manual_seed(3002)).to(DEV) + 1
+    logits = torch.randn(T, E, generator=g, device=DEV) - 1.1 * torch.log(rank.float())
+    w, idx = torch.topk(torch.softmax(logits, -1), k, dim=-1)
+    w = (w / w.sum(-1, keepdim=True)).to(torch.bfloat16)
+    e4b.enable_fast(mod)
+    with torch.no_grad():
+        got = mod(x, idx, w)
+    assert torch.isfinite(got).all()
+    rows = [0, 1, 2, 1000, 2047, 4095]
+    oracle = _oracle_rows(mod, x, idx, w, rows)
+    fro, maxabs, _ = moe.rel_errors(got[rows].float().cpu().numpy(), oracle)
+    assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
+    # the GEMV and MFMA families agree on the same prefill (size-independent cross-check)
+    F.set_kernel_path("gemv")
+    with torch.no_grad():
+        got_gemv = mod(x[:512], idx[:512], w[:512])
+    F.set_kernel_path("mfma")
+    with torch.no_grad():
+        got_mfma = mod(x[:512], idx[:512], w[:512])
+    fro2, _, _ = moe.rel_errors(got_gemv.float().cpu().numpy(), got_mfma.float().cpu().numpy())
+    assert fro2 <= 1e-2
+
+
+@pytest.mark.parametrize("T", [1, 2048])
+def test_gptoss_config_shapes(T):
+    _announce(f"gpt-oss config T={T}")
+    E, H, I, k = 32, 2880, 2880, 4
+    g = torch.Generator(device=DEV).manual_seed(4000 + T)
+    gu = torch.randn(E, 2 * I, H, generator=g, device=DEV) * 0.02
+    dn = torch.randn(E, H, I, generator=g, device=DEV) * 0.02
+    b1 = torch.randn(E, 2 * I, generator=g, device=DEV) * 0.02
+    b2 = torch.randn(E, H, generator=g, device=DEV) * 0.02
+    mod = e4b.GptOssExpertsMxfp4.from_float(gu, b1, dn, b2).eval()
+    del gu, dn
+    x = torch.randn(T, H, generator=g, device=DEV).to(torch.bfloat16)
+    val, idx = torch.topk(torch.randn(T, E, generator=g, device=DEV), k, dim=-1)
+    w = torch.softmax(val, -1).to(torch.bfloat16)
+    e4b.enable_fast(mod)
+    with torch.no_grad():
+        got = mod(x, idx, w)
+        ref = mod._e4b_fast_ref(x[:4], idx[:4], w[:4])
+    rows = list(range(min(T, 4)))
+    sub = idx[rows].cpu().numpy()
+    w1 = np.zeros((E, 2 * I, H), np.float32)
+    w2 = np.zeros((E, H, I), np.float32)
+    for e in sorted(set(sub.reshape(-1).tolist())):
+        w1[e] = mod._dequantize_expert("gate_up", e, torch.float32).cpu().numpy()
+        w2[e] = mod._dequantize_expert("down", e, torch.float32).cpu().numpy()
+    oracle = moe.forward_fp32(x[rows].float().cpu().numpy(), sub, w[rows].float().cpu().numpy(), w1, w2,
+                              ("gptoss", 1.702, 7.0), b1=mod.gate_up_bias.float().cpu().numpy(),
+                              b2=mod.down_bias.float().cpu().numpy())
+    _assert_fidelity(got[rows], ref[rows], oracle, f"gptoss T={T}")

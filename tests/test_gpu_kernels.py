@@ -1,0 +1,283 @@
+"""GPU parity of each kernel, called through the C ABI, against the CPU oracle.
+
+Bars: bit-exact for dequant, routing and the combine; rel-Frobenius <= 1e-2 and max-abs <= 2e-2
+(on outputs normalised by the oracle's RMS) for the GEMMs, whose fp32 accumulation order
+differs from the oracle's.
+"""
+import numpy as np
+import pytest
+import torch
+
+from experts4bit_qlora_amd import _native as N
+from experts4bit_qlora_amd import ops, quant as Q
+from oracle import c_oracle, codes, moe, numerics, quant as oq, routing as orouting
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _announce(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    t = t.cpu()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy().view(np.uint32)
+
+
+def _nf4_stack(E, n, k, seed, dq=False):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    w = torch.randn(E, n * k, generator=g) * 0.02
+    packed, absmax = Q.quantize_4bit(w)
+    code = Q.code_4bit("nf4")
+    if dq:
+        q, a2, off = Q.double_quant(absmax)
+        code2 = Q.dynamic_map()
+        qw = ops.nf4_dq_qweight(packed.to(DEV), q.to(DEV), a2.to(DEV), off.to(DEV), code.to(DEV), code2.to(DEV), n, k,
+                                num_experts=E)
+        absmax_f = oq.dequant_absmax_dq(q.numpy(), a2.numpy(), off.numpy(), code2.numpy())
+        return qw, packed.numpy(), absmax_f
+    qw = ops.nf4_qweight(packed.to(DEV), absmax.to(DEV), code.to(DEV), n, k, num_experts=E)
+    return qw, packed.numpy(), absmax.numpy()
+
+
+# ------------------------------------------------------------------------------- dequant
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dq", [False, True])
+def test_dequant_nf4_bit_exact(dt, dq):
+    _announce(f"dequant nf4 dq={dq} {dt}")
+    E, n, k = 3, 96, 256
+    qw, packed, absmax = _nf4_stack(E, n, k, seed=1, dq=dq)
+    got = ops.dequant(qw, 0, E, dtype=dt)
+    want = c_oracle.dequant_4bit(packed.reshape(-1), absmax.reshape(-1), codes.NF4_CODE).reshape(E, n, k)
+    if dt == torch.float32:
+        assert np.array_equal(_bits(got), want.view(np.uint32))
+    elif dt == torch.bfloat16:
+        assert np.array_equal(_bits(got), numerics.f32_to_bf16_bits(want))
+    else:
+        assert np.array_equal(_bits(got), want.astype(np.float16).view(np.uint16))
+
+
+def test_dequant_nf4_expert_range_and_full_size_expert():
+    _announce("dequant nf4 OLMoE gate_up expert slice")
+    E, n, k = 4, 2048, 2048
+    qw, packed, absmax = _nf4_stack(E, n, k, seed=2)
+    got = ops.dequant(qw, 2, 1, dtype=torch.bfloat16)[0]
+    want = c_oracle.dequant_4bit(packed[2], absmax[2], codes.NF4_CODE, out="bf16").reshape(n, k)
+    assert np.array_equal(_bits(got), want)
+
+
+def test_dequant_mxfp4_bit_exact():
+    _announce("dequant mxfp4")
+    E, n, k = 2, 64, 2880
+    g = torch.Generator().manual_seed(3)
+    blocks = torch.randint(0, 256, (E, n, k // 2), generator=g, dtype=torch.uint8)
+    scales = torch.randint(100, 150, (E, n, k // 32), generator=g, dtype=torch.uint8)
+    qw = ops.mxfp4_qweight(blocks.to(DEV), scales.to(DEV), n, k, num_experts=E)
+    for dt, tag in ((torch.float32, "fp32"), (torch.bfloat16, "bf16")):
+        got = ops.dequant(qw, 0, E, dtype=dt)
+        want = oq.dequant_mxfp4_rows(blocks.numpy().reshape(E, n, k // 32, 16), scales.numpy(), dtype=tag)
+        if tag == "fp32":
+            assert np.array_equal(_bits(got), want.reshape(E, n, k).view(np.uint32))
+        else:
+            assert np.array_equal(_bits(got), numerics.f32_to_bf16_bits(want.reshape(E, n, k)))
+
+
+# ------------------------------------------------------------------------------- routing
+
+
+def _check_route(idx: np.ndarray, E: int):
+    T, k = idx.shape
+    rb = ops.route(torch.from_numpy(idx).to(DEV), E)
+    torch.cuda.synchronize()
+    M = T * k
+    valid = (idx >= 0) & (idx < E)
+    ref = orouting.route(np.where(valid, idx, 0), E) if valid.all() else None
+    meta = rb.meta.cpu().numpy()
+    if ref is not None:
+        assert np.array_equal(rb.sorted_flat[:M].cpu().numpy(), ref["order"])
+        assert np.array_equal(rb.inv[:M].cpu().numpy(), ref["inv"])
+        assert np.array_equal(rb.offsets.cpu().numpy(), ref["offsets"])
+        assert meta[1] == ref["active"].size and meta[2] == 0
+        assert np.array_equal(rb.active[:meta[1]].cpu().numpy(), ref["active"])
+        tiles = orouting.m_tiles(ref["counts"], rb.tile_m)
+        assert meta[0] == len(tiles)
+        assert rb.tiles[:2 * meta[0]].cpu().numpy().reshape(-1, 2).tolist() == [list(t) for t in tiles]
+    return rb, meta
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 8, 64), (8, 8, 64), (64, 8, 64), (1, 8, 128), (32, 8, 128), (256, 8, 128),
+                                   (1, 4, 32), (2048, 4, 32), (4096, 8, 128), (37, 3, 1024), (5, 2, 4)])
+def test_route_bit_exact(T, k, E):
+    _announce(f"route T={T} k={k} E={E}")
+    rng = np.random.default_rng(T * 1000 + E)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
+    _check_route(idx, E)
+
+
+def test_route_zipf_prefill_and_duplicates():
+    _announce("route zipf 4096x8 over 128 + duplicate ids")
+    rng = np.random.default_rng(0)
+    p = 1.0 / np.arange(1, 129) ** 1.1
+    idx = np.stack([rng.choice(128, 8, replace=False, p=p / p.sum()) for _ in range(4096)]).astype(np.int64)
+    _check_route(idx, 128)
+    dup = rng.integers(0, 3, (300, 4)).astype(np.int64)  # duplicates within tokens, empty experts
+    _check_route(dup, 8)
+
+
+def test_route_drops_out_of_range_ids():
+    _announce("route invalid ids")
+    idx = np.array([[0, 5], [9, 1], [-1, 2]], dtype=np.int64)  # E = 6
+    rb, meta = _check_route(idx, 6)
+    assert meta[2] == 2
+    inv = rb.inv[:6].cpu().numpy()
+    assert inv[2] == -1 and inv[4] == -1
+    ref = orouting.route(np.array([[0, 5], [1, 2]]), 6)  # the valid ids keep their relative order
+    assert rb.offsets.cpu().numpy()[-1] == 4
+    order = rb.sorted_flat[:4].cpu().numpy()
+    assert order.tolist() == [0, 3, 5, 1]
+    assert ref["counts"].sum() == 4
+
+
+# --------------------------------------------------------------------------------- GEMMs
+
+
+def _dense_from_kernel(qw) -> np.ndarray:
+    return ops.dequant(qw, 0, qw.num_experts, dtype=torch.float32).cpu().numpy()
+
+
+def _gemm_oracle(a_rows, W, rows_expert, bias=None):
+    """fp64 per-row GEMM against the dequantized fp32 weights."""
+    out = np.empty((a_rows.shape[0], W.shape[1]), np.float64)
+    for r in range(a_rows.shape[0]):
+        out[r] = W[rows_expert[r]].astype(np.float64) @ a_rows[r].astype(np.float64)
+        if bias is not None:
+            out[r] += bias[rows_expert[r]]
+    return out
+
+
+def _errs(got, want):
+    fro, maxabs, _ = moe.rel_errors(got, want)
+    return fro, maxabs
+
+
+@pytest.mark.parametrize("path", [N.PATH_GEMV, N.PATH_MFMA])
+@pytest.mark.parametrize("fmt", ["nf4", "nf4_dq", "mxfp4"])
+@pytest.mark.parametrize("T", [1, 3, 40])
+def test_grouped_gemm_plain(path, fmt, T):
+    _announce(f"grouped gemm plain path={path} fmt={fmt} T={T}")
+    E, n, k, top = 8, 192, 320, 2
+    if fmt == "mxfp4":
+        g = torch.Generator().manual_seed(5)
+        w = torch.randn(E, n, k, generator=g) * 0.02
+        b, s = Q.quantize_mxfp4(w)
+        qw = ops.mxfp4_qweight(b.reshape(E, -1).to(DEV), s.reshape(E, -1).to(DEV), n, k, num_experts=E)
+    else:
+        qw, _, _ = _nf4_stack(E, n, k, seed=6, dq=(fmt == "nf4_dq"))
+    W = _dense_from_kernel(qw)
+    rng = np.random.default_rng(T)
+    idx = np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)
+    x = torch.randn(T, k, generator=torch.Generator().manual_seed(T)).to(torch.bfloat16)
+    rb = ops.route(torch.from_numpy(idx).to(DEV), E)
+    out = ops.grouped_gemm(x.to(DEV), qw, rb, T, T * top, N.EPI_NONE, gather_k=top, path=path)
+    ref = orouting.route(idx, E)
+    want = _gemm_oracle(x.float().numpy()[ref["token_rows"]], W, idx.reshape(-1)[ref["order"]])
+    fro, maxabs = _errs(out.float().cpu().numpy(), want)
+    assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
+
+
+@pytest.mark.parametrize("path", [N.PATH_GEMV, N.PATH_MFMA])
+@pytest.mark.parametrize("epi", ["swiglu", "act", "clamp", "gptoss"])
+def test_grouped_gemm_fused_epilogues(path, epi):
+    _announce(f"grouped gemm epilogue path={path} epi={epi}")
+    E, H, I, top, T = 6, 256, 128, 2, 9
+    gated = epi != "act"
+    n = 2 * I if gated else I
+    qw, _, _ = _nf4_stack(E, n, H, seed=7)
+    g = torch.Generator().manual_seed(8)
+    bias = None
+    if epi == "gptoss":
+        bias = (torch.randn(E, n, generator=g) * 0.5).to(torch.bfloat16)
+        qw.bias = bias.to(DEV)
+    W = _dense_from_kernel(qw)
+    rng = np.random.default_rng(9)
+    idx = np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)
+    x = (torch.randn(T, H, generator=g) * 3).to(torch.bfloat16)
+    rb = ops.route(torch.from_numpy(idx).to(DEV), E)
+    code = {"swiglu": N.EPI_SWIGLU, "act": N.EPI_ACT, "clamp": N.EPI_CLAMP_SWIGLU, "gptoss": N.EPI_GPTOSS}[epi]
+    out = ops.grouped_gemm(x.to(DEV), qw, rb, T, T * top, code, gather_k=top, alpha=1.702, limit=1.5, path=path)
+    ref = orouting.route(idx, E)
+    proj = _gemm_oracle(x.float().numpy()[ref["token_rows"]], W, idx.reshape(-1)[ref["order"]])
+    # the oracle epilogue on the bf16-rounded projection, per expert row
+    proj_r = numerics.round_bf16(proj.astype(np.float32))
+    e_rows = idx.reshape(-1)[ref["order"]]
+    if epi == "gptoss":
+        want = np.concatenate([moe.epilogue_rounded(proj_r[r:r + 1], ("gptoss", 1.702, 1.5), I, "bf16",
+                                                    b1=bias.float().numpy()[e_rows[r]]) for r in range(len(e_rows))])
+    else:
+        spec = {"swiglu": "swiglu", "act": "act", "clamp": ("clamp_swiglu", 1.5)}[epi]
+        want = moe.epilogue_rounded(proj_r, spec, I, "bf16")
+    fro, maxabs = _errs(out.float().cpu().numpy(), want)
+    assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
+
+
+def test_grouped_gemm_fp16_activations():
+    _announce("grouped gemm fp16")
+    E, n, k, top, T = 4, 128, 256, 2, 20
+    qw, _, _ = _nf4_stack(E, n, k, seed=10)
+    W = _dense_from_kernel(qw)
+    rng = np.random.default_rng(11)
+    idx = np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)
+    x = torch.randn(T, k, generator=torch.Generator().manual_seed(12)).to(torch.float16)
+    rb = ops.route(torch.from_numpy(idx).to(DEV), E)
+    ref = orouting.route(idx, E)
+    want = _gemm_oracle(x.float().numpy()[ref["token_rows"]], W, idx.reshape(-1)[ref["order"]])
+    for path in (N.PATH_GEMV, N.PATH_MFMA):
+        out = ops.grouped_gemm(x.to(DEV), qw, rb, T, T * top, N.EPI_NONE, gather_k=top, path=path)
+        assert out.dtype == torch.float16
+        fro, maxabs = _errs(out.float().cpu().numpy(), want)
+        assert fro <= 1e-2 and maxabs <= 2e-2, (path, fro, maxabs)
+
+
+def test_gemm_4bit_grouped_api_shape():
+    _announce("gemm_4bit_grouped API")
+    E, n, k = 5, 64, 128
+    qw, packed, absmax = _nf4_stack(E, n, k, seed=13)
+    W = _dense_from_kernel(qw)
+    sizes, ids = [3, 1, 7], [0, 2, 4]
+    a = torch.randn(sum(sizes), k, generator=torch.Generator().manual_seed(14)).to(torch.bfloat16)
+    out = ops.gemm_4bit_grouped(a.to(DEV), qw.packed.view(E, n, k // 2), qw.absmax.view(E, n, k // 64), sizes, ids)
+    rows_e = np.repeat(ids, sizes)
+    want = _gemm_oracle(a.float().numpy(), W, rows_e)
+    fro, maxabs = _errs(out.float().cpu().numpy(), want)
+    assert out.shape == (11, n) and fro <= 1e-2 and maxabs <= 2e-2
+
+
+# ------------------------------------------------------------------------------- combine
+
+
+@pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("H", [256, 2880, 100])
+def test_combine_bit_exact(wdt, H):
+    _announce(f"combine H={H} w={wdt}")
+    T, k, E = 33, 4, 16
+    rng = np.random.default_rng(H)
+    idx = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
+    rb = ops.route(torch.from_numpy(idx).to(DEV), E)
+    down = torch.randn(T * k, H, generator=torch.Generator().manual_seed(15)).to(torch.bfloat16)
+    w = torch.rand(T, k, generator=torch.Generator().manual_seed(16)).to(wdt)
+    out = ops.combine(down.to(DEV), rb, w.to(DEV), T, k, torch.float32)
+    ref = orouting.route(idx, E)
+    d = down.float().numpy()
+    wf = w.float().numpy()
+    acc = np.zeros((T, H), np.float32)
+    for s in range(k):
+        rows = ref["inv"].reshape(T, k)[:, s]
+        acc = (acc + (d[rows] * wf[:, s:s + 1]).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(_bits(out), acc.view(np.uint32))
+    out16 = ops.combine(down.to(DEV), rb, w.to(DEV), T, k, torch.bfloat16)
+    assert np.array_equal(_bits(out16), numerics.f32_to_bf16_bits(acc))
