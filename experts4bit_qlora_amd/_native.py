@@ -95,7 +95,7 @@ def _bind(L):
     L.e4b_route.restype = ctypes.c_int
     L.e4b_route.argtypes = [P, I64, I32, I32, RT, P]
     L.e4b_grouped_gemm.restype = ctypes.c_int
-    L.e4b_grouped_gemm.argtypes = [P, I32, I32, QW, RT, I64, I64, I32, F32, F32, I32, P, P]
+    L.e4b_grouped_gemm.argtypes = [P, I32, I32, QW, RT, I64, I64, I32, F32, F32, I32, P, I32, P]
     L.e4b_combine.restype = ctypes.c_int
     L.e4b_combine.argtypes = [P, I32, P, P, I32, I64, I32, I64, P, I32, P]
     L.e4b_moe_workspace_bytes.restype = ctypes.c_size_t

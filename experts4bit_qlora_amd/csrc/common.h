@@ -68,44 +68,41 @@ E4B_DEV uint32_t pack2(uint16_t lo, uint16_t hi) {
 E4B_DEV float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 E4B_DEV float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
 
-// Gated activation of one (gate, up) pair. Inputs are fp32 GEMM sums; the result is the
-// activation value already rounded to DT. Rounding points follow the reference:
-//   SWIGLU        lora.py:125-127       bf16 ops: rnd(rnd(silu(g)) * u)
-//   CLAMP_SWIGLU  deepseek_v4.py:190-195 fp32 GLU, one rounding
-//   GPTOSS        hot_residency.py:72-80 bias add then five rounded bf16 ops
-template <int DT>
-E4B_DEV float gated(int epi, float g, float u, float alpha, float limit, float bg, float bu) {
-  g = rnd<DT>(g);
-  u = rnd<DT>(u);
-  if (epi == E4B_EPI_GPTOSS) {
-    g = rnd<DT>(g + bg);
-    u = rnd<DT>(u + bu);
-    g = fminf(g, limit);
-    u = fminf(fmaxf(u, -limit), limit);
-    const float t = rnd<DT>(g * alpha);
-    const float sg = rnd<DT>(sigmoid_f32(t));
-    const float gs = rnd<DT>(g * sg);
-    const float u1 = rnd<DT>(u + 1.0f);
-    return rnd<DT>(u1 * gs);
-  }
-  if (epi == E4B_EPI_CLAMP_SWIGLU) {
-    if (limit > 0.0f) {
-      g = fminf(g, limit);
-      u = fminf(fmaxf(u, -limit), limit);
-    }
-    return rnd<DT>(silu_f32(g) * u);
-  }
-  // E4B_EPI_SWIGLU
-  return rnd<DT>(rnd<DT>(silu_f32(g)) * u);
+// fp32 product rounded to fp32 before any later conversion. The empty asm hides the product
+// from instruction selection, which would otherwise fold a multiply followed by an fp16
+// conversion into one v_fma_mix (a single rounding of the exact product) -- the reference
+// rounds to fp32 first (code[idx] * absmax), then to the output dtype.
+E4B_DEV float mul_f32(float a, float b) {
+  float p = a * b;
+  asm volatile("" : "+v"(p));
+  return p;
 }
 
-// Single-output epilogue: NONE (optionally + bias, gpt-oss down_proj) or ACT.
-template <int DT>
-E4B_DEV float single(int epi, float p, float b, bool has_bias) {
-  p = rnd<DT>(p);
-  if (has_bias) p = rnd<DT>(p + b);
-  if (epi == E4B_EPI_ACT) return rnd<DT>(silu_f32(p));
-  return p;
+// Gated activation of one (gate, up) pair, evaluated in fp32 on the fp32 GEMM sums; the
+// caller rounds the result once into the activation dtype. The reference rounds at every
+// torch op of its epilogue (lora.py:125-127, hot_residency.py:72-80); keeping the fused
+// epilogue in registers at fp32 removes those intermediate roundings.
+//   SWIGLU        silu(g) * u
+//   CLAMP_SWIGLU  silu(min(g, L)) * clamp(u, -L, L)        (L <= 0: no clamp)
+//   GPTOSS        g += bg, u += bu, g = min(g, L), u = clamp(u, -L, L),
+//                 (u + 1) * (g * sigmoid(alpha * g))
+E4B_DEV float gated(int epi, float g, float u, float alpha, float limit, float bg, float bu) {
+  if (epi == E4B_EPI_GPTOSS) {
+    g = fminf(g + bg, limit);
+    u = fminf(fmaxf(u + bu, -limit), limit);
+    return (u + 1.0f) * (g * sigmoid_f32(alpha * g));
+  }
+  if (epi == E4B_EPI_CLAMP_SWIGLU && limit > 0.0f) {
+    g = fminf(g, limit);
+    u = fminf(fmaxf(u, -limit), limit);
+  }
+  return silu_f32(g) * u;
+}
+
+// Single-output epilogue in fp32: NONE (+ bias, gpt-oss down_proj) or ACT (silu).
+E4B_DEV float single(int epi, float p, float b) {
+  p = p + b;
+  return epi == E4B_EPI_ACT ? silu_f32(p) : p;
 }
 
 E4B_DEV bool is_gated(int epi) {
@@ -123,7 +120,7 @@ E4B_DEV float nf4_block_scale(const e4b_qweight& w, int e, int64_t block) {
     const uint8_t q = static_cast<const uint8_t*>(w.absmax)[e * nb + block];
     const int64_t nb2 = (nb + 255) / 256;
     // fp32(fp32(code2[q] * absmax2) + offset): two separately rounded operations.
-    const float p = __fmul_rn(w.code2[q], w.absmax2[e * nb2 + block / 256]);
+    const float p = mul_f32(w.code2[q], w.absmax2[e * nb2 + block / 256]);
     return __fadd_rn(p, w.offset[e]);
   }
 }

@@ -45,8 +45,8 @@ __global__ void __launch_bounds__(256) dequant_kernel(e4b_qweight w, int expert_
       const uint32_t byte = (v >> (8 * j)) & 0xffu;
       const uint32_t first = (FMT == E4B_FMT_MXFP4) ? (byte & 0xfu) : (byte >> 4);
       const uint32_t second = (FMT == E4B_FMT_MXFP4) ? (byte >> 4) : (byte & 0xfu);
-      vals[2 * j] = __fmul_rn(code_s[first], scale);
-      vals[2 * j + 1] = __fmul_rn(code_s[second], scale);
+      vals[2 * j] = mul_f32(code_s[first], scale);
+      vals[2 * j + 1] = mul_f32(code_s[second], scale);
     }
     if constexpr (OUT == E4B_FP32) {
       float4* o = reinterpret_cast<float4*>(out) + 2 * i;

@@ -147,31 +147,31 @@ int launch_gemm_dt(const e4b::GemmArgs& a, bool gemv, int64_t max_active, hipStr
   return check_launch(gemv ? "gemv_kernel" : "gemm_mfma_kernel");
 }
 
-template <int DT, int WDT>
-void launch_combine_w(const uint16_t* down, const int32_t* inv, const void* w, int64_t T, int k, int64_t H,
+template <int DDT, int WDT>
+void launch_combine_w(const void* down, const int32_t* inv, const void* w, int64_t T, int k, int64_t H,
                       void* out, int od, hipStream_t s) {
   const int64_t work = T * ((H % 8) == 0 ? H / 8 : H);
   const int grid = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(cdiv(work, 256), 16384)));
   switch (od) {
     case E4B_FP32:
-      hipLaunchKernelGGL((e4b::combine_kernel<DT, WDT, E4B_FP32>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
+      hipLaunchKernelGGL((e4b::combine_kernel<DDT, WDT, E4B_FP32>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
       break;
     case E4B_BF16:
-      hipLaunchKernelGGL((e4b::combine_kernel<DT, WDT, E4B_BF16>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
+      hipLaunchKernelGGL((e4b::combine_kernel<DDT, WDT, E4B_BF16>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
       break;
     default:
-      hipLaunchKernelGGL((e4b::combine_kernel<DT, WDT, E4B_FP16>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
+      hipLaunchKernelGGL((e4b::combine_kernel<DDT, WDT, E4B_FP16>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
       break;
   }
 }
 
-template <int DT>
-void launch_combine_dt(const uint16_t* down, const int32_t* inv, const void* w, int wd, int64_t T, int k,
-                       int64_t H, void* out, int od, hipStream_t s) {
+template <int DDT>
+void launch_combine_dt(const void* down, const int32_t* inv, const void* w, int wd, int64_t T, int k, int64_t H,
+                       void* out, int od, hipStream_t s) {
   switch (wd) {
-    case E4B_FP32: launch_combine_w<DT, E4B_FP32>(down, inv, w, T, k, H, out, od, s); break;
-    case E4B_BF16: launch_combine_w<DT, E4B_BF16>(down, inv, w, T, k, H, out, od, s); break;
-    default: launch_combine_w<DT, E4B_FP16>(down, inv, w, T, k, H, out, od, s); break;
+    case E4B_FP32: launch_combine_w<DDT, E4B_FP32>(down, inv, w, T, k, H, out, od, s); break;
+    case E4B_BF16: launch_combine_w<DDT, E4B_BF16>(down, inv, w, T, k, H, out, od, s); break;
+    default: launch_combine_w<DDT, E4B_FP16>(down, inv, w, T, k, H, out, od, s); break;
   }
 }
 
@@ -232,12 +232,14 @@ int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t
 
 int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e4b_qweight* w, const e4b_routing* rt,
                      int64_t tokens, int64_t M, int32_t epilogue, float alpha, float limit, int32_t flags, void* out,
-                     hipStream_t stream) {
+                     int32_t out_dtype, hipStream_t stream) {
   int rc = check_weight(w);
   if (rc) return rc;
   rc = check_routing(rt, M);
   if (rc) return rc;
   if (!act_dtype_ok(act_dtype)) return fail(E4B_EINVAL, "act_dtype must be bf16 or fp16 (got %d)", act_dtype);
+  if (out_dtype != act_dtype && out_dtype != E4B_FP32)
+    return fail(E4B_EINVAL, "out_dtype must be the activation dtype or fp32 (got %d)", out_dtype);
   if (epilogue < E4B_EPI_NONE || epilogue > E4B_EPI_GPTOSS) return fail(E4B_EINVAL, "bad epilogue %d", epilogue);
   const bool pair = is_gated_epi(epilogue);
   if (pair && (w->n % 2)) return fail(E4B_EINVAL, "gated epilogue needs an even n (got %lld)", (long long)w->n);
@@ -264,27 +266,34 @@ int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e
   args.epi = epilogue;
   args.alpha = alpha;
   args.limit = limit;
-  args.out = static_cast<uint16_t*>(out);
+  args.out = out;
   args.n_out = pair ? w->n / 2 : w->n;
+  args.out_f32 = out_dtype == E4B_FP32;
   const int64_t max_active = std::min<int64_t>(w->num_experts, M);
   return act_dtype == E4B_BF16 ? launch_gemm_dt<E4B_BF16>(args, gemv, max_active, stream)
                                : launch_gemm_dt<E4B_FP16>(args, gemv, max_active, stream);
 }
 
-int e4b_combine(const void* down, int32_t act_dtype, const int32_t* inv, const void* top_k_weights,
+int e4b_combine(const void* down, int32_t down_dtype, const int32_t* inv, const void* top_k_weights,
                 int32_t weight_dtype, int64_t tokens, int32_t top_k, int64_t hidden, void* out, int32_t out_dtype,
                 hipStream_t stream) {
-  if (!act_dtype_ok(act_dtype)) return fail(E4B_EINVAL, "act_dtype must be bf16 or fp16");
+  if (!any_dtype_ok(down_dtype)) return fail(E4B_EINVAL, "bad down dtype %d", down_dtype);
   if (!any_dtype_ok(weight_dtype) || !any_dtype_ok(out_dtype)) return fail(E4B_EINVAL, "bad weight/out dtype");
   if (tokens < 0 || top_k <= 0 || hidden <= 0) return fail(E4B_EINVAL, "bad sizes");
   if (tokens == 0) return E4B_OK;
   if (!down || !inv || !top_k_weights || !out) return fail(E4B_EINVAL, "NULL pointer");
   if (hidden % 8 == 0 && !aligned16(down)) return fail(E4B_EINVAL, "down must be 16-byte aligned");
-  const uint16_t* d = static_cast<const uint16_t*>(down);
-  if (act_dtype == E4B_BF16)
-    launch_combine_dt<E4B_BF16>(d, inv, top_k_weights, weight_dtype, tokens, top_k, hidden, out, out_dtype, stream);
-  else
-    launch_combine_dt<E4B_FP16>(d, inv, top_k_weights, weight_dtype, tokens, top_k, hidden, out, out_dtype, stream);
+  switch (down_dtype) {
+    case E4B_FP32:
+      launch_combine_dt<E4B_FP32>(down, inv, top_k_weights, weight_dtype, tokens, top_k, hidden, out, out_dtype, stream);
+      break;
+    case E4B_BF16:
+      launch_combine_dt<E4B_BF16>(down, inv, top_k_weights, weight_dtype, tokens, top_k, hidden, out, out_dtype, stream);
+      break;
+    default:
+      launch_combine_dt<E4B_FP16>(down, inv, top_k_weights, weight_dtype, tokens, top_k, hidden, out, out_dtype, stream);
+      break;
+  }
   return check_launch("combine_kernel");
 }
 
@@ -301,7 +310,7 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
   b += align256(sizeof(int32_t) * 2 * max_tiles_for(M, num_experts, e4b::kTileM));  // tiles
   b += align256(sizeof(int32_t) * 4);                                  // meta
   b += align256(sizeof(uint16_t) * M * h_cols);                        // h
-  b += align256(sizeof(uint16_t) * M * n2);                            // down
+  b += align256(sizeof(float) * M * n2);                               // down rows (fp32)
   return b;
 }
 
@@ -344,15 +353,17 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   rt.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rt.max_tiles));
   rt.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
   void* h = take(sizeof(uint16_t) * M * h_cols);
-  void* down = take(sizeof(uint16_t) * M * w2->n);
+  void* down = take(sizeof(float) * M * w2->n);
 
   rc = e4b_route(top_k_index, tokens, top_k, E, &rt, stream);
   if (rc) return rc;
-  rc = e4b_grouped_gemm(hidden, act_dtype, top_k, w1, &rt, tokens, M, epilogue, alpha, limit, flags, h, stream);
+  rc = e4b_grouped_gemm(hidden, act_dtype, top_k, w1, &rt, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
+                        stream);
   if (rc) return rc;
-  rc = e4b_grouped_gemm(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, stream);
+  rc = e4b_grouped_gemm(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
+                        stream);
   if (rc) return rc;
-  return e4b_combine(down, act_dtype, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
+  return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
                      stream);
 }
 

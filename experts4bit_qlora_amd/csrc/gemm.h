@@ -12,7 +12,7 @@
 //   * 2 x (2 x 4) v_mfma_f32_16x16x32_{bf16,f16} per wave, fp32 accumulators.
 // Gated epilogues pair gate row j with up row n/2 + j in the same tile: LDS rows 0..63 hold
 // the gate rows of 64 output columns and rows 64..127 their up rows, and a wave's gate and up
-// accumulators sit in the same lanes, so SwiGLU runs on registers before the only store.
+// accumulators sit in the same lanes, so SwiGLU runs on registers (fp32) before the only store.
 #pragma once
 
 #include "common.h"
@@ -133,8 +133,8 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_mfma_kernel(GemmArgs p) {
         const uint32_t byte = (words[wi] >> (8 * b)) & 0xffu;
         const uint32_t first = (FMT == E4B_FMT_MXFP4) ? (byte & 0xfu) : (byte >> 4);
         const uint32_t second = (FMT == E4B_FMT_MXFP4) ? (byte >> 4) : (byte & 0xfu);
-        wv[4 * wi + b] = pack2(from_f<DT>(__fmul_rn(lut[first], scale)),
-                               from_f<DT>(__fmul_rn(lut[second], scale)));
+        wv[4 * wi + b] = pack2(from_f<DT>(mul_f32(lut[first], scale)),
+                               from_f<DT>(mul_f32(lut[second], scale)));
       }
     }
     uint4* ws = reinterpret_cast<uint4*>(Ws + lrow * kLdsPitch + half * 32);
@@ -176,7 +176,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_mfma_kernel(GemmArgs p) {
     for (int i = 0; i < 4; ++i) {
       const int rr = row0 + wave_m * 32 + ms * 16 + 4 * (lane >> 4) + i;
       if (rr >= row_end) continue;
-      uint16_t* orow = p.out + int64_t(rr) * p.n_out;
+      const int64_t orow = int64_t(rr) * p.n_out;
       if (pair) {
 #pragma unroll
         for (int ns = 0; ns < 2; ++ns) {
@@ -184,7 +184,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_mfma_kernel(GemmArgs p) {
           if (jj >= p.n_out) continue;
           const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + jj]) : 0.0f;
           const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + n / 2 + jj]) : 0.0f;
-          orow[jj] = from_f<DT>(gated<DT>(p.epi, acc[ms][ns][i], acc[ms][ns + 2][i], p.alpha, p.limit, bg, bu));
+          store_elem<DT>(p, orow + jj, gated(p.epi, acc[ms][ns][i], acc[ms][ns + 2][i], p.alpha, p.limit, bg, bu));
         }
       } else {
 #pragma unroll
@@ -192,7 +192,7 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_mfma_kernel(GemmArgs p) {
           const int64_t nn = col0 + wave_n * 64 + ns * 16 + (lane & 15);
           if (nn >= p.n_out) continue;
           const float b = has_bias ? to_f<DT>(bias[int64_t(e) * n + nn]) : 0.0f;
-          orow[nn] = from_f<DT>(single<DT>(p.epi, acc[ms][ns][i], b, has_bias));
+          store_elem<DT>(p, orow + nn, single(p.epi, acc[ms][ns][i], b));
         }
       }
     }

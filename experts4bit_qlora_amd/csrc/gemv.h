@@ -9,7 +9,8 @@
 //     acc += scale * sum_{32 values} code[nib] * x
 // Scale factoring is exact for MXFP4 (power-of-two scales) and reassociates the fp32 sum for
 // NF4; both accumulate in fp32. The G partial sums reduce with lane shuffles and lane 0 of the
-// group runs the fused epilogue (bias, SwiGLU / clamped GLU) and writes the activation dtype.
+// group runs the fused epilogue (bias, SwiGLU / clamped GLU) in fp32 and stores the result
+// rounded once to the activation dtype, or as fp32.
 #pragma once
 
 #include "common.h"
@@ -25,9 +26,20 @@ struct GemmArgs {
   int64_t M;          // sorted rows
   int epi;
   float alpha, limit;
-  uint16_t* out;      // [M, n_out]
+  void* out;          // [M, n_out] in the activation dtype, or fp32 when out_f32
   int64_t n_out;
+  int out_f32;
 };
+
+// Store one output element: fp32, or rounded once into the activation dtype.
+template <int DT>
+E4B_DEV void store_elem(const GemmArgs& p, int64_t i, float v) {
+  if (p.out_f32) {
+    static_cast<float*>(p.out)[i] = v;
+  } else {
+    static_cast<uint16_t*>(p.out)[i] = from_f<DT>(v);
+  }
+}
 
 constexpr int kGemvThreads = 256;
 constexpr int kGemvRowsPerPass = 4;  // routed rows held in registers per weight pass
@@ -165,12 +177,12 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(GemmArgs p) {
         if (pair) {
           const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + row_a]) : 0.0f;
           const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + row_b]) : 0.0f;
-          v = gated<DT>(p.epi, acc_a[mm], acc_b[mm], p.alpha, p.limit, bg, bu);
+          v = gated(p.epi, acc_a[mm], acc_b[mm], p.alpha, p.limit, bg, bu);
         } else {
           const float b = has_bias ? to_f<DT>(bias[int64_t(e) * n + row_a]) : 0.0f;
-          v = single<DT>(p.epi, acc_a[mm], b, has_bias);
+          v = single(p.epi, acc_a[mm], b);
         }
-        p.out[int64_t(rb + mm) * p.n_out + j] = from_f<DT>(v);
+        store_elem<DT>(p, int64_t(rb + mm) * p.n_out + j, v);
       }
     }
   }

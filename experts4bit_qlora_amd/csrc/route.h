@@ -168,7 +168,7 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __r
 // out[t, :] = out_t( sum_s float(down[inv[t*k+s], :]) * w[t, s] ), s ascending, fp32 adds of
 // rounded fp32 products -- engines/fast.py:158 and 276-278 (buf[order] = down.float() * w;
 // buf.view(T, k, H).sum(1).to(dtype)). Dropped slots (inv < 0) contribute nothing.
-template <int DT, int WDT>
+template <int WDT>
 E4B_DEV float load_weight(const void* w, int64_t i) {
   if constexpr (WDT == E4B_FP32) {
     return static_cast<const float*>(w)[i];
@@ -186,8 +186,17 @@ E4B_DEV void store_out(void* out, int64_t i, float v) {
   }
 }
 
-template <int DT, int WDT, int ODT>
-__global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict__ down,
+template <int DDT>
+E4B_DEV float load_down(const void* d, int64_t i) {
+  if constexpr (DDT == E4B_FP32) {
+    return static_cast<const float*>(d)[i];
+  } else {
+    return to_f<DDT>(static_cast<const uint16_t*>(d)[i]);
+  }
+}
+
+template <int DDT, int WDT, int ODT>
+__global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ down,
                                                       const int32_t* __restrict__ inv,
                                                       const void* __restrict__ wts, int64_t T, int k,
                                                       int64_t H, void* __restrict__ out) {
@@ -205,14 +214,24 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
       for (int s = 0; s < k; ++s) {
         const int r = inv[t * k + s];
         if (r < 0) continue;
-        const float w = load_weight<DT, WDT>(wts, t * k + s);
-        const uint4 d = *reinterpret_cast<const uint4*>(down + int64_t(r) * H + 8 * c);
-        const uint32_t dv[4] = {d.x, d.y, d.z, d.w};
+        const float w = load_weight<WDT>(wts, t * k + s);
+        float dv[8];
+        if constexpr (DDT == E4B_FP32) {
+          const float4* dp = reinterpret_cast<const float4*>(static_cast<const float*>(down) + int64_t(r) * H + 8 * c);
+          const float4 d0 = dp[0], d1 = dp[1];
+          dv[0] = d0.x; dv[1] = d0.y; dv[2] = d0.z; dv[3] = d0.w;
+          dv[4] = d1.x; dv[5] = d1.y; dv[6] = d1.z; dv[7] = d1.w;
+        } else {
+          const uint4 d = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(down) + int64_t(r) * H + 8 * c);
+          const uint32_t q[4] = {d.x, d.y, d.z, d.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          acc[2 * j] = __fadd_rn(acc[2 * j], __fmul_rn(lo_f<DT>(dv[j]), w));
-          acc[2 * j + 1] = __fadd_rn(acc[2 * j + 1], __fmul_rn(hi_f<DT>(dv[j]), w));
+          for (int j = 0; j < 4; ++j) {
+            dv[2 * j] = lo_f<DDT>(q[j]);
+            dv[2 * j + 1] = hi_f<DDT>(q[j]);
+          }
         }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __fadd_rn(acc[j], mul_f32(dv[j], w));
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) store_out<ODT>(out, t * H + 8 * c + j, acc[j]);
@@ -221,8 +240,8 @@ __global__ void __launch_bounds__(256) combine_kernel(const uint16_t* __restrict
       for (int s = 0; s < k; ++s) {
         const int r = inv[t * k + s];
         if (r < 0) continue;
-        const float w = load_weight<DT, WDT>(wts, t * k + s);
-        acc = __fadd_rn(acc, __fmul_rn(to_f<DT>(down[int64_t(r) * H + c]), w));
+        const float w = load_weight<WDT>(wts, t * k + s);
+        acc = __fadd_rn(acc, mul_f32(load_down<DDT>(down, int64_t(r) * H + c), w));
       }
       store_out<ODT>(out, t * H + c, acc);
     }

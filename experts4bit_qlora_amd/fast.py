@@ -142,16 +142,17 @@ def fused_experts_forward(mod, hidden_states, top_k_index, top_k_weights):
     # custom epilogue: unfused GEMMs around the base's own Python epilogue
     M = tokens * k
     rb = ops.route(top_k_index, mod.num_experts)
-    up = ops.grouped_gemm(x, w1, rb, tokens, M, N.EPI_NONE, gather_k=k, path=_kernel_path)
+    up = ops.grouped_gemm(x, w1, rb, tokens, M, N.EPI_NONE, gather_k=k, path=_kernel_path, out_dtype=torch.float32)
     h = _epilogue(mod, up).to(compute_dtype).contiguous()
-    down = ops.grouped_gemm(h, w2, rb, tokens, M, N.EPI_NONE, path=_kernel_path)
+    down = ops.grouped_gemm(h, w2, rb, tokens, M, N.EPI_NONE, path=_kernel_path, out_dtype=torch.float32)
     return ops.combine(down, rb, top_k_weights, tokens, k, input_dtype)
 
 
 def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
     """Fused inference forward of an ``ExpertsLoRA`` (``fast.py:163-257``): grouped GEMMs over the
     expert-sorted rows with the low-rank delta added per expert group before the base's
-    epilogue. The group sizes come to the host once (as in the reference) to slice the groups."""
+    epilogue. The group sizes come to the host once (as in the reference) to slice the groups.
+    The GEMM outputs stay fp32 until the activation is rounded for the down projection."""
     base = mod.base
     if _wants_reference(mod, hidden_states):
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
@@ -176,13 +177,13 @@ def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
     rb = ops.route(top_k_index, E)
     offsets = rb.offsets.tolist()
     a_cat = x.index_select(0, (rb.sorted_flat[:M] // k).long())
-    up = ops.grouped_gemm(x, w1, rb, tokens, M, N.EPI_NONE, gather_k=k, path=_kernel_path)
+    up = ops.grouped_gemm(x, w1, rb, tokens, M, N.EPI_NONE, gather_k=k, path=_kernel_path, out_dtype=torch.float32)
     active = [e for e in range(E) if offsets[e + 1] > offsets[e]]
     for e in active:
         s, t = offsets[e], offsets[e + 1]
         up[s:t] += mod._lora(a_cat[s:t], mod.gate_up_lora_A[e], mod.gate_up_lora_B[e])
     h = _epilogue(base, up).to(compute_dtype).contiguous()
-    down = ops.grouped_gemm(h, w2, rb, tokens, M, N.EPI_NONE, path=_kernel_path)
+    down = ops.grouped_gemm(h, w2, rb, tokens, M, N.EPI_NONE, path=_kernel_path, out_dtype=torch.float32)
     for e in active:
         s, t = offsets[e], offsets[e + 1]
         down[s:t] += mod._lora(h[s:t], mod.down_lora_A[e], mod.down_lora_B[e])

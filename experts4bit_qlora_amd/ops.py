@@ -172,19 +172,22 @@ def route(top_k_index: torch.Tensor, num_experts: int, tile_m: int | None = None
 
 
 def grouped_gemm(a: torch.Tensor, qw: QW, rb: RoutingBuffers, tokens: int, M: int, epilogue: int = N.EPI_NONE,
-                 gather_k: int = 0, alpha: float = 1.702, limit: float = 7.0, path: int = N.PATH_AUTO) -> torch.Tensor:
-    """Grouped GEMM over expert-sorted rows with an optional fused epilogue; ``[M, n_out]``."""
+                 gather_k: int = 0, alpha: float = 1.702, limit: float = 7.0, path: int = N.PATH_AUTO,
+                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Grouped GEMM over expert-sorted rows with an optional fused epilogue; ``[M, n_out]`` in
+    ``out_dtype`` (default: ``a``'s dtype; ``torch.float32`` keeps the fp32 result)."""
     _require_cuda(a, qw.packed)
     L = N.lib()
     a = a.contiguous()
     gated = epilogue in (N.EPI_SWIGLU, N.EPI_CLAMP_SWIGLU, N.EPI_GPTOSS)
     n_out = qw.n // 2 if gated else qw.n
-    out = torch.empty(M, n_out, dtype=a.dtype, device=a.device)
+    od = a.dtype if out_dtype is None else out_dtype
+    out = torch.empty(M, n_out, dtype=od, device=a.device)
     s = qw.struct()
     rs = rb.struct()
     N.check("e4b_grouped_gemm",
             L.e4b_grouped_gemm(a.data_ptr(), dtype_code(a.dtype), gather_k, ctypes.byref(s), ctypes.byref(rs),
-                               tokens, M, epilogue, float(alpha), float(limit), path, out.data_ptr(),
+                               tokens, M, epilogue, float(alpha), float(limit), path, out.data_ptr(), dtype_code(od),
                                _stream(a.device)))
     return out
 

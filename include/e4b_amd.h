@@ -103,21 +103,23 @@ int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t
 
 /* Grouped GEMM over the expert-sorted rows: out[r, :] = epilogue(a_row(r) @ deq(W[e(r)]).T).
  * a_row(r) = a[sorted_flat[r] / gather_k] when gather_k > 0 (the gather of fast.py:135 fused
- * into the A loads), else a[r]. out is [M, n] (E4B_EPI_NONE) or [M, n/2] (gated epilogues) or
- * [M, n] (E4B_EPI_ACT), in act_dtype. The per-expert bias (w->bias) is added to the rounded
- * projection before the epilogue, as gpt-oss does.
+ * into the A loads), else a[r]. out is [M, n] (E4B_EPI_NONE, E4B_EPI_ACT) or [M, n/2] (gated
+ * epilogues), in out_dtype: the activation dtype (one rounding of the fp32 result) or E4B_FP32.
+ * The per-expert bias (w->bias) is added to the fp32 projection before the epilogue, as gpt-oss
+ * does; the epilogue itself runs in fp32.
  * Replaces: nf4_grouped.gemm_4bit_grouped (engines/fast.py:137-143, 150-156, 220-226, 242-248)
  * and mxfp4_grouped.gemm_mxfp4_grouped (engines/nvme_experts.py:852-865), plus the epilogue
  * of lora.py:102-128 / hot_residency.py:72-80 fused into the same launch. */
 int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e4b_qweight* w,
                      const e4b_routing* rt, int64_t tokens, int64_t M, int32_t epilogue, float alpha,
-                     float limit, int32_t flags, void* out, hipStream_t stream);
+                     float limit, int32_t flags, void* out, int32_t out_dtype, hipStream_t stream);
 
 /* Deterministic weighted combine back to token order:
  * out[t, :] = out_dtype( sum_{s<k} float(down[inv[t*k+s], :]) * float(top_k_weights[t, s]) ),
  * the slots summed in slot order in fp32 -- unique writes + a fixed-axis sum, never atomics.
+ * down is [M, hidden] in down_dtype (bf16, fp16 or fp32).
  * Replaces: engines/fast.py:158 and _scatter_combine at fast.py:260-278. */
-int e4b_combine(const void* down, int32_t act_dtype, const int32_t* inv, const void* top_k_weights,
+int e4b_combine(const void* down, int32_t down_dtype, const int32_t* inv, const void* top_k_weights,
                 int32_t weight_dtype, int64_t tokens, int32_t top_k, int64_t hidden, void* out,
                 int32_t out_dtype, hipStream_t stream);
 
@@ -125,7 +127,8 @@ int e4b_combine(const void* down, int32_t act_dtype, const int32_t* inv, const v
 size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts, int64_t n1,
                                int64_t n2, int32_t epilogue, int32_t act_dtype);
 
-/* The whole frozen-expert forward: route -> gate_up (+epilogue) -> down (+bias) -> combine.
+/* The whole frozen-expert forward: route -> gate_up (+epilogue, h rounded once to act_dtype)
+ * -> down (+bias, kept in fp32) -> combine (one rounding into out_dtype).
  * hidden [tokens, w1->k] in act_dtype; top_k_index [tokens, top_k] int64; top_k_weights
  * [tokens, top_k] in weight_dtype; out [tokens, w2->n] in out_dtype.
  * Replaces: engines/fast.py:100-160 fused_experts_forward (the bare-module forward that

@@ -110,21 +110,24 @@ def test_grouped_gemm_rejects_bad_arguments():
     L = N.lib()
     s, r = _qw(n=63), _rt()
     assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r), 1, 2, N.EPI_SWIGLU, 1.0, 7.0, 0,
-                              8192, None) == -1
+                              8192, N.BF16, None) == -1
     assert "even n" in _err()
     s = _qw()
     assert L.e4b_grouped_gemm(4096, N.FP32, 0, ctypes.byref(s), ctypes.byref(r), 1, 2, N.EPI_NONE, 1.0, 7.0, 0,
-                              8192, None) == -1
+                              8192, N.FP32, None) == -1
     assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r), 1, 2, N.EPI_GPTOSS, 1.0, 7.0, 0,
-                              8192, None) == -1
+                              8192, N.BF16, None) == -1
     assert "bias" in _err()
     r32 = _rt(tile_m=32)
     assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r32), 64, 128, N.EPI_NONE, 1.0, 7.0,
-                              N.PATH_MFMA, 8192, None) == -1
+                              N.PATH_MFMA, 8192, N.BF16, None) == -1
     assert "tile_m" in _err()
+    assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r), 1, 2, N.EPI_NONE, 1.0, 7.0, 0,
+                              8192, N.FP16, None) == -1
+    assert "out_dtype" in _err()
     # M == 0 is a valid no-op
     assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r), 0, 0, N.EPI_NONE, 1.0, 7.0, 0,
-                              8192, None) == 0
+                              8192, N.BF16, None) == 0
 
 
 def test_moe_forward_checks_shapes_and_workspace():

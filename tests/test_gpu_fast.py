@@ -34,7 +34,8 @@ def _auto_path():
 
 
 def _b_rel(a, b):
-    return ((a.float() - b.float()).abs().max() / b.float().abs().max().clamp_min(1e-6)).item()
+    a, b = a.float().cpu(), b.float().cpu()
+    return ((a - b).abs().max() / b.abs().max().clamp_min(1e-6)).item()
 
 
 def _make(E=4, H=128, inter=64, k=2, tokens=16, seed=0, has_gate=True, scale=1.0, dq=False):
@@ -61,8 +62,10 @@ def _oracle(mod, hs, top_i, top_w):
 
 
 def _assert_fidelity(fast, ref, oracle, label=""):
-    fro, maxabs, _ = moe.rel_errors(fast.float().cpu().numpy(), oracle)
-    fro_ref, _, _ = moe.rel_errors(ref.float().cpu().numpy(), oracle)
+    fro, maxabs, brel = moe.rel_errors(fast.float().cpu().numpy(), oracle)
+    fro_ref, maxabs_ref, brel_ref = moe.rel_errors(ref.float().cpu().numpy(), oracle)
+    print(f"[fidelity] {label}: fused rel-fro {fro:.2e} max-abs/rms {maxabs:.2e} max-abs/max {brel:.2e} | "
+          f"reference loop rel-fro {fro_ref:.2e} max-abs/rms {maxabs_ref:.2e} max-abs/max {brel_ref:.2e}", flush=True)
     assert fro <= 1e-2 and maxabs <= 2e-2, (label, fro, maxabs)
     assert fro <= max(2 * fro_ref, 5e-3), (label, fro, fro_ref)
 

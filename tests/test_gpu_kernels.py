@@ -59,7 +59,10 @@ def test_dequant_nf4_bit_exact(dt, dq):
     elif dt == torch.bfloat16:
         assert np.array_equal(_bits(got), numerics.f32_to_bf16_bits(want))
     else:
-        assert np.array_equal(_bits(got), want.astype(np.float16).view(np.uint16))
+        gb, wb = _bits(got), want.astype(np.float16).view(np.uint16)
+        bad = np.argwhere(gb != wb)
+        detail = [(tuple(i), float(want[tuple(i)]), hex(int(gb[tuple(i)])), hex(int(wb[tuple(i)]))) for i in bad[:8]]
+        assert bad.size == 0, f"{len(bad)} mismatches: {detail}"
 
 
 def test_dequant_nf4_expert_range_and_full_size_expert():
@@ -150,6 +153,12 @@ def _dense_from_kernel(qw) -> np.ndarray:
     return ops.dequant(qw, 0, qw.num_experts, dtype=torch.float32).cpu().numpy()
 
 
+def _weights_for(path, W):
+    """The weights each kernel family multiplies: fp32 decode (GEMV) or the reference's exact
+    bf16 dequantized weight (MFMA operands)."""
+    return numerics.round_bf16(W) if path == N.PATH_MFMA else W
+
+
 def _gemm_oracle(a_rows, W, rows_expert, bias=None):
     """fp64 per-row GEMM against the dequantized fp32 weights."""
     out = np.empty((a_rows.shape[0], W.shape[1]), np.float64)
@@ -185,9 +194,14 @@ def test_grouped_gemm_plain(path, fmt, T):
     rb = ops.route(torch.from_numpy(idx).to(DEV), E)
     out = ops.grouped_gemm(x.to(DEV), qw, rb, T, T * top, N.EPI_NONE, gather_k=top, path=path)
     ref = orouting.route(idx, E)
-    want = _gemm_oracle(x.float().numpy()[ref["token_rows"]], W, idx.reshape(-1)[ref["order"]])
+    want = _gemm_oracle(x.float().numpy()[ref["token_rows"]], _weights_for(path, W), idx.reshape(-1)[ref["order"]])
     fro, maxabs = _errs(out.float().cpu().numpy(), want)
     assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
+    # the fp32 output of the same GEMM is the unrounded sum
+    out32 = ops.grouped_gemm(x.to(DEV), qw, rb, T, T * top, N.EPI_NONE, gather_k=top, path=path,
+                             out_dtype=torch.float32)
+    fro32, _ = _errs(out32.cpu().numpy(), want)
+    assert out32.dtype == torch.float32 and fro32 < 1e-5, fro32
 
 
 @pytest.mark.parametrize("path", [N.PATH_GEMV, N.PATH_MFMA])
@@ -211,16 +225,12 @@ def test_grouped_gemm_fused_epilogues(path, epi):
     code = {"swiglu": N.EPI_SWIGLU, "act": N.EPI_ACT, "clamp": N.EPI_CLAMP_SWIGLU, "gptoss": N.EPI_GPTOSS}[epi]
     out = ops.grouped_gemm(x.to(DEV), qw, rb, T, T * top, code, gather_k=top, alpha=1.702, limit=1.5, path=path)
     ref = orouting.route(idx, E)
-    proj = _gemm_oracle(x.float().numpy()[ref["token_rows"]], W, idx.reshape(-1)[ref["order"]])
-    # the oracle epilogue on the bf16-rounded projection, per expert row
-    proj_r = numerics.round_bf16(proj.astype(np.float32))
     e_rows = idx.reshape(-1)[ref["order"]]
-    if epi == "gptoss":
-        want = np.concatenate([moe.epilogue_rounded(proj_r[r:r + 1], ("gptoss", 1.702, 1.5), I, "bf16",
-                                                    b1=bias.float().numpy()[e_rows[r]]) for r in range(len(e_rows))])
-    else:
-        spec = {"swiglu": "swiglu", "act": "act", "clamp": ("clamp_swiglu", 1.5)}[epi]
-        want = moe.epilogue_rounded(proj_r, spec, I, "bf16")
+    b = None if bias is None else bias.float().numpy().astype(np.float64)
+    proj = _gemm_oracle(x.float().numpy()[ref["token_rows"]], _weights_for(path, W), e_rows, bias=b)
+    # the fused epilogue runs in fp32 on the unrounded projection; h is rounded once
+    spec = {"swiglu": "swiglu", "act": "act", "clamp": ("clamp_swiglu", 1.5), "gptoss": ("gptoss", 1.702, 1.5)}[epi]
+    want = numerics.round_bf16(moe._glu_exact(proj, spec, I).astype(np.float32))
     fro, maxabs = _errs(out.float().cpu().numpy(), want)
     assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
 
@@ -239,7 +249,9 @@ def test_grouped_gemm_fp16_activations():
     for path in (N.PATH_GEMV, N.PATH_MFMA):
         out = ops.grouped_gemm(x.to(DEV), qw, rb, T, T * top, N.EPI_NONE, gather_k=top, path=path)
         assert out.dtype == torch.float16
-        fro, maxabs = _errs(out.float().cpu().numpy(), want)
+        want_p = want if path == N.PATH_GEMV else _gemm_oracle(
+            x.float().numpy()[ref["token_rows"]], numerics.round_fp16(W), idx.reshape(-1)[ref["order"]])
+        fro, maxabs = _errs(out.float().cpu().numpy(), want_p)
         assert fro <= 1e-2 and maxabs <= 2e-2, (path, fro, maxabs)
 
 
