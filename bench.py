@@ -1,0 +1,423 @@
+"""Benchmark of the frozen-expert MoE forward on one MI355X.
+
+Workload: OLMoE-1B-7B geometry, all 16 MoE layers stacked, decode.
+E=64 experts, hidden 2048, moe_intermediate 1024, top-8 softmax routing (not renormalised),
+SwiGLU; weights N(0, 0.02) from per-layer seeds, NF4 / blocksize 64 / fp32 absmax; bf16 N(0,1)
+activations. One "step" = one decode pass through the 16 layers at batch 1 (route, gate_up +
+SwiGLU, down, combine per layer), replayed from a HIP graph (the fused path never syncs). Inputs
+and weights are resident in HBM when the timed region starts.
+
+``value`` = routed-expert HBM bytes per step / step time (GB/s): each distinct routed expert's
+3,538,944 bytes (packed NF4 + fp32 absmax, both projections) counted once per layer. The line
+also carries us/layer and tok/s at batches 1, 8 and 64, the Qwen3-30B-A3B-geometry 4096-token
+Zipf prefill in TFLOP/s, the dominant kernel's roofline measured with HIP events
+on the launch stream, and the reference per-expert loop timed on the host CPU.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--extra]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE layer µs + achieved HBM GB/s at bs=1; MFMA TFLOP/s at 4096-token prefill"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+OLMOE = dict(E=64, H=2048, I=1024, k=8, layers=16, renorm=False)
+QWEN3 = dict(E=128, H=2048, I=768, k=8, renorm=True)
+GPTOSS = dict(E=32, H=2880, I=2880, k=4)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def nf4_expert_bytes(H, I):
+    """Packed NF4 + fp32 absmax bytes of one expert, both projections."""
+    gu = 2 * I * H // 2 + 2 * I * H // 64 * 4
+    dn = H * I // 2 + H * I // 64 * 4
+    return gu, dn
+
+
+def dq_expert_bytes(H, I):
+    """Packed NF4 + u8 absmax codes + fp32 absmax2 + fp32 offset, both projections."""
+    tot = 0
+    for n, k in ((2 * I, H), (H, I)):
+        nb = n * k // 64
+        tot += n * k // 2 + nb + math.ceil(nb / 256) * 4 + 4
+    return tot
+
+
+def make_layer(cfg, seed, dq=False):
+    import torch
+
+    import experts4bit_qlora_amd as e4b
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    E, H, I = cfg["E"], cfg["H"], cfg["I"]
+    gu = torch.randn(E, 2 * I, H, generator=g, device="cuda") * 0.02
+    dn = torch.randn(E, H, I, generator=g, device="cuda") * 0.02
+    mod = e4b.Experts4bit.from_float(gu, dn, compute_dtype=torch.bfloat16, compress_statistics=dq).eval()
+    del gu, dn
+    return mod
+
+
+def make_inputs(cfg, T, seed, zipf=None):
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(T, cfg["H"], generator=g, device="cuda").to(torch.bfloat16)
+    logits = torch.randn(T, cfg["E"], generator=g, device="cuda")
+    if zipf is not None:
+        rank = torch.randperm(cfg["E"], generator=torch.Generator().manual_seed(seed + 1)).cuda() + 1
+        logits = logits - zipf * torch.log(rank.float())
+    w, idx = torch.topk(torch.softmax(logits, -1), cfg["k"], dim=-1)
+    if cfg.get("renorm"):
+        w = w / w.sum(-1, keepdim=True)
+    return x, idx, w.to(torch.bfloat16)
+
+
+def graph_of(fn):
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fn()
+    return g, out
+
+
+def time_graph(g, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per replay
+
+
+def decode_bench(mods, cfg, T, steps, warmup, seed0):
+    """Time the 16-layer decode step at batch T; returns a dict of figures."""
+    import torch
+
+    inputs = [make_inputs(cfg, T, seed0 + 10 * l) for l in range(len(mods))]
+    distinct = [int(torch.unique(idx).numel()) for _, idx, _ in inputs]
+    gu_b, dn_b = nf4_expert_bytes(cfg["H"], cfg["I"])
+    step_bytes = sum(distinct) * (gu_b + dn_b)
+
+    def step():
+        with torch.no_grad():
+            return [m(x, idx, w) for m, (x, idx, w) in zip(mods, inputs)]
+
+    eager = step()
+    g, outs = graph_of(step)
+    g.replay()
+    torch.cuda.synchronize()
+    for a, b in zip(eager, outs):  # the graph replays the exact eager computation
+        assert torch.equal(a, b), "graph replay differs from the eager forward"
+    # eager wall time (Python + launches), for reference
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(max(3, steps // 4)):
+        step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3 / max(3, steps // 4)
+    ms = time_graph(g, steps, warmup)
+    L = len(mods)
+    return {
+        "batch": T,
+        "ms_per_step": ms,
+        "us_per_layer": ms * 1e3 / L,
+        "tok_per_s": T / (ms / 1e3),
+        "routed_bytes_per_step": step_bytes,
+        "distinct_experts_per_layer": round(sum(distinct) / L, 2),
+        "hbm_gbs": step_bytes / (ms / 1e3) / 1e9,
+        "hbm_frac": step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
+        "eager_ms_per_step": eager_ms,
+    }
+
+
+def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
+    """gate_up + SwiGLU grouped GEMV at bs=1 alone, 16 layers per replay, HIP events on the
+    launch stream: achieved = routed gate_up bytes per launch / average launch duration."""
+    import torch
+
+    from experts4bit_qlora_amd import _native as N
+    from experts4bit_qlora_amd import fast as F
+    from experts4bit_qlora_amd import ops
+
+    inputs = [make_inputs(cfg, 1, seed0 + 10 * l) for l in range(len(mods))]
+    qws = [F._qweights(m)[0] for m in mods]
+    routes = [ops.route(idx, cfg["E"]) for _, idx, _ in inputs]
+    torch.cuda.synchronize()
+
+    def launches():
+        return [ops.grouped_gemm(x, qw, rb, 1, cfg["k"], N.EPI_SWIGLU, gather_k=cfg["k"])
+                for (x, _, _), qw, rb in zip(inputs, qws, routes)]
+
+    g, _ = graph_of(launches)
+    ms = time_graph(g, steps * 4, warmup)
+    per_launch_us = ms * 1e3 / len(mods)
+    gu_b, _ = nf4_expert_bytes(cfg["H"], cfg["I"])
+    bytes_per_launch = cfg["k"] * gu_b  # 8 distinct routed experts at bs=1
+    achieved = bytes_per_launch / (per_launch_us * 1e-6) / 1e9
+    return {
+        "bound": "hbm",
+        "kernel": "gemv_kernel<bf16, nf4, 16> (gate_up + SwiGLU, bs=1)",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": None,
+        "bytes_per_launch": bytes_per_launch,
+        "avg_launch_us": round(per_launch_us, 3),
+    }
+
+
+def prefill_bench(steps, warmup):
+    """Qwen3-30B-A3B geometry, one layer, 4096 tokens, Zipf(1.1) routing, double-quant."""
+    import torch
+
+    cfg = QWEN3
+    mod = make_layer(cfg, seed=1000 + 300, dq=True)
+    import experts4bit_qlora_amd as e4b
+
+    e4b.enable_fast(mod)
+    x, idx, w = make_inputs(cfg, 4096, seed=1000 + 301, zipf=1.1)
+    counts = torch.bincount(idx.reshape(-1), minlength=cfg["E"])
+
+    def step():
+        with torch.no_grad():
+            return mod(x, idx, w)
+
+    g, _ = graph_of(step)
+    ms = time_graph(g, max(steps, 10), warmup)
+    flops = 2 * cfg["k"] * 4096 * (2 * cfg["I"] * cfg["H"] + cfg["H"] * cfg["I"])
+    tflops = flops / (ms / 1e3) / 1e12
+    return {
+        "workload": "Qwen3-30B-A3B geometry, 1 layer, 4096-token prefill, Zipf(1.1), NF4 double-quant",
+        "ms": ms,
+        "tflops": tflops,
+        "mfma_frac": tflops / BF16_PEAK_TFLOPS,
+        "flop": flops,
+        "max_rows_per_expert": int(counts.max().item()),
+        "min_rows_per_expert": int(counts.min().item()),
+    }
+
+
+def extra_benches(steps, warmup):
+    """configs[2] (Qwen3 decode, double-quant) and configs[4] (gpt-oss MXFP4 + biases)."""
+    import torch
+
+    import experts4bit_qlora_amd as e4b
+
+    out = {}
+    cfg = QWEN3
+    mod = make_layer(cfg, seed=1000 + 200, dq=True)
+    e4b.enable_fast(mod)
+    per_expert = dq_expert_bytes(cfg["H"], cfg["I"])
+    for T in (1, 32, 256):
+        x, idx, w = make_inputs(cfg, T, seed=1000 + 210 + T)
+
+        def step():
+            with torch.no_grad():
+                return mod(x, idx, w)
+
+        g, _ = graph_of(step)
+        ms = time_graph(g, steps * 4, warmup)
+        nbytes = int(torch.unique(idx).numel()) * per_expert
+        out[f"qwen3_dq_bs{T}"] = {"us": ms * 1e3, "hbm_gbs": nbytes / (ms / 1e3) / 1e9}
+    del mod
+    cfg = GPTOSS
+    g0 = torch.Generator(device="cuda").manual_seed(1400)
+    E, H, I = cfg["E"], cfg["H"], cfg["I"]
+    gu = torch.randn(E, 2 * I, H, generator=g0, device="cuda") * 0.02
+    dn = torch.randn(E, H, I, generator=g0, device="cuda") * 0.02
+    b1 = torch.randn(E, 2 * I, generator=g0, device="cuda") * 0.02
+    b2 = torch.randn(E, H, generator=g0, device="cuda") * 0.02
+    mod = e4b.GptOssExpertsMxfp4.from_float(gu, b1, dn, b2).eval()
+    del gu, dn
+    e4b.enable_fast(mod)
+    per_expert = (2 * I * H + H * I) // 2 + (2 * I * H + H * I) // 32 + (2 * I + H) * 2
+    for T in (1, 2048):
+        gi = torch.Generator(device="cuda").manual_seed(1410 + T)
+        x = torch.randn(T, H, generator=gi, device="cuda").to(torch.bfloat16)
+        val, idx = torch.topk(torch.randn(T, E, generator=gi, device="cuda"), cfg["k"], dim=-1)
+        w = torch.softmax(val, -1).to(torch.bfloat16)
+
+        def step():
+            with torch.no_grad():
+                return mod(x, idx, w)
+
+        g, _ = graph_of(step)
+        ms = time_graph(g, steps * 2, warmup)
+        nbytes = int(torch.unique(idx).numel()) * per_expert
+        flops = 2 * cfg["k"] * T * (2 * I * H + H * I)
+        out[f"gptoss_mxfp4_bs{T}"] = {"us": ms * 1e3, "hbm_gbs": nbytes / (ms / 1e3) / 1e9,
+                                      "tflops": flops / (ms / 1e3) / 1e12}
+    return out
+
+
+def cpu_baseline(mod, cfg, budget_s=20.0):
+    """The reference per-expert loop (the oracle's torch-CPU restatement of ExpertsNbit.forward)
+    on the host cores, one OLMoE layer at batch 1, same weights and inputs."""
+    import torch
+
+    from oracle import moe as omoe
+
+    # the box's CPU share (OMP_NUM_THREADS), not os.cpu_count() of the whole host
+    threads = torch.get_num_threads()
+    packed1, absmax1 = mod.gate_up_proj.cpu(), mod.gate_up_absmax.cpu()
+    packed2, absmax2 = mod.down_proj.cpu(), mod.down_absmax.cpu()
+    code = mod.code.cpu()
+    n1, k1 = mod._gate_up_shape
+    n2, k2 = mod._down_shape
+    x, idx, w = make_inputs(cfg, 1, seed=1000 + 100 + 0)
+    x, idx, w = x.cpu(), idx.cpu(), w.cpu()
+
+    def w1(e, dt):
+        return omoe.dequant_torch_expert(packed1[e], absmax1[e], code, n1, k1, dt)
+
+    def w2(e, dt):
+        return omoe.dequant_torch_expert(packed2[e], absmax2[e], code, n2, k2, dt)
+
+    def run():
+        return omoe.reference_loop(x, idx, w, w1, w2, cfg["E"], compute_dtype=torch.bfloat16)
+
+    for _ in range(3):
+        run()
+    times = []
+    t_begin = time.perf_counter()
+    while len(times) < 10 or (time.perf_counter() - t_begin < budget_s and len(times) < 50):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_begin > budget_s and len(times) >= 3:
+            break
+    med = statistics.median(times)
+    gu_b, dn_b = nf4_expert_bytes(cfg["H"], cfg["I"])
+    nbytes = cfg["k"] * (gu_b + dn_b)
+    return {
+        "value": round(nbytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "us_per_layer": round(med * 1e6, 1),
+        "sample": f"1 OLMoE layer (E=64, H=2048, I=1024, top-8), batch 1, {len(times)} timed reps after 3 "
+                  "warm-ups, median; torch-CPU restatement of ExpertsNbit.forward with the pure-torch NF4 "
+                  "dequant (bitsandbytes' CPU dequant is not installed)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--extra", action="store_true", help="also run configs[2] and configs[4]")
+    ap.add_argument("--kernel-only", action="store_true", help="only the dominant-kernel loop (for profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import experts4bit_qlora_amd as e4b
+    from experts4bit_qlora_amd import _native as N
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+    N.lib()  # fail loudly if the kernel library is missing
+    cfg = OLMOE
+    log("building 16 OLMoE-geometry NF4 layers")
+    mods = [make_layer(cfg, seed=1000 + 100 + l) for l in range(cfg["layers"])]
+    for m in mods:
+        assert e4b.enable_fast(m) == 1
+    torch.cuda.synchronize()
+
+    log("dominant kernel roofline (gate_up GEMV, bs=1)")
+    roof = dominant_kernel_roofline(mods, cfg, args.steps, args.warmup, seed0=1000 + 100)
+    if args.kernel_only:
+        print(json.dumps({"roofline": roof}))
+        return
+
+    decode = {}
+    for T in (1, 8, 64):
+        log(f"decode step, batch {T}")
+        decode[T] = decode_bench(mods, cfg, T, args.steps, args.warmup, seed0=1000 + 100)
+    main_line = decode[1]
+
+    prefill = None
+    if not args.no_prefill:
+        log("Qwen3 4096-token Zipf prefill")
+        prefill = prefill_bench(args.steps, args.warmup)
+
+    extra = extra_benches(args.steps, args.warmup) if args.extra else None
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline (reference per-expert loop on the host)")
+        cpu = cpu_baseline(mods[0], cfg)
+
+    line = {
+        "metric": METRIC,
+        "value": round(main_line["hbm_gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_line["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "OLMoE-1B-7B geometry, 16 stacked MoE layers, decode batch 1 (configs[1])",
+            "experts": cfg["E"], "hidden": cfg["H"], "moe_intermediate": cfg["I"], "top_k": cfg["k"],
+            "layers": cfg["layers"], "quant": "NF4, blocksize 64, fp32 absmax", "global_batch": 1,
+            "parallelism": "single GPU",
+        },
+        "us_per_layer": round(main_line["us_per_layer"], 3),
+        "tok_per_s": round(main_line["tok_per_s"], 1),
+        "hbm_frac": round(main_line["hbm_frac"], 4),
+        "decode": {f"bs{T}": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}
+                   for T, d in decode.items()},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+    }
+    if prefill is not None:
+        line["prefill"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in prefill.items()}
+    if extra is not None:
+        line["extra"] = extra
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
