@@ -159,8 +159,9 @@ def decode_bench(mods, cfg, T, steps, warmup, seed0):
 
 
 def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
-    """gate_up + SwiGLU grouped GEMV at bs=1 alone, 16 layers per replay, HIP events on the
-    launch stream: achieved = routed gate_up bytes per launch / average launch duration."""
+    """The decode gate_up kernel (routing + gate_up GEMV + SwiGLU) at bs=1 alone, 16 layers per
+    graph replay, timed with HIP events on the launch stream: achieved = routed gate_up bytes
+    per launch / average launch duration."""
     import torch
 
     from experts4bit_qlora_amd import _native as N
@@ -169,12 +170,10 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
 
     inputs = [make_inputs(cfg, 1, seed0 + 10 * l) for l in range(len(mods))]
     qws = [F._qweights(m)[0] for m in mods]
-    routes = [ops.route(idx, cfg["E"]) for _, idx, _ in inputs]
     torch.cuda.synchronize()
 
     def launches():
-        return [ops.grouped_gemm(x, qw, rb, 1, cfg["k"], N.EPI_SWIGLU, gather_k=cfg["k"])
-                for (x, _, _), qw, rb in zip(inputs, qws, routes)]
+        return [ops.decode_gate_up(x, idx, qw, N.EPI_SWIGLU) for (x, idx, _), qw in zip(inputs, qws)]
 
     g, _ = graph_of(launches)
     ms = time_graph(g, steps * 4, warmup)
@@ -184,7 +183,7 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
     achieved = bytes_per_launch / (per_launch_us * 1e-6) / 1e9
     return {
         "bound": "hbm",
-        "kernel": "gemv_kernel<bf16, nf4, 16> (gate_up + SwiGLU, bs=1)",
+        "kernel": "decode_up_kernel<bf16, nf4, G=16, CPL=4> (routing + gate_up + SwiGLU, bs=1)",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",

@@ -31,6 +31,8 @@ EXPORTS = (
     "e4b_route",
     "e4b_grouped_gemm",
     "e4b_combine",
+    "e4b_decode_gate_up",
+    "e4b_decode_down_combine",
     "e4b_moe_workspace_bytes",
     "e4b_moe_forward",
 )
@@ -98,6 +100,10 @@ def _bind(L):
     L.e4b_grouped_gemm.argtypes = [P, I32, I32, QW, RT, I64, I64, I32, F32, F32, I32, P, I32, P]
     L.e4b_combine.restype = ctypes.c_int
     L.e4b_combine.argtypes = [P, I32, P, P, I32, I64, I32, I64, P, I32, P]
+    L.e4b_decode_gate_up.restype = ctypes.c_int
+    L.e4b_decode_gate_up.argtypes = [P, I32, I64, P, I32, QW, I32, F32, F32, P, P]
+    L.e4b_decode_down_combine.restype = ctypes.c_int
+    L.e4b_decode_down_combine.argtypes = [P, I32, I64, P, P, I32, I32, QW, P, I32, P]
     L.e4b_moe_workspace_bytes.restype = ctypes.c_size_t
     L.e4b_moe_workspace_bytes.argtypes = [I64, I32, I32, I64, I64, I32, I32]
     L.e4b_moe_forward.restype = ctypes.c_int

@@ -11,6 +11,7 @@
 #include <string>
 
 #include "common.h"
+#include "decode.h"
 #include "dequant.h"
 #include "gemm.h"
 #include "gemv.h"
@@ -175,6 +176,73 @@ void launch_combine_dt(const void* down, const int32_t* inv, const void* w, int 
   }
 }
 
+// Decode path: G lanes per weight row (a power of two in [4, 32], about four 16-byte chunks
+// each) and CPL chunks per lane, rounded up to an instantiated count. 0 = not supported.
+void decode_shape(int64_t k, int* G, int* CPL) {
+  const int64_t chunks = k / 32;
+  int g = 4;
+  while (g < 32 && chunks / (2 * g) >= 4) g *= 2;
+  int64_t c = (chunks + g - 1) / g;
+  int cpl = c <= 2 ? 2 : c <= 4 ? 4 : c <= 6 ? 6 : c <= 8 ? 8 : 0;
+  if (g > 4 && cpl < 4) cpl = 4;
+  *G = g;
+  *CPL = cpl;
+}
+
+template <int DT, int FMT, int G, int CPL>
+void launch_up_gc(const e4b::DecodeArgs& a, int64_t max_active, hipStream_t s) {
+  constexpr int cols_per_block = (e4b::kDecThreads / e4b::kWave) * (e4b::kWave / G);
+  dim3 grid(static_cast<unsigned>(cdiv(a.n_out, cols_per_block)), static_cast<unsigned>(max_active));
+  hipLaunchKernelGGL((e4b::decode_up_kernel<DT, FMT, G, CPL>), grid, dim3(e4b::kDecThreads), 0, s, a);
+}
+
+template <int DT, int FMT, int G, int CPL>
+void launch_down_gc(const e4b::DecodeArgs& a, int64_t, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>(cdiv(a.w.n, e4b::kDownCols)));
+  hipLaunchKernelGGL((e4b::decode_down_kernel<DT, FMT, G, CPL>), grid, dim3(e4b::kDecThreads), 0, s, a);
+}
+
+// Dispatch over (G, CPL) for one of the two decode kernels (UP = gate_up, else down).
+template <bool UP, int DT, int FMT>
+void launch_decode_shape(const e4b::DecodeArgs& a, int64_t max_active, hipStream_t s) {
+  int G, CPL;
+  decode_shape(a.w.k, &G, &CPL);
+#define E4B_DEC_CASE(g, c)                                                \
+  if (G == g && CPL == c) {                                               \
+    if (UP) launch_up_gc<DT, FMT, g, c>(a, max_active, s);                \
+    else launch_down_gc<DT, FMT, g, c>(a, max_active, s);                 \
+    return;                                                               \
+  }
+  E4B_DEC_CASE(4, 2) E4B_DEC_CASE(4, 4) E4B_DEC_CASE(4, 6) E4B_DEC_CASE(4, 8)
+  E4B_DEC_CASE(8, 4) E4B_DEC_CASE(8, 6) E4B_DEC_CASE(8, 8)
+  E4B_DEC_CASE(16, 4) E4B_DEC_CASE(16, 6) E4B_DEC_CASE(16, 8)
+  E4B_DEC_CASE(32, 4) E4B_DEC_CASE(32, 6) E4B_DEC_CASE(32, 8)
+#undef E4B_DEC_CASE
+}
+
+template <bool UP>
+void launch_decode(const e4b::DecodeArgs& a, int act_dtype, int64_t max_active, hipStream_t s) {
+  if (act_dtype == E4B_BF16) {
+    switch (a.w.format) {
+      case E4B_FMT_NF4: launch_decode_shape<UP, E4B_BF16, E4B_FMT_NF4>(a, max_active, s); break;
+      case E4B_FMT_NF4_DQ: launch_decode_shape<UP, E4B_BF16, E4B_FMT_NF4_DQ>(a, max_active, s); break;
+      default: launch_decode_shape<UP, E4B_BF16, E4B_FMT_MXFP4>(a, max_active, s); break;
+    }
+  } else {
+    switch (a.w.format) {
+      case E4B_FMT_NF4: launch_decode_shape<UP, E4B_FP16, E4B_FMT_NF4>(a, max_active, s); break;
+      case E4B_FMT_NF4_DQ: launch_decode_shape<UP, E4B_FP16, E4B_FMT_NF4_DQ>(a, max_active, s); break;
+      default: launch_decode_shape<UP, E4B_FP16, E4B_FMT_MXFP4>(a, max_active, s); break;
+    }
+  }
+}
+
+bool decode_supported(int64_t M, int E, const e4b_qweight* w) {
+  int G, CPL;
+  decode_shape(w->k, &G, &CPL);
+  return M <= e4b::kDecMaxRows && E <= e4b::kDecMaxExperts && CPL > 0;
+}
+
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 int64_t max_tiles_for(int64_t M, int E, int tile_m) { return cdiv(M, tile_m) + std::min<int64_t>(E, M); }
@@ -297,6 +365,73 @@ int e4b_combine(const void* down, int32_t down_dtype, const int32_t* inv, const 
   return check_launch("combine_kernel");
 }
 
+int e4b_decode_gate_up(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                       int32_t top_k, const e4b_qweight* w1, int32_t epilogue, float alpha, float limit, void* h,
+                       hipStream_t stream) {
+  int rc = check_weight(w1);
+  if (rc) return rc;
+  if (!act_dtype_ok(act_dtype)) return fail(E4B_EINVAL, "act_dtype must be bf16 or fp16 (got %d)", act_dtype);
+  if (epilogue < E4B_EPI_NONE || epilogue > E4B_EPI_GPTOSS) return fail(E4B_EINVAL, "bad epilogue %d", epilogue);
+  const bool pair = is_gated_epi(epilogue);
+  if (pair && (w1->n % 2)) return fail(E4B_EINVAL, "gated epilogue needs an even n");
+  if (epilogue == E4B_EPI_GPTOSS && !w1->bias) return fail(E4B_EINVAL, "gpt-oss epilogue needs the gate_up bias");
+  if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "bad tokens/top_k");
+  if (tokens == 0) return E4B_OK;
+  const int64_t M = tokens * top_k;
+  if (!decode_supported(M, w1->num_experts, w1))
+    return fail(E4B_EUNSUPPORTED, "decode path needs tokens*top_k <= %d, E <= %d and k <= 8192 (got M=%lld E=%d)",
+                e4b::kDecMaxRows, e4b::kDecMaxExperts, (long long)M, w1->num_experts);
+  if (!hidden || !top_k_index || !h) return fail(E4B_EINVAL, "NULL pointer");
+  if (!aligned16(hidden) || !aligned16(h)) return fail(E4B_EINVAL, "hidden / h must be 16-byte aligned");
+  e4b::DecodeArgs a{};
+  a.x = static_cast<const uint16_t*>(hidden);
+  a.topk = top_k_index;
+  a.tokens = static_cast<int>(tokens);
+  a.k = top_k;
+  a.E = w1->num_experts;
+  a.w = *w1;
+  a.epi = epilogue;
+  a.alpha = alpha;
+  a.limit = limit;
+  a.out = h;
+  a.odt = act_dtype;
+  a.n_out = pair ? w1->n / 2 : w1->n;
+  launch_decode<true>(a, act_dtype, std::min<int64_t>(w1->num_experts, M), stream);
+  return check_launch("decode_up_kernel");
+}
+
+int e4b_decode_down_combine(const void* h, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                            const void* top_k_weights, int32_t weight_dtype, int32_t top_k, const e4b_qweight* w2,
+                            void* out, int32_t out_dtype, hipStream_t stream) {
+  int rc = check_weight(w2);
+  if (rc) return rc;
+  if (!act_dtype_ok(act_dtype)) return fail(E4B_EINVAL, "act_dtype must be bf16 or fp16 (got %d)", act_dtype);
+  if (!any_dtype_ok(weight_dtype) || !any_dtype_ok(out_dtype)) return fail(E4B_EINVAL, "bad weight/out dtype");
+  if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "bad tokens/top_k");
+  if (tokens == 0) return E4B_OK;
+  const int64_t M = tokens * top_k;
+  if (!decode_supported(M, w2->num_experts, w2))
+    return fail(E4B_EUNSUPPORTED, "decode path needs tokens*top_k <= %d, E <= %d and k <= 8192 (got M=%lld E=%d)",
+                e4b::kDecMaxRows, e4b::kDecMaxExperts, (long long)M, w2->num_experts);
+  if (!h || !top_k_index || !top_k_weights || !out) return fail(E4B_EINVAL, "NULL pointer");
+  if (!aligned16(h)) return fail(E4B_EINVAL, "h must be 16-byte aligned");
+  e4b::DecodeArgs a{};
+  a.x = static_cast<const uint16_t*>(h);
+  a.topk = top_k_index;
+  a.topk_w = top_k_weights;
+  a.wdt = weight_dtype;
+  a.tokens = static_cast<int>(tokens);
+  a.k = top_k;
+  a.E = w2->num_experts;
+  a.w = *w2;
+  a.epi = E4B_EPI_NONE;
+  a.out = out;
+  a.odt = out_dtype;
+  a.n_out = w2->n;
+  launch_decode<false>(a, act_dtype, 0, stream);
+  return check_launch("decode_down_kernel");
+}
+
 size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts, int64_t n1, int64_t n2,
                                int32_t epilogue, int32_t act_dtype) {
   (void)act_dtype;
@@ -336,6 +471,24 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   if (!workspace || workspace_bytes < need)
     return fail(E4B_ESPACE, "workspace %zu bytes < %zu needed", workspace_bytes, need);
   if (!aligned16(workspace)) return fail(E4B_EINVAL, "workspace must be 16-byte aligned");
+  if (!act_dtype_ok(act_dtype)) return fail(E4B_EINVAL, "act_dtype must be bf16 or fp16 (got %d)", act_dtype);
+  if (!any_dtype_ok(weight_dtype) || !any_dtype_ok(out_dtype)) return fail(E4B_EINVAL, "bad weight/out dtype");
+  if (epilogue < E4B_EPI_NONE || epilogue > E4B_EPI_GPTOSS) return fail(E4B_EINVAL, "bad epilogue %d", epilogue);
+  if (w1->format != w2->format) return fail(E4B_EINVAL, "w1 and w2 use different formats");
+  if (epilogue == E4B_EPI_GPTOSS && !w1->bias) return fail(E4B_EINVAL, "gpt-oss epilogue needs the gate_up bias");
+  if (!top_k_index || !top_k_weights || !hidden || !out) return fail(E4B_EINVAL, "NULL pointer");
+  if (!aligned16(hidden)) return fail(E4B_EINVAL, "hidden must be 16-byte aligned");
+
+  // Decode path: two launches, routing recomputed in LDS, combine fused into the down kernel.
+  const bool decode_ok = decode_supported(M, E, w1) && decode_supported(M, E, w2);
+  const bool use_decode = decode_ok && ((flags == E4B_PATH_AUTO && tokens <= 8) || flags == E4B_PATH_GEMV);
+  if (use_decode) {
+    void* h = workspace;
+    rc = e4b_decode_gate_up(hidden, act_dtype, tokens, top_k_index, top_k, w1, epilogue, alpha, limit, h, stream);
+    if (rc) return rc;
+    return e4b_decode_down_combine(h, act_dtype, tokens, top_k_index, top_k_weights, weight_dtype, top_k, w2, out,
+                                   out_dtype, stream);
+  }
 
   char* p = static_cast<char*>(workspace);
   auto take = [&](size_t bytes) {

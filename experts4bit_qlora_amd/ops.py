@@ -207,6 +207,41 @@ def combine(down: torch.Tensor, rb: RoutingBuffers, top_k_weights: torch.Tensor,
     return out
 
 
+def decode_gate_up(hidden: torch.Tensor, top_k_index: torch.Tensor, w1: QW, epilogue: int, alpha: float = 1.702,
+                   limit: float = 7.0) -> torch.Tensor:
+    """Decode-path gate_up (routing recomputed on the device): ``h [tokens * k, h_cols]`` in flat
+    (token, slot) order."""
+    _require_cuda(hidden, top_k_index, w1.packed)
+    L = N.lib()
+    x = hidden.contiguous()
+    idx = top_k_index.to(torch.int64).contiguous()
+    T, k = idx.shape
+    gated = epilogue in (N.EPI_SWIGLU, N.EPI_CLAMP_SWIGLU, N.EPI_GPTOSS)
+    h = torch.empty(T * k, w1.n // 2 if gated else w1.n, dtype=x.dtype, device=x.device)
+    s1 = w1.struct()
+    N.check("e4b_decode_gate_up",
+            L.e4b_decode_gate_up(x.data_ptr(), dtype_code(x.dtype), T, idx.data_ptr(), k, ctypes.byref(s1), epilogue,
+                                 float(alpha), float(limit), h.data_ptr(), _stream(x.device)))
+    return h
+
+
+def decode_down_combine(h: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: torch.Tensor, w2: QW,
+                        out_dtype: torch.dtype) -> torch.Tensor:
+    """Decode-path down projection fused with the deterministic k-slot combine: ``[tokens, n]``."""
+    _require_cuda(h, top_k_index, top_k_weights, w2.packed)
+    L = N.lib()
+    idx = top_k_index.to(torch.int64).contiguous()
+    w = top_k_weights.contiguous()
+    T, k = idx.shape
+    out = torch.empty(T, w2.n, dtype=out_dtype, device=h.device)
+    s2 = w2.struct()
+    N.check("e4b_decode_down_combine",
+            L.e4b_decode_down_combine(h.contiguous().data_ptr(), dtype_code(h.dtype), T, idx.data_ptr(), w.data_ptr(),
+                                      dtype_code(w.dtype), k, ctypes.byref(s2), out.data_ptr(), dtype_code(out_dtype),
+                                      _stream(h.device)))
+    return out
+
+
 def moe_forward(hidden: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: torch.Tensor, w1: QW, w2: QW,
                 epilogue: int, out_dtype: torch.dtype, alpha: float = 1.702, limit: float = 7.0,
                 path: int = N.PATH_AUTO) -> torch.Tensor:

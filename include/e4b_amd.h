@@ -123,6 +123,25 @@ int e4b_combine(const void* down, int32_t down_dtype, const int32_t* inv, const 
                 int32_t weight_dtype, int64_t tokens, int32_t top_k, int64_t hidden, void* out,
                 int32_t out_dtype, hipStream_t stream);
 
+/* Decode path, first half: routing of top_k_index recomputed on the device (no route launch),
+ * gate_up GEMV with the fused epilogue. h is [tokens * top_k, h_cols] in act_dtype, row
+ * t * top_k + s holding token t's activation for slot s (flat order, not expert order).
+ * Needs tokens * top_k <= 512, E <= 256, w1->k <= 8192 (E4B_EUNSUPPORTED otherwise).
+ * Replaces: engines/fast.py:125-148 (sort, gather, gemm_4bit_grouped gate_up, _epilogue) for
+ * small batches. */
+int e4b_decode_gate_up(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                       int32_t top_k, const e4b_qweight* w1, int32_t epilogue, float alpha, float limit,
+                       void* h, hipStream_t stream);
+
+/* Decode path, second half: down GEMV over every routed row plus the deterministic k-slot
+ * combine, fused (out[t] = sum over s in slot order of (h[t*k+s] @ W2[e].T + bias) * w[t, s]).
+ * Same limits as e4b_decode_gate_up.
+ * Replaces: engines/fast.py:150-160 (gemm_4bit_grouped down, router-weight gather) and
+ * _scatter_combine at fast.py:260-278. */
+int e4b_decode_down_combine(const void* h, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                            const void* top_k_weights, int32_t weight_dtype, int32_t top_k,
+                            const e4b_qweight* w2, void* out, int32_t out_dtype, hipStream_t stream);
+
 /* Bytes of workspace e4b_moe_forward needs for these sizes. */
 size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts, int64_t n1,
                                int64_t n2, int32_t epilogue, int32_t act_dtype);
@@ -131,6 +150,8 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
  * -> down (+bias, kept in fp32) -> combine (one rounding into out_dtype).
  * hidden [tokens, w1->k] in act_dtype; top_k_index [tokens, top_k] int64; top_k_weights
  * [tokens, top_k] in weight_dtype; out [tokens, w2->n] in out_dtype.
+ * Small batches (tokens <= 8, or flags == E4B_PATH_GEMV within the decode limits) take the
+ * two-launch decode path; larger ones route once and run the grouped GEMMs.
  * Replaces: engines/fast.py:100-160 fused_experts_forward (the bare-module forward that
  * enable_fast binds, fast.py:371-372), with no device->host synchronisation. */
 int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,

@@ -518,3 +518,42 @@ def test_gptoss_config_shapes(T):
                               ("gptoss", 1.702, 7.0), b1=mod.gate_up_bias.float().cpu().numpy(),
                               b2=mod.down_bias.float().cpu().numpy())
     _assert_fidelity(got[rows], ref[rows], oracle, f"gptoss T={T}")
+
+
+@pytest.mark.parametrize("T", [2, 64])
+def test_decode_path_forced_up_to_its_row_limit(T):
+    """The two-launch decode path (routing recomputed in LDS, combine fused into down) at
+    tokens*k up to its 512-row limit, forced so it also covers batches the auto rule sends to MFMA."""
+    _announce(f"decode path forced T={T}")
+    E, H, I, k = 64, 2048, 1024, 8
+    mod = _cfg_module(E, H, I, seed=5000 + T, dq=False)
+    x, idx, w = _cfg_inputs(T, E, H, k, seed=5100 + T, renorm=False)
+    with torch.no_grad():
+        ref = mod(x, idx, w)
+        e4b.enable_fast(mod)
+        F.set_kernel_path("gemv")
+        got = mod(x, idx, w)
+        F.set_kernel_path("mfma")
+        got_mfma = mod(x, idx, w)
+    rows = list(range(min(T, 6)))
+    _assert_fidelity(got[rows], ref[rows], _oracle_rows(mod, x, idx, w, rows), f"decode forced T={T}")
+    fro, _, _ = moe.rel_errors(got.float().cpu().numpy(), got_mfma.float().cpu().numpy())
+    assert fro <= 1e-2
+
+
+def test_out_of_range_ids_contribute_nothing():
+    _announce("dropped ids")
+    mod, hs, top_i, top_w = _make(E=8, tokens=6, k=2, seed=11)
+    e4b.enable_fast(mod)
+    bad = top_i.clone()
+    bad[0, 1] = 99
+    bad[3, 0] = -1
+    with torch.no_grad():
+        got = mod(hs, bad, top_w)
+    w_keep = top_w.clone()
+    w_keep[0, 1] = 0
+    w_keep[3, 0] = 0
+    safe = bad.clamp(0, 7)
+    with torch.no_grad():
+        want = mod(hs, safe, w_keep)
+    assert _b_rel(got, want) < 1e-2

@@ -293,3 +293,58 @@ def test_combine_bit_exact(wdt, H):
     assert np.array_equal(_bits(out), acc.view(np.uint32))
     out16 = ops.combine(down.to(DEV), rb, w.to(DEV), T, k, torch.bfloat16)
     assert np.array_equal(_bits(out16), numerics.f32_to_bf16_bits(acc))
+
+
+# ------------------------------------------------------------------- decode halves
+
+
+def _stack(fmt, E, n, k, seed):
+    if fmt == "mxfp4":
+        g = torch.Generator().manual_seed(seed)
+        w = torch.randn(E, n, k, generator=g) * 0.05
+        b, s = Q.quantize_mxfp4(w)
+        return ops.mxfp4_qweight(b.reshape(E, -1).to(DEV), s.reshape(E, -1).to(DEV), n, k, num_experts=E)
+    qw, _, _ = _nf4_stack(E, n, k, seed=seed, dq=(fmt == "nf4_dq"))
+    return qw
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "nf4_dq", "mxfp4"])
+@pytest.mark.parametrize("T", [1, 5, 64])
+def test_decode_halves_match_oracle(fmt, T):
+    """e4b_decode_gate_up (routing in LDS + gate_up + epilogue, h in flat order) and
+    e4b_decode_down_combine (down + k-slot combine) against the fp64 oracle per flat row."""
+    _announce(f"decode halves fmt={fmt} T={T}")
+    E, H, I, top = 8, 768, 320, 2
+    w1 = _stack(fmt, E, 2 * I, H, seed=20)
+    w2 = _stack(fmt, E, H, I, seed=21)
+    epi, spec = N.EPI_SWIGLU, "swiglu"
+    if fmt == "mxfp4":
+        g = torch.Generator().manual_seed(22)
+        w1.bias = (torch.randn(E, 2 * I, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+        w2.bias = (torch.randn(E, H, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+        epi, spec = N.EPI_GPTOSS, ("gptoss", 1.702, 7.0)
+    W1, W2 = _dense_from_kernel(w1), _dense_from_kernel(w2)
+    rng = np.random.default_rng(23 + T)
+    idx = np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)
+    x = (torch.randn(T, H, generator=torch.Generator().manual_seed(24)) * 2).to(torch.bfloat16)
+    wts = torch.rand(T, top, generator=torch.Generator().manual_seed(25)).to(torch.bfloat16)
+    h = ops.decode_gate_up(x.to(DEV), torch.from_numpy(idx).to(DEV), w1, epi)
+    flat_e = idx.reshape(-1)
+    b1 = None if w1.bias is None else w1.bias.float().cpu().numpy().astype(np.float64)
+    proj = _gemm_oracle(x.float().numpy()[np.arange(T * top) // top], W1, flat_e, bias=b1)
+    want_h = numerics.round_bf16(moe._glu_exact(proj, spec, I).astype(np.float32))
+    fro, maxabs = _errs(h.float().cpu().numpy(), want_h)
+    assert fro <= 1e-2 and maxabs <= 2e-2, ("gate_up", fro, maxabs)
+    out = ops.decode_down_combine(h, torch.from_numpy(idx).to(DEV), wts.to(DEV), w2, torch.float32)
+    b2 = None if w2.bias is None else w2.bias.float().cpu().numpy().astype(np.float64)
+    dn = _gemm_oracle(h.float().cpu().numpy(), W2, flat_e, bias=b2)
+    want = (dn.reshape(T, top, H) * wts.float().numpy()[..., None]).sum(1)
+    fro2, maxabs2 = _errs(out.cpu().numpy(), want)
+    assert out.dtype == torch.float32 and fro2 <= 1e-4, ("down+combine", fro2, maxabs2)
+
+
+def test_decode_rejects_batches_beyond_its_limit():
+    qw, _, _ = _nf4_stack(4, 128, 128, seed=26)
+    idx = torch.zeros(600, 1, dtype=torch.int64, device=DEV)
+    with pytest.raises(N.NativeError, match="decode path"):
+        ops.decode_gate_up(torch.zeros(600, 128, dtype=torch.bfloat16, device=DEV), idx, qw, N.EPI_NONE)
