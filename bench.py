@@ -37,6 +37,15 @@ QWEN3 = dict(E=128, H=2048, I=768, k=8, renorm=True)
 GPTOSS = dict(E=32, H=2880, I=2880, k=4)
 
 
+# HBM bytes per launch of the dominant kernel, from the two counter runs summarised in
+# profiles/decode_up_kernel_olmoe_bs1.txt (FETCH_SIZE x 1.9998 and WRITE_SIZE x 1.0, the scales a
+# 256 MiB device copy gives in the same runs). Keyed by the kernel it was measured on, so a
+# changed kernel reports null until it is measured again.
+MEASURED_TRAFFIC = {
+    "decode_up_kernel<bf16, nf4, G=16, CPL=4>": 19_106_000,
+}
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -181,17 +190,44 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
     gu_b, _ = nf4_expert_bytes(cfg["H"], cfg["I"])
     bytes_per_launch = cfg["k"] * gu_b  # 8 distinct routed experts at bs=1
     achieved = bytes_per_launch / (per_launch_us * 1e-6) / 1e9
+    kernel = "decode_up_kernel<bf16, nf4, G=16, CPL=4>"
     return {
         "bound": "hbm",
-        "kernel": "decode_up_kernel<bf16, nf4, G=16, CPL=4> (routing + gate_up + SwiGLU, bs=1)",
+        "kernel": kernel + " (routing + gate_up + SwiGLU, bs=1)",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": None,
+        "traffic": MEASURED_TRAFFIC.get(kernel),
         "bytes_per_launch": bytes_per_launch,
         "avg_launch_us": round(per_launch_us, 3),
     }
+
+
+def pmc_pass(mods, cfg, seed0):
+    """One eager launch of the dominant kernel per layer (no graph, so a counter run sees each
+    dispatch), then one 256 MiB device-to-device copy: its FETCH_SIZE / WRITE_SIZE per dispatch
+    against the 268,435,456 bytes it must move give the counters' bytes-per-KiB scale."""
+    import torch
+
+    from experts4bit_qlora_amd import _native as N
+    from experts4bit_qlora_amd import fast as F
+    from experts4bit_qlora_amd import ops
+
+    inputs = [make_inputs(cfg, 1, seed0 + 10 * l) for l in range(len(mods))]
+    qws = [F._qweights(m)[0] for m in mods]
+    torch.cuda.synchronize()
+    for (x, idx, _), qw in zip(inputs, qws):
+        ops.decode_gate_up(x, idx, qw, N.EPI_SWIGLU)
+    torch.cuda.synchronize()
+    src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    gu_b, _ = nf4_expert_bytes(cfg["H"], cfg["I"])
+    print(json.dumps({"pmc_pass": {"kernel_bytes_per_launch": cfg["k"] * gu_b, "launches": len(mods),
+                                   "copy_bytes": src.numel()}}), flush=True)
 
 
 def prefill_bench(steps, warmup):
@@ -338,6 +374,9 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--extra", action="store_true", help="also run configs[2] and configs[4]")
     ap.add_argument("--kernel-only", action="store_true", help="only the dominant-kernel loop (for profiling)")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="for counter runs: the dominant kernel eagerly once per layer, then a 256 MiB "
+                         "device copy whose counter reading calibrates bytes per counted KiB")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -359,6 +398,10 @@ def main():
     for m in mods:
         assert e4b.enable_fast(m) == 1
     torch.cuda.synchronize()
+
+    if args.pmc_pass:
+        pmc_pass(mods, cfg, seed0=1000 + 100)
+        return
 
     log("dominant kernel roofline (gate_up GEMV, bs=1)")
     roof = dominant_kernel_roofline(mods, cfg, args.steps, args.warmup, seed0=1000 + 100)
