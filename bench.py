@@ -205,9 +205,10 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
 
 
 def pmc_pass(mods, cfg, seed0):
-    """One eager launch of the dominant kernel per layer (no graph, so a counter run sees each
-    dispatch), then one 256 MiB device-to-device copy: its FETCH_SIZE / WRITE_SIZE per dispatch
-    against the 268,435,456 bytes it must move give the counters' bytes-per-KiB scale."""
+    """One eager decode layer (gate_up kernel, then down + combine kernel) per layer at batch 1
+    (no graph, so a counter run sees each dispatch), then one 256 MiB device-to-device copy:
+    its FETCH_SIZE / WRITE_SIZE per dispatch against the 268,435,456 bytes it must move give
+    the counters' bytes-per-KiB scale."""
     import torch
 
     from experts4bit_qlora_amd import _native as N
@@ -215,10 +216,11 @@ def pmc_pass(mods, cfg, seed0):
     from experts4bit_qlora_amd import ops
 
     inputs = [make_inputs(cfg, 1, seed0 + 10 * l) for l in range(len(mods))]
-    qws = [F._qweights(m)[0] for m in mods]
     torch.cuda.synchronize()
-    for (x, idx, _), qw in zip(inputs, qws):
-        ops.decode_gate_up(x, idx, qw, N.EPI_SWIGLU)
+    for (x, idx, w), m in zip(inputs, mods):
+        w1, w2 = F._qweights(m)
+        h = ops.decode_gate_up(x, idx, w1, N.EPI_SWIGLU)
+        ops.decode_down_combine(h, idx, w, w2, x.dtype)
     torch.cuda.synchronize()
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)

@@ -1,8 +1,10 @@
 """In-tree build of ``libe4b_amd.so`` for gfx950 with ``hipcc`` (no cmake, no JIT cache).
 
 ``python -m experts4bit_qlora_amd._build`` (or ``__graft_entry__.build()``) compiles
-``csrc/e4b_amd.hip`` into ``experts4bit_qlora_amd/libe4b_amd.so``. The output is written to a
-temporary name and renamed, so a failed build never leaves a half-written library behind.
+``csrc/e4b_amd.hip`` (entry points and the routing / dequant / grouped-GEMM kernels) and
+``csrc/decode_inst.hip`` once per (activation dtype, weight format) pair, all in parallel, then
+links them into ``experts4bit_qlora_amd/libe4b_amd.so``. The output is written to a temporary
+name and renamed, so a failed build never leaves a half-written library behind.
 """
 from __future__ import annotations
 
@@ -10,9 +12,15 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-SRC = os.path.join(_HERE, "csrc", "e4b_amd.hip")
+CSRC = os.path.join(_HERE, "csrc")
+SRC = os.path.join(CSRC, "e4b_amd.hip")
+DECODE_SRC = os.path.join(CSRC, "decode_inst.hip")
+INCLUDE = os.path.join(os.path.dirname(_HERE), "include")
+# (E4B_INST_DT, E4B_INST_FMT): bf16/fp16 x NF4/NF4_DQ/MXFP4
+DECODE_PAIRS = [(dt, fmt) for dt in (0, 1) for fmt in (0, 1, 2)]
 OUT = os.path.join(_HERE, "libe4b_amd.so")
 ARCH = os.environ.get("E4B_OFFLOAD_ARCH", "gfx950")
 
@@ -21,7 +29,6 @@ FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # no silent a*b+c contraction: FMAs are written explicitly where they are wanted, and the
     # dequant / combine products must round exactly once
     "-ffp-contract=off",
@@ -37,16 +44,40 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def build(verbose: bool = False) -> str:
-    tmp = OUT + ".tmp"
-    cmd = [hipcc(), *FLAGS, "-o", tmp, SRC]
-    res = subprocess.run(cmd, capture_output=True, text=True)
+def _run_all(cmds):
+    procs = [(cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)) for cmd in cmds]
     noise = "is not a recognized feature for this target"
-    errs = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
-    if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{errs}")
-    if verbose and errs.strip():
-        print(errs, file=sys.stderr)
+    msgs, failed = [], []
+    for cmd, p in procs:
+        _, err = p.communicate()
+        err = "\n".join(l for l in err.splitlines() if noise not in l)
+        if p.returncode != 0:
+            failed.append(f"hipcc failed ({p.returncode}):\n{' '.join(cmd)}\n{err}")
+        elif err.strip():
+            msgs.append(err)
+    if failed:
+        raise RuntimeError("\n\n".join(failed))
+    return msgs
+
+
+def build(verbose: bool = False) -> str:
+    cc = hipcc()
+    inc = [f"-I{CSRC}", f"-I{INCLUDE}"]
+    with tempfile.TemporaryDirectory(prefix="e4b_build_") as tmpdir:
+        objs, cmds = [], []
+        obj = os.path.join(tmpdir, "e4b_amd.o")
+        cmds.append([cc, *FLAGS, *inc, "-c", "-o", obj, SRC])
+        objs.append(obj)
+        for dt, fmt in DECODE_PAIRS:
+            obj = os.path.join(tmpdir, f"decode_{dt}_{fmt}.o")
+            cmds.append([cc, *FLAGS, *inc, f"-DE4B_INST_DT={dt}", f"-DE4B_INST_FMT={fmt}", "-c", "-o", obj,
+                         DECODE_SRC])
+            objs.append(obj)
+        msgs = _run_all(cmds)
+        tmp = OUT + ".tmp"
+        msgs += _run_all([[cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]])
+    if verbose and msgs:
+        print("\n".join(msgs), file=sys.stderr)
     os.replace(tmp, OUT)
     return OUT
 

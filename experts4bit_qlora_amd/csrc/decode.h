@@ -1,33 +1,45 @@
-// Decode path (few tokens): the whole MoE layer in two launches, no routing round trip.
+// Decode path (tokens * top_k <= 64): the whole MoE layer in two launches, no routing round trip.
 //
-//   decode_up_kernel    routing of this block's expert in LDS, then gate_up GEMV with the
-//                       fused epilogue; writes h[flat, :] (flat = token * k + slot).
-//   decode_down_kernel  full routing in LDS, down GEMV over every routed row for a block of
-//                       output columns, then the deterministic k-slot combine of those
-//                       columns in slot order -- the combine never leaves the block.
+//   decode_up_kernel    block (column tile, a): gate_up GEMV of the a-th routed expert (ascending
+//                       id) for a tile of output columns, fused epilogue, writes h[flat, :]
+//                       (flat = token * k + slot).
+//   decode_down_kernel  block = kDownCols output columns: the down GEMV of every routed row for
+//                       those columns, then the deterministic k-slot combine of the columns in
+//                       slot order -- the combine never leaves the block. A G-lane group takes
+//                       one routed expert at a time (a "job") for all the block's columns, so a
+//                       routed row's activation chunk is loaded once per job.
 //
-// Both recompute the (tiny) routing from top_k_index instead of reading a route kernel's
-// output, so a layer costs two dependent global round trips per kernel: the ids, then the
-// weights and activations.
+// Critical path of either kernel: one global round trip for the ids (issued together with the
+// code table), a wave-local routing step, then every weight / scale / activation load of the
+// block is issued -- interleaved by chunk, so the dot products can start on the first chunk
+// while later ones are in flight -- before the LDS decode table is built, so building the
+// table overlaps the weight round trip. One __syncthreads separates the table build from its
+// use. Each wave computes the routing itself (one id per lane, a per-wave LDS bitmap of routed
+// experts, one LDS atomic per lane for the row masks), so no block barrier waits on it.
 //
 // Weight decode. A 64 KB LDS table holds, for every byte value b, the two codes the byte
 // encodes as activation-dtype pairs -- hi = dt(code) and lo = dt(code - hi) -- so hi + lo
 // carries the fp32 code to ~16 significant bits; the table is replicated 32 times and a lane
-// reads copy (lane % 32), so 32 lanes touch 64 distinct banks. A byte's table address is one
-// v_perm_b32 (byte -> bits 8..15, lane copy -> bits 3..7), and each element pair costs one
-// ds_read_b64 plus two v_dot2 (hi, lo) against the packed activation pair, which is used as
-// loaded (no conversion). The block scale multiplies the fp32 chunk sum once per 32 values.
+// reads copy (lane % 32), so the lanes of a wave spread over the banks. A byte's table address
+// is one v_perm_b32 (byte -> bits 8..15, lane copy -> bits 3..7), and each element pair costs
+// one ds_read_b64 plus two v_dot2 (hi, lo) against the packed activation pair as loaded. The
+// block scale multiplies the fp32 sum once per 32 values.
+//
+// Chunk c (16 packed bytes = 32 values) of a row goes to lane gl = c % G of the row's group,
+// as its (c / G)-th chunk. When the row's chunk count is not a multiple of G the spare slots
+// load chunk 0 and their products are dropped by a select, so no load is behind a branch.
 #pragma once
 
 #include "common.h"
 #include "dequant.h"
-#include "gemv.h"
 
 namespace e4b {
 
 constexpr int kDecThreads = 256;
-constexpr int kDecMaxRows = 512;     // tokens * top_k handled by the decode path
+constexpr int kDecWaves = kDecThreads / kWave;
+constexpr int kDecMaxRows = kWave;   // tokens * top_k: one routed row per lane
 constexpr int kDecMaxExperts = 256;
+constexpr int kDecExpWords = kDecMaxExperts / 64;
 constexpr int kLutCopies = 32;
 constexpr int kDownCols = 4;         // output columns per decode_down block
 
@@ -58,59 +70,118 @@ struct DecodeArgs {
   int64_t n_out;
 };
 
-// LDS pair table: entry (byte, copy) at byte offset byte * 256 + copy * 8. The 16 codes are
-// staged in LDS first, so building the 64 KB table costs one global round trip, not one per
-// entry.
+// Per-wave routing state in LDS: the bitmap of routed experts, their ascending list and, for
+// each listed expert, the mask of flat rows routed to it.
+struct WaveRoute {
+  unsigned long long bm[kDecExpWords];
+  int act[kDecMaxRows];
+  unsigned long long rows[kDecMaxRows];
+};
+
+// The id of flat row `lane` (-1: beyond M or outside [0, E)).
+E4B_DEV int load_row_id(const DecodeArgs& p, int M) {
+  const int lane = threadIdx.x & (kWave - 1);
+  if (lane >= M) return -1;
+  const int64_t v = p.topk[lane];
+  return (v >= 0 && v < p.E) ? static_cast<int>(v) : -1;
+}
+
+// Wave-local routing: fills r (this wave's copy) and returns the number of routed experts.
+// Lane f holds flat row f's expert id; its position in the ascending list is the number of
+// routed experts below it, and it ORs its own bit into that expert's row mask.
+E4B_DEV int wave_route(int id, WaveRoute& r) {
+  const int lane = threadIdx.x & (kWave - 1);
+  if (lane < kDecExpWords) r.bm[lane] = 0ull;
+  r.rows[lane] = 0ull;
+  __builtin_amdgcn_wave_barrier();
+  if (id >= 0) atomicOr(&r.bm[id >> 6], 1ull << (id & 63));
+  __builtin_amdgcn_wave_barrier();
+  const unsigned long long below = (lane == 0) ? 0ull : ((~0ull) >> (kWave - lane));
+  const int idw = id >> 6;
+  const unsigned long long id_below = (1ull << (id & 63)) - 1ull;
+  int n = 0, pos = 0;
+#pragma unroll
+  for (int w = 0; w < kDecExpWords; ++w) {
+    const unsigned long long m = r.bm[w];
+    if ((m >> lane) & 1ull) r.act[n + __popcll(m & below)] = w * 64 + lane;
+    if (idw == w) pos = n + __popcll(m & id_below);
+    n += __popcll(m);
+  }
+  if (id >= 0) atomicOr(&r.rows[pos], 1ull << lane);
+  __builtin_amdgcn_wave_barrier();
+  return n;
+}
+
+// Table entry for byte b: the pair (first, second) element codes, hi and lo parts.
 template <int DT, int FMT>
-E4B_DEV void build_pair_table(uint2* lut, const float* codes_s) {
-  for (int i = threadIdx.x; i < 256 * kLutCopies; i += blockDim.x) {
-    const uint32_t b = static_cast<uint32_t>(i) / kLutCopies;
-    const uint32_t first = (FMT == E4B_FMT_MXFP4) ? (b & 0xfu) : (b >> 4);
-    const uint32_t second = (FMT == E4B_FMT_MXFP4) ? (b >> 4) : (b & 0xfu);
-    const float v1 = codes_s[first];
-    const float v2 = codes_s[second];
-    const uint16_t h1 = from_f<DT>(v1), h2 = from_f<DT>(v2);
-    const uint16_t l1 = from_f<DT>(v1 - to_f<DT>(h1)), l2 = from_f<DT>(v2 - to_f<DT>(h2));
-    lut[i] = make_uint2(pack2(h1, h2), pack2(l1, l2));
-  }
+E4B_DEV uint2 pair_entry(float first, float second) {
+  const uint16_t h1 = from_f<DT>(first), h2 = from_f<DT>(second);
+  const uint16_t l1 = from_f<DT>(first - to_f<DT>(h1)), l2 = from_f<DT>(second - to_f<DT>(h2));
+  return make_uint2(pack2(h1, h2), pack2(l1, l2));
 }
 
-// Codes (and, for double-quant, the 256-entry second-level code) into LDS.
+// The two codes byte threadIdx.x encodes, read straight from the code table (first element:
+// high nibble for NF4, low nibble for e2m1).
 template <int FMT>
-E4B_DEV void stage_codes(const e4b_qweight& w, float* codes_s, float* code2_s) {
-  if (threadIdx.x < 16) codes_s[threadIdx.x] = (FMT == E4B_FMT_MXFP4) ? kFp4E2M1[threadIdx.x] : w.code[threadIdx.x];
-  if constexpr (FMT == E4B_FMT_NF4_DQ) {
-    for (int i = threadIdx.x; i < 256; i += blockDim.x) code2_s[i] = w.code2[i];
-  }
-}
-
-// Scale of the chunk c (32 values) of weight row `row` of expert e; double-quant codes come
-// from the LDS copy of code2.
-template <int FMT>
-E4B_DEV float dec_scale(const e4b_qweight& w, int e, int64_t row, int c, const float* code2_s) {
+E4B_DEV void load_pair_codes(const e4b_qweight& w, float& first, float& second) {
+  const uint32_t b = threadIdx.x & 0xffu;
   if constexpr (FMT == E4B_FMT_MXFP4) {
-    const uint8_t* sc = static_cast<const uint8_t*>(w.absmax);
-    return e8m0_to_f32(sc[(int64_t(e) * w.n + row) * (w.k / 32) + c]);
+    first = kFp4E2M1[b & 0xfu];
+    second = kFp4E2M1[b >> 4];
+  } else {
+    first = w.code[b >> 4];
+    second = w.code[b & 0xfu];
+  }
+}
+
+// Thread t writes byte t's entry into all 32 copies, two copies per 16-byte store, rotating the
+// copies with t so the lanes of a wave spread their stores over the banks. Needs 256 threads.
+E4B_DEV void store_pair_entry(uint2* lut, uint2 e) {
+  const uint32_t b = threadIdx.x;
+  const uint4 v = make_uint4(e.x, e.y, e.x, e.y);
+  uint4* row = reinterpret_cast<uint4*>(lut + b * kLutCopies);
+#pragma unroll
+  for (uint32_t c = 0; c < kLutCopies / 2; ++c) row[(c + b) & (kLutCopies / 2 - 1)] = v;
+}
+
+// Raw per-chunk scale data (loaded before the table is built), resolved after the barrier.
+struct RawScale {
+  float a;      // NF4: absmax; NF4_DQ: absmax2; MXFP4: unused
+  uint32_t q;   // NF4_DQ: u8 code; MXFP4: e8m0
+};
+
+// Scale of chunk c of weight row `row` of expert e.
+template <int FMT>
+E4B_DEV RawScale load_scale(const e4b_qweight& w, int e, int64_t row, int c) {
+  RawScale s{0.0f, 0u};
+  if constexpr (FMT == E4B_FMT_MXFP4) {
+    s.q = static_cast<const uint8_t*>(w.absmax)[(int64_t(e) * w.n + row) * (w.k / 32) + c];
   } else if constexpr (FMT == E4B_FMT_NF4) {
-    return static_cast<const float*>(w.absmax)[(int64_t(e) * w.n + row) * (w.k / 64) + c / 2];
+    s.a = static_cast<const float*>(w.absmax)[(int64_t(e) * w.n + row) * (w.k / 64) + c / 2];
   } else {
     const int64_t nb = w.n * (w.k / 64);
     const int64_t blk = row * (w.k / 64) + c / 2;
-    const uint8_t q = static_cast<const uint8_t*>(w.absmax)[e * nb + blk];
-    const int64_t nb2 = (nb + 255) / 256;
-    return __fadd_rn(mul_f32(code2_s[q], w.absmax2[e * nb2 + blk / 256]), w.offset[e]);
+    s.q = static_cast<const uint8_t*>(w.absmax)[e * nb + blk];
+    s.a = w.absmax2[e * ((nb + 255) / 256) + blk / 256];
   }
+  return s;
+}
+
+template <int FMT>
+E4B_DEV float resolve_scale(const RawScale& s, const float* code2_s, float offset) {
+  if constexpr (FMT == E4B_FMT_MXFP4) return e8m0_to_f32(s.q);
+  else if constexpr (FMT == E4B_FMT_NF4) return s.a;
+  else return __fadd_rn(mul_f32(code2_s[s.q], s.a), offset);
 }
 
 // sum over one 16-byte chunk (32 values) of code * x, unscaled, fp32.
 template <int DT, int FMT>
-E4B_DEV float chunk_dot(const uint4& q, const uint4* xq, const char* lut_bytes, uint32_t lane_off) {
+E4B_DEV float chunk_dot(const uint4& q, const uint4 (&xq)[4], const char* lut_bytes, uint32_t lane_off) {
   const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
   float acc = 0.0f;
 #pragma unroll
   for (int wi = 0; wi < 4; ++wi) {
-    const uint4 xv = xq[wi];
-    const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+    const uint32_t xs[4] = {xq[wi].x, xq[wi].y, xq[wi].z, xq[wi].w};
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       // address = (byte b of the word) << 8 | lane_off
@@ -130,263 +201,257 @@ E4B_DEV float group_reduce(float v) {
   return v;
 }
 
-// One lane's share (CPL chunks, stride G) of the dot products of one activation row with one
-// or two weight rows. Every global load of the share is issued before the first use.
-template <int DT, int FMT, int G, int CPL, bool PAIR>
-E4B_DEV void row_dots(const e4b_qweight& w, int e, int64_t row_a, int64_t row_b, const uint16_t* xr, int gl,
-                      const char* lut_bytes, uint32_t lane_off, const float* code2_s, float& acc_a, float& acc_b) {
+// The i-th chunk slot of lane gl: its chunk index, and whether it is a real chunk.
+template <int G, bool FULL>
+E4B_DEV int slot_chunk(int gl, int i, int nchunk, bool& valid) {
+  const int c = gl + i * G;
+  valid = FULL || c < nchunk;
+  return valid ? c : 0;
+}
+
+E4B_DEV void load_chunk_x(const uint16_t* xr, int c, uint4 (&xv)[4]) {
+  const uint4* xp = reinterpret_cast<const uint4*>(xr + 32 * c);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) xv[q] = xp[q];
+}
+
+E4B_DEV uint4 load_chunk_w(const e4b_qweight& w, int e, int64_t row, int c) {
+  return *reinterpret_cast<const uint4*>(w.packed + (int64_t(e) * w.n + row) * (w.k / 2) + 16 * c);
+}
+
+// gate_up GEMV + fused epilogue for the a-th routed expert (blockIdx.y), G lanes per column.
+template <int DT, int FMT, int G, int CPL, bool FULL>
+__global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
+  __shared__ __align__(16) uint2 lut[256 * kLutCopies];
+  __shared__ WaveRoute route[kDecWaves];
+  __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int M = p.tokens * p.k;
+  const e4b_qweight& w = p.w;
+
+  // round trip 1: ids, the code pair of this thread's table entry, code2
+  const int id = load_row_id(p, M);
+  float cf, cs;
+  load_pair_codes<FMT>(w, cf, cs);
+  if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = w.code2[threadIdx.x];
+
+  WaveRoute& r = route[wid];
+  const int nact = wave_route(id, r);
+  const int a = blockIdx.y;
+  if (a >= nact) return;  // uniform over the block: every wave computed the same routing
+  const int e = r.act[a];
+  unsigned long long rows = r.rows[a];
+
+  const int gl = lane % G;
   const int nchunk = static_cast<int>(w.k / 32);
-  const uint8_t* wa = w.packed + (int64_t(e) * w.n + row_a) * (w.k / 2);
-  const uint8_t* wb = w.packed + (int64_t(e) * w.n + row_b) * (w.k / 2);
+  const bool pair = is_gated(p.epi);
+  const int64_t n = w.n, k = w.k;
+  const int64_t j = (int64_t(blockIdx.x) * kDecWaves + wid) * (kWave / G) + lane / G;
+  const bool live = j < p.n_out;  // whole G-lane groups share it
+  const int64_t row_a = live ? j : 0, row_b = pair ? row_a + n / 2 : row_a;
+  int f = __ffsll(static_cast<long long>(rows)) - 1;
+  const uint16_t* xr = p.x + int64_t(f / p.k) * k;
+
+  // round trip 2: activations, weights and scales, chunk by chunk
   uint4 qa[CPL], qb[CPL], xv[CPL][4];
+  RawScale ra[CPL], rb[CPL];
+  bool valid[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int c = slot_chunk<G, FULL>(gl, i, nchunk, valid[i]);
+    load_chunk_x(xr, c, xv[i]);
+    qa[i] = load_chunk_w(w, e, row_a, c);
+    if (pair) qb[i] = load_chunk_w(w, e, row_b, c);
+    ra[i] = load_scale<FMT>(w, e, row_a, c);
+    if (pair) rb[i] = load_scale<FMT>(w, e, row_b, c);
+  }
+  const bool has_bias = w.bias != nullptr;
+  const uint16_t* bias = static_cast<const uint16_t*>(w.bias);
+  const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + row_a]) : 0.0f;
+  const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + row_b]) : 0.0f;
+  const float off = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
+
+  // the decode table, while the weights are in flight
+  store_pair_entry(lut, pair_entry<DT, FMT>(cf, cs));
+  __syncthreads();
+
+  uint32_t lane_off = static_cast<uint32_t>(lane % kLutCopies) * 8u;
+  const char* lut_bytes = reinterpret_cast<const char*>(lut);
   float sa[CPL], sb[CPL];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
-    const int c = gl + i * G;
-    if (c < nchunk) {
-      qa[i] = *reinterpret_cast<const uint4*>(wa + 16 * c);
-      if (PAIR) qb[i] = *reinterpret_cast<const uint4*>(wb + 16 * c);
-      const uint4* xp = reinterpret_cast<const uint4*>(xr + 32 * c);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) xv[i][q] = xp[q];
-    }
+    sa[i] = valid[i] ? resolve_scale<FMT>(ra[i], code2_s, off) : 0.0f;
+    sb[i] = (pair && valid[i]) ? resolve_scale<FMT>(rb[i], code2_s, off) : 0.0f;
   }
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    const int c = gl + i * G;
-    if (c < nchunk) {
-      sa[i] = dec_scale<FMT>(w, e, row_a, c, code2_s);
-      if (PAIR) sb[i] = dec_scale<FMT>(w, e, row_b, c, code2_s);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    const int c = gl + i * G;
-    if (c < nchunk) {
-      acc_a = fmaf(chunk_dot<DT, FMT>(qa[i], xv[i], lut_bytes, lane_off), sa[i], acc_a);
-      if (PAIR) acc_b = fmaf(chunk_dot<DT, FMT>(qb[i], xv[i], lut_bytes, lane_off), sb[i], acc_b);
-    }
-  }
-}
-
-// Routing ids of this launch into LDS: ids[i] = expert of flat row i, or -1 when out of range.
-E4B_DEV void load_ids(const DecodeArgs& p, int* ids) {
-  const int M = p.tokens * p.k;
-  for (int i = threadIdx.x; i < M; i += blockDim.x) {
-    const int64_t v = p.topk[i];
-    ids[i] = (v >= 0 && v < p.E) ? static_cast<int>(v) : -1;
-  }
-}
-
-// Wave 0: the a-th active expert (ascending) and its rows in flat order. Returns via LDS.
-E4B_DEV void find_expert_rows(const int* ids, int M, int E, int a, int* present, int* sel, int* rows) {
-  const int lane = threadIdx.x & (kWave - 1);
-  if (threadIdx.x >= kWave) return;
-  for (int e = lane; e < E; e += kWave) present[e] = 0;
-  __builtin_amdgcn_wave_barrier();
-  for (int i = lane; i < M; i += kWave) {
-    const int e = ids[i];
-    if (e >= 0) present[e] = 1;
-  }
-  __builtin_amdgcn_wave_barrier();
-  int expert = -1, seen = 0;
-  for (int base = 0; base < E && expert < 0; base += kWave) {
-    const int e = base + lane;
-    const unsigned long long m = __ballot(e < E && present[e] != 0);
-    const int c = __popcll(m);
-    if (a < seen + c) {
-      unsigned long long mm = m;  // drop the lowest (a - seen) set bits
-      for (int s = 0; s < a - seen; ++s) mm &= mm - 1;
-      expert = base + __ffsll(static_cast<long long>(mm)) - 1;
-    }
-    seen += c;
-  }
-  int n = 0;
-  if (expert >= 0) {
-    const unsigned long long below = (lane == 0) ? 0ull : ((~0ull) >> (kWave - lane));
-    for (int base = 0; base < M; base += kWave) {
-      const int i = base + lane;
-      const bool hit = i < M && ids[i] == expert;
-      const unsigned long long m = __ballot(hit);
-      if (hit) rows[n + __popcll(m & below)] = i;
-      n += __popcll(m);
-    }
-  }
-  if (lane == 0) {
-    sel[0] = expert;
-    sel[1] = n;
-  }
-}
-
-// gate_up GEMV + fused epilogue for the a-th active expert (blockIdx.y), G lanes per column.
-template <int DT, int FMT, int G, int CPL>
-__global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
-  __shared__ uint2 lut[256 * kLutCopies];
-  __shared__ int ids[kDecMaxRows];
-  __shared__ int present[kDecMaxExperts];
-  __shared__ int rows[kDecMaxRows];
-  __shared__ float codes_s[16];
-  __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
-  __shared__ int sel[2];
-  const int M = p.tokens * p.k;
-  load_ids(p, ids);
-  stage_codes<FMT>(p.w, codes_s, code2_s);
-  __syncthreads();
-  build_pair_table<DT, FMT>(lut, codes_s);
-  find_expert_rows(ids, M, p.E, blockIdx.y, present, sel, rows);
-  __syncthreads();
-  const int e = sel[0];
-  const int nrows = sel[1];
-  if (e < 0) return;
-
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wid = threadIdx.x / kWave;
-  const int gl = lane % G;
-  const uint32_t lane_off = static_cast<uint32_t>(lane % kLutCopies) * 8u;
-  const char* lut_bytes = reinterpret_cast<const char*>(lut);
-  const bool pair = is_gated(p.epi);
-  const int64_t n = p.w.n, k = p.w.k;
-  const int64_t j = (int64_t(blockIdx.x) * (kDecThreads / kWave) + wid) * (kWave / G) + lane / G;
-  if (j >= p.n_out) return;  // whole G-lane groups exit together
-  const int64_t row_a = j, row_b = pair ? j + n / 2 : j;
-  const bool has_bias = p.w.bias != nullptr;
-  const uint16_t* bias = static_cast<const uint16_t*>(p.w.bias);
-  const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + row_a]) : 0.0f;
-  const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + row_b]) : 0.0f;
-
-  for (int ri = 0; ri < nrows; ++ri) {
-    const int f = rows[ri];
-    const uint16_t* xr = p.x + int64_t(f / p.k) * k;
+  for (;;) {
+    // the table addresses depend only on the weights, which do not change from row to row;
+    // recomputing them per row keeps 128 addresses from being hoisted and held in registers
+    asm volatile("" : "+v"(lane_off));
     float acc_a = 0.0f, acc_b = 0.0f;
-    if (pair) {
-      row_dots<DT, FMT, G, CPL, true>(p.w, e, row_a, row_b, xr, gl, lut_bytes, lane_off, code2_s, acc_a, acc_b);
-    } else {
-      row_dots<DT, FMT, G, CPL, false>(p.w, e, row_a, row_b, xr, gl, lut_bytes, lane_off, code2_s, acc_a, acc_b);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const float da = chunk_dot<DT, FMT>(qa[i], xv[i], lut_bytes, lane_off) * sa[i];
+      acc_a += valid[i] ? da : 0.0f;
+      __builtin_amdgcn_sched_barrier(0);  // keep each chunk's 16 table reads together
+      if (pair) {
+        const float db = chunk_dot<DT, FMT>(qb[i], xv[i], lut_bytes, lane_off) * sb[i];
+        acc_b += valid[i] ? db : 0.0f;
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     acc_a = group_reduce<G>(acc_a);
     if (pair) acc_b = group_reduce<G>(acc_b);
-    if (gl == 0) {
+    if (live && gl == 0) {
       const float v = pair ? gated(p.epi, acc_a, acc_b, p.alpha, p.limit, bg, bu) : single(p.epi, acc_a, bg);
       static_cast<uint16_t*>(p.out)[int64_t(f) * p.n_out + j] = from_f<DT>(v);
+    }
+    rows &= rows - 1;
+    if (!rows) break;
+    f = __ffsll(static_cast<long long>(rows)) - 1;
+    const uint16_t* xn = p.x + int64_t(f / p.k) * k;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      bool v;
+      load_chunk_x(xn, slot_chunk<G, FULL>(gl, i, nchunk, v), xv[i]);
     }
   }
 }
 
 // down GEMV over every routed row for kDownCols output columns, then the k-slot combine.
-template <int DT, int FMT, int G, int CPL>
+// Jobs (one routed expert, all kDownCols columns) go to G-lane groups, JOBS per group in flight.
+template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL>
 __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) {
-  __shared__ uint2 lut[256 * kLutCopies];
-  __shared__ int ids[kDecMaxRows];
-  __shared__ int cnt[kDecMaxExperts];
-  __shared__ int order[kDecMaxRows];   // flat rows grouped by expert, flat order within
-  __shared__ int active[kDecMaxExperts];
-  __shared__ int ebeg[kDecMaxExperts + 1];
+  __shared__ __align__(16) uint2 lut[256 * kLutCopies];
+  __shared__ WaveRoute route[kDecWaves];
   __shared__ float res[kDecMaxRows * kDownCols];
-  __shared__ float codes_s[16];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
-  __shared__ int nact;
-  const int M = p.tokens * p.k;
+  constexpr int C = kDownCols;
+  constexpr int kGroups = kDecThreads / G;
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
-  load_ids(p, ids);
-  stage_codes<FMT>(p.w, codes_s, code2_s);
-  for (int e = threadIdx.x; e < p.E; e += blockDim.x) cnt[e] = 0;
-  __syncthreads();
-  build_pair_table<DT, FMT>(lut, codes_s);
-  for (int i = threadIdx.x; i < M; i += blockDim.x) {
-    if (ids[i] >= 0) atomicAdd(&cnt[ids[i]], 1);
-  }
-  __syncthreads();
-  if (wid == 0) {
-    // active experts ascending + row offsets, then a stable placement of the rows
-    int run = 0, na = 0;
-    for (int base = 0; base < p.E; base += kWave) {
-      const int e = base + lane;
-      const int c = e < p.E ? cnt[e] : 0;
-      int x = c;  // inclusive scans (row counts, active flags) within the wave
-      int act = c > 0;
-#pragma unroll
-      for (int o = 1; o < kWave; o <<= 1) {
-        const int y = __shfl_up(x, o);
-        const int z = __shfl_up(act, o);
-        if (lane >= o) {
-          x += y;
-          act += z;
-        }
-      }
-      if (e < p.E) ebeg[e] = run + x - c;
-      if (c > 0) active[na + act - 1] = e;
-      run += __shfl(x, kWave - 1);
-      na += __shfl(act, kWave - 1);
-    }
-    if (lane == 0) {
-      ebeg[p.E] = run;
-      nact = na;
-    }
-    __builtin_amdgcn_wave_barrier();
-    for (int e = lane; e < p.E; e += kWave) cnt[e] = ebeg[e];  // cursors
-    __builtin_amdgcn_wave_barrier();
-    const unsigned long long below = (lane == 0) ? 0ull : ((~0ull) >> (kWave - lane));
-    for (int base = 0; base < M; base += kWave) {
-      const int i = base + lane;
-      const int e = i < M ? ids[i] : -1;
-      unsigned long long pending = __ballot(e >= 0);
-      while (pending) {
-        const int leader = __ffsll(static_cast<long long>(pending)) - 1;
-        const int e0 = __shfl(e, leader);
-        const unsigned long long m = __ballot(e == e0);
-        const int c0 = cnt[e0];
-        if (e == e0) order[c0 + __popcll(m & below)] = i;
-        if (lane == leader) cnt[e0] = c0 + __popcll(m);
-        pending &= ~m;
-      }
-    }
-  }
-  __syncthreads();
+  const int M = p.tokens * p.k;
+  const e4b_qweight& w = p.w;
+
+  const int id = load_row_id(p, M);
+  float cf, cs;
+  load_pair_codes<FMT>(w, cf, cs);
+  if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = w.code2[threadIdx.x];
+
+  WaveRoute& r = route[wid];
+  const int nact = wave_route(id, r);
 
   const int gl = lane % G;
-  const uint32_t lane_off = static_cast<uint32_t>(lane % kLutCopies) * 8u;
-  const char* lut_bytes = reinterpret_cast<const char*>(lut);
-  const int64_t n = p.w.n, k = p.w.k;
-  const int64_t col0 = int64_t(blockIdx.x) * kDownCols;
-  const bool has_bias = p.w.bias != nullptr;
-  const uint16_t* bias = static_cast<const uint16_t*>(p.w.bias);
-  const int groups = kDecThreads / G;
   const int group = threadIdx.x / G;
-  const int jobs = nact * kDownCols;
-  for (int job = group; job < jobs; job += groups) {
-    const int ai = job / kDownCols;
-    const int cl = job % kDownCols;
-    const int64_t col = col0 + cl;
-    if (col >= n) continue;  // whole group skips together
-    const int e = active[ai];
-    const float b = has_bias ? to_f<DT>(bias[int64_t(e) * n + col]) : 0.0f;
-    for (int ri = ebeg[e]; ri < ebeg[e + 1]; ++ri) {
-      const int f = order[ri];
-      float acc = 0.0f, unused = 0.0f;
-      row_dots<DT, FMT, G, CPL, false>(p.w, e, col, col, p.x + int64_t(f) * k, gl, lut_bytes, lane_off, code2_s,
-                                       acc, unused);
-      acc = group_reduce<G>(acc);
-      if (gl == 0) res[f * kDownCols + cl] = acc + b;
+  const int nchunk = static_cast<int>(w.k / 32);
+  const int64_t n = w.n, k = w.k;
+  const int64_t col0 = int64_t(blockIdx.x) * C;
+  const bool has_bias = w.bias != nullptr;
+  const uint16_t* bias = static_cast<const uint16_t*>(w.bias);
+  uint32_t lane_off = static_cast<uint32_t>(lane % kLutCopies) * 8u;
+  const char* lut_bytes = reinterpret_cast<const char*>(lut);
+  int64_t cols[C];
+#pragma unroll
+  for (int cl = 0; cl < C; ++cl) cols[cl] = (col0 + cl < n) ? col0 + cl : col0;  // spare columns repeat col0
+
+  bool table_ready = false;
+  for (int base = group * JOBS; base < nact || !table_ready; base += kGroups * JOBS) {
+    // issue every load of this pass: the first routed row's activation chunks, then each
+    // column's weight chunk and scale, chunk by chunk
+    uint4 q[JOBS][CPL][C], xv[JOBS][CPL][4];
+    RawScale rs[JOBS][CPL][C];
+    bool valid[CPL];
+    int je[JOBS], jf[JOBS];
+    unsigned long long jrows[JOBS];
+#pragma unroll
+    for (int t = 0; t < JOBS; ++t) {
+      const int job = base + t;
+      const bool ok = job < nact;
+      je[t] = ok ? r.act[job] : -1;
+      jrows[t] = ok ? r.rows[job] : 0ull;
+      jf[t] = ok ? __ffsll(static_cast<long long>(jrows[t])) - 1 : 0;
+      const int e = ok ? je[t] : 0;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const int c = slot_chunk<G, FULL>(gl, i, nchunk, valid[i]);
+        if (ok) {
+          load_chunk_x(p.x + int64_t(jf[t]) * k, c, xv[t][i]);
+#pragma unroll
+          for (int cl = 0; cl < C; ++cl) {
+            q[t][i][cl] = load_chunk_w(w, e, cols[cl], c);
+            rs[t][i][cl] = load_scale<FMT>(w, e, cols[cl], c);
+          }
+        }
+      }
+    }
+    if (!table_ready) {
+      store_pair_entry(lut, pair_entry<DT, FMT>(cf, cs));
+      __syncthreads();
+      table_ready = true;
+    }
+#pragma unroll
+    for (int t = 0; t < JOBS; ++t) {
+      if (je[t] < 0) continue;  // whole group skips together
+      const int e = je[t];
+      const float off = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
+      float sc[CPL][C], b[C];
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+#pragma unroll
+        for (int cl = 0; cl < C; ++cl) sc[i][cl] = valid[i] ? resolve_scale<FMT>(rs[t][i][cl], code2_s, off) : 0.0f;
+      }
+#pragma unroll
+      for (int cl = 0; cl < C; ++cl) b[cl] = has_bias ? to_f<DT>(bias[int64_t(e) * n + cols[cl]]) : 0.0f;
+      unsigned long long rows = jrows[t];
+      int f = jf[t];
+      for (;;) {
+        asm volatile("" : "+v"(lane_off));  // no hoisting of the per-row table addresses
+        float acc[C];
+#pragma unroll
+        for (int cl = 0; cl < C; ++cl) acc[cl] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+#pragma unroll
+          for (int cl = 0; cl < C; ++cl) {
+            const float d = chunk_dot<DT, FMT>(q[t][i][cl], xv[t][i], lut_bytes, lane_off) * sc[i][cl];
+            acc[cl] += valid[i] ? d : 0.0f;
+            __builtin_amdgcn_sched_barrier(0);  // keep each chunk's 16 table reads together
+          }
+        }
+#pragma unroll
+        for (int cl = 0; cl < C; ++cl) {
+          const float v = group_reduce<G>(acc[cl]);
+          if (gl == 0) res[f * C + cl] = v + b[cl];
+        }
+        rows &= rows - 1;
+        if (!rows) break;
+        f = __ffsll(static_cast<long long>(rows)) - 1;
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+          bool v;
+          load_chunk_x(p.x + int64_t(f) * k, slot_chunk<G, FULL>(gl, i, nchunk, v), xv[t][i]);
+        }
+      }
     }
   }
   __syncthreads();
 
   // combine: out[t, col] = sum_s res[t*k+s][col] * w[t, s], slots in order, fp32
-  for (int i = threadIdx.x; i < p.tokens * kDownCols; i += blockDim.x) {
-    const int t = i / kDownCols;
-    const int cl = i % kDownCols;
+  for (int i = threadIdx.x; i < p.tokens * C; i += blockDim.x) {
+    const int t = i / C;
+    const int cl = i % C;
     const int64_t col = col0 + cl;
     if (col >= n) continue;
     float acc = 0.0f;
     for (int s = 0; s < p.k; ++s) {
       const int f = t * p.k + s;
-      if (ids[f] < 0) continue;
-      float w;
-      if (p.wdt == E4B_FP32) w = static_cast<const float*>(p.topk_w)[f];
-      else if (p.wdt == E4B_BF16) w = to_f<E4B_BF16>(static_cast<const uint16_t*>(p.topk_w)[f]);
-      else w = to_f<E4B_FP16>(static_cast<const uint16_t*>(p.topk_w)[f]);
-      acc = __fadd_rn(acc, mul_f32(res[f * kDownCols + cl], w));
+      const int64_t v = p.topk[f];
+      if (v < 0 || v >= p.E) continue;
+      float wt;
+      if (p.wdt == E4B_FP32) wt = static_cast<const float*>(p.topk_w)[f];
+      else if (p.wdt == E4B_BF16) wt = to_f<E4B_BF16>(static_cast<const uint16_t*>(p.topk_w)[f]);
+      else wt = to_f<E4B_FP16>(static_cast<const uint16_t*>(p.topk_w)[f]);
+      acc = __fadd_rn(acc, mul_f32(res[f * C + cl], wt));
     }
     const int64_t o = int64_t(t) * n + col;
     if (p.odt == E4B_FP32) static_cast<float*>(p.out)[o] = acc;

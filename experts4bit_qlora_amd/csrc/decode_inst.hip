@@ -1,0 +1,61 @@
+// Decode-kernel instantiations for one (activation dtype, weight format) pair, selected by
+// -DE4B_INST_DT=<e4b_dtype> -DE4B_INST_FMT=<e4b_format> (the build compiles this file once per
+// pair, in parallel).
+#include "decode.h"
+#include "decode_launch.h"
+
+#ifndef E4B_INST_DT
+#error "E4B_INST_DT must be defined"
+#endif
+#ifndef E4B_INST_FMT
+#error "E4B_INST_FMT must be defined"
+#endif
+
+namespace e4b {
+
+namespace {
+
+template <int DT, int FMT, int G, int CPL, bool FULL>
+void up_gc(const DecodeArgs& a, int64_t max_active, hipStream_t s) {
+  constexpr int cols_per_block = kDecWaves * (kWave / G);
+  dim3 grid(static_cast<unsigned>((a.n_out + cols_per_block - 1) / cols_per_block), static_cast<unsigned>(max_active));
+  hipLaunchKernelGGL((decode_up_kernel<DT, FMT, G, CPL, FULL>), grid, dim3(kDecThreads), 0, s, a);
+}
+
+template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL>
+void down_gc(const DecodeArgs& a, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>((a.w.n + kDownCols - 1) / kDownCols));
+  hipLaunchKernelGGL((decode_down_kernel<DT, FMT, G, CPL, JOBS, FULL>), grid, dim3(kDecThreads), 0, s, a);
+}
+
+}  // namespace
+
+template <int DT, int FMT>
+void launch_decode_up(const DecodeArgs& a, DecShape d, int64_t max_active, hipStream_t s) {
+#define E4B_UP(g, c)                                                    \
+  if (d.G == g && d.CPL == c) {                                         \
+    if (d.full) up_gc<DT, FMT, g, c, true>(a, max_active, s);           \
+    else up_gc<DT, FMT, g, c, false>(a, max_active, s);                 \
+    return;                                                             \
+  }
+  E4B_UP(4, 2) E4B_UP(4, 4) E4B_UP(8, 4) E4B_UP(16, 4) E4B_UP(16, 6) E4B_UP(32, 4)
+#undef E4B_UP
+}
+
+template <int DT, int FMT>
+void launch_decode_down(const DecodeArgs& a, DecShape d, hipStream_t s) {
+#define E4B_DOWN(g, c, j)                                               \
+  if (d.G == g && d.CPL == c && d.JOBS == j) {                          \
+    if (d.full) down_gc<DT, FMT, g, c, j, true>(a, s);                  \
+    else down_gc<DT, FMT, g, c, j, false>(a, s);                        \
+    return;                                                             \
+  }
+  E4B_DOWN(16, 1, 2) E4B_DOWN(16, 2, 1) E4B_DOWN(32, 1, 1) E4B_DOWN(32, 2, 1) E4B_DOWN(32, 3, 1)
+  E4B_DOWN(32, 4, 1)
+#undef E4B_DOWN
+}
+
+template void launch_decode_up<E4B_INST_DT, E4B_INST_FMT>(const DecodeArgs&, DecShape, int64_t, hipStream_t);
+template void launch_decode_down<E4B_INST_DT, E4B_INST_FMT>(const DecodeArgs&, DecShape, hipStream_t);
+
+}  // namespace e4b

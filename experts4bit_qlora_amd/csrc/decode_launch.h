@@ -1,0 +1,68 @@
+// Launch-side view of the decode kernels: shape selection (host) and the per-(dtype, format)
+// launchers. The launchers are instantiated in decode_inst.hip, compiled once per
+// (E4B_INST_DT, E4B_INST_FMT) pair so the decode instantiations build in parallel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "e4b_amd.h"
+
+namespace e4b {
+
+struct DecodeArgs;
+
+// G lanes per weight row, CPL 16-byte chunks per lane, JOBS routed experts per group in flight
+// (down kernel), and whether the row's chunk count is exactly G * CPL. G == 0: unsupported.
+struct DecShape {
+  int G, CPL, JOBS;
+  bool full;
+};
+
+inline DecShape dec_finish(int64_t chunks, int G, int CPL, int JOBS) {
+  return DecShape{G, CPL, JOBS, chunks == int64_t(G) * CPL};
+}
+
+// gate_up: about four chunks per lane (two weight rows per lane).
+inline DecShape decode_up_shape(int64_t k) {
+  const int64_t c = k / 32;
+  if (c <= 8) return dec_finish(c, 4, 2, 1);
+  if (c <= 16) return dec_finish(c, 4, 4, 1);
+  if (c <= 32) return dec_finish(c, 8, 4, 1);
+  if (c <= 64) return dec_finish(c, 16, 4, 1);
+  if (c <= 96) return dec_finish(c, 16, 6, 1);
+  if (c <= 128) return dec_finish(c, 32, 4, 1);
+  return DecShape{0, 0, 0, false};
+}
+
+// down: a group takes one routed expert for all of the block's columns. With at most 8 routed
+// rows (at most 8 experts) a block has 8 groups of 32 lanes; with more, 16-lane groups, so a
+// pass serves 16 experts (two per group in flight when a row is at most 16 chunks).
+inline DecShape decode_down_shape(int64_t k, int64_t M) {
+  const int64_t c = k / 32;
+  if (c > 128) return DecShape{0, 0, 0, false};
+  if (M > 8 && c <= 16) return dec_finish(c, 16, 1, 2);
+  if (M > 8 && c <= 32) return dec_finish(c, 16, 2, 1);
+  const int cpl = c <= 32 ? 1 : c <= 64 ? 2 : c <= 96 ? 3 : 4;
+  return dec_finish(c, 32, cpl, 1);
+}
+
+template <int DT, int FMT>
+void launch_decode_up(const DecodeArgs& a, DecShape d, int64_t max_active, hipStream_t s);
+
+template <int DT, int FMT>
+void launch_decode_down(const DecodeArgs& a, DecShape d, hipStream_t s);
+
+#define E4B_DECODE_EXTERN(DT, FMT)                                                                   \
+  extern template void launch_decode_up<DT, FMT>(const DecodeArgs&, DecShape, int64_t, hipStream_t); \
+  extern template void launch_decode_down<DT, FMT>(const DecodeArgs&, DecShape, hipStream_t);
+E4B_DECODE_EXTERN(E4B_BF16, E4B_FMT_NF4)
+E4B_DECODE_EXTERN(E4B_BF16, E4B_FMT_NF4_DQ)
+E4B_DECODE_EXTERN(E4B_BF16, E4B_FMT_MXFP4)
+E4B_DECODE_EXTERN(E4B_FP16, E4B_FMT_NF4)
+E4B_DECODE_EXTERN(E4B_FP16, E4B_FMT_NF4_DQ)
+E4B_DECODE_EXTERN(E4B_FP16, E4B_FMT_MXFP4)
+#undef E4B_DECODE_EXTERN
+
+}  // namespace e4b

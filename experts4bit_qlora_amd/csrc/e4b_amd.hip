@@ -12,6 +12,7 @@
 
 #include "common.h"
 #include "decode.h"
+#include "decode_launch.h"
 #include "dequant.h"
 #include "gemm.h"
 #include "gemv.h"
@@ -176,71 +177,24 @@ void launch_combine_dt(const void* down, const int32_t* inv, const void* w, int 
   }
 }
 
-// Decode path: G lanes per weight row (a power of two in [4, 32], about four 16-byte chunks
-// each) and CPL chunks per lane, rounded up to an instantiated count. 0 = not supported.
-void decode_shape(int64_t k, int* G, int* CPL) {
-  const int64_t chunks = k / 32;
-  int g = 4;
-  while (g < 32 && chunks / (2 * g) >= 4) g *= 2;
-  int64_t c = (chunks + g - 1) / g;
-  int cpl = c <= 2 ? 2 : c <= 4 ? 4 : c <= 6 ? 6 : c <= 8 ? 8 : 0;
-  if (g > 4 && cpl < 4) cpl = 4;
-  *G = g;
-  *CPL = cpl;
-}
-
-template <int DT, int FMT, int G, int CPL>
-void launch_up_gc(const e4b::DecodeArgs& a, int64_t max_active, hipStream_t s) {
-  constexpr int cols_per_block = (e4b::kDecThreads / e4b::kWave) * (e4b::kWave / G);
-  dim3 grid(static_cast<unsigned>(cdiv(a.n_out, cols_per_block)), static_cast<unsigned>(max_active));
-  hipLaunchKernelGGL((e4b::decode_up_kernel<DT, FMT, G, CPL>), grid, dim3(e4b::kDecThreads), 0, s, a);
-}
-
-template <int DT, int FMT, int G, int CPL>
-void launch_down_gc(const e4b::DecodeArgs& a, int64_t, hipStream_t s) {
-  dim3 grid(static_cast<unsigned>(cdiv(a.w.n, e4b::kDownCols)));
-  hipLaunchKernelGGL((e4b::decode_down_kernel<DT, FMT, G, CPL>), grid, dim3(e4b::kDecThreads), 0, s, a);
-}
-
-// Dispatch over (G, CPL) for one of the two decode kernels (UP = gate_up, else down).
-template <bool UP, int DT, int FMT>
-void launch_decode_shape(const e4b::DecodeArgs& a, int64_t max_active, hipStream_t s) {
-  int G, CPL;
-  decode_shape(a.w.k, &G, &CPL);
-#define E4B_DEC_CASE(g, c)                                                \
-  if (G == g && CPL == c) {                                               \
-    if (UP) launch_up_gc<DT, FMT, g, c>(a, max_active, s);                \
-    else launch_down_gc<DT, FMT, g, c>(a, max_active, s);                 \
-    return;                                                               \
-  }
-  E4B_DEC_CASE(4, 2) E4B_DEC_CASE(4, 4) E4B_DEC_CASE(4, 6) E4B_DEC_CASE(4, 8)
-  E4B_DEC_CASE(8, 4) E4B_DEC_CASE(8, 6) E4B_DEC_CASE(8, 8)
-  E4B_DEC_CASE(16, 4) E4B_DEC_CASE(16, 6) E4B_DEC_CASE(16, 8)
-  E4B_DEC_CASE(32, 4) E4B_DEC_CASE(32, 6) E4B_DEC_CASE(32, 8)
-#undef E4B_DEC_CASE
-}
-
+// Decode path: shapes come from decode_launch.h; the launchers live in decode_inst.hip.
 template <bool UP>
-void launch_decode(const e4b::DecodeArgs& a, int act_dtype, int64_t max_active, hipStream_t s) {
-  if (act_dtype == E4B_BF16) {
-    switch (a.w.format) {
-      case E4B_FMT_NF4: launch_decode_shape<UP, E4B_BF16, E4B_FMT_NF4>(a, max_active, s); break;
-      case E4B_FMT_NF4_DQ: launch_decode_shape<UP, E4B_BF16, E4B_FMT_NF4_DQ>(a, max_active, s); break;
-      default: launch_decode_shape<UP, E4B_BF16, E4B_FMT_MXFP4>(a, max_active, s); break;
-    }
-  } else {
-    switch (a.w.format) {
-      case E4B_FMT_NF4: launch_decode_shape<UP, E4B_FP16, E4B_FMT_NF4>(a, max_active, s); break;
-      case E4B_FMT_NF4_DQ: launch_decode_shape<UP, E4B_FP16, E4B_FMT_NF4_DQ>(a, max_active, s); break;
-      default: launch_decode_shape<UP, E4B_FP16, E4B_FMT_MXFP4>(a, max_active, s); break;
-    }
+void launch_decode(const e4b::DecodeArgs& a, int act_dtype, int64_t max_active, int64_t M, hipStream_t s) {
+  const e4b::DecShape d = UP ? e4b::decode_up_shape(a.w.k) : e4b::decode_down_shape(a.w.k, M);
+#define E4B_DEC(DT, FMT)                                         \
+  if (act_dtype == DT && a.w.format == FMT) {                    \
+    if (UP) e4b::launch_decode_up<DT, FMT>(a, d, max_active, s); \
+    else e4b::launch_decode_down<DT, FMT>(a, d, s);              \
+    return;                                                      \
   }
+  E4B_DEC(E4B_BF16, E4B_FMT_NF4) E4B_DEC(E4B_BF16, E4B_FMT_NF4_DQ) E4B_DEC(E4B_BF16, E4B_FMT_MXFP4)
+  E4B_DEC(E4B_FP16, E4B_FMT_NF4) E4B_DEC(E4B_FP16, E4B_FMT_NF4_DQ) E4B_DEC(E4B_FP16, E4B_FMT_MXFP4)
+#undef E4B_DEC
 }
 
-bool decode_supported(int64_t M, int E, const e4b_qweight* w) {
-  int G, CPL;
-  decode_shape(w->k, &G, &CPL);
-  return M <= e4b::kDecMaxRows && E <= e4b::kDecMaxExperts && CPL > 0;
+bool decode_supported(int64_t M, int E, const e4b_qweight* w, bool up) {
+  const e4b::DecShape d = up ? e4b::decode_up_shape(w->k) : e4b::decode_down_shape(w->k, M);
+  return M <= e4b::kDecMaxRows && E <= e4b::kDecMaxExperts && d.G > 0;
 }
 
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -378,8 +332,8 @@ int e4b_decode_gate_up(const void* hidden, int32_t act_dtype, int64_t tokens, co
   if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "bad tokens/top_k");
   if (tokens == 0) return E4B_OK;
   const int64_t M = tokens * top_k;
-  if (!decode_supported(M, w1->num_experts, w1))
-    return fail(E4B_EUNSUPPORTED, "decode path needs tokens*top_k <= %d, E <= %d and k <= 8192 (got M=%lld E=%d)",
+  if (!decode_supported(M, w1->num_experts, w1, true))
+    return fail(E4B_EUNSUPPORTED, "decode path needs tokens*top_k <= %d, E <= %d and k <= 4096 (got M=%lld E=%d)",
                 e4b::kDecMaxRows, e4b::kDecMaxExperts, (long long)M, w1->num_experts);
   if (!hidden || !top_k_index || !h) return fail(E4B_EINVAL, "NULL pointer");
   if (!aligned16(hidden) || !aligned16(h)) return fail(E4B_EINVAL, "hidden / h must be 16-byte aligned");
@@ -396,7 +350,7 @@ int e4b_decode_gate_up(const void* hidden, int32_t act_dtype, int64_t tokens, co
   a.out = h;
   a.odt = act_dtype;
   a.n_out = pair ? w1->n / 2 : w1->n;
-  launch_decode<true>(a, act_dtype, std::min<int64_t>(w1->num_experts, M), stream);
+  launch_decode<true>(a, act_dtype, std::min<int64_t>(w1->num_experts, M), M, stream);
   return check_launch("decode_up_kernel");
 }
 
@@ -410,8 +364,8 @@ int e4b_decode_down_combine(const void* h, int32_t act_dtype, int64_t tokens, co
   if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "bad tokens/top_k");
   if (tokens == 0) return E4B_OK;
   const int64_t M = tokens * top_k;
-  if (!decode_supported(M, w2->num_experts, w2))
-    return fail(E4B_EUNSUPPORTED, "decode path needs tokens*top_k <= %d, E <= %d and k <= 8192 (got M=%lld E=%d)",
+  if (!decode_supported(M, w2->num_experts, w2, false))
+    return fail(E4B_EUNSUPPORTED, "decode path needs tokens*top_k <= %d, E <= %d and k <= 4096 (got M=%lld E=%d)",
                 e4b::kDecMaxRows, e4b::kDecMaxExperts, (long long)M, w2->num_experts);
   if (!h || !top_k_index || !top_k_weights || !out) return fail(E4B_EINVAL, "NULL pointer");
   if (!aligned16(h)) return fail(E4B_EINVAL, "h must be 16-byte aligned");
@@ -428,7 +382,7 @@ int e4b_decode_down_combine(const void* h, int32_t act_dtype, int64_t tokens, co
   a.out = out;
   a.odt = out_dtype;
   a.n_out = w2->n;
-  launch_decode<false>(a, act_dtype, 0, stream);
+  launch_decode<false>(a, act_dtype, 0, M, stream);
   return check_launch("decode_down_kernel");
 }
 
@@ -480,7 +434,7 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   if (!aligned16(hidden)) return fail(E4B_EINVAL, "hidden must be 16-byte aligned");
 
   // Decode path: two launches, routing recomputed in LDS, combine fused into the down kernel.
-  const bool decode_ok = decode_supported(M, E, w1) && decode_supported(M, E, w2);
+  const bool decode_ok = decode_supported(M, E, w1, true) && decode_supported(M, E, w2, false);
   const bool use_decode = decode_ok && ((flags == E4B_PATH_AUTO && tokens <= 8) || flags == E4B_PATH_GEMV);
   if (use_decode) {
     void* h = workspace;

@@ -126,7 +126,7 @@ int e4b_combine(const void* down, int32_t down_dtype, const int32_t* inv, const 
 /* Decode path, first half: routing of top_k_index recomputed on the device (no route launch),
  * gate_up GEMV with the fused epilogue. h is [tokens * top_k, h_cols] in act_dtype, row
  * t * top_k + s holding token t's activation for slot s (flat order, not expert order).
- * Needs tokens * top_k <= 512, E <= 256, w1->k <= 8192 (E4B_EUNSUPPORTED otherwise).
+ * Needs tokens * top_k <= 64, E <= 256, w1->k <= 4096 (E4B_EUNSUPPORTED otherwise).
  * Replaces: engines/fast.py:125-148 (sort, gather, gemm_4bit_grouped gate_up, _epilogue) for
  * small batches. */
 int e4b_decode_gate_up(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,

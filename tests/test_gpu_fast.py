@@ -520,10 +520,11 @@ def test_gptoss_config_shapes(T):
     _assert_fidelity(got[rows], ref[rows], oracle, f"gptoss T={T}")
 
 
-@pytest.mark.parametrize("T", [2, 64])
+@pytest.mark.parametrize("T", [2, 8, 64])
 def test_decode_path_forced_up_to_its_row_limit(T):
-    """The two-launch decode path (routing recomputed in LDS, combine fused into down) at
-    tokens*k up to its 512-row limit, forced so it also covers batches the auto rule sends to MFMA."""
+    """The GEMV kernels forced: the two-launch decode path (wave-local routing, combine fused into
+    down) up to its 64-row limit (T=8, k=8), and beyond it (T=64) the grouped GEMV kernels after
+    one routing launch -- batches the automatic rule sends to MFMA."""
     _announce(f"decode path forced T={T}")
     E, H, I, k = 64, 2048, 1024, 8
     mod = _cfg_module(E, H, I, seed=5000 + T, dq=False)

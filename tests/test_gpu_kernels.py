@@ -309,10 +309,11 @@ def _stack(fmt, E, n, k, seed):
 
 
 @pytest.mark.parametrize("fmt", ["nf4", "nf4_dq", "mxfp4"])
-@pytest.mark.parametrize("T", [1, 5, 64])
+@pytest.mark.parametrize("T", [1, 5, 32])
 def test_decode_halves_match_oracle(fmt, T):
-    """e4b_decode_gate_up (routing in LDS + gate_up + epilogue, h in flat order) and
-    e4b_decode_down_combine (down + k-slot combine) against the fp64 oracle per flat row."""
+    """e4b_decode_gate_up (wave-local routing + gate_up + epilogue, h in flat order) and
+    e4b_decode_down_combine (down + k-slot combine) against the fp64 oracle per flat row.
+    T=32 with top-2 over 8 experts fills the 64-row limit with ~8 rows per expert."""
     _announce(f"decode halves fmt={fmt} T={T}")
     E, H, I, top = 8, 768, 320, 2
     w1 = _stack(fmt, E, 2 * I, H, seed=20)
@@ -343,8 +344,9 @@ def test_decode_halves_match_oracle(fmt, T):
     assert out.dtype == torch.float32 and fro2 <= 1e-4, ("down+combine", fro2, maxabs2)
 
 
-def test_decode_rejects_batches_beyond_its_limit():
+@pytest.mark.parametrize("rows", [65, 600])
+def test_decode_rejects_batches_beyond_its_limit(rows):
     qw, _, _ = _nf4_stack(4, 128, 128, seed=26)
-    idx = torch.zeros(600, 1, dtype=torch.int64, device=DEV)
+    idx = torch.zeros(rows, 1, dtype=torch.int64, device=DEV)
     with pytest.raises(N.NativeError, match="decode path"):
-        ops.decode_gate_up(torch.zeros(600, 128, dtype=torch.bfloat16, device=DEV), idx, qw, N.EPI_NONE)
+        ops.decode_gate_up(torch.zeros(rows, 128, dtype=torch.bfloat16, device=DEV), idx, qw, N.EPI_NONE)
