@@ -194,10 +194,25 @@ E4B_DEV float chunk_dot(const uint4& q, const uint4 (&xq)[4], const char* lut_by
   return acc;
 }
 
+// v + the value of the lane selected by a DPP pattern within each 16-lane row.
+template <int CTRL>
+E4B_DEV float dpp_add(float v) {
+  const int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false);
+  return v + __int_as_float(o);
+}
+
+// Sum over aligned groups of G lanes (G a power of two, 2..64); every lane gets its group's sum.
+// Within a 16-lane row the steps are DPP moves (xor 1 and xor 2 by quad_perm, then the
+// half-row and row mirrors, which pair each lane with one holding the complementary partial
+// sum); wider groups finish with cross-row swaps.
 template <int G>
 E4B_DEV float group_reduce(float v) {
-#pragma unroll
-  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  v = dpp_add<0xb1>(v);                          // quad_perm [1,0,3,2]
+  if constexpr (G >= 4) v = dpp_add<0x4e>(v);    // quad_perm [2,3,0,1]
+  if constexpr (G >= 8) v = dpp_add<0x141>(v);   // row_half_mirror
+  if constexpr (G >= 16) v = dpp_add<0x140>(v);  // row_mirror
+  if constexpr (G >= 32) v += __shfl_xor(v, 16);
+  if constexpr (G >= 64) v += __shfl_xor(v, 32);
   return v;
 }
 
