@@ -376,6 +376,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--extra", action="store_true", help="also run configs[2] and configs[4]")
     ap.add_argument("--kernel-only", action="store_true", help="only the dominant-kernel loop (for profiling)")
+    ap.add_argument("--prefill-only", action="store_true", help="only the configs[3] prefill (for profiling)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for counter runs: the dominant kernel eagerly once per layer, then a 256 MiB "
                          "device copy whose counter reading calibrates bytes per counted KiB")
@@ -394,6 +395,9 @@ def main():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(2)
     N.lib()  # fail loudly if the kernel library is missing
+    if args.prefill_only:
+        print(json.dumps({"prefill": prefill_bench(args.steps, args.warmup)}), flush=True)
+        return
     cfg = OLMOE
     log("building 16 OLMoE-geometry NF4 layers")
     mods = [make_layer(cfg, seed=1000 + 100 + l) for l in range(cfg["layers"])]

@@ -28,6 +28,7 @@ EXPORTS = (
     "e4b_last_error",
     "e4b_mfma_tile_m",
     "e4b_dequant",
+    "e4b_route_scratch_ints",
     "e4b_route",
     "e4b_grouped_gemm",
     "e4b_combine",
@@ -76,6 +77,7 @@ class Routing(ctypes.Structure):
         ("meta", ctypes.c_void_p),
         ("max_tiles", ctypes.c_int32),
         ("tile_m", ctypes.c_int32),
+        ("scratch", ctypes.c_void_p),
     ]
 
 
@@ -94,6 +96,8 @@ def _bind(L):
     L.e4b_mfma_tile_m.argtypes = []
     L.e4b_dequant.restype = ctypes.c_int
     L.e4b_dequant.argtypes = [QW, I32, I32, I32, P, P]
+    L.e4b_route_scratch_ints.restype = I64
+    L.e4b_route_scratch_ints.argtypes = [I64, I32]
     L.e4b_route.restype = ctypes.c_int
     L.e4b_route.argtypes = [P, I64, I32, I32, RT, P]
     L.e4b_grouped_gemm.restype = ctypes.c_int

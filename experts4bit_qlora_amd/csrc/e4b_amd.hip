@@ -247,9 +247,25 @@ int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t
   if (M > 0 && rt->max_tiles < max_tiles_for(M, num_experts, rt->tile_m))
     return fail(E4B_ESPACE, "max_tiles=%d < %lld needed", rt->max_tiles,
                 (long long)max_tiles_for(M, num_experts, rt->tile_m));
-  hipLaunchKernelGGL(e4b::route_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, top_k_index, M, num_experts,
-                     *rt);
-  return check_launch("route_kernel");
+  if (M <= e4b::kRouteSingleMaxRows) {
+    hipLaunchKernelGGL(e4b::route_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, top_k_index, M, num_experts,
+                       *rt);
+    return check_launch("route_kernel");
+  }
+  if (!rt->scratch) return fail(E4B_EINVAL, "routing scratch is NULL (needed above %d rows)", e4b::kRouteSingleMaxRows);
+  const int64_t nchunks = cdiv(M, e4b::kRouteChunk);
+  hipLaunchKernelGGL(e4b::route_count_kernel, dim3(static_cast<unsigned>(nchunks)), dim3(e4b::kRouteChunk), 0, stream,
+                     top_k_index, M, num_experts, rt->scratch);
+  hipLaunchKernelGGL(e4b::route_scan_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, nchunks, num_experts,
+                     rt->scratch, *rt);
+  hipLaunchKernelGGL(e4b::route_place_kernel, dim3(static_cast<unsigned>(nchunks)), dim3(e4b::kRouteChunk), 0, stream,
+                     top_k_index, M, num_experts, rt->scratch, *rt);
+  return check_launch("route_count/scan/place kernels");
+}
+
+int64_t e4b_route_scratch_ints(int64_t M, int32_t num_experts) {
+  if (M <= e4b::kRouteSingleMaxRows || num_experts <= 0) return 0;
+  return cdiv(M, e4b::kRouteChunk) * (int64_t(num_experts) + 1);
 }
 
 int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e4b_qweight* w, const e4b_routing* rt,
@@ -398,6 +414,7 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
   b += align256(sizeof(int32_t) * num_experts);                        // active
   b += align256(sizeof(int32_t) * 2 * max_tiles_for(M, num_experts, e4b::kTileM));  // tiles
   b += align256(sizeof(int32_t) * 4);                                  // meta
+  b += align256(sizeof(int32_t) * e4b_route_scratch_ints(M, num_experts));  // route scratch
   b += align256(sizeof(uint16_t) * M * h_cols);                        // h
   b += align256(sizeof(float) * M * n2);                               // down rows (fp32)
   return b;
@@ -459,6 +476,7 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   rt.tile_m = e4b::kTileM;
   rt.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rt.max_tiles));
   rt.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
+  rt.scratch = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * e4b_route_scratch_ints(M, E)));
   void* h = take(sizeof(uint16_t) * M * h_cols);
   void* down = take(sizeof(float) * M * w2->n);
 

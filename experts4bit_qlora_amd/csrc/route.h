@@ -11,6 +11,13 @@
 //      segment order, then chunk order, then lane order == flat order.
 // It also emits the tile list (expert, first row) the grouped MFMA GEMM schedules from, so
 // no count ever travels to the host (the reference's .tolist() sync, fast.py:132-133).
+//
+// Beyond kRouteSingleMaxRows ids one workgroup is too narrow, and the same counting sort runs
+// in three launches over 256-id chunks (four waves of 64 ids each):
+//   route_count_kernel  per-chunk histograms (one LDS add per distinct expert per 64 ids);
+//   route_scan_kernel   one workgroup: per-expert totals, offsets, tiles, active list, meta,
+//                       and each chunk's first sorted row per expert (chunk order = flat order);
+//   route_place_kernel  each chunk re-walks its ids in order from those bases.
 #pragma once
 
 #include "common.h"
@@ -20,6 +27,8 @@ namespace e4b {
 constexpr int kRouteThreads = 512;
 constexpr int kRouteWaves = kRouteThreads / kWave;
 constexpr int kRouteMaxExperts = 1024;
+constexpr int kRouteSingleMaxRows = 4096;  // above: the three-launch chunked route
+constexpr int kRouteChunk = 4 * kWave;     // ids per chunk (one workgroup) in the chunked route
 
 // Exclusive scan of one int per thread across the 512-thread block (order = thread order).
 E4B_DEV int block_exclusive_scan(int v, int* total, int* wsum) {
@@ -43,6 +52,50 @@ E4B_DEV int block_exclusive_scan(int v, int* total, int* wsum) {
   __syncthreads();
   *total = tot;
   return base + x - v;
+}
+
+// Offsets, tile list, active list and meta from per-expert totals. Thread t of the 512-thread
+// block owns experts 2t and 2t+1 with totals ta and tb; offa / offb receive their first sorted
+// rows. `dropped` must be the same value in every thread.
+E4B_DEV void emit_expert_tables(int ta, int tb, int E, int dropped, const e4b_routing& rt, int* wsum, int& offa,
+                                int& offb) {
+  const int tid = threadIdx.x;
+  const int ea = 2 * tid, eb = 2 * tid + 1;
+  int total;
+  offa = block_exclusive_scan(ta + tb, &total, wsum);
+  offb = offa + ta;
+  if (ea < E) rt.offsets[ea] = offa;
+  if (eb < E) rt.offsets[eb] = offb;
+  if (tid == 0) rt.offsets[E] = total;
+
+  const int tm = rt.tile_m;
+  const int na = (ta + tm - 1) / tm, nb = (tb + tm - 1) / tm;
+  int num_tiles;
+  const int tbase = block_exclusive_scan(na + nb, &num_tiles, wsum);
+  for (int j = 0; j < na; ++j) {
+    const int t = tbase + j;
+    if (t < rt.max_tiles) {
+      rt.tiles[2 * t] = ea;
+      rt.tiles[2 * t + 1] = offa + j * tm;
+    }
+  }
+  for (int j = 0; j < nb; ++j) {
+    const int t = tbase + na + j;
+    if (t < rt.max_tiles) {
+      rt.tiles[2 * t] = eb;
+      rt.tiles[2 * t + 1] = offb + j * tm;
+    }
+  }
+  int num_active;
+  const int abase = block_exclusive_scan((ta > 0) + (tb > 0), &num_active, wsum);
+  if (ta > 0) rt.active[abase] = ea;
+  if (tb > 0) rt.active[abase + (ta > 0)] = eb;
+  if (tid == 0) {
+    rt.meta[0] = min(num_tiles, rt.max_tiles);
+    rt.meta[1] = num_active;
+    rt.meta[2] = dropped;
+    rt.meta[3] = tm;
+  }
 }
 
 __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __restrict__ idx, int64_t M,
@@ -82,11 +135,10 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __r
     for (int w = 0; w < kRouteWaves; ++w) ta += cnt[w * E + ea];
   if (eb < E)
     for (int w = 0; w < kRouteWaves; ++w) tb += cnt[w * E + eb];
-  int total;
-  const int offa = block_exclusive_scan(ta + tb, &total, wsum);
-  const int offb = offa + ta;
+  const int ndropped = dropped;
+  int offa, offb;
+  emit_expert_tables(ta, tb, E, ndropped, rt, wsum, offa, offb);
   if (ea < E) {
-    rt.offsets[ea] = offa;
     int run = offa;
     for (int w = 0; w < kRouteWaves; ++w) {
       const int c = cnt[w * E + ea];
@@ -95,7 +147,6 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __r
     }
   }
   if (eb < E) {
-    rt.offsets[eb] = offb;
     int run = offb;
     for (int w = 0; w < kRouteWaves; ++w) {
       const int c = cnt[w * E + eb];
@@ -103,37 +154,7 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __r
       run += c;
     }
   }
-  if (tid == 0) rt.offsets[E] = total;
-
-  const int tm = rt.tile_m;
-  const int na = (ta + tm - 1) / tm, nb = (tb + tm - 1) / tm;
-  int num_tiles;
-  const int tbase = block_exclusive_scan(na + nb, &num_tiles, wsum);
-  for (int j = 0; j < na; ++j) {
-    const int t = tbase + j;
-    if (t < rt.max_tiles) {
-      rt.tiles[2 * t] = ea;
-      rt.tiles[2 * t + 1] = offa + j * tm;
-    }
-  }
-  for (int j = 0; j < nb; ++j) {
-    const int t = tbase + na + j;
-    if (t < rt.max_tiles) {
-      rt.tiles[2 * t] = eb;
-      rt.tiles[2 * t + 1] = offb + j * tm;
-    }
-  }
-  int num_active;
-  const int abase = block_exclusive_scan((ta > 0) + (tb > 0), &num_active, wsum);
-  if (ta > 0) rt.active[abase] = ea;
-  if (tb > 0) rt.active[abase + (ta > 0)] = eb;
   __syncthreads();
-  if (tid == 0) {
-    rt.meta[0] = min(num_tiles, rt.max_tiles);
-    rt.meta[1] = num_active;
-    rt.meta[2] = dropped;
-    rt.meta[3] = tm;
-  }
 
   // 3. stable placement, one 64-id chunk at a time per wave, chunks in order.
   const unsigned long long below = (lane == 0) ? 0ull : ((~0ull) >> (kWave - lane));
@@ -163,6 +184,165 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __r
       pending &= ~m;
     }
   }
+}
+
+// ---- chunked route (M > kRouteSingleMaxRows); counts is [nchunks, E + 1] int32, column E the
+// chunk's dropped ids. A chunk of kRouteChunk ids is one workgroup of 4 waves, 64 ids each.
+
+constexpr int kChunkWaves = kRouteChunk / kWave;
+
+// Visit each distinct expert id of the wave once (e < 0: no id), in order of first lane:
+// f(expert, mask of the lanes holding it).
+template <class F>
+E4B_DEV void for_each_expert(int e, F&& f) {
+  unsigned long long pending = __ballot(e >= 0);
+  while (pending) {
+    const int leader = __ffsll(static_cast<long long>(pending)) - 1;
+    const int e0 = __shfl(e, leader);
+    const unsigned long long m = __ballot(e == e0);
+    f(e0, m);
+    pending &= ~m;
+  }
+}
+
+E4B_DEV int chunk_id(const int64_t* idx, int64_t i, int64_t M, int E, bool& dropped) {
+  dropped = false;
+  if (i >= M) return -1;
+  const int64_t v = idx[i];
+  if (v >= 0 && v < E) return static_cast<int>(v);
+  dropped = true;
+  return -1;
+}
+
+// Per-wave histogram of the wave's 64 ids into its LDS row c (E entries), returning the
+// number of dropped ids.
+E4B_DEV int wave_histogram(int e, bool drop, int* c, int E) {
+  const int lane = threadIdx.x & (kWave - 1);
+  for (int x = lane; x < E; x += kWave) c[x] = 0;
+  __builtin_amdgcn_wave_barrier();
+  for_each_expert(e, [&](int e0, unsigned long long m) {
+    if (lane == 0) c[e0] += __popcll(m);
+    __builtin_amdgcn_wave_barrier();
+  });
+  return __popcll(__ballot(drop));
+}
+
+__global__ void __launch_bounds__(kRouteChunk) route_count_kernel(const int64_t* __restrict__ idx, int64_t M, int E,
+                                                                  int32_t* __restrict__ counts) {
+  __shared__ int c[kChunkWaves][kRouteMaxExperts];
+  __shared__ int nd[kChunkWaves];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  bool drop;
+  const int e = chunk_id(idx, int64_t(blockIdx.x) * kRouteChunk + threadIdx.x, M, E, drop);
+  const int d = wave_histogram(e, drop, c[wid], E);
+  if (lane == 0) nd[wid] = d;
+  __syncthreads();
+  int32_t* row = counts + int64_t(blockIdx.x) * (E + 1);
+  for (int x = threadIdx.x; x < E; x += kRouteChunk) {
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < kChunkWaves; ++w) t += c[w][x];
+    row[x] = t;
+  }
+  if (threadIdx.x == 0) {
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < kChunkWaves; ++w) t += nd[w];
+    row[E] = t;
+  }
+}
+
+// One workgroup: totals, tables, and counts rewritten in place as each chunk's first sorted
+// row per expert (column E untouched). `per` threads share an expert, each summing a
+// contiguous span of chunks, so the column sums take a few batched round trips.
+__global__ void __launch_bounds__(kRouteThreads) route_scan_kernel(int64_t nchunks, int E, int32_t* __restrict__ counts,
+                                                                   e4b_routing rt) {
+  __shared__ int tot[kRouteMaxExperts];
+  __shared__ int part[kRouteMaxExperts * 8];
+  __shared__ int wsum[kRouteWaves];
+  const int tid = threadIdx.x;
+  const int64_t pitch = E + 1;
+  int per = 1;
+  while (per < 8 && per * 2 * E <= kRouteThreads) per *= 2;
+  const int epp = kRouteThreads / per;  // experts per pass
+  const int64_t span = (nchunks + per - 1) / per;
+
+  for (int e0 = 0; e0 < E; e0 += epp) {
+    const int e = e0 + tid / per, q = tid % per;
+    int sum = 0;
+    if (e < E) {
+      const int64_t b1 = min(nchunks, (q + 1) * span);
+#pragma unroll 8
+      for (int64_t b = q * span; b < b1; ++b) sum += counts[b * pitch + e];
+      part[e * per + q] = sum;
+    }
+  }
+  int nd = 0;
+  for (int64_t b = tid; b < nchunks; b += kRouteThreads) nd += counts[b * pitch + E];
+  __syncthreads();
+  for (int x = tid; x < E; x += kRouteThreads) {
+    int t = 0;
+    for (int q = 0; q < per; ++q) t += part[x * per + q];
+    tot[x] = t;
+  }
+  int dropped;
+  block_exclusive_scan(nd, &dropped, wsum);  // also orders the tot[] writes before the reads
+  const int ta = (2 * tid < E) ? tot[2 * tid] : 0;
+  const int tb = (2 * tid + 1 < E) ? tot[2 * tid + 1] : 0;
+  int offa, offb;
+  emit_expert_tables(ta, tb, E, dropped, rt, wsum, offa, offb);
+  if (2 * tid < E) tot[2 * tid] = offa;
+  if (2 * tid + 1 < E) tot[2 * tid + 1] = offb;
+  __syncthreads();
+  for (int e0 = 0; e0 < E; e0 += epp) {
+    const int e = e0 + tid / per, q = tid % per;
+    if (e < E) {
+      int run = tot[e];
+      for (int r = 0; r < q; ++r) run += part[e * per + r];
+      const int64_t b1 = min(nchunks, (q + 1) * span);
+      for (int64_t b = q * span; b < b1; ++b) {
+        const int c = counts[b * pitch + e];
+        counts[b * pitch + e] = run;
+        run += c;
+      }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(kRouteChunk) route_place_kernel(const int64_t* __restrict__ idx, int64_t M, int E,
+                                                                  const int32_t* __restrict__ counts, e4b_routing rt) {
+  __shared__ int c[kChunkWaves][kRouteMaxExperts];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wid = threadIdx.x / kWave;
+  const int64_t i = int64_t(blockIdx.x) * kRouteChunk + threadIdx.x;
+  bool drop;
+  const int e = chunk_id(idx, i, M, E, drop);
+  wave_histogram(e, drop, c[wid], E);
+  __syncthreads();
+  // cursors: this chunk's base per expert plus the ids of the same expert in earlier waves
+  const int32_t* row = counts + int64_t(blockIdx.x) * (E + 1);
+  for (int x = threadIdx.x; x < E; x += kRouteChunk) {
+    int run = row[x];
+#pragma unroll
+    for (int w = 0; w < kChunkWaves; ++w) {
+      const int cw = c[w][x];
+      c[w][x] = run;
+      run += cw;
+    }
+  }
+  __syncthreads();
+  if (drop) rt.inv[i] = -1;
+  int* cur = c[wid];
+  const unsigned long long below = (lane == 0) ? 0ull : ((~0ull) >> (kWave - lane));
+  for_each_expert(e, [&](int e0, unsigned long long m) {
+    const int c0 = cur[e0];
+    if (e == e0) {
+      const int pos = c0 + __popcll(m & below);
+      rt.sorted_flat[pos] = static_cast<int>(i);
+      rt.inv[i] = pos;
+    }
+  });
 }
 
 // out[t, :] = out_t( sum_s float(down[inv[t*k+s], :]) * w[t, s] ), s ascending, fp32 adds of

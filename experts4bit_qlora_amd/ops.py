@@ -124,6 +124,7 @@ class RoutingBuffers:
     meta: torch.Tensor
     max_tiles: int
     tile_m: int
+    scratch: torch.Tensor | None = None
 
     def struct(self) -> N.Routing:
         r = N.Routing()
@@ -135,6 +136,7 @@ class RoutingBuffers:
         r.meta = self.meta.data_ptr()
         r.max_tiles = self.max_tiles
         r.tile_m = self.tile_m
+        r.scratch = self.scratch.data_ptr() if self.scratch is not None else None
         return r
 
 
@@ -163,6 +165,9 @@ def route(top_k_index: torch.Tensor, num_experts: int, tile_m: int | None = None
         max_tiles=max_tiles,
         tile_m=tm,
     )
+    n_scratch = int(L.e4b_route_scratch_ints(M, num_experts))
+    if n_scratch > 0:
+        rb.scratch = torch.empty(n_scratch, **i32)
     rs = rb.struct()
     N.check("e4b_route", L.e4b_route(idx.data_ptr(), T, k, num_experts, ctypes.byref(rs), _stream(dev)))
     return rb

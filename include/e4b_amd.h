@@ -77,6 +77,8 @@ typedef struct e4b_routing {
   int32_t* meta;        /* [4]     num_tiles, num_active, num_dropped, tile_m */
   int32_t max_tiles;    /* capacity of `tiles`: >= ceil(M / tile_m) + min(E, M) */
   int32_t tile_m;       /* rows per tile (the MFMA path uses 64) */
+  int32_t* scratch;     /* [e4b_route_scratch_ints(M, E)] per-chunk counts of the chunked route
+                           (M > 4096); may be NULL when that size is 0 */
 } e4b_routing;
 
 /* Library version string and the last error message of the calling host thread. */
@@ -94,6 +96,11 @@ int32_t e4b_mfma_tile_m(void);
  * MXFP4, formats/mxfp4.py:35-105 dequantize_mxfp4 before its final transpose. */
 int e4b_dequant(const e4b_qweight* w, int32_t expert_begin, int32_t expert_count, int32_t out_dtype,
                 void* out, hipStream_t stream);
+
+/* int32 scratch the route needs for M = tokens * top_k routed rows over E experts: 0 up to
+ * 4096 rows (one workgroup routes them), else ceil(M / 256) * (E + 1) (three launches over
+ * 256-row chunks). */
+int64_t e4b_route_scratch_ints(int64_t M, int32_t num_experts);
 
 /* Token -> expert permutation, bit-exact to a stable argsort of top_k_index.reshape(-1).
  * Replaces: engines/fast.py:125-133 (argsort(stable), //k, %k, bincount, nonzero, .tolist());

@@ -47,7 +47,7 @@ def test_enums_match_header():
 
 def test_struct_layouts():
     assert ctypes.sizeof(N.QWeight) == 4 + 4 + 8 + 8 + 7 * 8
-    assert ctypes.sizeof(N.Routing) == 6 * 8 + 4 + 4
+    assert ctypes.sizeof(N.Routing) == 6 * 8 + 4 + 4 + 8
 
 
 def _qw(**kw):
@@ -104,6 +104,16 @@ def test_route_rejects_bad_arguments():
     bad = _rt()
     bad.meta = None
     assert L.e4b_route(4096, 4, 2, 8, ctypes.byref(bad), None) == -1
+
+
+def test_route_scratch_sizes():
+    L = N.lib()
+    assert L.e4b_route_scratch_ints(4096, 128) == 0  # one workgroup routes up to 4096 rows
+    assert L.e4b_route_scratch_ints(4097, 128) == 17 * 129
+    assert L.e4b_route_scratch_ints(32768, 128) == 128 * 129
+    r = _rt(max_tiles=1000)
+    assert L.e4b_route(4096, 8192, 1, 8, ctypes.byref(r), None) == -1  # 8192 rows, scratch NULL
+    assert "scratch" in _err()
 
 
 def test_grouped_gemm_rejects_bad_arguments():

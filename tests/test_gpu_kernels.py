@@ -146,6 +146,31 @@ def test_route_drops_out_of_range_ids():
     assert ref["counts"].sum() == 4
 
 
+@pytest.mark.parametrize("M,E", [(4096, 64), (4097, 64), (4353, 1024), (40000, 256)])
+def test_chunked_route_boundaries_and_dropped_ids(M, E):
+    """Around the one-workgroup limit (4096 rows) and on the chunked route: ragged last chunk,
+    many experts, ~1% invalid ids spread through the chunks."""
+    _announce(f"chunked route M={M} E={E}")
+    rng = np.random.default_rng(M + E)
+    flat = rng.integers(0, E, M).astype(np.int64)
+    bad = rng.random(M) < 0.01
+    flat[bad] = np.where(rng.random(bad.sum()) < 0.5, -1, E + 3)
+    idx = flat.reshape(M, 1)
+    rb = ops.route(torch.from_numpy(idx).to(DEV), E)
+    meta = rb.meta.cpu().numpy()
+    assert meta[2] == bad.sum()
+    valid = np.flatnonzero(~bad)
+    order = valid[np.argsort(flat[valid], kind="stable")]
+    n = len(order)
+    assert rb.sorted_flat[:n].cpu().numpy().tolist() == order.tolist()
+    inv = rb.inv[:M].cpu().numpy()
+    assert (inv[bad] == -1).all()
+    assert (inv[order] == np.arange(n)).all()
+    counts = np.bincount(flat[valid], minlength=E)
+    assert rb.offsets.cpu().numpy().tolist() == np.concatenate([[0], np.cumsum(counts)]).tolist()
+    assert meta[1] == (counts > 0).sum()
+
+
 # --------------------------------------------------------------------------------- GEMMs
 
 
