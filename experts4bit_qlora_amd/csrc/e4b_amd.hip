@@ -129,8 +129,19 @@ template <int DT, int FMT>
 void launch_mfma_fmt(const e4b::GemmArgs& a, hipStream_t s) {
   const bool pair = a.epi == E4B_EPI_SWIGLU || a.epi == E4B_EPI_CLAMP_SWIGLU || a.epi == E4B_EPI_GPTOSS;
   const int64_t cols = pair ? e4b::kTileNW / 2 : e4b::kTileNW;
-  dim3 grid(static_cast<unsigned>(a.rt.max_tiles), static_cast<unsigned>(cdiv(a.n_out, cols)));
-  hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT>), grid, dim3(e4b::kGemmThreads), 0, s, a);
+  // 8 XCDs x ceil(max_tiles / 8) M tiles x n_tiles blocks, mapped to tiles in the kernel
+  const int64_t n_tiles = cdiv(a.n_out, cols);
+  dim3 grid(static_cast<unsigned>(e4b::kXcds * cdiv(a.rt.max_tiles, e4b::kXcds) * n_tiles));
+  if (a.rt.tile_m == e4b::kTileMSmall) {
+    hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, e4b::kTileMSmall>), grid,
+                       dim3(e4b::gemm_threads(e4b::kTileMSmall)), 0, s, a);
+  } else if (a.rt.tile_m == e4b::kTileMBig) {
+    hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, e4b::kTileMBig>), grid,
+                       dim3(e4b::gemm_threads(e4b::kTileMBig)), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, e4b::kTileM>), grid, dim3(e4b::gemm_threads(e4b::kTileM)), 0,
+                       s, a);
+  }
 }
 
 template <int DT>
@@ -200,6 +211,13 @@ bool decode_supported(int64_t M, int E, const e4b_qweight* w, bool up) {
 size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 int64_t max_tiles_for(int64_t M, int E, int tile_m) { return cdiv(M, tile_m) + std::min<int64_t>(E, M); }
+
+// MFMA tile rows for a forward of M routed rows over E experts: 128-row tiles once experts
+// average 64 rows or more, else 32-row tiles (less padding when experts get few rows each).
+int mfma_tile_for(int64_t M, int E) {
+  const int64_t groups = std::min<int64_t>(E, M);
+  return M >= 64 * groups ? e4b::kTileM : e4b::kTileMSmall;
+}
 
 bool is_gated_epi(int epi) {
   return epi == E4B_EPI_SWIGLU || epi == E4B_EPI_CLAMP_SWIGLU || epi == E4B_EPI_GPTOSS;
@@ -292,8 +310,9 @@ int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e
   else if (flags == E4B_PATH_MFMA) gemv = false;
   else if (flags == E4B_PATH_AUTO) gemv = tokens <= 4;
   else return fail(E4B_EINVAL, "bad flags %d", flags);
-  if (!gemv && rt->tile_m != e4b::kTileM)
-    return fail(E4B_EINVAL, "routing tile_m=%d but the MFMA GEMM needs %d", rt->tile_m, e4b::kTileM);
+  if (!gemv && rt->tile_m != e4b::kTileM && rt->tile_m != e4b::kTileMSmall && rt->tile_m != e4b::kTileMBig)
+    return fail(E4B_EINVAL, "routing tile_m=%d but the MFMA GEMM takes %d, %d or %d", rt->tile_m, e4b::kTileMBig,
+                e4b::kTileM, e4b::kTileMSmall);
 
   e4b::GemmArgs args;
   args.a = static_cast<const uint16_t*>(a);
@@ -412,7 +431,7 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
   b += align256(sizeof(int32_t) * M);                                  // inv
   b += align256(sizeof(int32_t) * (num_experts + 1));                  // offsets
   b += align256(sizeof(int32_t) * num_experts);                        // active
-  b += align256(sizeof(int32_t) * 2 * max_tiles_for(M, num_experts, e4b::kTileM));  // tiles
+  b += align256(sizeof(int32_t) * 2 * max_tiles_for(M, num_experts, mfma_tile_for(M, num_experts)));  // tiles
   b += align256(sizeof(int32_t) * 4);                                  // meta
   b += align256(sizeof(int32_t) * e4b_route_scratch_ints(M, num_experts));  // route scratch
   b += align256(sizeof(uint16_t) * M * h_cols);                        // h
@@ -472,8 +491,8 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   rt.inv = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));
   rt.offsets = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (E + 1)));
   rt.active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
-  rt.max_tiles = static_cast<int32_t>(max_tiles_for(M, E, e4b::kTileM));
-  rt.tile_m = e4b::kTileM;
+  rt.tile_m = mfma_tile_for(M, E);
+  rt.max_tiles = static_cast<int32_t>(max_tiles_for(M, E, rt.tile_m));
   rt.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rt.max_tiles));
   rt.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
   rt.scratch = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * e4b_route_scratch_ints(M, E)));

@@ -1,18 +1,27 @@
 // Prefill / large-batch grouped GEMM on the bf16 (fp16) matrix cores of gfx950.
 //
-// One workgroup (4 waves) computes a 64-row x 128-weight-row tile of one expert. Tiles come
-// from the route kernel's (expert, first sorted row) list, so skewed expert sizes cost at most
-// one partial tile per expert and the grid never depends on host-side counts.
-// Per 64-deep K step:
-//   * A: 64 routed rows x 64 activations, gathered through sorted_flat when gather_k > 0
-//     (the index_select of fast.py:135 fused into the loads) -> LDS;
-//   * W: 128 packed rows x 32 bytes -> each thread decodes 32 nibbles with ONE fp32 product
-//     code[nib] * scale and one RNE rounding (bit-identical to the reference's dequantized
-//     bf16 weight) -> LDS;
-//   * 2 x (2 x 4) v_mfma_f32_16x16x32_{bf16,f16} per wave, fp32 accumulators.
+// One workgroup computes a BM-row x 128-weight-row tile of one expert: BM = 256 (8 waves) for
+// the full 256-row runs of large experts, 128 (4 waves) for prefill-sized groups, 32 (4 waves)
+// for mid-size batches where experts get few rows. Every dequantized weight feeds BM rows, so
+// the decode work per MFMA falls as BM grows. Tiles come from
+// the route kernel's (expert, first sorted row) list, so skewed expert sizes cost at most one
+// partial tile per expert and the grid never depends on host-side counts.
+//
+// Pipeline, per 64-deep K step (one NF4 absmax block per weight row):
+//   * global -> registers runs kStages steps ahead (A rows gathered through sorted_flat when
+//     gather_k > 0, the index_select of fast.py:135 fused into the loads; 16 packed bytes +
+//     the scale of each weight half-row), in kStages rotating register sets, so several
+//     global round trips overlap the MFMAs of step s, which read LDS buffer s % 2;
+//   * after the MFMAs, step s+1's registers are written to the other LDS buffer: activations as
+//     loaded, weights decoded with ONE fp32 product code[nib] * scale and one RNE rounding --
+//     bit-identical to the reference's dequantized bf16 (fp16) weight. Codes come from a
+//     256-entry LDS table of (first, second) fp32 code pairs, one entry per packed byte;
+//   * one barrier per step. Each wave runs (BM / WAVES_M / 16) x (128 / WAVES_N / 16)
+//     v_mfma_f32_16x16x32_{bf16,f16} per 32-deep half step with fp32 accumulators.
 // Gated epilogues pair gate row j with up row n/2 + j in the same tile: LDS rows 0..63 hold
 // the gate rows of 64 output columns and rows 64..127 their up rows, and a wave's gate and up
-// accumulators sit in the same lanes, so SwiGLU runs on registers (fp32) before the only store.
+// accumulators sit in the same lanes, so the activation runs on registers (fp32) before the
+// only store.
 #pragma once
 
 #include "common.h"
@@ -25,11 +34,14 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kTileM = 64;
-constexpr int kTileNW = 128;  // weight rows per tile
+constexpr int kTileMBig = 256;   // rows per tile for the full 256-row runs of large experts
+constexpr int kTileM = 128;      // rows per tile of the prefill-sized GEMM
+constexpr int kTileMSmall = 32;  // rows per tile for mid-size batches
+constexpr int kTileNW = 128;     // weight rows per tile
 constexpr int kTileK = 64;
 constexpr int kLdsPitch = kTileK + 8;  // elements; 144-byte rows keep 16-byte alignment
-constexpr int kGemmThreads = 256;
+constexpr int kStages = 3;  // K steps of global loads in flight ahead of the MFMAs
+constexpr int kXcds = 8;    // accelerator dies of an MI355X; blocks go round-robin over them
 
 template <int DT>
 E4B_DEV f32x4_t mfma_16x16x32(const uint4& a, const uint4& b, const f32x4_t& c) {
@@ -42,41 +54,93 @@ E4B_DEV f32x4_t mfma_16x16x32(const uint4& a, const uint4& b, const f32x4_t& c) 
   }
 }
 
-template <int DT, int FMT>
-__global__ void __launch_bounds__(kGemmThreads) gemm_mfma_kernel(GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[kTileM * kLdsPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t Ws[kTileNW * kLdsPitch];
-  __shared__ float lut[16];
+// NB packed bytes (2 * NB values) -> NB words of DT pairs, each value dt(fp32(code * scale)),
+// codes from the 256-entry LDS table of (first, second) fp32 code pairs.
+template <int DT, int NB>
+E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float2* pairs, float scale, uint32_t (&wv)[NB]) {
+#pragma unroll
+  for (int wi = 0; wi < NB / 4; ++wi) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float2 c = pairs[(words[wi] >> (8 * b)) & 0xffu];
+      wv[4 * wi + b] = pack2(from_f<DT>(mul_f32(c.x, scale)), from_f<DT>(mul_f32(c.y, scale)));
+    }
+  }
+}
 
-  const int tile = blockIdx.x;
-  if (tile >= p.rt.meta[0]) return;
+// Threads of the tile shape: 8 waves for 256-row tiles, else 4.
+constexpr int gemm_threads(int bm) { return bm >= 256 ? 512 : 256; }
+
+template <int DT, int FMT, int BM>
+__global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p) {
+  constexpr int NT = gemm_threads(BM);
+  constexpr int WAVES = NT / kWave;
+  constexpr int WAVES_M = BM >= 256 ? 4 : BM >= 128 ? 2 : 1;
+  constexpr int WAVES_N = WAVES / WAVES_M;
+  constexpr int WM = BM / WAVES_M;       // rows per wave
+  constexpr int WN = kTileNW / WAVES_N;  // weight rows per wave
+  constexpr int MS = WM / 16, NS = WN / 16;
+  constexpr int TPR = NT / BM;            // threads per A row
+  constexpr int AV = kTileK / TPR / 8;    // uint4 of A per thread per step
+  constexpr int TPW = NT / kTileNW;       // threads per weight row
+  constexpr int WB = kTileK / 2 / TPW;    // packed weight bytes per thread per step
+  static_assert(AV >= 1 && NS % 2 == 0 && (WB == 16 || WB == 8), "tile shape");
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLdsPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][kTileNW * kLdsPitch];
+  __shared__ float2 pairs[256];
+  __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
+
+  // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so linear
+  // block L runs on XCD L % 8. XCD x takes the contiguous run of M tiles
+  // [x * chunk, (x + 1) * chunk) and sweeps all N tiles of one M tile before the next: the
+  // activation tile stays in that XCD's L2 across the N sweep, and an expert's consecutive M
+  // tiles (same weights) stay on one XCD as well.
+  const int num_tiles = p.rt.meta[0];
+  const int n_tiles = static_cast<int>((p.n_out + (is_gated(p.epi) ? kTileNW / 2 : kTileNW) - 1) /
+                                       (is_gated(p.epi) ? kTileNW / 2 : kTileNW));
+  const int xcd = static_cast<int>(blockIdx.x % kXcds);
+  const int q = static_cast<int>(blockIdx.x / kXcds);
+  const int chunk = (num_tiles + kXcds - 1) / kXcds;
+  const int m_local = q / n_tiles;
+  const int tile = xcd * chunk + m_local;
+  if (m_local >= chunk || tile >= num_tiles) return;
+  const int n_tile = q % n_tiles;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wid = tid / kWave;
-  const int wave_m = wid & 1;
-  const int wave_n = wid >> 1;
+  const int wave_m = wid % WAVES_M;
+  const int wave_n = wid / WAVES_M;
   const int e = p.rt.tiles[2 * tile];
   const int row0 = p.rt.tiles[2 * tile + 1];
-  const int row_end = min(row0 + kTileM, p.rt.offsets[e + 1]);
+  const int row_end = min(row0 + BM, p.rt.offsets[e + 1]);
   const bool pair = is_gated(p.epi);
   const int64_t n = p.w.n;
   const int64_t k = p.w.k;
-  const int64_t col0 = int64_t(blockIdx.y) * (pair ? kTileNW / 2 : kTileNW);
+  const int64_t col0 = int64_t(n_tile) * (pair ? kTileNW / 2 : kTileNW);
   if (col0 >= p.n_out) return;
 
-  if (tid < 16) lut[tid] = (FMT == E4B_FMT_MXFP4) ? kFp4E2M1[tid] : p.w.code[tid];
+  if (tid < 256) {  // decode tables: byte -> (first, second) codes; the second-level code
+    const uint32_t b = static_cast<uint32_t>(tid);
+    if constexpr (FMT == E4B_FMT_MXFP4) {
+      pairs[b] = make_float2(kFp4E2M1[b & 0xfu], kFp4E2M1[b >> 4]);
+    } else {
+      pairs[b] = make_float2(p.w.code[b >> 4], p.w.code[b & 0xfu]);
+    }
+    if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[tid] = p.w.code2[tid];
+  }
 
-  // A-load assignment: row tid/4, 16 activations at column (tid%4)*16.
-  const int ar = tid >> 2;
-  const int aseg = (tid & 3) * 16;
+  // A assignment: row tid / TPR, AV * 8 activations at column (tid % TPR) * AV * 8.
+  const int ar = tid / TPR;
+  const int aseg = (tid % TPR) * AV * 8;
   const int r = row0 + ar;
   const bool avalid = r < row_end;
   const int64_t src = avalid ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
   const uint16_t* aptr = p.a + src * k + aseg;
 
-  // W-load assignment: LDS row tid/2 (0..127), 32 values of the 64-deep step at (tid%2)*32.
-  const int lrow = tid >> 1;
-  const int half = tid & 1;
+  // W assignment: LDS row tid / TPW (0..127), 2 * WB values of the 64-deep step at
+  // (tid % TPW) * 2 * WB.
+  const int lrow = tid / TPW;
+  const int half = tid % TPW;  // which WB-byte part of the row's 32 packed bytes
   int64_t grow;
   bool wvalid;
   if (pair) {
@@ -88,108 +152,143 @@ __global__ void __launch_bounds__(kGemmThreads) gemm_mfma_kernel(GemmArgs p) {
     wvalid = grow < p.n_out;
   }
   if (!wvalid) grow = 0;
-  const uint8_t* wptr = p.w.packed + (int64_t(e) * n + grow) * (k / 2) + half * 16;
+  const uint8_t* wptr = p.w.packed + (int64_t(e) * n + grow) * (k / 2) + half * WB;
+  const int64_t nb = n * (k / 64);
+  const float offset = (FMT == E4B_FMT_NF4_DQ) ? p.w.offset[e] : 0.0f;
 
-  f32x4_t acc[2][4];
+  f32x4_t acc[MS][NS];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < MS; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < NS; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  int nbase[4];
+  int nbase[NS];
 #pragma unroll
-  for (int ns = 0; ns < 4; ++ns) {
-    nbase[ns] = pair ? ((ns < 2) ? wave_n * 32 + ns * 16 : 64 + wave_n * 32 + (ns - 2) * 16)
-                     : wave_n * 64 + ns * 16;
+  for (int ns = 0; ns < NS; ++ns) {
+    nbase[ns] = pair ? ((ns < NS / 2) ? wave_n * (WN / 2) + ns * 16 : 64 + wave_n * (WN / 2) + (ns - NS / 2) * 16)
+                     : wave_n * WN + ns * 16;
   }
-  __syncthreads();
 
-  const int64_t ksteps = k / kTileK;
-  for (int64_t kb = 0; kb < ksteps; ++kb) {
-    uint4 a0 = make_uint4(0, 0, 0, 0), a1 = make_uint4(0, 0, 0, 0);
+  // ---- step registers: kStages sets, step j in set j % kStages, loaded kStages steps before
+  // the step that writes it to LDS, so that many global round trips overlap the MFMAs
+  uint4 areg[kStages][AV];
+  uint32_t wq[kStages][WB / 4];
+  float sa[kStages];     // NF4 absmax, or double-quant absmax2
+  uint32_t sq[kStages];  // double-quant code, or e8m0
+  auto load_step = [&](int set, int64_t kb) {
+#pragma unroll
+    for (int i = 0; i < AV; ++i) areg[set][i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < WB / 4; ++i) wq[set][i] = 0u;
+    sa[set] = 0.0f;
+    sq[set] = 0;
     if (avalid) {
       const uint4* ap = reinterpret_cast<const uint4*>(aptr + kb * kTileK);
-      a0 = ap[0];
-      a1 = ap[1];
+#pragma unroll
+      for (int i = 0; i < AV; ++i) areg[set][i] = ap[i];
     }
-    uint4 q = make_uint4(0, 0, 0, 0);
-    float scale = 0.0f;
     if (wvalid) {
-      q = *reinterpret_cast<const uint4*>(wptr + kb * 32);
-      if constexpr (FMT == E4B_FMT_MXFP4) {
-        const uint8_t* sc = static_cast<const uint8_t*>(p.w.absmax);
-        scale = e8m0_to_f32(sc[(int64_t(e) * n + grow) * (k / 32) + kb * 2 + half]);
+      if constexpr (WB == 16) {
+        const uint4 v = *reinterpret_cast<const uint4*>(wptr + kb * 32);
+        wq[set][0] = v.x; wq[set][1] = v.y; wq[set][2] = v.z; wq[set][3] = v.w;
       } else {
-        scale = nf4_block_scale<FMT>(p.w, e, grow * (k / 64) + kb);
+        const uint2 v = *reinterpret_cast<const uint2*>(wptr + kb * 32);
+        wq[set][0] = v.x; wq[set][1] = v.y;
+      }
+      if constexpr (FMT == E4B_FMT_MXFP4) {
+        sq[set] = static_cast<const uint8_t*>(p.w.absmax)[(int64_t(e) * n + grow) * (k / 32) + kb * 2 + half * WB / 16];
+      } else if constexpr (FMT == E4B_FMT_NF4) {
+        sa[set] = static_cast<const float*>(p.w.absmax)[e * nb + grow * (k / 64) + kb];
+      } else {
+        const int64_t blk = grow * (k / 64) + kb;
+        sq[set] = static_cast<const uint8_t*>(p.w.absmax)[e * nb + blk];
+        sa[set] = p.w.absmax2[e * ((nb + 255) / 256) + blk / 256];
       }
     }
-    // decode 32 values -> exact DT weights
-    uint32_t wv[16];
-    const uint32_t words[4] = {q.x, q.y, q.z, q.w};
+  };
+  auto stage = [&](int set, int buf) {
+    float scale;
+    if constexpr (FMT == E4B_FMT_MXFP4) scale = wvalid ? e8m0_to_f32(sq[set]) : 0.0f;
+    else if constexpr (FMT == E4B_FMT_NF4) scale = sa[set];
+    else scale = wvalid ? __fadd_rn(mul_f32(code2_s[sq[set]], sa[set]), offset) : 0.0f;
+    uint32_t wv[WB];
+    dequant_bytes<DT, WB>(wq[set], pairs, scale, wv);
+    uint4* ws = reinterpret_cast<uint4*>(&Ws[buf][lrow * kLdsPitch + half * 2 * WB]);
 #pragma unroll
-    for (int wi = 0; wi < 4; ++wi) {
+    for (int i = 0; i < WB / 4; ++i) ws[i] = make_uint4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
+    uint4* as = reinterpret_cast<uint4*>(&As[buf][ar * kLdsPitch + aseg]);
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t byte = (words[wi] >> (8 * b)) & 0xffu;
-        const uint32_t first = (FMT == E4B_FMT_MXFP4) ? (byte & 0xfu) : (byte >> 4);
-        const uint32_t second = (FMT == E4B_FMT_MXFP4) ? (byte >> 4) : (byte & 0xfu);
-        wv[4 * wi + b] = pack2(from_f<DT>(mul_f32(lut[first], scale)),
-                               from_f<DT>(mul_f32(lut[second], scale)));
-      }
-    }
-    uint4* ws = reinterpret_cast<uint4*>(Ws + lrow * kLdsPitch + half * 32);
-    ws[0] = make_uint4(wv[0], wv[1], wv[2], wv[3]);
-    ws[1] = make_uint4(wv[4], wv[5], wv[6], wv[7]);
-    ws[2] = make_uint4(wv[8], wv[9], wv[10], wv[11]);
-    ws[3] = make_uint4(wv[12], wv[13], wv[14], wv[15]);
-    uint4* as = reinterpret_cast<uint4*>(As + ar * kLdsPitch + aseg);
-    as[0] = a0;
-    as[1] = a1;
-    __syncthreads();
-
+    for (int i = 0; i < AV; ++i) as[i] = areg[set][i];
+  };
+  auto mfma_step = [&](int buf) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int kcol = ks * 32 + (lane >> 4) * 8;
-      uint4 av[2], bv[4];
+      uint4 av[MS], bv[NS];
 #pragma unroll
-      for (int ms = 0; ms < 2; ++ms) {
-        av[ms] = *reinterpret_cast<const uint4*>(As + (wave_m * 32 + ms * 16 + (lane & 15)) * kLdsPitch + kcol);
+      for (int ms = 0; ms < MS; ++ms) {
+        av[ms] = *reinterpret_cast<const uint4*>(&As[buf][(wave_m * WM + ms * 16 + (lane & 15)) * kLdsPitch + kcol]);
       }
 #pragma unroll
-      for (int ns = 0; ns < 4; ++ns) {
-        bv[ns] = *reinterpret_cast<const uint4*>(Ws + (nbase[ns] + (lane & 15)) * kLdsPitch + kcol);
+      for (int ns = 0; ns < NS; ++ns) {
+        bv[ns] = *reinterpret_cast<const uint4*>(&Ws[buf][(nbase[ns] + (lane & 15)) * kLdsPitch + kcol]);
       }
 #pragma unroll
-      for (int ms = 0; ms < 2; ++ms)
+      for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-        for (int ns = 0; ns < 4; ++ns) acc[ms][ns] = mfma_16x16x32<DT>(av[ms], bv[ns], acc[ms][ns]);
+        for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = mfma_16x16x32<DT>(av[ms], bv[ns], acc[ms][ns]);
     }
-    __syncthreads();
+  };
+
+  const int64_t ksteps = k / kTileK;
+  load_step(0, 0);
+  __syncthreads();  // tables
+  stage(0, 0);
+#pragma unroll
+  for (int j = 1; j <= kStages; ++j) {
+    if (j < ksteps) load_step(j % kStages, j);
+  }
+  __syncthreads();
+  for (int64_t kb0 = 0; kb0 < ksteps; kb0 += kStages) {
+#pragma unroll
+    for (int u = 0; u < kStages; ++u) {
+      const int64_t kb = kb0 + u;
+      if (kb < ksteps) {
+        const int cur = static_cast<int>(kb & 1);
+        mfma_step(cur);
+        if (kb + 1 < ksteps) {
+          stage((u + 1) % kStages, cur ^ 1);
+          if (kb + 1 + kStages < ksteps) load_step((u + 1) % kStages, kb + 1 + kStages);
+        }
+        __syncthreads();
+      }
+    }
   }
 
   // Epilogue: lane holds D[4*(lane/16) + i][lane % 16] of each 16x16 sub-tile.
   const bool has_bias = p.w.bias != nullptr;
   const uint16_t* bias = static_cast<const uint16_t*>(p.w.bias);
 #pragma unroll
-  for (int ms = 0; ms < 2; ++ms) {
+  for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int rr = row0 + wave_m * 32 + ms * 16 + 4 * (lane >> 4) + i;
+      const int rr = row0 + wave_m * WM + ms * 16 + 4 * (lane >> 4) + i;
       if (rr >= row_end) continue;
       const int64_t orow = int64_t(rr) * p.n_out;
       if (pair) {
 #pragma unroll
-        for (int ns = 0; ns < 2; ++ns) {
-          const int64_t jj = col0 + wave_n * 32 + ns * 16 + (lane & 15);
+        for (int ns = 0; ns < NS / 2; ++ns) {
+          const int64_t jj = col0 + wave_n * (WN / 2) + ns * 16 + (lane & 15);
           if (jj >= p.n_out) continue;
           const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + jj]) : 0.0f;
           const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + n / 2 + jj]) : 0.0f;
-          store_elem<DT>(p, orow + jj, gated(p.epi, acc[ms][ns][i], acc[ms][ns + 2][i], p.alpha, p.limit, bg, bu));
+          store_elem<DT>(p, orow + jj,
+                         gated(p.epi, acc[ms][ns][i], acc[ms][ns + NS / 2][i], p.alpha, p.limit, bg, bu));
         }
       } else {
 #pragma unroll
-        for (int ns = 0; ns < 4; ++ns) {
-          const int64_t nn = col0 + wave_n * 64 + ns * 16 + (lane & 15);
+        for (int ns = 0; ns < NS; ++ns) {
+          const int64_t nn = col0 + wave_n * WN + ns * 16 + (lane & 15);
           if (nn >= p.n_out) continue;
           const float b = has_bias ? to_f<DT>(bias[int64_t(e) * n + nn]) : 0.0f;
           store_elem<DT>(p, orow + nn, single(p.epi, acc[ms][ns][i], b));

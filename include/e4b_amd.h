@@ -76,7 +76,7 @@ typedef struct e4b_routing {
   int32_t* tiles;       /* [2 * max_tiles] (expert, first sorted row) of each tile_m-row tile */
   int32_t* meta;        /* [4]     num_tiles, num_active, num_dropped, tile_m */
   int32_t max_tiles;    /* capacity of `tiles`: >= ceil(M / tile_m) + min(E, M) */
-  int32_t tile_m;       /* rows per tile (the MFMA path uses 64) */
+  int32_t tile_m;       /* rows per tile (the MFMA path takes 128 or 32) */
   int32_t* scratch;     /* [e4b_route_scratch_ints(M, E)] per-chunk counts of the chunked route
                            (M > 4096); may be NULL when that size is 0 */
 } e4b_routing;
@@ -85,7 +85,8 @@ typedef struct e4b_routing {
 const char* e4b_version(void);
 const char* e4b_last_error(void);
 
-/* Rows per tile the grouped MFMA GEMM expects in e4b_routing.tile_m. */
+/* Rows per tile (128) of the grouped MFMA GEMM for prefill-sized groups; e4b_routing.tile_m
+ * may also be 32, which the GEMM runs with 32-row tiles. */
 int32_t e4b_mfma_tile_m(void);
 
 /* Dequantize experts [expert_begin, expert_begin + expert_count) to a dense row-major

@@ -128,8 +128,8 @@ def test_grouped_gemm_rejects_bad_arguments():
     assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r), 1, 2, N.EPI_GPTOSS, 1.0, 7.0, 0,
                               8192, N.BF16, None) == -1
     assert "bias" in _err()
-    r32 = _rt(tile_m=32)
-    assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r32), 64, 128, N.EPI_NONE, 1.0, 7.0,
+    r64 = _rt(tile_m=64)
+    assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r64), 64, 128, N.EPI_NONE, 1.0, 7.0,
                               N.PATH_MFMA, 8192, N.BF16, None) == -1
     assert "tile_m" in _err()
     assert L.e4b_grouped_gemm(4096, N.BF16, 0, ctypes.byref(s), ctypes.byref(r), 1, 2, N.EPI_NONE, 1.0, 7.0, 0,
