@@ -10,20 +10,23 @@
 //                       routed row's activation chunk is loaded once per job.
 //
 // Critical path of either kernel: one global round trip for the ids (issued together with the
-// code table), a wave-local routing step, then every weight / scale / activation load of the
-// block is issued -- interleaved by chunk, so the dot products can start on the first chunk
-// while later ones are in flight -- before the LDS decode table is built, so building the
-// table overlaps the weight round trip. One __syncthreads separates the table build from its
+// code table and, for down, the router weights the combine uses), a wave-local routing step,
+// then every weight / scale / activation load of the block is issued -- interleaved by chunk,
+// so the dot products can start on the first chunk while later ones are in flight -- before
+// the LDS decode table is built, so building the table overlaps the weight round trip. One __syncthreads separates the table build from its
 // use. Each wave computes the routing itself (one id per lane, a per-wave LDS bitmap of routed
 // experts, one LDS atomic per lane for the row masks), so no block barrier waits on it.
 //
 // Weight decode. A 64 KB LDS table holds, for every byte value b, the two codes the byte
-// encodes as activation-dtype pairs -- hi = dt(code) and lo = dt(code - hi) -- so hi + lo
-// carries the fp32 code to ~16 significant bits; the table is replicated 32 times and a lane
-// reads copy (lane % 32), so the lanes of a wave spread over the banks. A byte's table address
-// is one v_perm_b32 (byte -> bits 8..15, lane copy -> bits 3..7), and each element pair costs
-// one ds_read_b64 plus two v_dot2 (hi, lo) against the packed activation pair as loaded. The
-// block scale multiplies the fp32 sum once per 32 values.
+// encodes as activation-dtype pairs. NF4 codes are split as hi = dt(code) and lo =
+// dt(code - hi), so hi + lo carries the fp32 code to ~16 significant bits (8-byte entries, 32
+// copies, lane l reads copy l % 32); e2m1 codes are exact in either dtype, so MXFP4 keeps hi
+// alone (4-byte entries, 64 copies, lane l reads copy l). Either way a table row is 256 bytes
+// and the lanes of a wave spread over the banks. A byte's table address is one v_perm_b32
+// (byte -> bits 8..15, lane copy offset -> bits 0..7), and each element pair costs one
+// ds_read_b64 plus two v_dot2 (hi, lo) for NF4, one ds_read_b32 plus one v_dot2 for MXFP4,
+// against the packed activation pair as loaded. The block scale multiplies the fp32 sum once
+// per 32 values.
 //
 // Chunk c (16 packed bytes = 32 values) of a row goes to lane gl = c % G of the row's group,
 // as its (c / G)-th chunk. When the row's chunk count is not a multiple of G the spare slots
@@ -40,7 +43,17 @@ constexpr int kDecWaves = kDecThreads / kWave;
 constexpr int kDecMaxRows = kWave;   // tokens * top_k: one routed row per lane
 constexpr int kDecMaxExperts = 256;
 constexpr int kDecExpWords = kDecMaxExperts / 64;
-constexpr int kLutCopies = 32;
+constexpr int kLutRowBytes = 256;  // one table row per byte value: 256 rows, 64 KB
+
+// Table geometry of a weight format: NF4 entries carry (hi, lo) pairs, MXFP4 entries hi alone.
+template <int FMT>
+struct LutGeom {
+  static constexpr bool kSplit = FMT != E4B_FMT_MXFP4;
+  static constexpr int kEntryBytes = kSplit ? 8 : 4;
+  static constexpr int kCopies = kLutRowBytes / kEntryBytes;
+  // byte offset of lane's copy within a row
+  static E4B_DEV uint32_t lane_off(int lane) { return static_cast<uint32_t>(lane % kCopies) * kEntryBytes; }
+};
 constexpr int kDownCols = 4;         // output columns per decode_down block
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -69,6 +82,15 @@ struct DecodeArgs {
   int odt;
   int64_t n_out;
 };
+
+// Router weight of flat row `lane` as fp32 (0 beyond M), loaded beside its id.
+E4B_DEV float load_row_weight(const DecodeArgs& p, int M) {
+  const int lane = threadIdx.x & (kWave - 1);
+  if (lane >= M) return 0.0f;
+  if (p.wdt == E4B_FP32) return static_cast<const float*>(p.topk_w)[lane];
+  const uint16_t b = static_cast<const uint16_t*>(p.topk_w)[lane];
+  return p.wdt == E4B_BF16 ? to_f<E4B_BF16>(b) : to_f<E4B_FP16>(b);
+}
 
 // Per-wave routing state in LDS: the bitmap of routed experts, their ascending list and, for
 // each listed expert, the mask of flat rows routed to it.
@@ -112,10 +134,12 @@ E4B_DEV int wave_route(int id, WaveRoute& r) {
   return n;
 }
 
-// Table entry for byte b: the pair (first, second) element codes, hi and lo parts.
+// Table entry for byte b: the (first, second) element codes as activation-dtype pairs, hi
+// parts in x and lo parts in y (y is zero, and unused, for e2m1 codes).
 template <int DT, int FMT>
 E4B_DEV uint2 pair_entry(float first, float second) {
   const uint16_t h1 = from_f<DT>(first), h2 = from_f<DT>(second);
+  if constexpr (!LutGeom<FMT>::kSplit) return make_uint2(pack2(h1, h2), 0u);
   const uint16_t l1 = from_f<DT>(first - to_f<DT>(h1)), l2 = from_f<DT>(second - to_f<DT>(h2));
   return make_uint2(pack2(h1, h2), pack2(l1, l2));
 }
@@ -134,14 +158,16 @@ E4B_DEV void load_pair_codes(const e4b_qweight& w, float& first, float& second) 
   }
 }
 
-// Thread t writes byte t's entry into all 32 copies, two copies per 16-byte store, rotating the
-// copies with t so the lanes of a wave spread their stores over the banks. Needs 256 threads.
-E4B_DEV void store_pair_entry(uint2* lut, uint2 e) {
+// Thread t fills row t (byte t's entry in every copy) with 16-byte stores, rotating the stores
+// with t so the lanes of a wave spread them over the banks. Needs 256 threads.
+template <int FMT>
+E4B_DEV void store_pair_entry(uint4* lut, uint2 e) {
   const uint32_t b = threadIdx.x;
-  const uint4 v = make_uint4(e.x, e.y, e.x, e.y);
-  uint4* row = reinterpret_cast<uint4*>(lut + b * kLutCopies);
+  const uint4 v = LutGeom<FMT>::kSplit ? make_uint4(e.x, e.y, e.x, e.y) : make_uint4(e.x, e.x, e.x, e.x);
+  constexpr uint32_t kStores = kLutRowBytes / 16;
+  uint4* row = lut + b * kStores;
 #pragma unroll
-  for (uint32_t c = 0; c < kLutCopies / 2; ++c) row[(c + b) & (kLutCopies / 2 - 1)] = v;
+  for (uint32_t c = 0; c < kStores; ++c) row[(c + b) & (kStores - 1)] = v;
 }
 
 // Raw per-chunk scale data (loaded before the table is built), resolved after the barrier.
@@ -186,9 +212,13 @@ E4B_DEV float chunk_dot(const uint4& q, const uint4 (&xq)[4], const char* lut_by
     for (int b = 0; b < 4; ++b) {
       // address = (byte b of the word) << 8 | lane_off
       const uint32_t addr = __builtin_amdgcn_perm(lane_off, qw[wi], 0x0c0c0004u | (static_cast<uint32_t>(b) << 8));
-      const uint2 e = *reinterpret_cast<const uint2*>(lut_bytes + addr);
-      acc = dot2<DT>(e.x, xs[b], acc);
-      if constexpr (FMT != E4B_FMT_MXFP4) acc = dot2<DT>(e.y, xs[b], acc);  // e2m1 codes are exact: lo == 0
+      if constexpr (LutGeom<FMT>::kSplit) {
+        const uint2 e = *reinterpret_cast<const uint2*>(lut_bytes + addr);
+        acc = dot2<DT>(e.x, xs[b], acc);
+        acc = dot2<DT>(e.y, xs[b], acc);
+      } else {
+        acc = dot2<DT>(*reinterpret_cast<const uint32_t*>(lut_bytes + addr), xs[b], acc);
+      }
     }
   }
   return acc;
@@ -237,7 +267,7 @@ E4B_DEV uint4 load_chunk_w(const e4b_qweight& w, int e, int64_t row, int c) {
 // gate_up GEMV + fused epilogue for the a-th routed expert (blockIdx.y), G lanes per column.
 template <int DT, int FMT, int G, int CPL, bool FULL>
 __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
-  __shared__ __align__(16) uint2 lut[256 * kLutCopies];
+  __shared__ __align__(16) uint4 lut[256 * kLutRowBytes / 16];
   __shared__ WaveRoute route[kDecWaves];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
   const int lane = threadIdx.x & (kWave - 1);
@@ -288,10 +318,10 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
   const float off = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
 
   // the decode table, while the weights are in flight
-  store_pair_entry(lut, pair_entry<DT, FMT>(cf, cs));
+  store_pair_entry<FMT>(lut, pair_entry<DT, FMT>(cf, cs));
   __syncthreads();
 
-  uint32_t lane_off = static_cast<uint32_t>(lane % kLutCopies) * 8u;
+  uint32_t lane_off = LutGeom<FMT>::lane_off(lane);
   const char* lut_bytes = reinterpret_cast<const char*>(lut);
   float sa[CPL], sb[CPL];
 #pragma unroll
@@ -337,9 +367,10 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
 // Jobs (one routed expert, all kDownCols columns) go to G-lane groups, JOBS per group in flight.
 template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL>
 __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) {
-  __shared__ __align__(16) uint2 lut[256 * kLutCopies];
+  __shared__ __align__(16) uint4 lut[256 * kLutRowBytes / 16];
   __shared__ WaveRoute route[kDecWaves];
   __shared__ float res[kDecMaxRows * kDownCols];
+  __shared__ float wts[kDecMaxRows];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
   constexpr int C = kDownCols;
   constexpr int kGroups = kDecThreads / G;
@@ -348,13 +379,17 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
   const int M = p.tokens * p.k;
   const e4b_qweight& w = p.w;
 
+  // round trip 1: ids and router weights (for the combine), code pair, code2
   const int id = load_row_id(p, M);
+  const float wt = load_row_weight(p, M);
   float cf, cs;
   load_pair_codes<FMT>(w, cf, cs);
   if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = w.code2[threadIdx.x];
 
   WaveRoute& r = route[wid];
   const int nact = wave_route(id, r);
+  const unsigned long long routed_rows = __ballot(id >= 0);  // the same in every wave
+  if (wid == 0) wts[lane] = wt;  // read after the block barriers below
 
   const int gl = lane % G;
   const int group = threadIdx.x / G;
@@ -363,7 +398,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
   const int64_t col0 = int64_t(blockIdx.x) * C;
   const bool has_bias = w.bias != nullptr;
   const uint16_t* bias = static_cast<const uint16_t*>(w.bias);
-  uint32_t lane_off = static_cast<uint32_t>(lane % kLutCopies) * 8u;
+  uint32_t lane_off = LutGeom<FMT>::lane_off(lane);
   const char* lut_bytes = reinterpret_cast<const char*>(lut);
   int64_t cols[C];
 #pragma unroll
@@ -400,7 +435,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
       }
     }
     if (!table_ready) {
-      store_pair_entry(lut, pair_entry<DT, FMT>(cf, cs));
+      store_pair_entry<FMT>(lut, pair_entry<DT, FMT>(cf, cs));
       __syncthreads();
       table_ready = true;
     }
@@ -460,13 +495,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
     float acc = 0.0f;
     for (int s = 0; s < p.k; ++s) {
       const int f = t * p.k + s;
-      const int64_t v = p.topk[f];
-      if (v < 0 || v >= p.E) continue;
-      float wt;
-      if (p.wdt == E4B_FP32) wt = static_cast<const float*>(p.topk_w)[f];
-      else if (p.wdt == E4B_BF16) wt = to_f<E4B_BF16>(static_cast<const uint16_t*>(p.topk_w)[f]);
-      else wt = to_f<E4B_FP16>(static_cast<const uint16_t*>(p.topk_w)[f]);
-      acc = __fadd_rn(acc, mul_f32(res[f * C + cl], wt));
+      if ((routed_rows >> f) & 1ull) acc = __fadd_rn(acc, mul_f32(res[f * C + cl], wts[f]));
     }
     const int64_t o = int64_t(t) * n + col;
     if (p.odt == E4B_FP32) static_cast<float*>(p.out)[o] = acc;

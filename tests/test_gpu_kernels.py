@@ -324,13 +324,15 @@ def test_combine_bit_exact(wdt, H):
 
 
 def _stack(fmt, E, n, k, seed):
+    """(qweight, the dense weights the decode kernels multiply, fp64 [E, n, k])."""
     if fmt == "mxfp4":
         g = torch.Generator().manual_seed(seed)
         w = torch.randn(E, n, k, generator=g) * 0.05
         b, s = Q.quantize_mxfp4(w)
-        return ops.mxfp4_qweight(b.reshape(E, -1).to(DEV), s.reshape(E, -1).to(DEV), n, k, num_experts=E)
+        qw = ops.mxfp4_qweight(b.reshape(E, -1).to(DEV), s.reshape(E, -1).to(DEV), n, k, num_experts=E)
+        return qw, _dense_from_kernel(qw).astype(np.float64)
     qw, _, _ = _nf4_stack(E, n, k, seed=seed, dq=(fmt == "nf4_dq"))
-    return qw
+    return qw, _dense_from_kernel(qw).astype(np.float64)  # hi + lo table entries carry the fp32 code
 
 
 @pytest.mark.parametrize("fmt", ["nf4", "nf4_dq", "mxfp4"])
@@ -341,15 +343,14 @@ def test_decode_halves_match_oracle(fmt, T):
     T=32 with top-2 over 8 experts fills the 64-row limit with ~8 rows per expert."""
     _announce(f"decode halves fmt={fmt} T={T}")
     E, H, I, top = 8, 768, 320, 2
-    w1 = _stack(fmt, E, 2 * I, H, seed=20)
-    w2 = _stack(fmt, E, H, I, seed=21)
+    w1, W1 = _stack(fmt, E, 2 * I, H, seed=20)
+    w2, W2 = _stack(fmt, E, H, I, seed=21)
     epi, spec = N.EPI_SWIGLU, "swiglu"
     if fmt == "mxfp4":
         g = torch.Generator().manual_seed(22)
         w1.bias = (torch.randn(E, 2 * I, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
         w2.bias = (torch.randn(E, H, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
         epi, spec = N.EPI_GPTOSS, ("gptoss", 1.702, 7.0)
-    W1, W2 = _dense_from_kernel(w1), _dense_from_kernel(w2)
     rng = np.random.default_rng(23 + T)
     idx = np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)
     x = (torch.randn(T, H, generator=torch.Generator().manual_seed(24)) * 2).to(torch.bfloat16)
