@@ -42,7 +42,7 @@ GPTOSS = dict(E=32, H=2880, I=2880, k=4)
 # device copy reads for each in the same runs). Keyed by the kernel it was measured on, so a
 # changed kernel reports null until it is measured again.
 MEASURED_TRAFFIC = {
-    "decode_up_kernel<bf16, nf4, G=16, CPL=4, full>": 19_085_000,
+    "decode_up_kernel<bf16, nf4, G=16, CPL=4, full, gated>": 19_085_000,
 }
 
 
@@ -190,7 +190,7 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
     gu_b, _ = nf4_expert_bytes(cfg["H"], cfg["I"])
     bytes_per_launch = cfg["k"] * gu_b  # 8 distinct routed experts at bs=1
     achieved = bytes_per_launch / (per_launch_us * 1e-6) / 1e9
-    kernel = "decode_up_kernel<bf16, nf4, G=16, CPL=4, full>"
+    kernel = "decode_up_kernel<bf16, nf4, G=16, CPL=4, full, gated>"
     return {
         "bound": "hbm",
         "kernel": kernel + " (routing + gate_up + SwiGLU, bs=1)",

@@ -105,7 +105,7 @@ E4B_DEV float single(int epi, float p, float b) {
   return epi == E4B_EPI_ACT ? silu_f32(p) : p;
 }
 
-E4B_DEV bool is_gated(int epi) {
+__host__ __device__ inline bool is_gated(int epi) {
   return epi == E4B_EPI_SWIGLU || epi == E4B_EPI_CLAMP_SWIGLU || epi == E4B_EPI_GPTOSS;
 }
 

@@ -55,6 +55,7 @@ struct LutGeom {
   static E4B_DEV uint32_t lane_off(int lane) { return static_cast<uint32_t>(lane % kCopies) * kEntryBytes; }
 };
 constexpr int kDownCols = 4;         // output columns per decode_down block
+constexpr int kDecMaxK = 4096;       // longest row the decode kernels take
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
@@ -83,12 +84,21 @@ struct DecodeArgs {
   int64_t n_out;
 };
 
-// Router weight of flat row `lane` as fp32 (0 beyond M), loaded beside its id.
-E4B_DEV float load_row_weight(const DecodeArgs& p, int M) {
+// The first round trip of both kernels loads raw values without branching on them (lanes
+// beyond M read row 0) and decodes them only after every load of the round trip is issued: a
+// value used inside the branch that loads it is waited for on its own, one round trip each.
+
+// Raw router-weight bits of flat row `lane`; row_weight converts them to fp32.
+E4B_DEV uint32_t load_row_weight_bits(const DecodeArgs& p, int M) {
   const int lane = threadIdx.x & (kWave - 1);
-  if (lane >= M) return 0.0f;
-  if (p.wdt == E4B_FP32) return static_cast<const float*>(p.topk_w)[lane];
-  const uint16_t b = static_cast<const uint16_t*>(p.topk_w)[lane];
+  const int f = lane < M ? lane : 0;
+  if (p.wdt == E4B_FP32) return static_cast<const uint32_t*>(p.topk_w)[f];
+  return static_cast<const uint16_t*>(p.topk_w)[f];
+}
+
+E4B_DEV float row_weight(const DecodeArgs& p, uint32_t bits) {
+  if (p.wdt == E4B_FP32) return __uint_as_float(bits);
+  const uint16_t b = static_cast<uint16_t>(bits);
   return p.wdt == E4B_BF16 ? to_f<E4B_BF16>(b) : to_f<E4B_FP16>(b);
 }
 
@@ -100,12 +110,16 @@ struct WaveRoute {
   unsigned long long rows[kDecMaxRows];
 };
 
-// The id of flat row `lane` (-1: beyond M or outside [0, E)).
-E4B_DEV int load_row_id(const DecodeArgs& p, int M) {
+// Raw id of flat row `lane`; row_id validates it.
+E4B_DEV int64_t load_row_id_raw(const DecodeArgs& p, int M) {
   const int lane = threadIdx.x & (kWave - 1);
-  if (lane >= M) return -1;
-  const int64_t v = p.topk[lane];
-  return (v >= 0 && v < p.E) ? static_cast<int>(v) : -1;
+  return p.topk[lane < M ? lane : 0];
+}
+
+// The id of flat row `lane` (-1: beyond M or outside [0, E)).
+E4B_DEV int row_id(const DecodeArgs& p, int M, int64_t v) {
+  const int lane = threadIdx.x & (kWave - 1);
+  return (lane < M && v >= 0 && v < p.E) ? static_cast<int>(v) : -1;
 }
 
 // Wave-local routing: fills r (this wave's copy) and returns the number of routed experts.
@@ -265,9 +279,10 @@ E4B_DEV uint4 load_chunk_w(const e4b_qweight& w, int e, int64_t row, int c) {
 }
 
 // gate_up GEMV + fused epilogue for the a-th routed expert (blockIdx.y), G lanes per column.
-template <int DT, int FMT, int G, int CPL, bool FULL>
+template <int DT, int FMT, int G, int CPL, bool FULL, bool PAIR>
 __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
   __shared__ __align__(16) uint4 lut[256 * kLutRowBytes / 16];
+  __shared__ __align__(16) uint4 xs[kDecMaxK / 8 + 1];  // the activation row being multiplied + a spare slot
   __shared__ WaveRoute route[kDecWaves];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
   const int lane = threadIdx.x & (kWave - 1);
@@ -276,13 +291,13 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
   const e4b_qweight& w = p.w;
 
   // round trip 1: ids, the code pair of this thread's table entry, code2
-  const int id = load_row_id(p, M);
+  const int64_t id_raw = load_row_id_raw(p, M);
   float cf, cs;
   load_pair_codes<FMT>(w, cf, cs);
-  if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = w.code2[threadIdx.x];
+  const float c2 = (FMT == E4B_FMT_NF4_DQ) ? w.code2[threadIdx.x] : 0.0f;
 
   WaveRoute& r = route[wid];
-  const int nact = wave_route(id, r);
+  const int nact = wave_route(row_id(p, M, id_raw), r);
   const int a = blockIdx.y;
   if (a >= nact) return;  // uniform over the block: every wave computed the same routing
   const int e = r.act[a];
@@ -290,35 +305,58 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
 
   const int gl = lane % G;
   const int nchunk = static_cast<int>(w.k / 32);
-  const bool pair = is_gated(p.epi);
+  constexpr bool pair = PAIR;  // gated epilogue: gate row j and up row j + n/2
   const int64_t n = w.n, k = w.k;
   const int64_t j = (int64_t(blockIdx.x) * kDecWaves + wid) * (kWave / G) + lane / G;
   const bool live = j < p.n_out;  // whole G-lane groups share it
   const int64_t row_a = live ? j : 0, row_b = pair ? row_a + n / 2 : row_a;
   int f = __ffsll(static_cast<long long>(rows)) - 1;
-  const uint16_t* xr = p.x + int64_t(f / p.k) * k;
+  const int nx4 = nchunk * 4;  // 16-byte pieces of an activation row
+  // The activation row of the expert's current routed row goes through LDS: thread t loads
+  // 16-byte pieces t and t + 256 (clamped, no branch) and stores the real ones. Loaded before
+  // the weights, so waiting for them leaves the weight loads in flight. (Two named registers,
+  // not an array: an array indexed in an unrolled loop can end up in scratch memory.)
+  static_assert(kDecMaxK / 8 == 2 * kDecThreads, "two 16-byte pieces per thread");
+  const int t0 = static_cast<int>(threadIdx.x), t1 = t0 + kDecThreads;
+  uint4 xp0, xp1;
+  auto load_x = [&](int row) {
+    const uint4* x4 = reinterpret_cast<const uint4*>(p.x + int64_t(row / p.k) * k);
+    xp0 = x4[t0 < nx4 ? t0 : 0];
+    xp1 = x4[t1 < nx4 ? t1 : 0];
+  };
+  auto store_x = [&]() {  // pieces beyond the row go to the spare slot: no branch to sink the loads into
+    xs[t0 < nx4 ? t0 : kDecMaxK / 8] = xp0;
+    xs[t1 < nx4 ? t1 : kDecMaxK / 8] = xp1;
+  };
 
-  // round trip 2: activations, weights and scales, chunk by chunk
-  uint4 qa[CPL], qb[CPL], xv[CPL][4];
+  // round trip 2: the activation row, then weights and scales chunk by chunk, biases
+  load_x(f);
+  uint4 qa[CPL], qb[CPL];
   RawScale ra[CPL], rb[CPL];
   bool valid[CPL];
+  int cidx[CPL];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int c = slot_chunk<G, FULL>(gl, i, nchunk, valid[i]);
-    load_chunk_x(xr, c, xv[i]);
+    cidx[i] = c;
     qa[i] = load_chunk_w(w, e, row_a, c);
-    if (pair) qb[i] = load_chunk_w(w, e, row_b, c);
+    if constexpr (pair) qb[i] = load_chunk_w(w, e, row_b, c);
     ra[i] = load_scale<FMT>(w, e, row_a, c);
-    if (pair) rb[i] = load_scale<FMT>(w, e, row_b, c);
+    if constexpr (pair) rb[i] = load_scale<FMT>(w, e, row_b, c);
   }
+  // biases as raw bits, loaded without a branch (a spare load of x[0] when there is none) and
+  // converted after the loop, so nothing here waits on the loads in flight
   const bool has_bias = w.bias != nullptr;
-  const uint16_t* bias = static_cast<const uint16_t*>(w.bias);
-  const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + row_a]) : 0.0f;
-  const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + row_b]) : 0.0f;
+  const uint16_t* bias = has_bias ? static_cast<const uint16_t*>(w.bias) + int64_t(e) * n : p.x;
+  const uint32_t bg_bits = bias[has_bias ? row_a : 0];
+  const uint32_t bu_bits = bias[has_bias ? row_b : 0];
   const float off = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
 
-  // the decode table, while the weights are in flight
+  // the decode table and the activation row, while the weights are in flight; the chunk loop
+  // then waits for each chunk's weights only
   store_pair_entry<FMT>(lut, pair_entry<DT, FMT>(cf, cs));
+  if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = c2;
+  store_x();
   __syncthreads();
 
   uint32_t lane_off = LutGeom<FMT>::lane_off(lane);
@@ -336,30 +374,38 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
     float acc_a = 0.0f, acc_b = 0.0f;
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
-      const float da = chunk_dot<DT, FMT>(qa[i], xv[i], lut_bytes, lane_off) * sa[i];
+      uint4 xv[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) xv[q] = xs[cidx[i] * 4 + q];
+      const float da = chunk_dot<DT, FMT>(qa[i], xv, lut_bytes, lane_off) * sa[i];
       acc_a += valid[i] ? da : 0.0f;
       __builtin_amdgcn_sched_barrier(0);  // keep each chunk's 16 table reads together
-      if (pair) {
-        const float db = chunk_dot<DT, FMT>(qb[i], xv[i], lut_bytes, lane_off) * sb[i];
+      if constexpr (pair) {
+        const float db = chunk_dot<DT, FMT>(qb[i], xv, lut_bytes, lane_off) * sb[i];
         acc_b += valid[i] ? db : 0.0f;
         __builtin_amdgcn_sched_barrier(0);
       }
     }
     acc_a = group_reduce<G>(acc_a);
-    if (pair) acc_b = group_reduce<G>(acc_b);
+    if constexpr (pair) acc_b = group_reduce<G>(acc_b);
     if (live && gl == 0) {
+      // the empty asm pins the bias conversion here: hoisted above the table barrier it would
+      // wait for every load in flight
+      uint32_t gb = bg_bits, ub = bu_bits;
+      asm volatile("" : "+v"(gb), "+v"(ub));
+      const float bg = has_bias ? to_f<DT>(static_cast<uint16_t>(gb)) : 0.0f;
+      const float bu = has_bias ? to_f<DT>(static_cast<uint16_t>(ub)) : 0.0f;
       const float v = pair ? gated(p.epi, acc_a, acc_b, p.alpha, p.limit, bg, bu) : single(p.epi, acc_a, bg);
       static_cast<uint16_t*>(p.out)[int64_t(f) * p.n_out + j] = from_f<DT>(v);
     }
     rows &= rows - 1;
     if (!rows) break;
+    // next routed row of this expert (the same for the whole block): restage its activations
     f = __ffsll(static_cast<long long>(rows)) - 1;
-    const uint16_t* xn = p.x + int64_t(f / p.k) * k;
-#pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      bool v;
-      load_chunk_x(xn, slot_chunk<G, FULL>(gl, i, nchunk, v), xv[i]);
-    }
+    load_x(f);
+    __syncthreads();  // every wave is done with the current row
+    store_x();
+    __syncthreads();
   }
 }
 
@@ -380,16 +426,16 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
   const e4b_qweight& w = p.w;
 
   // round trip 1: ids and router weights (for the combine), code pair, code2
-  const int id = load_row_id(p, M);
-  const float wt = load_row_weight(p, M);
+  const int64_t id_raw = load_row_id_raw(p, M);
+  const uint32_t wt_bits = load_row_weight_bits(p, M);
   float cf, cs;
   load_pair_codes<FMT>(w, cf, cs);
-  if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = w.code2[threadIdx.x];
+  const float c2 = (FMT == E4B_FMT_NF4_DQ) ? w.code2[threadIdx.x] : 0.0f;
 
   WaveRoute& r = route[wid];
+  const int id = row_id(p, M, id_raw);
   const int nact = wave_route(id, r);
   const unsigned long long routed_rows = __ballot(id >= 0);  // the same in every wave
-  if (wid == 0) wts[lane] = wt;  // read after the block barriers below
 
   const int gl = lane % G;
   const int group = threadIdx.x / G;
@@ -410,6 +456,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
     // column's weight chunk and scale, chunk by chunk
     uint4 q[JOBS][CPL][C], xv[JOBS][CPL][4];
     RawScale rs[JOBS][CPL][C];
+    uint16_t bb[JOBS][C];  // raw bias bits, converted when the job runs
     bool valid[CPL];
     int je[JOBS], jf[JOBS];
     unsigned long long jrows[JOBS];
@@ -433,9 +480,15 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
           }
         }
       }
+      // a spare load of x[0] when there is no bias: no branch on the loaded value
+      const uint16_t* bp = has_bias ? bias + int64_t(e) * n : p.x;
+#pragma unroll
+      for (int cl = 0; cl < C; ++cl) bb[t][cl] = bp[has_bias ? cols[cl] : 0];
     }
     if (!table_ready) {
       store_pair_entry<FMT>(lut, pair_entry<DT, FMT>(cf, cs));
+      if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = c2;
+      if (wid == 0) wts[lane] = row_weight(p, wt_bits);  // read by the combine
       __syncthreads();
       table_ready = true;
     }
@@ -451,7 +504,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
         for (int cl = 0; cl < C; ++cl) sc[i][cl] = valid[i] ? resolve_scale<FMT>(rs[t][i][cl], code2_s, off) : 0.0f;
       }
 #pragma unroll
-      for (int cl = 0; cl < C; ++cl) b[cl] = has_bias ? to_f<DT>(bias[int64_t(e) * n + cols[cl]]) : 0.0f;
+      for (int cl = 0; cl < C; ++cl) b[cl] = has_bias ? to_f<DT>(bb[t][cl]) : 0.0f;
       unsigned long long rows = jrows[t];
       int f = jf[t];
       for (;;) {

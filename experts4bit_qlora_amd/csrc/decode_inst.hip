@@ -19,7 +19,8 @@ template <int DT, int FMT, int G, int CPL, bool FULL>
 void up_gc(const DecodeArgs& a, int64_t max_active, hipStream_t s) {
   constexpr int cols_per_block = kDecWaves * (kWave / G);
   dim3 grid(static_cast<unsigned>((a.n_out + cols_per_block - 1) / cols_per_block), static_cast<unsigned>(max_active));
-  hipLaunchKernelGGL((decode_up_kernel<DT, FMT, G, CPL, FULL>), grid, dim3(kDecThreads), 0, s, a);
+  if (is_gated(a.epi)) hipLaunchKernelGGL((decode_up_kernel<DT, FMT, G, CPL, FULL, true>), grid, dim3(kDecThreads), 0, s, a);
+  else hipLaunchKernelGGL((decode_up_kernel<DT, FMT, G, CPL, FULL, false>), grid, dim3(kDecThreads), 0, s, a);
 }
 
 template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL>
