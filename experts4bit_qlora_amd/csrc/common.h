@@ -65,8 +65,13 @@ E4B_DEV uint32_t pack2(uint16_t lo, uint16_t hi) {
 }
 
 // ------------------------------------------------------------------------------ epilogues
-E4B_DEV float silu_f32(float x) { return x / (1.0f + expf(-x)); }
-E4B_DEV float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
+// sigmoid(x) = 1 / (1 + 2^(-x log2 e)) on the hardware exp2 and reciprocal (each within 1 ulp):
+// a few ulp of fp32 error, far below the bf16 / fp16 rounding every result goes through, for a
+// handful of instructions instead of a correctly rounded expf and an IEEE division.
+E4B_DEV float sigmoid_f32(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
+E4B_DEV float silu_f32(float x) { return x * sigmoid_f32(x); }
 
 // fp32 product rounded to fp32 before any later conversion. The empty asm hides the product
 // from instruction selection, which would otherwise fold a multiply followed by an fp16

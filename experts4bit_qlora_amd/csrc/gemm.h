@@ -33,6 +33,7 @@ namespace e4b {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kTileMBig = 256;   // rows per tile for the full 256-row runs of large experts
 constexpr int kTileM = 128;      // rows per tile of the prefill-sized GEMM
@@ -72,7 +73,7 @@ E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float2* pairs,
 constexpr int gemm_threads(int bm) { return bm >= 256 ? 512 : 256; }
 
 template <int DT, int FMT, int BM>
-__global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p) {
+__global__ void __launch_bounds__(gemm_threads(BM), (BM == 128 ? 2 : 1)) gemm_mfma_kernel(GemmArgs p) {
   constexpr int NT = gemm_threads(BM);
   constexpr int WAVES = NT / kWave;
   constexpr int WAVES_M = BM >= 256 ? 4 : BM >= 128 ? 2 : 1;
@@ -133,8 +134,7 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   const int ar = tid / TPR;
   const int aseg = (tid % TPR) * AV * 8;
   const int r = row0 + ar;
-  const bool avalid = r < row_end;
-  const int64_t src = avalid ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
+  const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
   const uint16_t* aptr = p.a + src * k + aseg;
 
   // W assignment: LDS row tid / TPW (0..127), 2 * WB values of the 64-deep step at
@@ -171,39 +171,33 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
 
   // ---- step registers: kStages sets, step j in set j % kStages, loaded kStages steps before
   // the step that writes it to LDS, so that many global round trips overlap the MFMAs
-  uint4 areg[kStages][AV];
+  // Every load is unconditional: tile rows past the expert's end read row 0, and weight rows
+  // past n_out read weight row 0; both feed only outputs that are never stored. (A load behind
+  // a branch leaves the compiler unsure how many loads are in flight, and it then waits for all
+  // of them, which would cancel the prefetch.) Native vector types keep the sets in registers.
+  u32x4_t areg[kStages][AV];
   uint32_t wq[kStages][WB / 4];
   float sa[kStages];     // NF4 absmax, or double-quant absmax2
   uint32_t sq[kStages];  // double-quant code, or e8m0
   auto load_step = [&](int set, int64_t kb) {
+    const u32x4_t* ap = reinterpret_cast<const u32x4_t*>(aptr + kb * kTileK);
 #pragma unroll
-    for (int i = 0; i < AV; ++i) areg[set][i] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < WB / 4; ++i) wq[set][i] = 0u;
-    sa[set] = 0.0f;
-    sq[set] = 0;
-    if (avalid) {
-      const uint4* ap = reinterpret_cast<const uint4*>(aptr + kb * kTileK);
-#pragma unroll
-      for (int i = 0; i < AV; ++i) areg[set][i] = ap[i];
+    for (int i = 0; i < AV; ++i) areg[set][i] = ap[i];
+    if constexpr (WB == 16) {
+      const uint4 v = *reinterpret_cast<const uint4*>(wptr + kb * 32);
+      wq[set][0] = v.x; wq[set][1] = v.y; wq[set][2] = v.z; wq[set][3] = v.w;
+    } else {
+      const uint2 v = *reinterpret_cast<const uint2*>(wptr + kb * 32);
+      wq[set][0] = v.x; wq[set][1] = v.y;
     }
-    if (wvalid) {
-      if constexpr (WB == 16) {
-        const uint4 v = *reinterpret_cast<const uint4*>(wptr + kb * 32);
-        wq[set][0] = v.x; wq[set][1] = v.y; wq[set][2] = v.z; wq[set][3] = v.w;
-      } else {
-        const uint2 v = *reinterpret_cast<const uint2*>(wptr + kb * 32);
-        wq[set][0] = v.x; wq[set][1] = v.y;
-      }
-      if constexpr (FMT == E4B_FMT_MXFP4) {
-        sq[set] = static_cast<const uint8_t*>(p.w.absmax)[(int64_t(e) * n + grow) * (k / 32) + kb * 2 + half * WB / 16];
-      } else if constexpr (FMT == E4B_FMT_NF4) {
-        sa[set] = static_cast<const float*>(p.w.absmax)[e * nb + grow * (k / 64) + kb];
-      } else {
-        const int64_t blk = grow * (k / 64) + kb;
-        sq[set] = static_cast<const uint8_t*>(p.w.absmax)[e * nb + blk];
-        sa[set] = p.w.absmax2[e * ((nb + 255) / 256) + blk / 256];
-      }
+    if constexpr (FMT == E4B_FMT_MXFP4) {
+      sq[set] = static_cast<const uint8_t*>(p.w.absmax)[(int64_t(e) * n + grow) * (k / 32) + kb * 2 + half * WB / 16];
+    } else if constexpr (FMT == E4B_FMT_NF4) {
+      sa[set] = static_cast<const float*>(p.w.absmax)[e * nb + grow * (k / 64) + kb];
+    } else {
+      const int64_t blk = grow * (k / 64) + kb;
+      sq[set] = static_cast<const uint8_t*>(p.w.absmax)[e * nb + blk];
+      sa[set] = p.w.absmax2[e * ((nb + 255) / 256) + blk / 256];
     }
   };
   auto stage = [&](int set, int buf) {
@@ -216,7 +210,7 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
     uint4* ws = reinterpret_cast<uint4*>(&Ws[buf][lrow * kLdsPitch + half * 2 * WB]);
 #pragma unroll
     for (int i = 0; i < WB / 4; ++i) ws[i] = make_uint4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
-    uint4* as = reinterpret_cast<uint4*>(&As[buf][ar * kLdsPitch + aseg]);
+    u32x4_t* as = reinterpret_cast<u32x4_t*>(&As[buf][ar * kLdsPitch + aseg]);
 #pragma unroll
     for (int i = 0; i < AV; ++i) as[i] = areg[set][i];
   };
@@ -240,29 +234,33 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
     }
   };
 
+  // Step indices past the last step are clamped (a cached re-read nobody uses), for the same
+  // reason the loads carry no conditions.
   const int64_t ksteps = k / kTileK;
+  const int64_t klast = ksteps - 1;
   load_step(0, 0);
   __syncthreads();  // tables
   stage(0, 0);
 #pragma unroll
-  for (int j = 1; j <= kStages; ++j) {
-    if (j < ksteps) load_step(j % kStages, j);
-  }
+  for (int j = 1; j <= kStages; ++j) load_step(j % kStages, min<int64_t>(j, klast));
   __syncthreads();
-  for (int64_t kb0 = 0; kb0 < ksteps; kb0 += kStages) {
+  // step kb: its MFMAs, then stage step kb + 1 (after the last step: a stale set into the idle
+  // buffer, never read) and refill that set with step kb + 1 + kStages
+  auto iteration = [&](int u, int64_t kb) __attribute__((always_inline)) {
+    const int cur = static_cast<int>(kb & 1);
+    mfma_step(cur);
+    stage((u + 1) % kStages, cur ^ 1);
+    load_step((u + 1) % kStages, min<int64_t>(kb + 1 + kStages, klast));
+    __syncthreads();
+  };
+  const int64_t kmain = ksteps - ksteps % kStages;
+  for (int64_t kb0 = 0; kb0 < kmain; kb0 += kStages) {
 #pragma unroll
-    for (int u = 0; u < kStages; ++u) {
-      const int64_t kb = kb0 + u;
-      if (kb < ksteps) {
-        const int cur = static_cast<int>(kb & 1);
-        mfma_step(cur);
-        if (kb + 1 < ksteps) {
-          stage((u + 1) % kStages, cur ^ 1);
-          if (kb + 1 + kStages < ksteps) load_step((u + 1) % kStages, kb + 1 + kStages);
-        }
-        __syncthreads();
-      }
-    }
+    for (int u = 0; u < kStages; ++u) iteration(u, kb0 + u);
+  }
+#pragma unroll
+  for (int u = 0; u < kStages - 1; ++u) {
+    if (kmain + u < ksteps) iteration(u, kmain + u);
   }
 
   // Epilogue: lane holds D[4*(lane/16) + i][lane % 16] of each 16x16 sub-tile.
