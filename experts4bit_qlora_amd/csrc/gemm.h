@@ -15,7 +15,8 @@
 //   * after the MFMAs, step s+1's registers are written to the other LDS buffer: activations as
 //     loaded, weights decoded with ONE fp32 product code[nib] * scale and one RNE rounding --
 //     bit-identical to the reference's dequantized bf16 (fp16) weight. Codes come from a
-//     256-entry LDS table of (first, second) fp32 code pairs, one entry per packed byte;
+//     16-entry fp32 LDS table indexed by nibble: its 16 words sit in 16 different banks, so a
+//     lookup never conflicts (lanes reading the same word share one broadcast);
 //   * one barrier per step. Each wave runs (BM / WAVES_M / 16) x (128 / WAVES_N / 16)
 //     v_mfma_f32_16x16x32_{bf16,f16} per 32-deep half step with fp32 accumulators.
 // Gated epilogues pair gate row j with up row n/2 + j in the same tile: LDS rows 0..63 hold
@@ -55,16 +56,46 @@ E4B_DEV f32x4_t mfma_16x16x32(const uint4& a, const uint4& b, const f32x4_t& c) 
   }
 }
 
-// NB packed bytes (2 * NB values) -> NB words of DT pairs, each value dt(fp32(code * scale)),
-// codes from the 256-entry LDS table of (first, second) fp32 code pairs.
-template <int DT, int NB>
-E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float2* pairs, float scale, uint32_t (&wv)[NB]) {
+// Two fp32 values rounded to nearest even into one packed DT pair (first in the low half):
+// one v_cvt_pk_{bf16,f16}_f32.
+template <int DT>
+E4B_DEV uint32_t cvt_pair(float a, float b) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  const f2_t v = {a, b};
+  if constexpr (DT == E4B_BF16) {
+    typedef __bf16 o2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, o2_t));
+  } else {
+    typedef _Float16 o2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, o2_t));
+  }
+}
+
+// fp32 product code * scale. For fp16 the product is kept away from the conversion (mul_f32),
+// which instruction selection could otherwise fuse into one rounding of the exact product.
+template <int DT>
+E4B_DEV float code_times_scale(float c, float s) {
+  if constexpr (DT == E4B_FP16) return mul_f32(c, s);
+  else return c * s;
+}
+
+// NB packed bytes (2 * NB values; byte i = elements 2i and 2i + 1, the first in the high nibble
+// for NF4, in the low one for e2m1) -> NB words of DT pairs, each value dt(fp32(code * scale)).
+// Table offsets are nibble * 4: bits 2..5 of byte b of (w << 2) hold its low nibble, of (w >> 2)
+// its high one.
+template <int DT, int FMT, int NB>
+E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float* code16, float scale, uint32_t (&wv)[NB]) {
+  const char* tb = reinterpret_cast<const char*>(code16);
 #pragma unroll
   for (int wi = 0; wi < NB / 4; ++wi) {
+    const uint32_t wl = words[wi] << 2, wh = words[wi] >> 2;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const float2 c = pairs[(words[wi] >> (8 * b)) & 0xffu];
-      wv[4 * wi + b] = pack2(from_f<DT>(mul_f32(c.x, scale)), from_f<DT>(mul_f32(c.y, scale)));
+      const float c_lo = *reinterpret_cast<const float*>(tb + ((wl >> (8 * b)) & 0x3cu));
+      const float c_hi = *reinterpret_cast<const float*>(tb + ((wh >> (8 * b)) & 0x3cu));
+      const float first = (FMT == E4B_FMT_MXFP4) ? c_lo : c_hi;
+      const float second = (FMT == E4B_FMT_MXFP4) ? c_hi : c_lo;
+      wv[4 * wi + b] = cvt_pair<DT>(code_times_scale<DT>(first, scale), code_times_scale<DT>(second, scale));
     }
   }
 }
@@ -88,7 +119,7 @@ __global__ void __launch_bounds__(gemm_threads(BM), (BM == 128 ? 2 : 1)) gemm_mf
   static_assert(AV >= 1 && NS % 2 == 0 && (WB == 16 || WB == 8), "tile shape");
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLdsPitch];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][kTileNW * kLdsPitch];
-  __shared__ float2 pairs[256];
+  __shared__ float code16[16];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
 
   // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so linear
@@ -120,14 +151,10 @@ __global__ void __launch_bounds__(gemm_threads(BM), (BM == 128 ? 2 : 1)) gemm_mf
   const int64_t col0 = int64_t(n_tile) * (pair ? kTileNW / 2 : kTileNW);
   if (col0 >= p.n_out) return;
 
-  if (tid < 256) {  // decode tables: byte -> (first, second) codes; the second-level code
-    const uint32_t b = static_cast<uint32_t>(tid);
-    if constexpr (FMT == E4B_FMT_MXFP4) {
-      pairs[b] = make_float2(kFp4E2M1[b & 0xfu], kFp4E2M1[b >> 4]);
-    } else {
-      pairs[b] = make_float2(p.w.code[b >> 4], p.w.code[b & 0xfu]);
-    }
-    if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[tid] = p.w.code2[tid];
+  // decode tables: the 16 codes, and the second-level code of double quantization
+  if (tid < 16) code16[tid] = (FMT == E4B_FMT_MXFP4) ? kFp4E2M1[tid] : p.w.code[tid];
+  if constexpr (FMT == E4B_FMT_NF4_DQ) {
+    if (tid < 256) code2_s[tid] = p.w.code2[tid];
   }
 
   // A assignment: row tid / TPR, AV * 8 activations at column (tid % TPR) * AV * 8.
@@ -206,7 +233,7 @@ __global__ void __launch_bounds__(gemm_threads(BM), (BM == 128 ? 2 : 1)) gemm_mf
     else if constexpr (FMT == E4B_FMT_NF4) scale = sa[set];
     else scale = wvalid ? __fadd_rn(mul_f32(code2_s[sq[set]], sa[set]), offset) : 0.0f;
     uint32_t wv[WB];
-    dequant_bytes<DT, WB>(wq[set], pairs, scale, wv);
+    dequant_bytes<DT, FMT, WB>(wq[set], code16, scale, wv);
     uint4* ws = reinterpret_cast<uint4*>(&Ws[buf][lrow * kLdsPitch + half * 2 * WB]);
 #pragma unroll
     for (int i = 0; i < WB / 4; ++i) ws[i] = make_uint4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
