@@ -128,7 +128,8 @@ void launch_gemv_fmt(const e4b::GemmArgs& a, int64_t max_active, hipStream_t s) 
 template <int DT, int FMT>
 void launch_mfma_fmt(const e4b::GemmArgs& a, hipStream_t s) {
   const bool pair = a.epi == E4B_EPI_SWIGLU || a.epi == E4B_EPI_CLAMP_SWIGLU || a.epi == E4B_EPI_GPTOSS;
-  const int64_t cols = pair ? e4b::kTileNW / 2 : e4b::kTileNW;
+  const int64_t nw = e4b::gemm_tile_nw(a.rt.tile_m);
+  const int64_t cols = pair ? nw / 2 : nw;
   // 8 XCDs x ceil(max_tiles / 8) M tiles x n_tiles blocks, mapped to tiles in the kernel
   const int64_t n_tiles = cdiv(a.n_out, cols);
   dim3 grid(static_cast<unsigned>(e4b::kXcds * cdiv(a.rt.max_tiles, e4b::kXcds) * n_tiles));

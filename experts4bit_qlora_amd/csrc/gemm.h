@@ -1,9 +1,10 @@
 // Prefill / large-batch grouped GEMM on the bf16 (fp16) matrix cores of gfx950.
 //
-// One workgroup computes a BM-row x 128-weight-row tile of one expert: BM = 256 (8 waves) for
-// the full 256-row runs of large experts, 128 (4 waves) for prefill-sized groups, 32 (4 waves)
-// for mid-size batches where experts get few rows. Every dequantized weight feeds BM rows, so
-// the decode work per MFMA falls as BM grows. Tiles come from
+// One workgroup computes a BM-row x BN-weight-row tile of one expert: 128 x 256 (8 waves) for
+// prefill-sized groups, 32 x 128 (4 waves) for mid-size batches where experts get few rows,
+// 256 x 128 (8 waves) for full 256-row runs. Every dequantized weight feeds BM rows, so the
+// decode work per MFMA falls as BM grows, and every activation tile feeds BN weight rows: its
+// global (L2) reads repeat once per N tile, so the prefill tile is wide. Tiles come from
 // the route kernel's (expert, first sorted row) list, so skewed expert sizes cost at most one
 // partial tile per expert and the grid never depends on host-side counts.
 //
@@ -19,8 +20,8 @@
 //     lookup never conflicts (lanes reading the same word share one broadcast);
 //   * one barrier per step. Each wave runs (BM / WAVES_M / 16) x (128 / WAVES_N / 16)
 //     v_mfma_f32_16x16x32_{bf16,f16} per 32-deep half step with fp32 accumulators.
-// Gated epilogues pair gate row j with up row n/2 + j in the same tile: LDS rows 0..63 hold
-// the gate rows of 64 output columns and rows 64..127 their up rows, and a wave's gate and up
+// Gated epilogues pair gate row j with up row n/2 + j in the same tile: LDS rows 0..BN/2-1 hold
+// the gate rows of BN/2 output columns and rows BN/2..BN-1 their up rows, and a wave's gate and up
 // accumulators sit in the same lanes, so the activation runs on registers (fp32) before the
 // only store.
 #pragma once
@@ -39,7 +40,8 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int kTileMBig = 256;   // rows per tile for the full 256-row runs of large experts
 constexpr int kTileM = 128;      // rows per tile of the prefill-sized GEMM
 constexpr int kTileMSmall = 32;  // rows per tile for mid-size batches
-constexpr int kTileNW = 128;     // weight rows per tile
+constexpr int kTileNW = 128;     // weight rows per tile of the 32- and 256-row shapes
+constexpr int kTileNWWide = 256; // weight rows per tile of the 128-row (prefill) shape
 constexpr int kTileK = 64;
 constexpr int kLdsPitch = kTileK + 8;  // elements; 144-byte rows keep 16-byte alignment
 constexpr int kStages = 3;  // K steps of global loads in flight ahead of the MFMAs
@@ -100,25 +102,27 @@ E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float* code16,
   }
 }
 
-// Threads of the tile shape: 8 waves for 256-row tiles, else 4.
-constexpr int gemm_threads(int bm) { return bm >= 256 ? 512 : 256; }
+// Tile shapes: weight rows per tile and threads (8 waves for the 128- and 256-row tiles, else 4).
+constexpr int gemm_tile_nw(int bm) { return bm == kTileM ? kTileNWWide : kTileNW; }
+constexpr int gemm_threads(int bm) { return bm >= kTileM ? 512 : 256; }
 
 template <int DT, int FMT, int BM>
-__global__ void __launch_bounds__(gemm_threads(BM), (BM == 128 ? 2 : 1)) gemm_mfma_kernel(GemmArgs p) {
+__global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p) {
   constexpr int NT = gemm_threads(BM);
+  constexpr int BN = gemm_tile_nw(BM);
   constexpr int WAVES = NT / kWave;
   constexpr int WAVES_M = BM >= 256 ? 4 : BM >= 128 ? 2 : 1;
   constexpr int WAVES_N = WAVES / WAVES_M;
   constexpr int WM = BM / WAVES_M;       // rows per wave
-  constexpr int WN = kTileNW / WAVES_N;  // weight rows per wave
+  constexpr int WN = BN / WAVES_N;       // weight rows per wave
   constexpr int MS = WM / 16, NS = WN / 16;
   constexpr int TPR = NT / BM;            // threads per A row
   constexpr int AV = kTileK / TPR / 8;    // uint4 of A per thread per step
-  constexpr int TPW = NT / kTileNW;       // threads per weight row
+  constexpr int TPW = NT / BN;            // threads per weight row
   constexpr int WB = kTileK / 2 / TPW;    // packed weight bytes per thread per step
   static_assert(AV >= 1 && NS % 2 == 0 && (WB == 16 || WB == 8), "tile shape");
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLdsPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][kTileNW * kLdsPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kLdsPitch];
   __shared__ float code16[16];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
 
@@ -128,8 +132,8 @@ __global__ void __launch_bounds__(gemm_threads(BM), (BM == 128 ? 2 : 1)) gemm_mf
   // activation tile stays in that XCD's L2 across the N sweep, and an expert's consecutive M
   // tiles (same weights) stay on one XCD as well.
   const int num_tiles = p.rt.meta[0];
-  const int n_tiles = static_cast<int>((p.n_out + (is_gated(p.epi) ? kTileNW / 2 : kTileNW) - 1) /
-                                       (is_gated(p.epi) ? kTileNW / 2 : kTileNW));
+  const int n_tiles = static_cast<int>((p.n_out + (is_gated(p.epi) ? BN / 2 : BN) - 1) /
+                                       (is_gated(p.epi) ? BN / 2 : BN));
   const int xcd = static_cast<int>(blockIdx.x % kXcds);
   const int q = static_cast<int>(blockIdx.x / kXcds);
   const int chunk = (num_tiles + kXcds - 1) / kXcds;
@@ -148,7 +152,7 @@ __global__ void __launch_bounds__(gemm_threads(BM), (BM == 128 ? 2 : 1)) gemm_mf
   const bool pair = is_gated(p.epi);
   const int64_t n = p.w.n;
   const int64_t k = p.w.k;
-  const int64_t col0 = int64_t(n_tile) * (pair ? kTileNW / 2 : kTileNW);
+  const int64_t col0 = int64_t(n_tile) * (pair ? BN / 2 : BN);
   if (col0 >= p.n_out) return;
 
   // decode tables: the 16 codes, and the second-level code of double quantization
@@ -164,16 +168,16 @@ __global__ void __launch_bounds__(gemm_threads(BM), (BM == 128 ? 2 : 1)) gemm_mf
   const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
   const uint16_t* aptr = p.a + src * k + aseg;
 
-  // W assignment: LDS row tid / TPW (0..127), 2 * WB values of the 64-deep step at
+  // W assignment: LDS row tid / TPW (0..BN-1), 2 * WB values of the 64-deep step at
   // (tid % TPW) * 2 * WB.
   const int lrow = tid / TPW;
   const int half = tid % TPW;  // which WB-byte part of the row's 32 packed bytes
   int64_t grow;
   bool wvalid;
   if (pair) {
-    const int64_t jj = col0 + (lrow & 63);
+    const int64_t jj = col0 + (lrow & (BN / 2 - 1));
     wvalid = jj < p.n_out;
-    grow = (lrow < 64) ? jj : n / 2 + jj;
+    grow = (lrow < BN / 2) ? jj : n / 2 + jj;
   } else {
     grow = col0 + lrow;
     wvalid = grow < p.n_out;
@@ -192,7 +196,7 @@ __global__ void __launch_bounds__(gemm_threads(BM), (BM == 128 ? 2 : 1)) gemm_mf
   int nbase[NS];
 #pragma unroll
   for (int ns = 0; ns < NS; ++ns) {
-    nbase[ns] = pair ? ((ns < NS / 2) ? wave_n * (WN / 2) + ns * 16 : 64 + wave_n * (WN / 2) + (ns - NS / 2) * 16)
+    nbase[ns] = pair ? ((ns < NS / 2) ? wave_n * (WN / 2) + ns * 16 : BN / 2 + wave_n * (WN / 2) + (ns - NS / 2) * 16)
                      : wave_n * WN + ns * 16;
   }
 
@@ -228,10 +232,19 @@ __global__ void __launch_bounds__(gemm_threads(BM), (BM == 128 ? 2 : 1)) gemm_mf
     }
   };
   auto stage = [&](int set, int buf) {
+    // weight rows past n_out hold row 0's bytes and feed only columns that are never stored, so
+    // their scale needs no condition (a select here becomes a branch that splits the schedule)
     float scale;
-    if constexpr (FMT == E4B_FMT_MXFP4) scale = wvalid ? e8m0_to_f32(sq[set]) : 0.0f;
-    else if constexpr (FMT == E4B_FMT_NF4) scale = sa[set];
-    else scale = wvalid ? __fadd_rn(mul_f32(code2_s[sq[set]], sa[set]), offset) : 0.0f;
+    if constexpr (FMT == E4B_FMT_MXFP4) {
+      scale = e8m0_to_f32(sq[set]);
+    } else if constexpr (FMT == E4B_FMT_NF4) {
+      scale = sa[set];
+    } else {
+      // fp32(fp32(code2 * absmax2) + offset): plain operators, two roundings (no contraction
+      // under -ffp-contract=off); an asm fence or constrained intrinsic would split the schedule
+      const float prod = code2_s[sq[set]] * sa[set];
+      scale = prod + offset;
+    }
     uint32_t wv[WB];
     dequant_bytes<DT, FMT, WB>(wq[set], code16, scale, wv);
     uint4* ws = reinterpret_cast<uint4*>(&Ws[buf][lrow * kLdsPitch + half * 2 * WB]);
@@ -273,10 +286,20 @@ __global__ void __launch_bounds__(gemm_threads(BM), (BM == 128 ? 2 : 1)) gemm_mf
   __syncthreads();
   // step kb: its MFMAs, then stage step kb + 1 (after the last step: a stale set into the idle
   // buffer, never read) and refill that set with step kb + 1 + kStages
+  // The MFMAs of step kb and the decode / staging of step kb + 1 form one scheduling block;
+  // the group barriers slot the decode's LDS reads and VALU work between MFMAs that are still
+  // executing. (Left to itself the compiler emits them one after the other, and the per-step
+  // block barrier then keeps every wave of a SIMD in the same phase, so nothing overlaps.)
   auto iteration = [&](int u, int64_t kb) __attribute__((always_inline)) {
     const int cur = static_cast<int>(kb & 1);
     mfma_step(cur);
     stage((u + 1) % kStages, cur ^ 1);
+#pragma unroll
+    for (int i = 0; i < 2 * MS * NS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two LDS reads
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+    }
     load_step((u + 1) % kStages, min<int64_t>(kb + 1 + kStages, klast));
     __syncthreads();
   };
