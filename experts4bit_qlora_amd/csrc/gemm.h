@@ -9,9 +9,9 @@
 // partial tile per expert and the grid never depends on host-side counts.
 //
 // Pipeline, per 64-deep K step (one NF4 absmax block per weight row):
-//   * global -> registers runs kStages steps ahead (A rows gathered through sorted_flat when
+//   * global -> registers runs ST steps ahead (A rows gathered through sorted_flat when
 //     gather_k > 0, the index_select of fast.py:135 fused into the loads; 16 packed bytes +
-//     the scale of each weight half-row), in kStages rotating register sets, so several
+//     the scale of each weight half-row), in ST rotating register sets, so several
 //     global round trips overlap the MFMAs of step s, which read LDS buffer s % 2;
 //   * after the MFMAs, step s+1's registers are written to the other LDS buffer: activations as
 //     loaded, weights decoded with ONE fp32 product code[nib] * scale and one RNE rounding --
@@ -44,7 +44,9 @@ constexpr int kTileNW = 128;     // weight rows per tile of the 32- and 256-row 
 constexpr int kTileNWWide = 256; // weight rows per tile of the 128-row (prefill) shape
 constexpr int kTileK = 64;
 constexpr int kLdsPitch = kTileK + 8;  // elements; 144-byte rows keep 16-byte alignment
-constexpr int kStages = 3;  // K steps of global loads in flight ahead of the MFMAs
+// K steps of global loads in flight ahead of the MFMAs (6 for the 32-row tiles was measured:
+// no change at bs=64, whose blocks are bound by their decode and LDS work, not by latency)
+constexpr int gemm_stages(int) { return 3; }
 constexpr int kXcds = 8;    // accelerator dies of an MI355X; blocks go round-robin over them
 
 template <int DT>
@@ -121,6 +123,7 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   constexpr int TPW = NT / BN;            // threads per weight row
   constexpr int WB = kTileK / 2 / TPW;    // packed weight bytes per thread per step
   static_assert(AV >= 1 && NS % 2 == 0 && (WB == 16 || WB == 8), "tile shape");
+  constexpr int ST = gemm_stages(BM);
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLdsPitch];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kLdsPitch];
   __shared__ float code16[16];
@@ -200,16 +203,16 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
                      : wave_n * WN + ns * 16;
   }
 
-  // ---- step registers: kStages sets, step j in set j % kStages, loaded kStages steps before
+  // ---- step registers: ST sets, step j in set j % ST, loaded ST steps before
   // the step that writes it to LDS, so that many global round trips overlap the MFMAs
   // Every load is unconditional: tile rows past the expert's end read row 0, and weight rows
   // past n_out read weight row 0; both feed only outputs that are never stored. (A load behind
   // a branch leaves the compiler unsure how many loads are in flight, and it then waits for all
   // of them, which would cancel the prefetch.) Native vector types keep the sets in registers.
-  u32x4_t areg[kStages][AV];
-  uint32_t wq[kStages][WB / 4];
-  float sa[kStages];     // NF4 absmax, or double-quant absmax2
-  uint32_t sq[kStages];  // double-quant code, or e8m0
+  u32x4_t areg[ST][AV];
+  uint32_t wq[ST][WB / 4];
+  float sa[ST];     // NF4 absmax, or double-quant absmax2
+  uint32_t sq[ST];  // double-quant code, or e8m0
   auto load_step = [&](int set, int64_t kb) {
     const u32x4_t* ap = reinterpret_cast<const u32x4_t*>(aptr + kb * kTileK);
 #pragma unroll
@@ -282,10 +285,10 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   __syncthreads();  // tables
   stage(0, 0);
 #pragma unroll
-  for (int j = 1; j <= kStages; ++j) load_step(j % kStages, min<int64_t>(j, klast));
+  for (int j = 1; j <= ST; ++j) load_step(j % ST, min<int64_t>(j, klast));
   __syncthreads();
   // step kb: its MFMAs, then stage step kb + 1 (after the last step: a stale set into the idle
-  // buffer, never read) and refill that set with step kb + 1 + kStages
+  // buffer, never read) and refill that set with step kb + 1 + ST
   // The MFMAs of step kb and the decode / staging of step kb + 1 form one scheduling block;
   // the group barriers slot the decode's LDS reads and VALU work between MFMAs that are still
   // executing. (Left to itself the compiler emits them one after the other, and the per-step
@@ -293,23 +296,23 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   auto iteration = [&](int u, int64_t kb) __attribute__((always_inline)) {
     const int cur = static_cast<int>(kb & 1);
     mfma_step(cur);
-    stage((u + 1) % kStages, cur ^ 1);
+    stage((u + 1) % ST, cur ^ 1);
 #pragma unroll
     for (int i = 0; i < 2 * MS * NS; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two LDS reads
       __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
     }
-    load_step((u + 1) % kStages, min<int64_t>(kb + 1 + kStages, klast));
+    load_step((u + 1) % ST, min<int64_t>(kb + 1 + ST, klast));
     __syncthreads();
   };
-  const int64_t kmain = ksteps - ksteps % kStages;
-  for (int64_t kb0 = 0; kb0 < kmain; kb0 += kStages) {
+  const int64_t kmain = ksteps - ksteps % ST;
+  for (int64_t kb0 = 0; kb0 < kmain; kb0 += ST) {
 #pragma unroll
-    for (int u = 0; u < kStages; ++u) iteration(u, kb0 + u);
+    for (int u = 0; u < ST; ++u) iteration(u, kb0 + u);
   }
 #pragma unroll
-  for (int u = 0; u < kStages - 1; ++u) {
+  for (int u = 0; u < ST - 1; ++u) {
     if (kmain + u < ksteps) iteration(u, kmain + u);
   }
 
