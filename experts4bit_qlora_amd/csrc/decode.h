@@ -12,21 +12,32 @@
 // Critical path of either kernel: one global round trip for the ids (issued together with the
 // code table and, for down, the router weights the combine uses), a wave-local routing step,
 // then every weight / scale / activation load of the block is issued -- interleaved by chunk,
-// so the dot products can start on the first chunk while later ones are in flight -- before
-// the LDS decode table is built, so building the table overlaps the weight round trip. One __syncthreads separates the table build from its
-// use. Each wave computes the routing itself (one id per lane, a per-wave LDS bitmap of routed
-// experts, one LDS atomic per lane for the row masks), so no block barrier waits on it.
+// so the dot products can start on the first chunk while later ones are in flight. The LDS
+// decode table is written around that issue (before it in the up kernel, after it in the down
+// kernel, whichever measured faster), and one __syncthreads separates the table build from
+// its use. Each wave computes the routing itself (one id per lane, a per-wave LDS bitmap of
+// routed experts, one LDS atomic per lane for the row masks), so no block barrier waits on it.
 //
 // Weight decode. A 64 KB LDS table holds, for every byte value b, the two codes the byte
-// encodes as activation-dtype pairs. NF4 codes are split as hi = dt(code) and lo =
-// dt(code - hi), so hi + lo carries the fp32 code to ~16 significant bits (8-byte entries, 32
-// copies, lane l reads copy l % 32); e2m1 codes are exact in either dtype, so MXFP4 keeps hi
-// alone (4-byte entries, 64 copies, lane l reads copy l). Either way a table row is 256 bytes
-// and the lanes of a wave spread over the banks. A byte's table address is one v_perm_b32
-// (byte -> bits 8..15, lane copy offset -> bits 0..7), and each element pair costs one
-// ds_read_b64 plus two v_dot2 (hi, lo) for NF4, one ds_read_b32 plus one v_dot2 for MXFP4,
-// against the packed activation pair as loaded. The block scale multiplies the fp32 sum once
-// per 32 values.
+// encodes, one 256-byte row per byte value, in one of two forms:
+//   single  one 4-byte entry (two 16-bit codes), 64 copies, lane l reads copy l: e2m1 codes in
+//           the activation dtype (exact in either), and, in the up kernel, NF4 codes in fp16.
+//   split   NF4 codes as activation-dtype pairs hi = dt(code), lo = dt(code - hi), so hi + lo
+//           carries the fp32 code to ~16 significant bits (8-byte entries, 32 copies, lane l
+//           reads copy l % 32): the down kernel, whose activations are read straight from
+//           global memory in the activation dtype.
+// A byte's table address is one v_perm_b32 (byte -> bits 8..15, lane copy offset -> bits
+// 0..7); an element pair then costs one ds_read_b32 and one v_dot2 (single) or one ds_read_b64
+// and two v_dot2 (split) against the packed activation pair. The block scale multiplies the
+// fp32 sum once per 32 values.
+//
+// fp16 NF4 codes (up kernel). An fp16 code is within 2^-11 relative of the fp32 code and an
+// fp16 x fp16 product is exact in fp32, so the only new error is that rounding of the code --
+// 8x below a bf16 code's and far below the rounding of h itself. bf16 activations are restaged
+// through LDS as fp16 scaled by a power of two per 32-value chunk (the chunk maximum lands in
+// [2^14, 2^15)): bf16's 8 significant bits fit fp16's 11, so every element at least 2^-28 of
+// its chunk's maximum converts exactly, and the chunk's dot product is scaled back once. Against
+// the split bf16 table this removes one of the two v_dot2 per byte and halves the table read.
 //
 // Chunk c (16 packed bytes = 32 values) of a row goes to lane gl = c % G of the row's group,
 // as its (c / G)-th chunk. When the row's chunk count is not a multiple of G the spare slots
@@ -45,11 +56,10 @@ constexpr int kDecMaxExperts = 256;
 constexpr int kDecExpWords = kDecMaxExperts / 64;
 constexpr int kLutRowBytes = 256;  // one table row per byte value: 256 rows, 64 KB
 
-// Table geometry of a weight format: NF4 entries carry (hi, lo) pairs, MXFP4 entries hi alone.
-template <int FMT>
+// Table geometry: split entries carry (hi, lo) pairs, single entries the codes alone.
+template <bool SPLIT>
 struct LutGeom {
-  static constexpr bool kSplit = FMT != E4B_FMT_MXFP4;
-  static constexpr int kEntryBytes = kSplit ? 8 : 4;
+  static constexpr int kEntryBytes = SPLIT ? 8 : 4;
   static constexpr int kCopies = kLutRowBytes / kEntryBytes;
   // byte offset of lane's copy within a row
   static E4B_DEV uint32_t lane_off(int lane) { return static_cast<uint32_t>(lane % kCopies) * kEntryBytes; }
@@ -148,12 +158,12 @@ E4B_DEV int wave_route(int id, WaveRoute& r) {
   return n;
 }
 
-// Table entry for byte b: the (first, second) element codes as activation-dtype pairs, hi
-// parts in x and lo parts in y (y is zero, and unused, for e2m1 codes).
-template <int DT, int FMT>
+// Table entry for byte b: the (first, second) element codes as 16-bit pairs in dtype DT, hi
+// parts in x and lo parts in y (y is zero, and unused, for single entries).
+template <int DT, bool SPLIT>
 E4B_DEV uint2 pair_entry(float first, float second) {
   const uint16_t h1 = from_f<DT>(first), h2 = from_f<DT>(second);
-  if constexpr (!LutGeom<FMT>::kSplit) return make_uint2(pack2(h1, h2), 0u);
+  if constexpr (!SPLIT) return make_uint2(pack2(h1, h2), 0u);
   const uint16_t l1 = from_f<DT>(first - to_f<DT>(h1)), l2 = from_f<DT>(second - to_f<DT>(h2));
   return make_uint2(pack2(h1, h2), pack2(l1, l2));
 }
@@ -174,10 +184,10 @@ E4B_DEV void load_pair_codes(const e4b_qweight& w, float& first, float& second) 
 
 // Thread t fills row t (byte t's entry in every copy) with 16-byte stores, rotating the stores
 // with t so the lanes of a wave spread them over the banks. Needs 256 threads.
-template <int FMT>
+template <bool SPLIT>
 E4B_DEV void store_pair_entry(uint4* lut, uint2 e) {
   const uint32_t b = threadIdx.x;
-  const uint4 v = LutGeom<FMT>::kSplit ? make_uint4(e.x, e.y, e.x, e.y) : make_uint4(e.x, e.x, e.x, e.x);
+  const uint4 v = SPLIT ? make_uint4(e.x, e.y, e.x, e.y) : make_uint4(e.x, e.x, e.x, e.x);
   constexpr uint32_t kStores = kLutRowBytes / 16;
   uint4* row = lut + b * kStores;
 #pragma unroll
@@ -214,8 +224,9 @@ E4B_DEV float resolve_scale(const RawScale& s, const float* code2_s, float offse
   else return __fadd_rn(mul_f32(code2_s[s.q], s.a), offset);
 }
 
-// sum over one 16-byte chunk (32 values) of code * x, unscaled, fp32.
-template <int DT, int FMT>
+// sum over one 16-byte chunk (32 values) of code * x, unscaled, fp32; table entries and x pairs
+// in dtype DT.
+template <int DT, bool SPLIT>
 E4B_DEV float chunk_dot(const uint4& q, const uint4 (&xq)[4], const char* lut_bytes, uint32_t lane_off) {
   const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
   float acc = 0.0f;
@@ -226,7 +237,7 @@ E4B_DEV float chunk_dot(const uint4& q, const uint4 (&xq)[4], const char* lut_by
     for (int b = 0; b < 4; ++b) {
       // address = (byte b of the word) << 8 | lane_off
       const uint32_t addr = __builtin_amdgcn_perm(lane_off, qw[wi], 0x0c0c0004u | (static_cast<uint32_t>(b) << 8));
-      if constexpr (LutGeom<FMT>::kSplit) {
+      if constexpr (SPLIT) {
         const uint2 e = *reinterpret_cast<const uint2*>(lut_bytes + addr);
         acc = dot2<DT>(e.x, xs[b], acc);
         acc = dot2<DT>(e.y, xs[b], acc);
@@ -236,6 +247,37 @@ E4B_DEV float chunk_dot(const uint4& q, const uint4 (&xq)[4], const char* lut_by
     }
   }
   return acc;
+}
+
+// bf16 -> scaled fp16 restaging of activations (up kernel, NF4 weights).
+// Largest biased exponent among the 8 bf16 values of a 16-byte piece, in bits 7..14.
+E4B_DEV uint32_t bf16_exp_max(const uint4& v) {
+  auto m2 = [](uint32_t w) { return max(w & 0x7f80u, (w >> 16) & 0x7f80u); };
+  return max(max(m2(v.x), m2(v.y)), max(m2(v.z), m2(v.w)));
+}
+
+// Maximum over the aligned quad of lanes (the four pieces of one 32-value chunk).
+E4B_DEV uint32_t quad_max(uint32_t v) {
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xb1, 0xf, 0xf, false)));
+  v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0x4e, 0xf, 0xf, false)));
+  return v;
+}
+
+// Shift that puts a chunk whose largest biased exponent is e into [2^14, 2^15); exponents below
+// 20 (|x| < 2^-107) count as 20, so both the shift and its inverse stay normal fp32 powers of two.
+E4B_DEV int chunk_shift(uint32_t exp_bits) { return 141 - max(static_cast<int>(exp_bits >> 7), 20); }
+
+// Two bf16 values times 2^d as an fp16 pair (exact for results of at least 2^-14; the values
+// carry 8 significant bits and the results stay below 2^15).
+E4B_DEV uint32_t bf16x2_to_f16x2(uint32_t w, int d) {
+  const float lo = __builtin_amdgcn_ldexpf(__uint_as_float(w << 16), d);
+  const float hi = __builtin_amdgcn_ldexpf(__uint_as_float(w & 0xffff0000u), d);
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+
+E4B_DEV uint4 piece_to_f16(const uint4& v, int d) {
+  return make_uint4(bf16x2_to_f16x2(v.x, d), bf16x2_to_f16x2(v.y, d), bf16x2_to_f16x2(v.z, d),
+                    bf16x2_to_f16x2(v.w, d));
 }
 
 // v + the value of the lane selected by a DPP pattern within each 16-lane row.
@@ -281,8 +323,12 @@ E4B_DEV uint4 load_chunk_w(const e4b_qweight& w, int e, int64_t row, int c) {
 // gate_up GEMV + fused epilogue for the a-th routed expert (blockIdx.y), G lanes per column.
 template <int DT, int FMT, int G, int CPL, bool FULL, bool PAIR>
 __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
+  // NF4 codes as fp16 single entries; e2m1 codes in the activation dtype
+  constexpr int CDT = FMT == E4B_FMT_MXFP4 ? DT : E4B_FP16;
+  constexpr bool kConv = CDT != DT;  // bf16 activations restaged as scaled fp16
   __shared__ __align__(16) uint4 lut[256 * kLutRowBytes / 16];
   __shared__ __align__(16) uint4 xs[kDecMaxK / 8 + 1];  // the activation row being multiplied + a spare slot
+  __shared__ int xsh[kConv ? kDecMaxK / 32 + 1 : 1];     // per chunk: the inverse of its restaging shift
   __shared__ WaveRoute route[kDecWaves];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
   const int lane = threadIdx.x & (kWave - 1);
@@ -325,9 +371,23 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
     xp1 = x4[t1 < nx4 ? t1 : 0];
   };
   auto store_x = [&]() {  // pieces beyond the row go to the spare slot: no branch to sink the loads into
-    xs[t0 < nx4 ? t0 : kDecMaxK / 8] = xp0;
-    xs[t1 < nx4 ? t1 : kDecMaxK / 8] = xp1;
+    const int i0 = t0 < nx4 ? t0 : kDecMaxK / 8, i1 = t1 < nx4 ? t1 : kDecMaxK / 8;
+    if constexpr (kConv) {
+      // the four lanes of a quad hold the four pieces of a chunk (thread t: pieces t, t + 256)
+      const int d0 = chunk_shift(quad_max(bf16_exp_max(xp0)));
+      const int d1 = chunk_shift(quad_max(bf16_exp_max(xp1)));
+      xs[i0] = piece_to_f16(xp0, d0);
+      xs[i1] = piece_to_f16(xp1, d1);
+      xsh[i0 / 4] = -d0;
+      xsh[i1 / 4] = -d1;
+    } else {
+      xs[i0] = xp0;
+      xs[i1] = xp1;
+    }
   };
+
+  // the decode table first: its stores then overlap the ids' wait, not the weight issue
+  store_pair_entry<false>(lut, pair_entry<CDT, false>(cf, cs));
 
   // round trip 2: the activation row, then weights and scales chunk by chunk, biases
   load_x(f);
@@ -352,14 +412,13 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
   const uint32_t bu_bits = bias[has_bias ? row_b : 0];
   const float off = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
 
-  // the decode table and the activation row, while the weights are in flight; the chunk loop
-  // then waits for each chunk's weights only
-  store_pair_entry<FMT>(lut, pair_entry<DT, FMT>(cf, cs));
+  // the activation row while the weights are in flight; the chunk loop then waits for each
+  // chunk's weights only
   if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = c2;
   store_x();
   __syncthreads();
 
-  uint32_t lane_off = LutGeom<FMT>::lane_off(lane);
+  uint32_t lane_off = LutGeom<false>::lane_off(lane);
   const char* lut_bytes = reinterpret_cast<const char*>(lut);
   float sa[CPL], sb[CPL];
 #pragma unroll
@@ -377,12 +436,15 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
       uint4 xv[4];
 #pragma unroll
       for (int q = 0; q < 4; ++q) xv[q] = xs[cidx[i] * 4 + q];
-      const float da = chunk_dot<DT, FMT>(qa[i], xv, lut_bytes, lane_off) * sa[i];
-      acc_a += valid[i] ? da : 0.0f;
+      const int sh = kConv ? xsh[cidx[i]] : 0;
+      float da = chunk_dot<CDT, false>(qa[i], xv, lut_bytes, lane_off);
+      if constexpr (kConv) da = __builtin_amdgcn_ldexpf(da, sh);
+      acc_a += valid[i] ? da * sa[i] : 0.0f;
       __builtin_amdgcn_sched_barrier(0);  // keep each chunk's 16 table reads together
       if constexpr (pair) {
-        const float db = chunk_dot<DT, FMT>(qb[i], xv, lut_bytes, lane_off) * sb[i];
-        acc_b += valid[i] ? db : 0.0f;
+        float db = chunk_dot<CDT, false>(qb[i], xv, lut_bytes, lane_off);
+        if constexpr (kConv) db = __builtin_amdgcn_ldexpf(db, sh);
+        acc_b += valid[i] ? db * sb[i] : 0.0f;
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -420,6 +482,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
   constexpr int C = kDownCols;
   constexpr int kGroups = kDecThreads / G;
+  constexpr bool kSplit = FMT != E4B_FMT_MXFP4;  // NF4: (hi, lo) entries in the activation dtype
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
   const int M = p.tokens * p.k;
@@ -444,7 +507,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
   const int64_t col0 = int64_t(blockIdx.x) * C;
   const bool has_bias = w.bias != nullptr;
   const uint16_t* bias = static_cast<const uint16_t*>(w.bias);
-  uint32_t lane_off = LutGeom<FMT>::lane_off(lane);
+  uint32_t lane_off = LutGeom<kSplit>::lane_off(lane);
   const char* lut_bytes = reinterpret_cast<const char*>(lut);
   int64_t cols[C];
 #pragma unroll
@@ -486,7 +549,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
       for (int cl = 0; cl < C; ++cl) bb[t][cl] = bp[has_bias ? cols[cl] : 0];
     }
     if (!table_ready) {
-      store_pair_entry<FMT>(lut, pair_entry<DT, FMT>(cf, cs));
+      store_pair_entry<kSplit>(lut, pair_entry<DT, kSplit>(cf, cs));
       if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = c2;
       if (wid == 0) wts[lane] = row_weight(p, wt_bits);  // read by the combine
       __syncthreads();
@@ -516,7 +579,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
         for (int i = 0; i < CPL; ++i) {
 #pragma unroll
           for (int cl = 0; cl < C; ++cl) {
-            const float d = chunk_dot<DT, FMT>(q[t][i][cl], xv[t][i], lut_bytes, lane_off) * sc[i][cl];
+            const float d = chunk_dot<DT, kSplit>(q[t][i][cl], xv[t][i], lut_bytes, lane_off) * sc[i][cl];
             acc[cl] += valid[i] ? d : 0.0f;
             __builtin_amdgcn_sched_barrier(0);  // keep each chunk's 16 table reads together
           }
@@ -545,10 +608,21 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
     const int cl = i % C;
     const int64_t col = col0 + cl;
     if (col >= n) continue;
+    // slots in groups of 8: every LDS read of a group is issued before the in-order sum, so the
+    // group costs one LDS round trip, not eight
     float acc = 0.0f;
-    for (int s = 0; s < p.k; ++s) {
-      const int f = t * p.k + s;
-      if ((routed_rows >> f) & 1ull) acc = __fadd_rn(acc, mul_f32(res[f * C + cl], wts[f]));
+    for (int s0 = 0; s0 < p.k; s0 += 8) {
+      float pr[8];
+      bool ok[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int s = s0 + j < p.k ? s0 + j : p.k - 1;
+        const int f = t * p.k + s;
+        ok[j] = s0 + j < p.k && ((routed_rows >> f) & 1ull);
+        pr[j] = mul_f32(res[f * C + cl], wts[f]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = ok[j] ? __fadd_rn(acc, pr[j]) : acc;
     }
     const int64_t o = int64_t(t) * n + col;
     if (p.odt == E4B_FP32) static_cast<float*>(p.out)[o] = acc;
