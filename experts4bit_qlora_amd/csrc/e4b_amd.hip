@@ -220,6 +220,11 @@ int mfma_tile_for(int64_t M, int E) {
   return M >= 64 * groups ? e4b::kTileM : e4b::kTileMSmall;
 }
 
+// Prefill re-tiling (split_tiles_kernel): 128-row tiles, except that an expert whose last
+// tile would hold at most 32 rows runs those rows in one 32-row tile.
+int64_t max_big_tiles(int64_t M, int E) { return max_tiles_for(M, E, e4b::kTileM); }
+int64_t max_small_tiles(int64_t M, int E) { return std::max<int64_t>(1, std::min<int64_t>(E, M)); }
+
 bool is_gated_epi(int epi) {
   return epi == E4B_EPI_SWIGLU || epi == E4B_EPI_CLAMP_SWIGLU || epi == E4B_EPI_GPTOSS;
 }
@@ -435,6 +440,10 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
   b += align256(sizeof(int32_t) * 2 * max_tiles_for(M, num_experts, mfma_tile_for(M, num_experts)));  // tiles
   b += align256(sizeof(int32_t) * 4);                                  // meta
   b += align256(sizeof(int32_t) * e4b_route_scratch_ints(M, num_experts));  // route scratch
+  if (mfma_tile_for(M, num_experts) == e4b::kTileM) {                  // prefill re-tiling
+    b += align256(sizeof(int32_t) * 2 * max_big_tiles(M, num_experts)) + align256(sizeof(int32_t) * 4);
+    b += align256(sizeof(int32_t) * 2 * max_small_tiles(M, num_experts)) + align256(sizeof(int32_t) * 4);
+  }
   b += align256(sizeof(uint16_t) * M * h_cols);                        // h
   b += align256(sizeof(float) * M * n2);                               // down rows (fp32)
   return b;
@@ -497,17 +506,50 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   rt.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rt.max_tiles));
   rt.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
   rt.scratch = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * e4b_route_scratch_ints(M, E)));
+  // Prefill-sized groups on the MFMA path run at two tile heights: 128-row tiles, and one
+  // 32-row tile for an expert whose last tile would hold at most 32 rows (the long Zipf tail
+  // of experts with a handful of rows each). A tile's cost is mostly the decoding of its
+  // expert's weights, which the smaller tile does with a quarter of the MFMA work beside it.
+  const bool split = rt.tile_m == e4b::kTileM && flags != E4B_PATH_GEMV;
+  e4b_routing rbig = rt, rsmall = rt;
+  if (split) {
+    rbig.tile_m = e4b::kTileM;
+    rbig.max_tiles = static_cast<int32_t>(max_big_tiles(M, E));
+    rbig.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rbig.max_tiles));
+    rbig.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
+    rsmall.tile_m = e4b::kTileMSmall;
+    rsmall.max_tiles = static_cast<int32_t>(max_small_tiles(M, E));
+    rsmall.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rsmall.max_tiles));
+    rsmall.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
+  }
   void* h = take(sizeof(uint16_t) * M * h_cols);
   void* down = take(sizeof(float) * M * w2->n);
 
   rc = e4b_route(top_k_index, tokens, top_k, E, &rt, stream);
   if (rc) return rc;
-  rc = e4b_grouped_gemm(hidden, act_dtype, top_k, w1, &rt, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
-                        stream);
-  if (rc) return rc;
-  rc = e4b_grouped_gemm(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
-                        stream);
-  if (rc) return rc;
+  if (split) {
+    hipLaunchKernelGGL(e4b::split_tiles_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, rt.offsets, rt.meta, E,
+                       rbig, rsmall);
+    rc = check_launch("split_tiles_kernel");
+    if (rc) return rc;
+    for (const e4b_routing* r : {&rbig, &rsmall}) {
+      rc = e4b_grouped_gemm(hidden, act_dtype, top_k, w1, r, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
+                            stream);
+      if (rc) return rc;
+    }
+    for (const e4b_routing* r : {&rbig, &rsmall}) {
+      rc = e4b_grouped_gemm(h, act_dtype, 0, w2, r, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
+                            stream);
+      if (rc) return rc;
+    }
+  } else {
+    rc = e4b_grouped_gemm(hidden, act_dtype, top_k, w1, &rt, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
+                          stream);
+    if (rc) return rc;
+    rc = e4b_grouped_gemm(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
+                          stream);
+    if (rc) return rc;
+  }
   return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
                      stream);
 }

@@ -18,6 +18,9 @@
 //   route_scan_kernel   one workgroup: per-expert totals, offsets, tiles, active list, meta,
 //                       and each chunk's first sorted row per expert (chunk order = flat order);
 //   route_place_kernel  each chunk re-walks its ids in order from those bases.
+//
+// split_tiles_kernel re-tiles the routed rows for prefill: big tiles, plus a small tile for an
+// expert whose last big tile would hold only a few rows.
 #pragma once
 
 #include "common.h"
@@ -354,6 +357,55 @@ E4B_DEV float load_weight(const void* w, int64_t i) {
     return static_cast<const float*>(w)[i];
   } else {
     return to_f<WDT>(static_cast<const uint16_t*>(w)[i]);
+  }
+}
+
+// Two tile lists from the routed offsets, for grouped GEMMs run at two tile heights. A tile
+// costs about the same whatever its height until its MFMA work catches up with its weight
+// decoding (the whole expert matrix per tile), so every expert keeps big tiles
+// (`big.tile_m` rows, the last one partial) unless its last big tile would hold at most
+// `small.tile_m` rows: those rows go to one small tile instead. One 512-thread block; thread t
+// owns experts 2t and 2t + 1. meta[1] / meta[2] (active, dropped) are copied from the routing
+// the offsets came from.
+__global__ void __launch_bounds__(kRouteThreads) split_tiles_kernel(const int32_t* __restrict__ offsets,
+                                                                   const int32_t* __restrict__ meta, int E,
+                                                                   e4b_routing big, e4b_routing small) {
+  __shared__ int wsum[kRouteWaves];
+  const int tid = threadIdx.x;
+  const int ea = 2 * tid, eb = 2 * tid + 1;
+  const int oa = ea < E ? offsets[ea] : 0, ob = eb < E ? offsets[eb] : 0;
+  const int ca = ea < E ? offsets[ea + 1] - oa : 0, cb = eb < E ? offsets[eb + 1] - ob : 0;
+  const int bt = big.tile_m, st = small.tile_m;
+  // remainder past the full big tiles: one more big tile, or one small tile when it fits
+  const int ra = ca % bt, rb = cb % bt;
+  const int nsa = (ra > 0 && ra <= st) ? 1 : 0, nsb = (rb > 0 && rb <= st) ? 1 : 0;
+  const int nba = ca / bt + (ra > st ? 1 : 0), nbb = cb / bt + (rb > st ? 1 : 0);
+  int nbig, nsmall;
+  const int b0 = block_exclusive_scan(nba + nbb, &nbig, wsum);
+  const int s0 = block_exclusive_scan(nsa + nsb, &nsmall, wsum);
+  for (int j = 0; j < nba + nbb; ++j) {
+    const int t = b0 + j;
+    const bool in_a = j < nba;
+    if (t < big.max_tiles) {
+      big.tiles[2 * t] = in_a ? ea : eb;
+      big.tiles[2 * t + 1] = in_a ? oa + j * bt : ob + (j - nba) * bt;
+    }
+  }
+  for (int j = 0; j < nsa + nsb; ++j) {
+    const int t = s0 + j;
+    const bool in_a = j < nsa;
+    if (t < small.max_tiles) {
+      small.tiles[2 * t] = in_a ? ea : eb;
+      small.tiles[2 * t + 1] = in_a ? oa + nba * bt : ob + nbb * bt;  // at most one small tile per expert
+    }
+  }
+  if (tid == 0) {
+    big.meta[0] = min(nbig, big.max_tiles);
+    small.meta[0] = min(nsmall, small.max_tiles);
+    big.meta[1] = small.meta[1] = meta[1];
+    big.meta[2] = small.meta[2] = meta[2];
+    big.meta[3] = bt;
+    small.meta[3] = st;
   }
 }
 

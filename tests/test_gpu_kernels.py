@@ -389,3 +389,47 @@ def test_decode_rejects_batches_beyond_its_limit(rows):
     idx = torch.zeros(rows, 1, dtype=torch.int64, device=DEV)
     with pytest.raises(N.NativeError, match="decode path"):
         ops.decode_gate_up(torch.zeros(rows, 128, dtype=torch.bfloat16, device=DEV), idx, qw, N.EPI_NONE)
+
+
+@pytest.mark.parametrize("fmt", ["nf4", "nf4_dq", "mxfp4"])
+def test_prefill_split_tiles_match_one_tile_list(fmt):
+    """Prefill-sized forwards run 128-row tiles plus, for an expert whose last tile would hold
+    at most 32 rows, one 32-row tile: two launches per projection. Every output element goes
+    through the same MFMA sequence along k at any tile height, so the layer equals the route ->
+    gate_up -> down -> combine chain over one 128-row tile list bit for bit; a few rows are also
+    checked against the oracle."""
+    _announce(f"prefill split tiles fmt={fmt}")
+    E, H, I, top, T = 8, 256, 192, 2, 1200
+    w1, W1 = _stack(fmt, E, 2 * I, H, seed=40)
+    w2, W2 = _stack(fmt, E, H, I, seed=41)
+    epi, spec = N.EPI_SWIGLU, "swiglu"
+    if fmt == "mxfp4":
+        g = torch.Generator().manual_seed(43)
+        w1.bias = (torch.randn(E, 2 * I, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+        w2.bias = (torch.randn(E, H, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+        epi, spec = N.EPI_GPTOSS, ("gptoss", 1.702, 7.0)
+    rng = np.random.default_rng(42)
+    p = 1.0 / np.arange(1, E + 1) ** 1.1
+    idx = np.stack([rng.choice(E, size=top, replace=False, p=p / p.sum()) for _ in range(T)]).astype(np.int64)
+    counts = np.bincount(idx.reshape(-1), minlength=E)
+    rem = counts % 128
+    assert ((rem > 0) & (rem <= 32)).any() and (rem > 32).any() and T * top >= 64 * E  # both tile lists in use
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(44)).to(torch.bfloat16).to(DEV)
+    wts = torch.rand(T, top, generator=torch.Generator().manual_seed(45)).to(torch.bfloat16).to(DEV)
+    ti = torch.from_numpy(idx).to(DEV)
+    got = ops.moe_forward(x, ti, wts, w1, w2, epi, torch.bfloat16)
+    rb = ops.route(ti, E, tile_m=128)
+    h = ops.grouped_gemm(x, w1, rb, T, T * top, epilogue=epi, gather_k=top, path=N.PATH_MFMA)
+    dn = ops.grouped_gemm(h, w2, rb, T, T * top, path=N.PATH_MFMA, out_dtype=torch.float32)
+    want = ops.combine(dn, rb, wts, T, top, torch.bfloat16)
+    assert torch.equal(got, want)
+    rows = [0, 1, 599, 1199]
+    b1 = None if w1.bias is None else w1.bias.float().cpu().numpy().astype(np.float64)
+    b2 = None if w2.bias is None else w2.bias.float().cpu().numpy().astype(np.float64)
+    flat = np.array([r * top + s for r in rows for s in range(top)])
+    proj = _gemm_oracle(x.float().cpu().numpy()[flat // top], numerics.round_bf16(W1), idx.reshape(-1)[flat], bias=b1)
+    hh = numerics.round_bf16(moe._glu_exact(proj, spec, I).astype(np.float32))
+    d = _gemm_oracle(hh, numerics.round_bf16(W2), idx.reshape(-1)[flat], bias=b2)
+    oracle = (d.reshape(len(rows), top, H) * wts.float().cpu().numpy()[rows][..., None]).sum(1)
+    fro, maxabs = _errs(got[rows].float().cpu().numpy(), oracle)
+    assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
