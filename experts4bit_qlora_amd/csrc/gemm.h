@@ -45,8 +45,9 @@ constexpr int kTileNWWide = 256; // weight rows per tile of the 128-row (prefill
 constexpr int kTileK = 64;
 constexpr int kLdsPitch = kTileK + 8;  // elements; 144-byte rows keep 16-byte alignment
 // K steps of global loads in flight ahead of the MFMAs (6 for the 32-row tiles was measured:
-// no change at bs=64, whose blocks are bound by their decode and LDS work, not by latency)
-constexpr int gemm_stages(int) { return 3; }
+// no change at bs=64, whose blocks are bound by their decode and LDS work, not by latency).
+// The 256-row tiles hold two: their activation sets are twice as large and a third spills.
+constexpr int gemm_stages(int bm) { return bm == kTileMBig ? 2 : 3; }
 constexpr int kXcds = 8;    // accelerator dies of an MI355X; blocks go round-robin over them
 
 template <int DT>
@@ -83,24 +84,52 @@ E4B_DEV float code_times_scale(float c, float s) {
   else return c * s;
 }
 
+E4B_DEV uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) { return (m & a) | (~m & b); }
+
 // NB packed bytes (2 * NB values; byte i = elements 2i and 2i + 1, the first in the high nibble
 // for NF4, in the low one for e2m1) -> NB words of DT pairs, each value dt(fp32(code * scale)).
-// Table offsets are nibble * 4: bits 2..5 of byte b of (w << 2) hold its low nibble, of (w >> 2)
-// its high one.
+//
+// All in registers, no memory lookups: the 16 possible values P[c] = dt(fp32(code[c] * scale))
+// of this weight row and K step are formed once (16 products, 8 conversions) and kept as byte
+// planes lo[k] / hi[k] = the low / high bytes of P[4k .. 4k+3]. Four nibbles (one per byte of a
+// word) then select their entries at once: v_perm_b32 over planes 0-1 (entries 0..7) and over
+// planes 2-3 (entries 8..15), merged by each nibble's bit 3 (v_bfi_b32), for the low and the
+// high bytes; four more v_perm_b32 interleave the bytes into the (first, second) pairs. Every
+// value is the same fp32 product and rounding as a per-element decode, so the result is
+// bit-identical to the dequantized weights.
 template <int DT, int FMT, int NB>
-E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float* code16, float scale, uint32_t (&wv)[NB]) {
-  const char* tb = reinterpret_cast<const char*>(code16);
+E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float (&code)[16], float scale, uint32_t (&wv)[NB]) {
+  uint32_t q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    q[i] = cvt_pair<DT>(code_times_scale<DT>(code[2 * i], scale), code_times_scale<DT>(code[2 * i + 1], scale));
+  uint32_t lo[4], hi[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    lo[k] = __builtin_amdgcn_perm(q[2 * k + 1], q[2 * k], 0x06040200u);
+    hi[k] = __builtin_amdgcn_perm(q[2 * k + 1], q[2 * k], 0x07050301u);
+  }
+  // x: one nibble value per byte -> the low and the high bytes of its four entries
+  auto look = [&](uint32_t x, uint32_t& l, uint32_t& h) {
+    const uint32_t sel = x & 0x07070707u;
+    const uint32_t t = x & 0x08080808u;
+    const uint32_t m = (t << 5) - (t >> 3);  // 0xff in each byte whose entry is 8..15
+    l = bfi(m, __builtin_amdgcn_perm(lo[3], lo[2], sel), __builtin_amdgcn_perm(lo[1], lo[0], sel));
+    h = bfi(m, __builtin_amdgcn_perm(hi[3], hi[2], sel), __builtin_amdgcn_perm(hi[1], hi[0], sel));
+  };
 #pragma unroll
   for (int wi = 0; wi < NB / 4; ++wi) {
-    const uint32_t wl = words[wi] << 2, wh = words[wi] >> 2;
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const float c_lo = *reinterpret_cast<const float*>(tb + ((wl >> (8 * b)) & 0x3cu));
-      const float c_hi = *reinterpret_cast<const float*>(tb + ((wh >> (8 * b)) & 0x3cu));
-      const float first = (FMT == E4B_FMT_MXFP4) ? c_lo : c_hi;
-      const float second = (FMT == E4B_FMT_MXFP4) ? c_hi : c_lo;
-      wv[4 * wi + b] = cvt_pair<DT>(code_times_scale<DT>(first, scale), code_times_scale<DT>(second, scale));
-    }
+    const uint32_t w = words[wi];
+    const uint32_t xl = w & 0x0f0f0f0fu, xh = (w >> 4) & 0x0f0f0f0fu;
+    uint32_t lf, hf, ls, hs;
+    look(FMT == E4B_FMT_MXFP4 ? xl : xh, lf, hf);  // first elements
+    look(FMT == E4B_FMT_MXFP4 ? xh : xl, ls, hs);  // second elements
+    const uint32_t f01 = __builtin_amdgcn_perm(hf, lf, 0x05010400u), f23 = __builtin_amdgcn_perm(hf, lf, 0x07030602u);
+    const uint32_t s01 = __builtin_amdgcn_perm(hs, ls, 0x05010400u), s23 = __builtin_amdgcn_perm(hs, ls, 0x07030602u);
+    wv[4 * wi + 0] = __builtin_amdgcn_perm(s01, f01, 0x05040100u);
+    wv[4 * wi + 1] = __builtin_amdgcn_perm(s01, f01, 0x07060302u);
+    wv[4 * wi + 2] = __builtin_amdgcn_perm(s23, f23, 0x05040100u);
+    wv[4 * wi + 3] = __builtin_amdgcn_perm(s23, f23, 0x07060302u);
   }
 }
 
@@ -126,7 +155,6 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   constexpr int ST = gemm_stages(BM);
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLdsPitch];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kLdsPitch];
-  __shared__ float code16[16];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
 
   // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so linear
@@ -158,8 +186,10 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   const int64_t col0 = int64_t(n_tile) * (pair ? BN / 2 : BN);
   if (col0 >= p.n_out) return;
 
-  // decode tables: the 16 codes, and the second-level code of double quantization
-  if (tid < 16) code16[tid] = (FMT == E4B_FMT_MXFP4) ? kFp4E2M1[tid] : p.w.code[tid];
+  // the 16 codes (the same in every lane), and the second-level code of double quantization
+  float code[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) code[i] = (FMT == E4B_FMT_MXFP4) ? kFp4E2M1[i] : p.w.code[i];
   if constexpr (FMT == E4B_FMT_NF4_DQ) {
     if (tid < 256) code2_s[tid] = p.w.code2[tid];
   }
@@ -249,7 +279,7 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
       scale = prod + offset;
     }
     uint32_t wv[WB];
-    dequant_bytes<DT, FMT, WB>(wq[set], code16, scale, wv);
+    dequant_bytes<DT, FMT, WB>(wq[set], code, scale, wv);
     uint4* ws = reinterpret_cast<uint4*>(&Ws[buf][lrow * kLdsPitch + half * 2 * WB]);
 #pragma unroll
     for (int i = 0; i < WB / 4; ++i) ws[i] = make_uint4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
@@ -257,24 +287,23 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
 #pragma unroll
     for (int i = 0; i < AV; ++i) as[i] = areg[set][i];
   };
-  auto mfma_step = [&](int buf) {
+  // MFMA operands of one 32-deep half step (ks) of LDS buffer buf, and the MFMAs on them
+  auto read_frags = [&](int buf, int ks, uint4 (&av)[MS], uint4 (&bv)[NS]) {
+    const int kcol = ks * 32 + (lane >> 4) * 8;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int kcol = ks * 32 + (lane >> 4) * 8;
-      uint4 av[MS], bv[NS];
-#pragma unroll
-      for (int ms = 0; ms < MS; ++ms) {
-        av[ms] = *reinterpret_cast<const uint4*>(&As[buf][(wave_m * WM + ms * 16 + (lane & 15)) * kLdsPitch + kcol]);
-      }
-#pragma unroll
-      for (int ns = 0; ns < NS; ++ns) {
-        bv[ns] = *reinterpret_cast<const uint4*>(&Ws[buf][(nbase[ns] + (lane & 15)) * kLdsPitch + kcol]);
-      }
-#pragma unroll
-      for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-        for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = mfma_16x16x32<DT>(av[ms], bv[ns], acc[ms][ns]);
+    for (int ms = 0; ms < MS; ++ms) {
+      av[ms] = *reinterpret_cast<const uint4*>(&As[buf][(wave_m * WM + ms * 16 + (lane & 15)) * kLdsPitch + kcol]);
     }
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) {
+      bv[ns] = *reinterpret_cast<const uint4*>(&Ws[buf][(nbase[ns] + (lane & 15)) * kLdsPitch + kcol]);
+    }
+  };
+  auto mfmas = [&](const uint4 (&av)[MS], const uint4 (&bv)[NS]) {
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = mfma_16x16x32<DT>(av[ms], bv[ns], acc[ms][ns]);
   };
 
   // Step indices past the last step are clamped (a cached re-read nobody uses), for the same
@@ -282,29 +311,44 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   const int64_t ksteps = k / kTileK;
   const int64_t klast = ksteps - 1;
   load_step(0, 0);
-  __syncthreads();  // tables
+  __syncthreads();  // code2 table
   stage(0, 0);
 #pragma unroll
   for (int j = 1; j <= ST; ++j) load_step(j % ST, min<int64_t>(j, klast));
   __syncthreads();
-  // step kb: its MFMAs, then stage step kb + 1 (after the last step: a stale set into the idle
-  // buffer, never read) and refill that set with step kb + 1 + ST
-  // The MFMAs of step kb and the decode / staging of step kb + 1 form one scheduling block;
-  // the group barriers slot the decode's LDS reads and VALU work between MFMAs that are still
-  // executing. (Left to itself the compiler emits them one after the other, and the per-step
-  // block barrier then keeps every wave of a SIMD in the same phase, so nothing overlaps.)
+  // Step kb, in two scheduling blocks around the step's one barrier:
+  //   before: the fragments of half step 1 are read while the MFMAs of half step 0 run, with
+  //           the decode and LDS staging of step kb + 1 (into the other buffer) and the refill
+  //           of its register set with step kb + 1 + ST slotted between them;
+  //   after:  the MFMAs of half step 1 run from registers while the fragments of step kb + 1's
+  //           half step 0 are read, so the LDS latency after the barrier is hidden.
+  // (After the last step the staging writes a stale set into the idle buffer and the last
+  // fragment reads fetch that buffer; neither is used.) The group barriers spread the decode's
+  // VALU work over the MFMAs; left to itself the compiler emits them one after the other.
+  uint4 fa0[MS], fb0[NS], fa1[MS], fb1[NS];
+  read_frags(0, 0, fa0, fb0);
   auto iteration = [&](int u, int64_t kb) __attribute__((always_inline)) {
     const int cur = static_cast<int>(kb & 1);
-    mfma_step(cur);
+    read_frags(cur, 1, fa1, fb1);
+    mfmas(fa0, fb0);
     stage((u + 1) % ST, cur ^ 1);
+    constexpr int kValu = (WB == 16 ? 200 : 136) / (MS * NS);
 #pragma unroll
-    for (int i = 0; i < 2 * MS * NS; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // two LDS reads
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // four VALU
+    for (int i = 0; i < MS * NS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);      // one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);  // VALU
     }
     load_step((u + 1) % ST, min<int64_t>(kb + 1 + ST, klast));
     __syncthreads();
+    read_frags(cur ^ 1, 0, fa0, fb0);
+    mfmas(fa1, fb1);
+#pragma unroll
+    for (int i = 0; i < MS * NS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the next step's block starts here
   };
   const int64_t kmain = ksteps - ksteps % ST;
   for (int64_t kb0 = 0; kb0 < kmain; kb0 += ST) {
