@@ -433,3 +433,31 @@ def test_prefill_split_tiles_match_one_tile_list(fmt):
     oracle = (d.reshape(len(rows), top, H) * wts.float().cpu().numpy()[rows][..., None]).sum(1)
     fro, maxabs = _errs(got[rows].float().cpu().numpy(), oracle)
     assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
+
+
+@pytest.mark.parametrize("gated", [False, True])
+def test_mfma_output_columns_not_a_multiple_of_eight(gated):
+    """Output rows of 100 columns (a partial tile in n, rows not 16-byte multiples); 40 tokens
+    over 4 experts leave partial tiles in m as well."""
+    _announce(f"mfma odd output width gated={gated}")
+    E, H, cols, top, T = 4, 256, 100, 2, 40
+    n = 2 * cols if gated else cols
+    qw, _, _ = _nf4_stack(E, n, H, seed=50)
+    W = _dense_from_kernel(qw)
+    rng = np.random.default_rng(51)
+    idx = np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)
+    x = torch.randn(T, H, generator=torch.Generator().manual_seed(52)).to(torch.bfloat16)
+    rb = ops.route(torch.from_numpy(idx).to(DEV), E)
+    ref = orouting.route(idx, E)
+    proj = _gemm_oracle(x.float().numpy()[ref["token_rows"]], numerics.round_bf16(W), idx.reshape(-1)[ref["order"]])
+    epi = N.EPI_SWIGLU if gated else N.EPI_NONE
+    exact = moe._glu_exact(proj, "swiglu", cols) if gated else proj
+    for od in (torch.bfloat16, torch.float32):
+        out = ops.grouped_gemm(x.to(DEV), qw, rb, T, T * top, epi, gather_k=top, path=N.PATH_MFMA, out_dtype=od)
+        assert out.shape == (T * top, cols) and out.dtype == od
+        if od == torch.float32:
+            fro, _ = _errs(out.cpu().numpy(), exact)
+            assert fro < 1e-5, fro
+        else:
+            fro, maxabs = _errs_rounded_bf16(out.float().cpu().numpy(), exact)
+            assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
