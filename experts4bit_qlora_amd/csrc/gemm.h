@@ -363,6 +363,43 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   // Epilogue: lane holds D[4*(lane/16) + i][lane % 16] of each 16x16 sub-tile.
   const bool has_bias = p.w.bias != nullptr;
   const uint16_t* bias = static_cast<const uint16_t*>(p.w.bias);
+  // The two prefill projections take a branch-free path: epilogue kind, bias and output type
+  // are kernel arguments, and the general path below tests them per element.
+  if (pair && p.epi == E4B_EPI_SWIGLU && !has_bias && !p.out_f32) {  // gate_up: silu(g) * u -> dt
+    uint16_t* const out = static_cast<uint16_t*>(p.out);
+    const int64_t cbase = col0 + wave_n * (WN / 2) + (lane & 15);
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = row0 + wave_m * WM + ms * 16 + 4 * (lane >> 4) + i;
+        uint16_t* const orow = out + int64_t(rr) * p.n_out + cbase;
+#pragma unroll
+        for (int ns = 0; ns < NS / 2; ++ns) {
+          const float v = silu_f32(acc[ms][ns][i]) * acc[ms][ns + NS / 2][i];
+          if (rr < row_end && cbase + ns * 16 < p.n_out) orow[ns * 16] = from_f<DT>(v);
+        }
+      }
+    }
+    return;
+  }
+  if (!pair && p.epi == E4B_EPI_NONE && !has_bias && p.out_f32) {  // down: fp32 rows
+    float* const out = static_cast<float*>(p.out);
+    const int64_t cbase = col0 + wave_n * WN + (lane & 15);
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = row0 + wave_m * WM + ms * 16 + 4 * (lane >> 4) + i;
+        float* const orow = out + int64_t(rr) * p.n_out + cbase;
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns) {
+          if (rr < row_end && cbase + ns * 16 < p.n_out) orow[ns * 16] = acc[ms][ns][i];
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
