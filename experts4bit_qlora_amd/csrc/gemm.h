@@ -93,8 +93,9 @@ E4B_DEV uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) { return (m & a) | (~m 
 // of this weight row and K step are formed once (16 products, 8 conversions) and kept as byte
 // planes lo[k] / hi[k] = the low / high bytes of P[4k .. 4k+3]. Four nibbles (one per byte of a
 // word) then select their entries at once: v_perm_b32 over planes 0-1 (entries 0..7) and over
-// planes 2-3 (entries 8..15), merged by each nibble's bit 3 (v_bfi_b32), for the low and the
-// high bytes; four more v_perm_b32 interleave the bytes into the (first, second) pairs. Every
+// planes 2-3 (entries 8..15), merged by each nibble's bit 3 (v_bfi_b32, the byte mask made by
+// one more v_perm_b32), for the low and the high bytes; four more v_perm_b32 interleave the
+// bytes into the (first, second) pairs. Every
 // value is the same fp32 product and rounding as a per-element decode, so the result is
 // bit-identical to the dequantized weights.
 template <int DT, int FMT, int NB>
@@ -109,21 +110,29 @@ E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float (&code)[
     lo[k] = __builtin_amdgcn_perm(q[2 * k + 1], q[2 * k], 0x06040200u);
     hi[k] = __builtin_amdgcn_perm(q[2 * k + 1], q[2 * k], 0x07050301u);
   }
-  // x: one nibble value per byte -> the low and the high bytes of its four entries
-  auto look = [&](uint32_t x, uint32_t& l, uint32_t& h) {
-    const uint32_t sel = x & 0x07070707u;
-    const uint32_t t = x & 0x08080808u;
-    const uint32_t m = (t << 5) - (t >> 3);  // 0xff in each byte whose entry is 8..15
+  // four nibbles: sel = their low three bits (one per byte), m = 0xff in each byte whose
+  // nibble is 8..15 -> the low and the high bytes of their four entries
+  auto look = [&](uint32_t sel, uint32_t m, uint32_t& l, uint32_t& h) {
     l = bfi(m, __builtin_amdgcn_perm(lo[3], lo[2], sel), __builtin_amdgcn_perm(lo[1], lo[0], sel));
     h = bfi(m, __builtin_amdgcn_perm(hi[3], hi[2], sel), __builtin_amdgcn_perm(hi[1], hi[0], sel));
   };
 #pragma unroll
   for (int wi = 0; wi < NB / 4; ++wi) {
     const uint32_t w = words[wi];
-    const uint32_t xl = w & 0x0f0f0f0fu, xh = (w >> 4) & 0x0f0f0f0fu;
+    // v_perm selectors 8..11 replicate bit 15 / 31 of either source into a whole byte; the
+    // nibbles' bit 3 are shifted there: low nibbles (w bits 3, 11, 19, 27) and high nibbles
+    // (w bits 7, 15, 23, 31)
+    const uint32_t sel_l = w & 0x07070707u, sel_h = (w >> 4) & 0x07070707u;
+    const uint32_t m_l = __builtin_amdgcn_perm(w << 4, w << 12, 0x0B090A08u);
+    const uint32_t m_h = __builtin_amdgcn_perm(w, w << 8, 0x0B090A08u);
     uint32_t lf, hf, ls, hs;
-    look(FMT == E4B_FMT_MXFP4 ? xl : xh, lf, hf);  // first elements
-    look(FMT == E4B_FMT_MXFP4 ? xh : xl, ls, hs);  // second elements
+    if constexpr (FMT == E4B_FMT_MXFP4) {
+      look(sel_l, m_l, lf, hf);  // first elements: low nibbles
+      look(sel_h, m_h, ls, hs);
+    } else {
+      look(sel_h, m_h, lf, hf);  // first elements: high nibbles
+      look(sel_l, m_l, ls, hs);
+    }
     const uint32_t f01 = __builtin_amdgcn_perm(hf, lf, 0x05010400u), f23 = __builtin_amdgcn_perm(hf, lf, 0x07030602u);
     const uint32_t s01 = __builtin_amdgcn_perm(hs, ls, 0x05010400u), s23 = __builtin_amdgcn_perm(hs, ls, 0x07030602u);
     wv[4 * wi + 0] = __builtin_amdgcn_perm(s01, f01, 0x05040100u);
