@@ -51,7 +51,7 @@ void launch_decode_down(const DecodeArgs& a, DecShape d, hipStream_t s) {
     else down_gc<DT, FMT, g, c, j, false>(a, s);                        \
     return;                                                             \
   }
-  E4B_DOWN(16, 1, 2) E4B_DOWN(16, 2, 1) E4B_DOWN(32, 1, 1) E4B_DOWN(32, 2, 1) E4B_DOWN(32, 3, 1)
+  E4B_DOWN(16, 1, 2) E4B_DOWN(32, 1, 1) E4B_DOWN(32, 2, 1) E4B_DOWN(32, 3, 1)
   E4B_DOWN(32, 4, 1)
 #undef E4B_DOWN
 }
