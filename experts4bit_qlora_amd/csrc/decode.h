@@ -471,6 +471,184 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
   }
 }
 
+// gate_up for 2..8 tokens. Every token's activations fit in LDS at once, so the layer's work is
+// split into items -- one routed expert x kWave / G output columns -- that each wave takes in
+// turn with no barrier after the setup: one block per CU builds the decode table, routes, and
+// stages all activation rows once, then each wave streams its items' weights, loading the next
+// item while it computes the current one. (decode_up_kernel runs one block per (column tile,
+// routed expert) and restages the activations per routed row behind two barriers: at 8 tokens
+// on 64 experts that is ~2600 blocks, each paying the id round trip and the table build.)
+constexpr int kItemThreads = 512;
+constexpr int kItemWaves = kItemThreads / kWave;
+constexpr int kItemMaxX = 16384;  // tokens * k1 activation elements staged (32 KB)
+
+template <int DT, int FMT, int G, int CPL, bool FULL, bool PAIR>
+__global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArgs p) {
+  constexpr int CDT = FMT == E4B_FMT_MXFP4 ? DT : E4B_FP16;
+  constexpr bool kConv = CDT != DT;
+  constexpr int kXU = kItemMaxX / 8 / kItemThreads;  // 16-byte activation pieces per thread
+  __shared__ __align__(16) uint4 lut[256 * kLutRowBytes / 16];
+  __shared__ __align__(16) uint4 xs[kItemMaxX / 8 + 1];  // every token's activations + a spare slot
+  __shared__ int xsh[kConv ? kItemMaxX / 32 + 1 : 1];     // per chunk: the inverse restaging shift
+  __shared__ WaveRoute route[kItemWaves];
+  __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
+  const int tid = static_cast<int>(threadIdx.x);
+  const int lane = tid & (kWave - 1);
+  const int wid = tid / kWave;
+  const int M = p.tokens * p.k;
+  const e4b_qweight& w = p.w;
+  const int64_t n = w.n, k = w.k;
+  const int nx = static_cast<int>(p.tokens * k / 8);  // <= kItemMaxX / 8: checked by the launcher
+
+  // round trip 1: ids, every activation piece (clamped, no branch), the code pair, code2
+  const int64_t id_raw = load_row_id_raw(p, M);
+  // (four named registers, not an array: an array here ends up in LDS or scratch memory)
+  static_assert(kXU == 4, "four 16-byte activation pieces per thread");
+  const uint4* x4 = reinterpret_cast<const uint4*>(p.x);
+  auto piece = [&](int u) { return tid + u * kItemThreads; };
+  const uint4 xp0 = x4[piece(0) < nx ? piece(0) : 0], xp1 = x4[piece(1) < nx ? piece(1) : 0];
+  const uint4 xp2 = x4[piece(2) < nx ? piece(2) : 0], xp3 = x4[piece(3) < nx ? piece(3) : 0];
+  float cf, cs;
+  load_pair_codes<FMT>(w, cf, cs);
+  const float c2 = (FMT == E4B_FMT_NF4_DQ) ? w.code2[tid & 255] : 0.0f;
+
+  WaveRoute& r = route[wid];
+  const int nact = wave_route(row_id(p, M, id_raw), r);
+  if (tid < 256) {
+    store_pair_entry<false>(lut, pair_entry<CDT, false>(cf, cs));
+    if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[tid] = c2;
+  }
+  // Piece (token t, chunk c, quarter q) goes to xs[t * xrow + q * nchunk + c]: the G lanes of a
+  // group then read 16 consecutive bytes each for the same quarter (conflict-free), where the
+  // row-major order puts them 64 bytes apart. The four pieces of a chunk sit in an aligned lane
+  // quad (kItemThreads is a multiple of 4, rows are whole chunks); pieces beyond the
+  // activations go to the spare slot.
+  const int xrow = static_cast<int>(k / 8), nchunk = static_cast<int>(k / 32);
+  auto stage = [&](int u, const uint4& v) {
+    const int pc = piece(u);
+    const int t = pc / xrow, rp = pc - t * xrow;
+    const bool real = pc < nx;
+    const int idx = real ? t * xrow + (rp & 3) * nchunk + (rp >> 2) : kItemMaxX / 8;
+    if constexpr (kConv) {
+      const int d = chunk_shift(quad_max(bf16_exp_max(v)));
+      xs[idx] = piece_to_f16(v, d);
+      xsh[real ? pc / 4 : kItemMaxX / 32] = -d;
+    } else {
+      xs[idx] = v;
+    }
+  };
+  stage(0, xp0);
+  stage(1, xp1);
+  stage(2, xp2);
+  stage(3, xp3);
+  __syncthreads();
+
+  constexpr bool pair = PAIR;  // gated epilogue: gate row j and up row j + n/2
+  constexpr int kCols = kWave / G;
+  // item it: routed expert it / ncg, column group it % ncg (32-bit: at most 64 x n_out / kCols)
+  const int n_out = static_cast<int>(p.n_out);
+  const int ncg = (n_out + kCols - 1) / kCols;
+  const int nitems = nact * ncg;
+  const int stride = static_cast<int>(gridDim.x) * kItemWaves;
+  const int gl = lane % G;
+  uint32_t lane_off = LutGeom<false>::lane_off(lane);
+  const char* lut_bytes = reinterpret_cast<const char*>(lut);
+  const bool has_bias = w.bias != nullptr;
+  bool valid[CPL];
+  int cidx[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) cidx[i] = slot_chunk<G, FULL>(gl, i, nchunk, valid[i]);
+
+  // one item's loads: weights and scales chunk by chunk, then the bias bits and the offset
+  struct Buf {
+    uint4 qa[CPL], qb[CPL];
+    RawScale ra[CPL], rb[CPL];
+    uint32_t bg, bu;
+    float off;
+  };
+  auto load = [&](int it, Buf& b) {
+    const int a = it / ncg;
+    const int e = r.act[a];
+    const int j = (it - a * ncg) * kCols + lane / G;
+    const int64_t row_a = j < n_out ? j : 0, row_b = pair ? row_a + n / 2 : row_a;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      b.qa[i] = load_chunk_w(w, e, row_a, cidx[i]);
+      if constexpr (pair) b.qb[i] = load_chunk_w(w, e, row_b, cidx[i]);
+      b.ra[i] = load_scale<FMT>(w, e, row_a, cidx[i]);
+      if constexpr (pair) b.rb[i] = load_scale<FMT>(w, e, row_b, cidx[i]);
+    }
+    const uint16_t* bias = has_bias ? static_cast<const uint16_t*>(w.bias) + int64_t(e) * n : p.x;
+    b.bg = bias[has_bias ? row_a : 0];
+    b.bu = bias[has_bias ? row_b : 0];
+    b.off = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
+  };
+  auto compute = [&](int it, const Buf& b) {
+    const int a = it / ncg;
+    const int j = (it - a * ncg) * kCols + lane / G;
+    const bool live = j < n_out;
+    unsigned long long rows = r.rows[a];
+    float sa[CPL], sb[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      sa[i] = valid[i] ? resolve_scale<FMT>(b.ra[i], code2_s, b.off) : 0.0f;
+      sb[i] = (pair && valid[i]) ? resolve_scale<FMT>(b.rb[i], code2_s, b.off) : 0.0f;
+    }
+    const float bg = has_bias ? to_f<DT>(static_cast<uint16_t>(b.bg)) : 0.0f;
+    const float bu = has_bias ? to_f<DT>(static_cast<uint16_t>(b.bu)) : 0.0f;
+    while (rows) {
+      const int f = __ffsll(static_cast<long long>(rows)) - 1;
+      rows &= rows - 1;
+      const int tok = f / p.k;
+      asm volatile("" : "+v"(lane_off));  // table addresses recomputed per row, not held
+      float acc_a = 0.0f, acc_b = 0.0f;
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        uint4 xv[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xv[q] = xs[tok * xrow + q * nchunk + cidx[i]];
+        const int sh = kConv ? xsh[tok * nchunk + cidx[i]] : 0;
+        float da = chunk_dot<CDT, false>(b.qa[i], xv, lut_bytes, lane_off);
+        if constexpr (kConv) da = __builtin_amdgcn_ldexpf(da, sh);
+        acc_a += valid[i] ? da * sa[i] : 0.0f;
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (pair) {
+          float db = chunk_dot<CDT, false>(b.qb[i], xv, lut_bytes, lane_off);
+          if constexpr (kConv) db = __builtin_amdgcn_ldexpf(db, sh);
+          acc_b += valid[i] ? db * sb[i] : 0.0f;
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      acc_a = group_reduce<G>(acc_a);
+      if constexpr (pair) acc_b = group_reduce<G>(acc_b);
+      if (live && gl == 0) {
+        const float v = pair ? gated(p.epi, acc_a, acc_b, p.alpha, p.limit, bg, bu) : single(p.epi, acc_a, bg);
+        static_cast<uint16_t*>(p.out)[int64_t(f) * n_out + j] = from_f<DT>(v);
+      }
+    }
+  };
+
+  // Two buffers in turn (named, not an indexed pair, so nothing goes to scratch memory). Every
+  // load is unconditional -- past the last item a wave reloads the item it is about to compute,
+  // which the cache holds -- so the compiler's wait before each compute counts exactly the
+  // loads issued after that item's.
+  int it = static_cast<int>(blockIdx.x) * kItemWaves + wid;
+  if (it >= nitems) return;  // no barrier follows
+  Buf b0, b1;
+  load(it, b0);
+  for (;;) {
+    const int i1 = it + stride;
+    load(i1 < nitems ? i1 : it, b1);
+    compute(it, b0);
+    if (i1 >= nitems) break;
+    const int i2 = i1 + stride;
+    load(i2 < nitems ? i2 : i1, b0);
+    compute(i1, b1);
+    if (i2 >= nitems) break;
+    it = i2;
+  }
+}
+
 // down GEMV over every routed row for kDownCols output columns, then the k-slot combine.
 // Jobs (one routed expert, all kDownCols columns) go to G-lane groups, JOBS per group in flight.
 template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL>

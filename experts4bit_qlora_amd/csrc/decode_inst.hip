@@ -4,6 +4,8 @@
 #include "decode.h"
 #include "decode_launch.h"
 
+#include <algorithm>
+
 #ifndef E4B_INST_DT
 #error "E4B_INST_DT must be defined"
 #endif
@@ -15,12 +17,35 @@ namespace e4b {
 
 namespace {
 
+// compute units of the current device, read once per device
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int v = 0;
+    cus[dev] = (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v : 256;
+  }
+  return cus[dev];
+}
+
 template <int DT, int FMT, int G, int CPL, bool FULL>
 void up_gc(const DecodeArgs& a, int64_t max_active, hipStream_t s) {
   constexpr int cols_per_block = kDecWaves * (kWave / G);
   dim3 grid(static_cast<unsigned>((a.n_out + cols_per_block - 1) / cols_per_block), static_cast<unsigned>(max_active));
   if (is_gated(a.epi)) hipLaunchKernelGGL((decode_up_kernel<DT, FMT, G, CPL, FULL, true>), grid, dim3(kDecThreads), 0, s, a);
   else hipLaunchKernelGGL((decode_up_kernel<DT, FMT, G, CPL, FULL, false>), grid, dim3(kDecThreads), 0, s, a);
+}
+
+// item kernel: one block per CU (its LDS holds one block), no more blocks than items / waves
+template <int DT, int FMT, int G, int CPL, bool FULL>
+void up_items_gc(const DecodeArgs& a, int64_t max_active, hipStream_t s) {
+  constexpr int cols_per_item = kWave / G;
+  const int64_t items = max_active * ((a.n_out + cols_per_item - 1) / cols_per_item);
+  const int64_t blocks = std::min<int64_t>(device_cus(), (items + kItemWaves - 1) / kItemWaves);
+  dim3 grid(static_cast<unsigned>(std::max<int64_t>(blocks, 1)));
+  if (is_gated(a.epi)) hipLaunchKernelGGL((decode_up_items_kernel<DT, FMT, G, CPL, FULL, true>), grid, dim3(kItemThreads), 0, s, a);
+  else hipLaunchKernelGGL((decode_up_items_kernel<DT, FMT, G, CPL, FULL, false>), grid, dim3(kItemThreads), 0, s, a);
 }
 
 template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL>
@@ -33,11 +58,14 @@ void down_gc(const DecodeArgs& a, hipStream_t s) {
 
 template <int DT, int FMT>
 void launch_decode_up(const DecodeArgs& a, DecShape d, int64_t max_active, hipStream_t s) {
-#define E4B_UP(g, c)                                                    \
-  if (d.G == g && d.CPL == c) {                                         \
-    if (d.full) up_gc<DT, FMT, g, c, true>(a, max_active, s);           \
-    else up_gc<DT, FMT, g, c, false>(a, max_active, s);                 \
-    return;                                                             \
+  const bool items = decode_up_items(a.tokens, a.w.k);
+#define E4B_UP(g, c)                                                          \
+  if (d.G == g && d.CPL == c) {                                               \
+    if (items && d.full) up_items_gc<DT, FMT, g, c, true>(a, max_active, s);  \
+    else if (items) up_items_gc<DT, FMT, g, c, false>(a, max_active, s);      \
+    else if (d.full) up_gc<DT, FMT, g, c, true>(a, max_active, s);            \
+    else up_gc<DT, FMT, g, c, false>(a, max_active, s);                       \
+    return;                                                                   \
   }
   E4B_UP(4, 2) E4B_UP(4, 4) E4B_UP(8, 4) E4B_UP(16, 4) E4B_UP(16, 6) E4B_UP(32, 4)
 #undef E4B_UP

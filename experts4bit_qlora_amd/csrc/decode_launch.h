@@ -36,6 +36,11 @@ inline DecShape decode_up_shape(int64_t k) {
   return DecShape{0, 0, 0, false};
 }
 
+// gate_up over work items (decode_up_items_kernel): 2..8 tokens whose activations fit the
+// kernel's 16384-element LDS stage. One token keeps decode_up_kernel, whose blocks each take
+// one routed expert for a column tile with the activations staged once.
+inline bool decode_up_items(int64_t tokens, int64_t k) { return tokens >= 2 && tokens <= 8 && tokens * k <= 16384; }
+
 // down: a group takes one routed expert for all of the block's columns. 32-lane groups (8 per
 // block) whatever the batch, except rows of at most 16 chunks with more than 8 routed rows:
 // 16-lane groups, two jobs in flight. (16-lane groups with two chunks per lane were measured at

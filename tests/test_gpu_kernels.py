@@ -383,6 +383,34 @@ def test_decode_halves_match_oracle(fmt, T):
     assert out.dtype == torch.float32 and fro2 <= 1e-4, ("down+combine", fro2, maxabs2)
 
 
+@pytest.mark.parametrize("fmt", ["nf4", "nf4_dq", "mxfp4"])
+@pytest.mark.parametrize("T,H,epi", [(8, 2048, "swiglu"), (2, 2048, "none"), (8, 1600, "swiglu"),
+                                     (5, 2880, "gptoss"), (6, 2880, "none")])
+def test_decode_items_match_one_token_kernel(fmt, T, H, epi):
+    """2..8 tokens whose activations fit 16384 LDS elements run gate_up as per-wave work items
+    over all tokens at once; one token runs one block per (column tile, routed expert). Both
+    take the same chunk slots, table entries and reduction order per output element, so every
+    h row of a batch equals the same token run alone, bit for bit. Covers the full stage
+    (8 x 2048), rows whose chunk count is not a multiple of the lane group (H = 1600, 2880),
+    the one-token-per-item edge (6 x 2880 > 16384 falls back to the per-expert kernel, also
+    bit-identical) and plain / SwiGLU / gpt-oss epilogues (biases for e2m1 and gpt-oss)."""
+    _announce(f"decode items fmt={fmt} T={T} H={H} epi={epi}")
+    E, I, top = 16, 192, 8
+    gated = epi != "none"
+    w1, _ = _stack(fmt, E, 2 * I if gated else I, H, seed=40)
+    code = {"none": N.EPI_NONE, "swiglu": N.EPI_SWIGLU, "gptoss": N.EPI_GPTOSS}[epi]
+    if fmt == "mxfp4" or epi == "gptoss":  # the gpt-oss epilogue takes the gate_up bias
+        g = torch.Generator().manual_seed(41)
+        w1.bias = (torch.randn(E, w1.n, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    rng = np.random.default_rng(42 + T)
+    idx = torch.from_numpy(np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)).to(DEV)
+    x = (torch.randn(T, H, generator=torch.Generator().manual_seed(43)) * 2).to(torch.bfloat16).to(DEV)
+    h = ops.decode_gate_up(x, idx, w1, code)
+    for t in range(T):
+        one = ops.decode_gate_up(x[t:t + 1], idx[t:t + 1], w1, code)
+        assert np.array_equal(_bits(h[t * top:(t + 1) * top]), _bits(one)), ("token", t)
+
+
 @pytest.mark.parametrize("rows", [65, 600])
 def test_decode_rejects_batches_beyond_its_limit(rows):
     qw, _, _ = _nf4_stack(4, 128, 128, seed=26)
