@@ -18,10 +18,12 @@
 // its use. Each wave computes the routing itself (one id per lane, a per-wave LDS bitmap of
 // routed experts, one LDS atomic per lane for the row masks), so no block barrier waits on it.
 //
-// Weight decode. A 64 KB LDS table holds, for every byte value b, the two codes the byte
+// Weight decode. e2m1 bytes are converted in registers: one v_cvt_scalef32_pk_{bf16,f16}_fp4
+// (scale 1) turns a byte into its two codes as an activation-dtype pair, exact in either type.
+// NF4 goes through a 64 KB LDS table that holds, for every byte value b, the two codes the byte
 // encodes, one 256-byte row per byte value, in one of two forms:
-//   single  one 4-byte entry (two 16-bit codes), 64 copies, lane l reads copy l: e2m1 codes in
-//           the activation dtype (exact in either), and, in the up kernel, NF4 codes in fp16.
+//   single  one 4-byte entry (two 16-bit codes), 64 copies, lane l reads copy l: NF4 codes in
+//           fp16 (up kernels).
 //   split   NF4 codes as activation-dtype pairs hi = dt(code), lo = dt(code - hi), so hi + lo
 //           carries the fp32 code to ~16 significant bits (8-byte entries, 32 copies, lane l
 //           reads copy l % 32): the down kernel, whose activations are read straight from
@@ -249,6 +251,42 @@ E4B_DEV float chunk_dot(const uint4& q, const uint4 (&xq)[4], const char* lut_by
   return acc;
 }
 
+// e2m1 byte SEL of w -> its two codes as a DT pair, the first element (low nibble) in the low
+// half: one v_cvt_scalef32_pk_{bf16,f16}_fp4 with scale 1, exact (every e2m1 value is exact in
+// either type), so it equals the table entry of that byte.
+template <int DT, int SEL>
+E4B_DEV uint32_t fp4_pair(uint32_t w) {
+  if constexpr (DT == E4B_BF16) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, 1.0f, SEL));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, SEL));
+  }
+}
+
+// chunk_dot for e2m1 weights, codes converted in registers: the same v_dot2 sequence on the
+// same operands as the table path, without the table reads.
+template <int DT>
+E4B_DEV float chunk_dot_fp4(const uint4& q, const uint4 (&xq)[4]) {
+  const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+  float acc = 0.0f;
+#pragma unroll
+  for (int wi = 0; wi < 4; ++wi) {
+    acc = dot2<DT>(fp4_pair<DT, 0>(qw[wi]), xq[wi].x, acc);
+    acc = dot2<DT>(fp4_pair<DT, 1>(qw[wi]), xq[wi].y, acc);
+    acc = dot2<DT>(fp4_pair<DT, 2>(qw[wi]), xq[wi].z, acc);
+    acc = dot2<DT>(fp4_pair<DT, 3>(qw[wi]), xq[wi].w, acc);
+  }
+  return acc;
+}
+
+// One 32-value chunk of a weight row against activations: e2m1 converted in registers, NF4
+// looked up in the LDS table (the decode kernels build no table for e2m1).
+template <int DT, int FMT, bool SPLIT>
+E4B_DEV float weight_dot(const uint4& q, const uint4 (&xq)[4], const char* lut_bytes, uint32_t lane_off) {
+  if constexpr (FMT == E4B_FMT_MXFP4) return chunk_dot_fp4<DT>(q, xq);
+  else return chunk_dot<DT, SPLIT>(q, xq, lut_bytes, lane_off);
+}
+
 // bf16 -> scaled fp16 restaging of activations (up kernel, NF4 weights).
 // Largest biased exponent among the 8 bf16 values of a 16-byte piece, in bits 7..14.
 E4B_DEV uint32_t bf16_exp_max(const uint4& v) {
@@ -326,7 +364,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
   // NF4 codes as fp16 single entries; e2m1 codes in the activation dtype
   constexpr int CDT = FMT == E4B_FMT_MXFP4 ? DT : E4B_FP16;
   constexpr bool kConv = CDT != DT;  // bf16 activations restaged as scaled fp16
-  __shared__ __align__(16) uint4 lut[256 * kLutRowBytes / 16];
+  __shared__ __align__(16) uint4 lut[FMT == E4B_FMT_MXFP4 ? 1 : 256 * kLutRowBytes / 16];  // none for e2m1
   __shared__ __align__(16) uint4 xs[kDecMaxK / 8 + 1];  // the activation row being multiplied + a spare slot
   __shared__ int xsh[kConv ? kDecMaxK / 32 + 1 : 1];     // per chunk: the inverse of its restaging shift
   __shared__ WaveRoute route[kDecWaves];
@@ -387,7 +425,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
   };
 
   // the decode table first: its stores then overlap the ids' wait, not the weight issue
-  store_pair_entry<false>(lut, pair_entry<CDT, false>(cf, cs));
+  if constexpr (FMT != E4B_FMT_MXFP4) store_pair_entry<false>(lut, pair_entry<CDT, false>(cf, cs));
 
   // round trip 2: the activation row, then weights and scales chunk by chunk, biases
   load_x(f);
@@ -437,12 +475,12 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) xv[q] = xs[cidx[i] * 4 + q];
       const int sh = kConv ? xsh[cidx[i]] : 0;
-      float da = chunk_dot<CDT, false>(qa[i], xv, lut_bytes, lane_off);
+      float da = weight_dot<CDT, FMT, false>(qa[i], xv, lut_bytes, lane_off);
       if constexpr (kConv) da = __builtin_amdgcn_ldexpf(da, sh);
       acc_a += valid[i] ? da * sa[i] : 0.0f;
       __builtin_amdgcn_sched_barrier(0);  // keep each chunk's 16 table reads together
       if constexpr (pair) {
-        float db = chunk_dot<CDT, false>(qb[i], xv, lut_bytes, lane_off);
+        float db = weight_dot<CDT, FMT, false>(qb[i], xv, lut_bytes, lane_off);
         if constexpr (kConv) db = __builtin_amdgcn_ldexpf(db, sh);
         acc_b += valid[i] ? db * sb[i] : 0.0f;
         __builtin_amdgcn_sched_barrier(0);
@@ -487,7 +525,7 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
   constexpr int CDT = FMT == E4B_FMT_MXFP4 ? DT : E4B_FP16;
   constexpr bool kConv = CDT != DT;
   constexpr int kXU = kItemMaxX / 8 / kItemThreads;  // 16-byte activation pieces per thread
-  __shared__ __align__(16) uint4 lut[256 * kLutRowBytes / 16];
+  __shared__ __align__(16) uint4 lut[FMT == E4B_FMT_MXFP4 ? 1 : 256 * kLutRowBytes / 16];  // none for e2m1
   __shared__ __align__(16) uint4 xs[kItemMaxX / 8 + 1];  // every token's activations + a spare slot
   __shared__ int xsh[kConv ? kItemMaxX / 32 + 1 : 1];     // per chunk: the inverse restaging shift
   __shared__ WaveRoute route[kItemWaves];
@@ -515,7 +553,7 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
   WaveRoute& r = route[wid];
   const int nact = wave_route(row_id(p, M, id_raw), r);
   if (tid < 256) {
-    store_pair_entry<false>(lut, pair_entry<CDT, false>(cf, cs));
+    if constexpr (FMT != E4B_FMT_MXFP4) store_pair_entry<false>(lut, pair_entry<CDT, false>(cf, cs));
     if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[tid] = c2;
   }
   // Piece (token t, chunk c, quarter q) goes to xs[t * xrow + q * nchunk + c]: the G lanes of a
@@ -608,12 +646,12 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
 #pragma unroll
         for (int q = 0; q < 4; ++q) xv[q] = xs[tok * xrow + q * nchunk + cidx[i]];
         const int sh = kConv ? xsh[tok * nchunk + cidx[i]] : 0;
-        float da = chunk_dot<CDT, false>(b.qa[i], xv, lut_bytes, lane_off);
+        float da = weight_dot<CDT, FMT, false>(b.qa[i], xv, lut_bytes, lane_off);
         if constexpr (kConv) da = __builtin_amdgcn_ldexpf(da, sh);
         acc_a += valid[i] ? da * sa[i] : 0.0f;
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (pair) {
-          float db = chunk_dot<CDT, false>(b.qb[i], xv, lut_bytes, lane_off);
+          float db = weight_dot<CDT, FMT, false>(b.qb[i], xv, lut_bytes, lane_off);
           if constexpr (kConv) db = __builtin_amdgcn_ldexpf(db, sh);
           acc_b += valid[i] ? db * sb[i] : 0.0f;
           __builtin_amdgcn_sched_barrier(0);
@@ -653,7 +691,7 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
 // Jobs (one routed expert, all kDownCols columns) go to G-lane groups, JOBS per group in flight.
 template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL>
 __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) {
-  __shared__ __align__(16) uint4 lut[256 * kLutRowBytes / 16];
+  __shared__ __align__(16) uint4 lut[FMT == E4B_FMT_MXFP4 ? 1 : 256 * kLutRowBytes / 16];  // none for e2m1
   __shared__ WaveRoute route[kDecWaves];
   __shared__ float res[kDecMaxRows * kDownCols];
   __shared__ float wts[kDecMaxRows];
@@ -727,7 +765,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
       for (int cl = 0; cl < C; ++cl) bb[t][cl] = bp[has_bias ? cols[cl] : 0];
     }
     if (!table_ready) {
-      store_pair_entry<kSplit>(lut, pair_entry<DT, kSplit>(cf, cs));
+      if constexpr (FMT != E4B_FMT_MXFP4) store_pair_entry<kSplit>(lut, pair_entry<DT, kSplit>(cf, cs));
       if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = c2;
       if (wid == 0) wts[lane] = row_weight(p, wt_bits);  // read by the combine
       __syncthreads();
@@ -757,7 +795,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
         for (int i = 0; i < CPL; ++i) {
 #pragma unroll
           for (int cl = 0; cl < C; ++cl) {
-            const float d = chunk_dot<DT, kSplit>(q[t][i][cl], xv[t][i], lut_bytes, lane_off) * sc[i][cl];
+            const float d = weight_dot<DT, FMT, kSplit>(q[t][i][cl], xv[t][i], lut_bytes, lane_off) * sc[i][cl];
             acc[cl] += valid[i] ? d : 0.0f;
             __builtin_amdgcn_sched_barrier(0);  // keep each chunk's 16 table reads together
           }

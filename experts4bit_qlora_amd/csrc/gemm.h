@@ -98,8 +98,30 @@ E4B_DEV uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) { return (m & a) | (~m 
 // bytes into the (first, second) pairs. Every
 // value is the same fp32 product and rounding as a per-element decode, so the result is
 // bit-identical to the dequantized weights.
+//
+// e2m1 (power-of-two scales): one v_cvt_scalef32_pk_{bf16,f16}_fp4 per byte forms the byte's
+// two values dt(code * scale) directly.
+template <int DT, int SEL>
+E4B_DEV uint32_t fp4_scaled_pair(uint32_t w, float scale) {
+  if constexpr (DT == E4B_BF16) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, SEL));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, scale, SEL));
+  }
+}
+
 template <int DT, int FMT, int NB>
 E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float (&code)[16], float scale, uint32_t (&wv)[NB]) {
+  if constexpr (FMT == E4B_FMT_MXFP4) {
+#pragma unroll
+    for (int wi = 0; wi < NB / 4; ++wi) {
+      wv[4 * wi + 0] = fp4_scaled_pair<DT, 0>(words[wi], scale);
+      wv[4 * wi + 1] = fp4_scaled_pair<DT, 1>(words[wi], scale);
+      wv[4 * wi + 2] = fp4_scaled_pair<DT, 2>(words[wi], scale);
+      wv[4 * wi + 3] = fp4_scaled_pair<DT, 3>(words[wi], scale);
+    }
+    return;
+  }
   uint32_t q[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
