@@ -280,8 +280,13 @@ int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t
   const int64_t nchunks = cdiv(M, e4b::kRouteChunk);
   hipLaunchKernelGGL(e4b::route_count_kernel, dim3(static_cast<unsigned>(nchunks)), dim3(e4b::kRouteChunk), 0, stream,
                      top_k_index, M, num_experts, rt->scratch);
-  hipLaunchKernelGGL(e4b::route_scan_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, nchunks, num_experts,
-                     rt->scratch, *rt);
+  if (nchunks * (int64_t(num_experts) + 1) <= e4b::kScanLdsInts) {
+    hipLaunchKernelGGL(e4b::route_scan_kernel<true>, dim3(1), dim3(e4b::kRouteThreads), 0, stream, nchunks,
+                       num_experts, rt->scratch, *rt);
+  } else {
+    hipLaunchKernelGGL(e4b::route_scan_kernel<false>, dim3(1), dim3(e4b::kRouteThreads), 0, stream, nchunks,
+                       num_experts, rt->scratch, *rt);
+  }
   hipLaunchKernelGGL(e4b::route_place_kernel, dim3(static_cast<unsigned>(nchunks)), dim3(e4b::kRouteChunk), 0, stream,
                      top_k_index, M, num_experts, rt->scratch, *rt);
   return check_launch("route_count/scan/place kernels");

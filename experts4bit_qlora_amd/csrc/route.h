@@ -57,6 +57,34 @@ E4B_DEV int block_exclusive_scan(int v, int* total, int* wsum) {
   return base + x - v;
 }
 
+// Stable rank of each lane's id among the wave's 64 ids: the number of lanes below holding the
+// same id (e < 0 for none; its rank is not used). The ids go through this wave's 16-byte
+// aligned 64-int LDS row s, written and read by the wave alone in program order, and each lane
+// compares its id with all 64, four per 16-byte read: ~200 VALU operations per chunk, where a
+// loop over the distinct ids (ballot, broadcast, cursor read per id) pays an LDS round trip per
+// distinct id.
+E4B_DEV int wave_rank(int e, int* s) {
+  const int lane = threadIdx.x & (kWave - 1);
+  s[lane] = e;
+  __builtin_amdgcn_wave_barrier();
+  const int4* s4 = reinterpret_cast<const int4*>(s);
+  // (the lane index is opaque to the compiler, so its 64 comparisons are not hoisted out of a
+  // caller's loop and held as 64 scalar masks)
+  int ln = lane;
+  asm volatile("" : "+v"(ln));
+  int r = 0;
+#pragma unroll
+  for (int j = 0; j < kWave / 4; ++j) {
+    const int4 v = s4[j];
+    r += (v.x == e && 4 * j + 0 < ln) ? 1 : 0;
+    r += (v.y == e && 4 * j + 1 < ln) ? 1 : 0;
+    r += (v.z == e && 4 * j + 2 < ln) ? 1 : 0;
+    r += (v.w == e && 4 * j + 3 < ln) ? 1 : 0;
+  }
+  __builtin_amdgcn_wave_barrier();
+  return r;
+}
+
 // Offsets, tile list, active list and meta from per-expert totals. Thread t of the 512-thread
 // block owns experts 2t and 2t+1 with totals ta and tb; offa / offb receive their first sorted
 // rows. `dropped` must be the same value in every thread.
@@ -106,6 +134,7 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __r
   __shared__ int cnt[kRouteWaves * kRouteMaxExperts];
   __shared__ int wsum[kRouteWaves];
   __shared__ int dropped;
+  __shared__ __align__(16) int rank_s[kRouteWaves][kWave];
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wid = tid / kWave;
@@ -159,8 +188,10 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __r
   }
   __syncthreads();
 
-  // 3. stable placement, one 64-id chunk at a time per wave, chunks in order.
-  const unsigned long long below = (lane == 0) ? 0ull : ((~0ull) >> (kWave - lane));
+  // 3. stable placement, one 64-id chunk at a time per wave, chunks in order: an id's position
+  // is its expert's cursor plus its rank among the chunk's equal ids; then each id bumps its
+  // expert's cursor (the wave's cursor reads precede its adds in LDS order).
+  int* rs = rank_s[wid];
   for (int64_t base = seg0; base < seg1; base += kWave) {
     const int64_t i = base + lane;
     int e = -1;
@@ -172,20 +203,15 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __r
         rt.inv[i] = -1;
       }
     }
-    unsigned long long pending = __ballot(e >= 0);
-    while (pending) {
-      const int leader = __ffsll(static_cast<long long>(pending)) - 1;
-      const int e0 = __shfl(e, leader);
-      const unsigned long long m = __ballot(e == e0);
-      const int c0 = mycnt[e0];
-      if (e == e0) {
-        const int pos = c0 + __popcll(m & below);
-        rt.sorted_flat[pos] = static_cast<int>(i);
-        rt.inv[i] = pos;
-      }
-      if (lane == leader) mycnt[e0] = c0 + __popcll(m);
-      pending &= ~m;
+    const int rank = wave_rank(e, rs);
+    if (e >= 0) {
+      const int pos = mycnt[e] + rank;
+      rt.sorted_flat[pos] = static_cast<int>(i);
+      rt.inv[i] = pos;
     }
+    __builtin_amdgcn_wave_barrier();
+    if (e >= 0) atomicAdd(&mycnt[e], 1);
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -193,20 +219,6 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __r
 // chunk's dropped ids. A chunk of kRouteChunk ids is one workgroup of 4 waves, 64 ids each.
 
 constexpr int kChunkWaves = kRouteChunk / kWave;
-
-// Visit each distinct expert id of the wave once (e < 0: no id), in order of first lane:
-// f(expert, mask of the lanes holding it).
-template <class F>
-E4B_DEV void for_each_expert(int e, F&& f) {
-  unsigned long long pending = __ballot(e >= 0);
-  while (pending) {
-    const int leader = __ffsll(static_cast<long long>(pending)) - 1;
-    const int e0 = __shfl(e, leader);
-    const unsigned long long m = __ballot(e == e0);
-    f(e0, m);
-    pending &= ~m;
-  }
-}
 
 E4B_DEV int chunk_id(const int64_t* idx, int64_t i, int64_t M, int E, bool& dropped) {
   dropped = false;
@@ -217,16 +229,14 @@ E4B_DEV int chunk_id(const int64_t* idx, int64_t i, int64_t M, int E, bool& drop
   return -1;
 }
 
-// Per-wave histogram of the wave's 64 ids into its LDS row c (E entries), returning the
-// number of dropped ids.
+// Per-wave histogram of the wave's 64 ids into its LDS row c (E entries, one LDS add per id),
+// returning the number of dropped ids.
 E4B_DEV int wave_histogram(int e, bool drop, int* c, int E) {
   const int lane = threadIdx.x & (kWave - 1);
   for (int x = lane; x < E; x += kWave) c[x] = 0;
   __builtin_amdgcn_wave_barrier();
-  for_each_expert(e, [&](int e0, unsigned long long m) {
-    if (lane == 0) c[e0] += __popcll(m);
-    __builtin_amdgcn_wave_barrier();
-  });
+  if (e >= 0) atomicAdd(&c[e], 1);
+  __builtin_amdgcn_wave_barrier();
   return __popcll(__ballot(drop));
 }
 
@@ -258,16 +268,45 @@ __global__ void __launch_bounds__(kRouteChunk) route_count_kernel(const int64_t*
 
 // One workgroup: totals, tables, and counts rewritten in place as each chunk's first sorted
 // row per expert (column E untouched). `per` threads share an expert, each summing a
-// contiguous span of chunks, so the column sums take a few batched round trips.
+// contiguous span of chunks. With LDS, the whole [nchunks, E + 1] count matrix (at most
+// kScanLdsInts entries) is first copied into LDS with every load in flight at once, the sums
+// and the rewrite run there, and the rewritten matrix is stored back; without it, the column
+// sums read global memory a few batched round trips at a time.
+constexpr int kScanLdsInts = 24576;
+
+template <bool LDS>
 __global__ void __launch_bounds__(kRouteThreads) route_scan_kernel(int64_t nchunks, int E, int32_t* __restrict__ counts,
                                                                    e4b_routing rt) {
   __shared__ int tot[kRouteMaxExperts];
   __shared__ int part[kRouteMaxExperts * 8];
   __shared__ int wsum[kRouteWaves];
+  __shared__ int cs[LDS ? kScanLdsInts : 1];
   const int tid = threadIdx.x;
   const int64_t pitch = E + 1;
+  auto at = [&](int64_t x) -> int& {
+    if constexpr (LDS) return cs[x];
+    else return counts[x];
+  };
+  constexpr int kU = kScanLdsInts / kRouteThreads;  // every load of the copy in flight at once
+  const int total = static_cast<int>(LDS ? nchunks * pitch : 0);
+  if constexpr (LDS) {
+    for (int x0 = 0; x0 < total; x0 += kRouteThreads * kU) {
+      int v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int x = x0 + u * kRouteThreads + tid;
+        v[u] = counts[x < total ? x : 0];
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int x = x0 + u * kRouteThreads + tid;
+        if (x < total) cs[x] = v[u];
+      }
+    }
+    __syncthreads();
+  }
   int per = 1;
-  while (per < 8 && per * 2 * E <= kRouteThreads) per *= 2;
+  while (per < 8 && per * 2 * E <= (LDS ? 2 : 1) * kRouteThreads) per *= 2;
   const int epp = kRouteThreads / per;  // experts per pass
   const int64_t span = (nchunks + per - 1) / per;
 
@@ -277,12 +316,12 @@ __global__ void __launch_bounds__(kRouteThreads) route_scan_kernel(int64_t nchun
     if (e < E) {
       const int64_t b1 = min(nchunks, (q + 1) * span);
 #pragma unroll 8
-      for (int64_t b = q * span; b < b1; ++b) sum += counts[b * pitch + e];
+      for (int64_t b = q * span; b < b1; ++b) sum += at(b * pitch + e);
       part[e * per + q] = sum;
     }
   }
   int nd = 0;
-  for (int64_t b = tid; b < nchunks; b += kRouteThreads) nd += counts[b * pitch + E];
+  for (int64_t b = tid; b < nchunks; b += kRouteThreads) nd += at(b * pitch + E);
   __syncthreads();
   for (int x = tid; x < E; x += kRouteThreads) {
     int t = 0;
@@ -304,18 +343,29 @@ __global__ void __launch_bounds__(kRouteThreads) route_scan_kernel(int64_t nchun
       int run = tot[e];
       for (int r = 0; r < q; ++r) run += part[e * per + r];
       const int64_t b1 = min(nchunks, (q + 1) * span);
-      for (int64_t b = q * span; b < b1; ++b) {
-        const int c = counts[b * pitch + e];
-        counts[b * pitch + e] = run;
-        run += c;
+      // 16 counts read before any is rewritten, so the reads are not ordered behind the writes
+      for (int64_t b0 = q * span; b0 < b1; b0 += 16) {
+        int cv[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) cv[u] = (b0 + u < b1) ? at((b0 + u) * pitch + e) : 0;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          if (b0 + u < b1) at((b0 + u) * pitch + e) = run;
+          run += cv[u];
+        }
       }
     }
+  }
+  if constexpr (LDS) {
+    __syncthreads();
+    for (int x = tid; x < total; x += kRouteThreads) counts[x] = cs[x];
   }
 }
 
 __global__ void __launch_bounds__(kRouteChunk) route_place_kernel(const int64_t* __restrict__ idx, int64_t M, int E,
                                                                   const int32_t* __restrict__ counts, e4b_routing rt) {
   __shared__ int c[kChunkWaves][kRouteMaxExperts];
+  __shared__ __align__(16) int rank_s[kChunkWaves][kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
   const int64_t i = int64_t(blockIdx.x) * kRouteChunk + threadIdx.x;
@@ -336,16 +386,12 @@ __global__ void __launch_bounds__(kRouteChunk) route_place_kernel(const int64_t*
   }
   __syncthreads();
   if (drop) rt.inv[i] = -1;
-  int* cur = c[wid];
-  const unsigned long long below = (lane == 0) ? 0ull : ((~0ull) >> (kWave - lane));
-  for_each_expert(e, [&](int e0, unsigned long long m) {
-    const int c0 = cur[e0];
-    if (e == e0) {
-      const int pos = c0 + __popcll(m & below);
-      rt.sorted_flat[pos] = static_cast<int>(i);
-      rt.inv[i] = pos;
-    }
-  });
+  const int rank = wave_rank(e, rank_s[wid]);
+  if (e >= 0) {
+    const int pos = c[wid][e] + rank;
+    rt.sorted_flat[pos] = static_cast<int>(i);
+    rt.inv[i] = pos;
+  }
 }
 
 // out[t, :] = out_t( sum_s float(down[inv[t*k+s], :]) * w[t, s] ), s ascending, fp32 adds of

@@ -242,6 +242,34 @@ def test_grouped_gemm_plain(path, fmt, T):
     assert out32.dtype == torch.float32 and fro32 < 1e-5, fro32
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_mxfp4_mfma_weights_at_every_scale(dt):
+    """One-hot activations turn the MFMA GEMM's output into the weights it multiplies: row i of
+    the output is column i of W (one product by 1.0, the rest zeros, fp32 accumulation). The
+    stack cycles through every e8m0 scale whose largest product stays finite in the activation
+    type (bf16: 0..252, fp16: 0..140; an inf weight would turn the zero products into NaN), so
+    the in-register scaled e2m1 conversion is pinned bit for bit to dt(ldexp(code, e - 127)) of
+    the oracle, subnormal results included (zeros compared without their sign)."""
+    _announce(f"mxfp4 mfma weights at every scale dt={dt}")
+    n, k = 128, 512
+    emax = 252 if dt == torch.bfloat16 else 140
+    rng = np.random.default_rng(50)
+    blocks = rng.integers(0, 256, size=(n, k // 32, 16), dtype=np.uint8)
+    scales = (np.arange(n * (k // 32)) % (emax + 1)).astype(np.uint8).reshape(n, k // 32)
+    qw = ops.mxfp4_qweight(torch.from_numpy(blocks).reshape(1, -1).to(DEV),
+                           torch.from_numpy(scales).reshape(1, -1).to(DEV), n, k, num_experts=1)
+    want = oq.dequant_mxfp4_rows(blocks, scales, "bf16" if dt == torch.bfloat16 else "fp16").T
+    x = torch.eye(k, dtype=dt)
+    rb = ops.route(torch.zeros(k, 1, dtype=torch.int64, device=DEV), 1)
+    out = ops.grouped_gemm(x.to(DEV), qw, rb, k, k, N.EPI_NONE, gather_k=1, path=N.PATH_MFMA)
+    got = _bits(out)
+    exp = (numerics.f32_to_bf16_bits(want) if dt == torch.bfloat16
+           else np.ascontiguousarray(want.astype(np.float16)).view(np.uint16)).copy()
+    # a -0 weight (e2m1 code 8) comes out +0: the fp32 sum adds +0 products to it
+    exp[exp == 0x8000] = 0
+    assert np.array_equal(got, exp), int((got != exp).sum())
+
+
 @pytest.mark.parametrize("path", [N.PATH_GEMV, N.PATH_MFMA])
 @pytest.mark.parametrize("epi", ["swiglu", "act", "clamp", "gptoss"])
 def test_grouped_gemm_fused_epilogues(path, epi):
