@@ -287,6 +287,78 @@ E4B_DEV float weight_dot(const uint4& q, const uint4 (&xq)[4], const char* lut_b
   else return chunk_dot<DT, SPLIT>(q, xq, lut_bytes, lane_off);
 }
 
+// The 16 single-table entries of one chunk's bytes (byte b of word wi -> t[4 * wi + b]).
+E4B_DEV void lut_lookup(const uint4& q, const char* lut_bytes, uint32_t lane_off, uint32_t (&t)[16]) {
+  const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int wi = 0; wi < 4; ++wi)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t addr = __builtin_amdgcn_perm(lane_off, qw[wi], 0x0c0c0004u | (static_cast<uint32_t>(b) << 8));
+      t[4 * wi + b] = *reinterpret_cast<const uint32_t*>(lut_bytes + addr);
+    }
+}
+
+// chunk_dot over entries already read: the same v_dot2 sequence on the same operands.
+template <int DT>
+E4B_DEV float lut_dot(const uint32_t (&t)[16], const uint4 (&xq)[4]) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int wi = 0; wi < 4; ++wi) {
+    acc = dot2<DT>(t[4 * wi + 0], xq[wi].x, acc);
+    acc = dot2<DT>(t[4 * wi + 1], xq[wi].y, acc);
+    acc = dot2<DT>(t[4 * wi + 2], xq[wi].z, acc);
+    acc = dot2<DT>(t[4 * wi + 3], xq[wi].w, acc);
+  }
+  return acc;
+}
+
+// A lane's CPL chunks of one weight row (qa), and of its gate partner (qb) when PAIR, against
+// the activation chunks xread(i, xv) fills (returning the chunk's restaging shift):
+// fin_a(i, dot, shift) / fin_b(i, dot, shift) take each chunk's unscaled dot product in chunk
+// order. With AHEAD, single-table NF4 reads chunk i + 1's entries before the dot products of
+// chunk i, so the table round trip of one chunk overlaps the arithmetic of the previous
+// (OLMoE bs=1 gate_up: 8.03 -> 7.45 us per launch; it holds 32 more registers); e2m1 converts
+// in registers.
+template <int DT, int FMT, int CPL, bool PAIR, bool AHEAD, class XR, class FA, class FB>
+E4B_DEV void pair_chunk_dots(const uint4 (&qa)[CPL], const uint4 (&qb)[CPL], const char* lut_bytes,
+                             uint32_t lane_off, XR&& xread, FA&& fin_a, FB&& fin_b) {
+  if constexpr (FMT == E4B_FMT_MXFP4 || !AHEAD) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      uint4 xv[4];
+      const int sh = xread(i, xv);
+      fin_a(i, weight_dot<DT, FMT, false>(qa[i], xv, lut_bytes, lane_off), sh);
+      __builtin_amdgcn_sched_barrier(0);  // keep each chunk's table reads together
+      if constexpr (PAIR) {
+        fin_b(i, weight_dot<DT, FMT, false>(qb[i], xv, lut_bytes, lane_off), sh);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  } else {
+    uint32_t ta[16], tb[16];
+    lut_lookup(qa[0], lut_bytes, lane_off, ta);
+    if constexpr (PAIR) lut_lookup(qb[0], lut_bytes, lane_off, tb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      constexpr int kLast = CPL - 1;
+      uint4 xv[4];
+      const int sh = xread(i, xv);
+      const float da = lut_dot<DT>(ta, xv);
+      if (i < kLast) lut_lookup(qa[i < kLast ? i + 1 : i], lut_bytes, lane_off, ta);
+      __builtin_amdgcn_sched_barrier(0);
+      fin_a(i, da, sh);
+      if constexpr (PAIR) {
+        const float db = lut_dot<DT>(tb, xv);
+        if (i < kLast) lut_lookup(qb[i < kLast ? i + 1 : i], lut_bytes, lane_off, tb);
+        __builtin_amdgcn_sched_barrier(0);
+        fin_b(i, db, sh);
+      }
+    }
+  }
+}
+
 // bf16 -> scaled fp16 restaging of activations (up kernel, NF4 weights).
 // Largest biased exponent among the 8 bf16 values of a 16-byte piece, in bits 7..14.
 E4B_DEV uint32_t bf16_exp_max(const uint4& v) {
@@ -469,23 +541,21 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
     // recomputing them per row keeps 128 addresses from being hoisted and held in registers
     asm volatile("" : "+v"(lane_off));
     float acc_a = 0.0f, acc_b = 0.0f;
+    pair_chunk_dots<CDT, FMT, CPL, pair, true>(
+        qa, qb, lut_bytes, lane_off,
+        [&](int i, uint4 (&xv)[4]) {
 #pragma unroll
-    for (int i = 0; i < CPL; ++i) {
-      uint4 xv[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) xv[q] = xs[cidx[i] * 4 + q];
-      const int sh = kConv ? xsh[cidx[i]] : 0;
-      float da = weight_dot<CDT, FMT, false>(qa[i], xv, lut_bytes, lane_off);
-      if constexpr (kConv) da = __builtin_amdgcn_ldexpf(da, sh);
-      acc_a += valid[i] ? da * sa[i] : 0.0f;
-      __builtin_amdgcn_sched_barrier(0);  // keep each chunk's 16 table reads together
-      if constexpr (pair) {
-        float db = weight_dot<CDT, FMT, false>(qb[i], xv, lut_bytes, lane_off);
-        if constexpr (kConv) db = __builtin_amdgcn_ldexpf(db, sh);
-        acc_b += valid[i] ? db * sb[i] : 0.0f;
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
+          for (int q = 0; q < 4; ++q) xv[q] = xs[cidx[i] * 4 + q];
+          return kConv ? xsh[cidx[i]] : 0;
+        },
+        [&](int i, float d, int sh) {
+          if constexpr (kConv) d = __builtin_amdgcn_ldexpf(d, sh);
+          acc_a += valid[i] ? d * sa[i] : 0.0f;
+        },
+        [&](int i, float d, int sh) {
+          if constexpr (kConv) d = __builtin_amdgcn_ldexpf(d, sh);
+          acc_b += valid[i] ? d * sb[i] : 0.0f;
+        });
     acc_a = group_reduce<G>(acc_a);
     if constexpr (pair) acc_b = group_reduce<G>(acc_b);
     if (live && gl == 0) {
@@ -640,23 +710,22 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
       const int tok = f / p.k;
       asm volatile("" : "+v"(lane_off));  // table addresses recomputed per row, not held
       float acc_a = 0.0f, acc_b = 0.0f;
+      // (no look-ahead past four chunks per lane: with two weight buffers it spills)
+      pair_chunk_dots<CDT, FMT, CPL, pair, (CPL <= 4)>(
+          b.qa, b.qb, lut_bytes, lane_off,
+          [&](int i, uint4 (&xv)[4]) {
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) {
-        uint4 xv[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) xv[q] = xs[tok * xrow + q * nchunk + cidx[i]];
-        const int sh = kConv ? xsh[tok * nchunk + cidx[i]] : 0;
-        float da = weight_dot<CDT, FMT, false>(b.qa[i], xv, lut_bytes, lane_off);
-        if constexpr (kConv) da = __builtin_amdgcn_ldexpf(da, sh);
-        acc_a += valid[i] ? da * sa[i] : 0.0f;
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (pair) {
-          float db = weight_dot<CDT, FMT, false>(b.qb[i], xv, lut_bytes, lane_off);
-          if constexpr (kConv) db = __builtin_amdgcn_ldexpf(db, sh);
-          acc_b += valid[i] ? db * sb[i] : 0.0f;
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
+            for (int q = 0; q < 4; ++q) xv[q] = xs[tok * xrow + q * nchunk + cidx[i]];
+            return kConv ? xsh[tok * nchunk + cidx[i]] : 0;
+          },
+          [&](int i, float d, int sh) {
+            if constexpr (kConv) d = __builtin_amdgcn_ldexpf(d, sh);
+            acc_a += valid[i] ? d * sa[i] : 0.0f;
+          },
+          [&](int i, float d, int sh) {
+            if constexpr (kConv) d = __builtin_amdgcn_ldexpf(d, sh);
+            acc_b += valid[i] ? d * sb[i] : 0.0f;
+          });
       acc_a = group_reduce<G>(acc_a);
       if constexpr (pair) acc_b = group_reduce<G>(acc_b);
       if (live && gl == 0) {

@@ -376,25 +376,27 @@ def _stack(fmt, E, n, k, seed):
     return qw, _dense_from_kernel(qw).astype(np.float64)  # the exact fp32 code * absmax
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("fmt", ["nf4", "nf4_dq", "mxfp4"])
 @pytest.mark.parametrize("T", [1, 5, 32])
-def test_decode_halves_match_oracle(fmt, T):
+def test_decode_halves_match_oracle(fmt, T, dt):
     """e4b_decode_gate_up (wave-local routing + gate_up + epilogue, h in flat order) and
-    e4b_decode_down_combine (down + k-slot combine) against the fp64 oracle per flat row.
-    T=32 with top-2 over 8 experts fills the 64-row limit with ~8 rows per expert."""
-    _announce(f"decode halves fmt={fmt} T={T}")
+    e4b_decode_down_combine (down + k-slot combine) against the fp64 oracle per flat row, in
+    both activation types. T=32 with top-2 over 8 experts fills the 64-row limit with ~8 rows
+    per expert; T=5 runs the per-wave item kernel, T=1 and T=32 the per-expert one."""
+    _announce(f"decode halves fmt={fmt} T={T} dt={dt}")
     E, H, I, top = 8, 768, 320, 2
     w1, W1 = _stack(fmt, E, 2 * I, H, seed=20)
     w2, W2 = _stack(fmt, E, H, I, seed=21)
     epi, spec = N.EPI_SWIGLU, "swiglu"
     if fmt == "mxfp4":
         g = torch.Generator().manual_seed(22)
-        w1.bias = (torch.randn(E, 2 * I, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
-        w2.bias = (torch.randn(E, H, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+        w1.bias = (torch.randn(E, 2 * I, generator=g) * 0.1).to(dt).to(DEV)  # biases in the activation type
+        w2.bias = (torch.randn(E, H, generator=g) * 0.1).to(dt).to(DEV)
         epi, spec = N.EPI_GPTOSS, ("gptoss", 1.702, 7.0)
     rng = np.random.default_rng(23 + T)
     idx = np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)
-    x = (torch.randn(T, H, generator=torch.Generator().manual_seed(24)) * 2).to(torch.bfloat16)
+    x = (torch.randn(T, H, generator=torch.Generator().manual_seed(24)) * 2).to(dt)
     wts = torch.rand(T, top, generator=torch.Generator().manual_seed(25)).to(torch.bfloat16)
     h = ops.decode_gate_up(x.to(DEV), torch.from_numpy(idx).to(DEV), w1, epi)
     flat_e = idx.reshape(-1)
@@ -411,10 +413,11 @@ def test_decode_halves_match_oracle(fmt, T):
     assert out.dtype == torch.float32 and fro2 <= 1e-4, ("down+combine", fro2, maxabs2)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("fmt", ["nf4", "nf4_dq", "mxfp4"])
 @pytest.mark.parametrize("T,H,epi", [(8, 2048, "swiglu"), (2, 2048, "none"), (8, 1600, "swiglu"),
                                      (5, 2880, "gptoss"), (6, 2880, "none")])
-def test_decode_items_match_one_token_kernel(fmt, T, H, epi):
+def test_decode_items_match_one_token_kernel(fmt, T, H, epi, dt):
     """2..8 tokens whose activations fit 16384 LDS elements run gate_up as per-wave work items
     over all tokens at once; one token runs one block per (column tile, routed expert). Both
     take the same chunk slots, table entries and reduction order per output element, so every
@@ -422,17 +425,17 @@ def test_decode_items_match_one_token_kernel(fmt, T, H, epi):
     (8 x 2048), rows whose chunk count is not a multiple of the lane group (H = 1600, 2880),
     the one-token-per-item edge (6 x 2880 > 16384 falls back to the per-expert kernel, also
     bit-identical) and plain / SwiGLU / gpt-oss epilogues (biases for e2m1 and gpt-oss)."""
-    _announce(f"decode items fmt={fmt} T={T} H={H} epi={epi}")
+    _announce(f"decode items fmt={fmt} T={T} H={H} epi={epi} dt={dt}")
     E, I, top = 16, 192, 8
     gated = epi != "none"
     w1, _ = _stack(fmt, E, 2 * I if gated else I, H, seed=40)
     code = {"none": N.EPI_NONE, "swiglu": N.EPI_SWIGLU, "gptoss": N.EPI_GPTOSS}[epi]
     if fmt == "mxfp4" or epi == "gptoss":  # the gpt-oss epilogue takes the gate_up bias
         g = torch.Generator().manual_seed(41)
-        w1.bias = (torch.randn(E, w1.n, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+        w1.bias = (torch.randn(E, w1.n, generator=g) * 0.1).to(dt).to(DEV)
     rng = np.random.default_rng(42 + T)
     idx = torch.from_numpy(np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)).to(DEV)
-    x = (torch.randn(T, H, generator=torch.Generator().manual_seed(43)) * 2).to(torch.bfloat16).to(DEV)
+    x = (torch.randn(T, H, generator=torch.Generator().manual_seed(43)) * 2).to(dt).to(DEV)
     h = ops.decode_gate_up(x, idx, w1, code)
     for t in range(T):
         one = ops.decode_gate_up(x[t:t + 1], idx[t:t + 1], w1, code)
