@@ -313,6 +313,34 @@ E4B_DEV float lut_dot(const uint32_t (&t)[16], const uint4 (&xq)[4]) {
   return acc;
 }
 
+// The split-table counterparts: (hi, lo) entries of one chunk's bytes, and their dot products
+// in chunk_dot<DT, true>'s order.
+E4B_DEV void lut_lookup_split(const uint4& q, const char* lut_bytes, uint32_t lane_off, uint2 (&t)[16]) {
+  const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int wi = 0; wi < 4; ++wi)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t addr = __builtin_amdgcn_perm(lane_off, qw[wi], 0x0c0c0004u | (static_cast<uint32_t>(b) << 8));
+      t[4 * wi + b] = *reinterpret_cast<const uint2*>(lut_bytes + addr);
+    }
+}
+
+template <int DT>
+E4B_DEV float lut_dot_split(const uint2 (&t)[16], const uint4 (&xq)[4]) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int wi = 0; wi < 4; ++wi) {
+    const uint32_t xs[4] = {xq[wi].x, xq[wi].y, xq[wi].z, xq[wi].w};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      acc = dot2<DT>(t[4 * wi + b].x, xs[b], acc);
+      acc = dot2<DT>(t[4 * wi + b].y, xs[b], acc);
+    }
+  }
+  return acc;
+}
+
 // A lane's CPL chunks of one weight row (qa), and of its gate partner (qb) when PAIR, against
 // the activation chunks xread(i, xv) fills (returning the chunk's restaging shift):
 // fin_a(i, dot, shift) / fin_b(i, dot, shift) take each chunk's unscaled dot product in chunk
@@ -860,13 +888,28 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
         float acc[C];
 #pragma unroll
         for (int cl = 0; cl < C; ++cl) acc[cl] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < CPL; ++i) {
+        if constexpr (kSplit && CPL == 1) {
+          // (chunk, column) pairs in order, the next pair's table entries read before the
+          // current pair's dot products (CPL == 1: beyond it the extra 32 registers spill)
+          uint2 te[16];
+          lut_lookup_split(q[t][0][0], lut_bytes, lane_off, te);
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int cl = 0; cl < C; ++cl) {
-            const float d = weight_dot<DT, FMT, kSplit>(q[t][i][cl], xv[t][i], lut_bytes, lane_off) * sc[i][cl];
-            acc[cl] += valid[i] ? d : 0.0f;
-            __builtin_amdgcn_sched_barrier(0);  // keep each chunk's 16 table reads together
+            const float d = lut_dot_split<DT>(te, xv[t][0]) * sc[0][cl];
+            if (cl + 1 < C) lut_lookup_split(q[t][0][cl + 1 < C ? cl + 1 : cl], lut_bytes, lane_off, te);
+            __builtin_amdgcn_sched_barrier(0);
+            acc[cl] += valid[0] ? d : 0.0f;
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < CPL; ++i) {
+#pragma unroll
+            for (int cl = 0; cl < C; ++cl) {
+              const float d = weight_dot<DT, FMT, kSplit>(q[t][i][cl], xv[t][i], lut_bytes, lane_off) * sc[i][cl];
+              acc[cl] += valid[i] ? d : 0.0f;
+              __builtin_amdgcn_sched_barrier(0);  // keep each chunk's 16 table reads together
+            }
           }
         }
 #pragma unroll
