@@ -415,18 +415,19 @@ def test_decode_halves_match_oracle(fmt, T, dt):
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("fmt", ["nf4", "nf4_dq", "mxfp4"])
-@pytest.mark.parametrize("T,H,epi", [(8, 2048, "swiglu"), (2, 2048, "none"), (8, 1600, "swiglu"),
-                                     (5, 2880, "gptoss"), (6, 2880, "none")])
-def test_decode_items_match_one_token_kernel(fmt, T, H, epi, dt):
+@pytest.mark.parametrize("T,H,I,epi", [(8, 2048, 192, "swiglu"), (2, 2048, 192, "none"), (8, 1600, 192, "swiglu"),
+                                       (5, 2880, 192, "gptoss"), (6, 2880, 192, "none"), (3, 2048, 190, "swiglu")])
+def test_decode_items_match_one_token_kernel(fmt, T, H, I, epi, dt):
     """2..8 tokens whose activations fit 16384 LDS elements run gate_up as per-wave work items
     over all tokens at once; one token runs one block per (column tile, routed expert). Both
     take the same chunk slots, table entries and reduction order per output element, so every
     h row of a batch equals the same token run alone, bit for bit. Covers the full stage
     (8 x 2048), rows whose chunk count is not a multiple of the lane group (H = 1600, 2880),
     the one-token-per-item edge (6 x 2880 > 16384 falls back to the per-expert kernel, also
-    bit-identical) and plain / SwiGLU / gpt-oss epilogues (biases for e2m1 and gpt-oss)."""
-    _announce(f"decode items fmt={fmt} T={T} H={H} epi={epi} dt={dt}")
-    E, I, top = 16, 192, 8
+    bit-identical), output widths that leave the last item's columns partly past the end
+    (I = 190) and plain / SwiGLU / gpt-oss epilogues (biases for e2m1 and gpt-oss)."""
+    _announce(f"decode items fmt={fmt} T={T} H={H} I={I} epi={epi} dt={dt}")
+    E, top = 16, 8
     gated = epi != "none"
     w1, _ = _stack(fmt, E, 2 * I if gated else I, H, seed=40)
     code = {"none": N.EPI_NONE, "swiglu": N.EPI_SWIGLU, "gptoss": N.EPI_GPTOSS}[epi]
