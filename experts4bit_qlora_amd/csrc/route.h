@@ -489,27 +489,43 @@ __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ d
       float acc[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
-      for (int s = 0; s < k; ++s) {
-        const int r = inv[t * k + s];
-        if (r < 0) continue;
-        const float w = load_weight<WDT>(wts, t * k + s);
-        float dv[8];
-        if constexpr (DDT == E4B_FP32) {
-          const float4* dp = reinterpret_cast<const float4*>(static_cast<const float*>(down) + int64_t(r) * H + 8 * c);
-          const float4 d0 = dp[0], d1 = dp[1];
-          dv[0] = d0.x; dv[1] = d0.y; dv[2] = d0.z; dv[3] = d0.w;
-          dv[4] = d1.x; dv[5] = d1.y; dv[6] = d1.z; dv[7] = d1.w;
-        } else {
-          const uint4 d = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(down) + int64_t(r) * H + 8 * c);
-          const uint32_t q[4] = {d.x, d.y, d.z, d.w};
+      // slots eight at a time: every load of the eight is issued before the in-order sum (a
+      // dropped slot reads row 0 and is left out by a select, not a branch around its loads)
+      constexpr int kS = 8;
+      for (int s0 = 0; s0 < k; s0 += kS) {
+        int rr[kS];
+        bool ok[kS];
+        float w[kS], dv[kS][8];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            dv[2 * j] = lo_f<DDT>(q[j]);
-            dv[2 * j + 1] = hi_f<DDT>(q[j]);
+        for (int u = 0; u < kS; ++u) {
+          const int s = s0 + u < k ? s0 + u : k - 1;
+          rr[u] = inv[t * k + s];
+          w[u] = load_weight<WDT>(wts, t * k + s);
+          ok[u] = s0 + u < k && rr[u] >= 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kS; ++u) {
+          const int64_t r = rr[u] >= 0 ? rr[u] : 0;
+          if constexpr (DDT == E4B_FP32) {
+            const float4* dp = reinterpret_cast<const float4*>(static_cast<const float*>(down) + r * H + 8 * c);
+            const float4 d0 = dp[0], d1 = dp[1];
+            dv[u][0] = d0.x; dv[u][1] = d0.y; dv[u][2] = d0.z; dv[u][3] = d0.w;
+            dv[u][4] = d1.x; dv[u][5] = d1.y; dv[u][6] = d1.z; dv[u][7] = d1.w;
+          } else {
+            const uint4 d = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(down) + r * H + 8 * c);
+            const uint32_t q[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              dv[u][2 * j] = lo_f<DDT>(q[j]);
+              dv[u][2 * j + 1] = hi_f<DDT>(q[j]);
+            }
           }
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = __fadd_rn(acc[j], mul_f32(dv[j], w));
+        for (int u = 0; u < kS; ++u) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[j] = ok[u] ? __fadd_rn(acc[j], mul_f32(dv[u][j], w[u])) : acc[j];
+        }
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j) store_out<ODT>(out, t * H + 8 * c + j, acc[j]);
