@@ -366,7 +366,6 @@ __global__ void __launch_bounds__(kRouteChunk) route_place_kernel(const int64_t*
                                                                   const int32_t* __restrict__ counts, e4b_routing rt) {
   __shared__ int c[kChunkWaves][kRouteMaxExperts];
   __shared__ __align__(16) int rank_s[kChunkWaves][kWave];
-  const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
   const int64_t i = int64_t(blockIdx.x) * kRouteChunk + threadIdx.x;
   bool drop;
