@@ -2,7 +2,10 @@
 //
 //   decode_up_kernel    block (column tile, a): gate_up GEMV of the a-th routed expert (ascending
 //                       id) for a tile of output columns, fused epilogue, writes h[flat, :]
-//                       (flat = token * k + slot).
+//                       (flat = token * k + slot). One token.
+//   decode_up_items_kernel  the same GEMV for 2..8 tokens whose activations fit in LDS: one
+//                       block per CU stages every token once, and its waves take (routed
+//                       expert, column group) items in turn.
 //   decode_down_kernel  block = kDownCols output columns: the down GEMV of every routed row for
 //                       those columns, then the deterministic k-slot combine of the columns in
 //                       slot order -- the combine never leaves the block. A G-lane group takes
