@@ -5,6 +5,7 @@
 #include "decode_launch.h"
 
 #include <algorithm>
+#include <atomic>
 
 #ifndef E4B_INST_DT
 #error "E4B_INST_DT must be defined"
@@ -17,16 +18,19 @@ namespace e4b {
 
 namespace {
 
-// compute units of the current device, read once per device
+// compute units of the current device, read once per device (threads racing on the first
+// read store the same value)
 int device_cus() {
-  static int cus[64] = {};
+  static std::atomic<int> cus[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
+  int c = cus[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
     int v = 0;
-    cus[dev] = (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v : 256;
+    c = (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v : 256;
+    cus[dev].store(c, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return c;
 }
 
 template <int DT, int FMT, int G, int CPL, bool FULL>
