@@ -16,6 +16,7 @@
 #include "dequant.h"
 #include "gemm.h"
 #include "gemv.h"
+#include "lora.h"
 #include "route.h"
 
 namespace {
@@ -340,6 +341,51 @@ int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e
   const int64_t max_active = std::min<int64_t>(w->num_experts, M);
   return act_dtype == E4B_BF16 ? launch_gemm_dt<E4B_BF16>(args, gemv, max_active, stream)
                                : launch_gemm_dt<E4B_FP16>(args, gemv, max_active, stream);
+}
+
+int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
+                   int32_t num_experts, const void* lora_a, const void* lora_b, int32_t adapter_dtype,
+                   int32_t rank, int64_t in_features, int64_t out_features, float scaling,
+                   int32_t delta_dtype, float* t_workspace, float* out, hipStream_t stream) {
+  if (!act_dtype_ok(x_dtype)) return fail(E4B_EINVAL, "x_dtype must be bf16 or fp16 (got %d)", x_dtype);
+  if (!any_dtype_ok(adapter_dtype) || !any_dtype_ok(delta_dtype)) return fail(E4B_EINVAL, "bad adapter/delta dtype");
+  if (M < 0 || M > 0x7fffffffLL) return fail(E4B_EINVAL, "bad row count %lld", (long long)M);
+  if (num_experts <= 0 || num_experts > 1024) return fail(E4B_EUNSUPPORTED, "num_experts=%d outside [1, 1024]", num_experts);
+  if (rank <= 0 || rank > e4b::kLoraMaxRank) return fail(E4B_EUNSUPPORTED, "rank=%d outside [1, %d]", rank, e4b::kLoraMaxRank);
+  if (in_features <= 0 || in_features % 8 != 0 || out_features <= 0)
+    return fail(E4B_EINVAL, "in_features (%lld) must be a positive multiple of 8, out_features (%lld) positive",
+                (long long)in_features, (long long)out_features);
+  if (gather_k < 0) return fail(E4B_EINVAL, "gather_k must be >= 0");
+  if (!rt || !rt->offsets || (gather_k > 0 && !rt->sorted_flat)) return fail(E4B_EINVAL, "routing offsets / order are NULL");
+  if (M == 0) return E4B_OK;
+  if (!x || !lora_a || !lora_b || !t_workspace || !out) return fail(E4B_EINVAL, "NULL pointer");
+  if (!aligned16(x) || !aligned16(lora_a)) return fail(E4B_EINVAL, "x and lora_a must be 16-byte aligned");
+  constexpr int kRowsPerBlock = e4b::kLoraThreads / e4b::kWave;
+  const dim3 ga(static_cast<unsigned>(cdiv(M, kRowsPerBlock)));
+#define E4B_LA(XD, AD)                                                                                       \
+  if (x_dtype == XD && adapter_dtype == AD)                                                                  \
+    hipLaunchKernelGGL((e4b::lora_a_kernel<XD, AD>), ga, dim3(e4b::kLoraThreads), 0, stream,                 \
+                       static_cast<const uint16_t*>(x), gather_k, rt->sorted_flat, rt->offsets, num_experts, \
+                       lora_a, rank, in_features, t_workspace, M);
+  E4B_LA(E4B_BF16, E4B_BF16) E4B_LA(E4B_BF16, E4B_FP16) E4B_LA(E4B_BF16, E4B_FP32)
+  E4B_LA(E4B_FP16, E4B_BF16) E4B_LA(E4B_FP16, E4B_FP16) E4B_LA(E4B_FP16, E4B_FP32)
+#undef E4B_LA
+  const unsigned nx = static_cast<unsigned>(cdiv(out_features, e4b::kLoraThreads));
+  for (int64_t m0 = 0; m0 < M; m0 += 65535) {  // grid y holds at most 65535 rows per launch
+    const int64_t mc = std::min<int64_t>(65535, M - m0);
+    const dim3 gb(nx, static_cast<unsigned>(mc));
+    const float* t0 = t_workspace + m0 * rank;
+    float* o0 = out + m0 * out_features;
+#define E4B_LB(AD, OD)                                                                                    \
+    if (adapter_dtype == AD && delta_dtype == OD)                                                         \
+      hipLaunchKernelGGL((e4b::lora_b_add_kernel<AD, OD>), gb, dim3(e4b::kLoraThreads), 0, stream, t0, rt->offsets, \
+                         num_experts, lora_b, rank, out_features, scaling, o0, mc, m0);
+    E4B_LB(E4B_BF16, E4B_BF16) E4B_LB(E4B_BF16, E4B_FP16) E4B_LB(E4B_BF16, E4B_FP32)
+    E4B_LB(E4B_FP16, E4B_BF16) E4B_LB(E4B_FP16, E4B_FP16) E4B_LB(E4B_FP16, E4B_FP32)
+    E4B_LB(E4B_FP32, E4B_BF16) E4B_LB(E4B_FP32, E4B_FP16) E4B_LB(E4B_FP32, E4B_FP32)
+#undef E4B_LB
+  }
+  return check_launch("lora kernels");
 }
 
 int e4b_combine(const void* down, int32_t down_dtype, const int32_t* inv, const void* top_k_weights,

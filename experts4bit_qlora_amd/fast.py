@@ -150,9 +150,10 @@ def fused_experts_forward(mod, hidden_states, top_k_index, top_k_weights):
 
 def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
     """Fused inference forward of an ``ExpertsLoRA`` (``fast.py:163-257``): grouped GEMMs over the
-    expert-sorted rows with the low-rank delta added per expert group before the base's
-    epilogue. The group sizes come to the host once (as in the reference) to slice the groups.
-    The GEMM outputs stay fp32 until the activation is rounded for the down projection."""
+    expert-sorted rows with the low-rank delta of every expert group added on the device
+    (``e4b_lora_delta``) before the base's epilogue, so no group size comes to the host (the
+    reference slices the groups in Python after a ``.tolist()``). The GEMM outputs stay fp32
+    until the activation is rounded for the down projection."""
     base = mod.base
     if _wants_reference(mod, hidden_states):
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
@@ -174,19 +175,15 @@ def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
     E = base.num_experts
     M = tokens * k
     w1, w2 = _qweights(base)
+    r = mod.gate_up_lora_A.shape[1]
+    if r > 64 or x.shape[1] % 8 or base._down_shape[1] % 8:  # beyond the delta kernel's limits
+        return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
     rb = ops.route(top_k_index, E)
-    offsets = rb.offsets.tolist()
-    a_cat = x.index_select(0, (rb.sorted_flat[:M] // k).long())
     up = ops.grouped_gemm(x, w1, rb, tokens, M, N.EPI_NONE, gather_k=k, path=_kernel_path, out_dtype=torch.float32)
-    active = [e for e in range(E) if offsets[e + 1] > offsets[e]]
-    for e in active:
-        s, t = offsets[e], offsets[e + 1]
-        up[s:t] += mod._lora(a_cat[s:t], mod.gate_up_lora_A[e], mod.gate_up_lora_B[e])
+    ops.lora_delta(x, rb, M, E, mod.gate_up_lora_A, mod.gate_up_lora_B, mod.scaling, up, gather_k=k)
     h = _epilogue(base, up).to(compute_dtype).contiguous()
     down = ops.grouped_gemm(h, w2, rb, tokens, M, N.EPI_NONE, path=_kernel_path, out_dtype=torch.float32)
-    for e in active:
-        s, t = offsets[e], offsets[e + 1]
-        down[s:t] += mod._lora(h[s:t], mod.down_lora_A[e], mod.down_lora_B[e])
+    ops.lora_delta(h, rb, M, E, mod.down_lora_A, mod.down_lora_B, mod.scaling, down)
     return ops.combine(down, rb, top_k_weights, tokens, k, input_dtype)
 
 

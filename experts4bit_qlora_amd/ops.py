@@ -212,6 +212,32 @@ def combine(down: torch.Tensor, rb: RoutingBuffers, top_k_weights: torch.Tensor,
     return out
 
 
+def lora_delta(x: torch.Tensor, rb: RoutingBuffers, M: int, num_experts: int, lora_a: torch.Tensor,
+               lora_b: torch.Tensor, scaling: float, out: torch.Tensor, gather_k: int = 0,
+               delta_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """Add the per-expert low-rank delta to ``out`` (``[M, out_features]`` fp32, expert-sorted
+    rows) in place: ``out[m] += delta_dtype(scaling * (x_m @ A[e].T) @ B[e].T)`` for every routed
+    row, all groups in one pass (``lora.py:251-256`` per group as ``fast.py:229-233`` applies it,
+    without the host's group sizes). ``x_m`` is ``x[sorted_flat[m] // gather_k]`` when
+    ``gather_k > 0`` (token rows), else ``x[m]``; ``delta_dtype`` defaults to ``x.dtype``."""
+    _require_cuda(x, lora_a, lora_b, out)
+    if out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous fp32 tensor")
+    L = N.lib()
+    xc = x.contiguous()
+    a = lora_a.contiguous()
+    b = lora_b.to(a.dtype).contiguous()
+    E, r, k_in = a.shape
+    n_out = b.shape[1]
+    t = torch.empty(max(M, 1), r, dtype=torch.float32, device=x.device)
+    rt = rb.struct()
+    N.check("e4b_lora_delta",
+            L.e4b_lora_delta(xc.data_ptr(), dtype_code(xc.dtype), gather_k, ctypes.byref(rt), M, num_experts,
+                             a.data_ptr(), b.data_ptr(), dtype_code(a.dtype), r, k_in, n_out, float(scaling),
+                             dtype_code(delta_dtype or xc.dtype), t.data_ptr(), out.data_ptr(), _stream(x.device)))
+    return out
+
+
 def decode_gate_up(hidden: torch.Tensor, top_k_index: torch.Tensor, w1: QW, epilogue: int, alpha: float = 1.702,
                    limit: float = 7.0) -> torch.Tensor:
     """Decode-path gate_up (routing recomputed on the device): ``h [tokens * k, h_cols]`` in flat

@@ -131,6 +131,22 @@ int e4b_combine(const void* down, int32_t down_dtype, const int32_t* inv, const 
                 int32_t weight_dtype, int64_t tokens, int32_t top_k, int64_t hidden, void* out,
                 int32_t out_dtype, hipStream_t stream);
 
+/* Low-rank (LoRA) delta added to a grouped projection's fp32 rows, all expert groups at once:
+ * for every expert-sorted row m below rt->offsets[E] (expert e: offsets[e] <= m < offsets[e+1])
+ *   out[m, n] += delta_dtype( scaling * sum_j t[m, j] * lora_b[e, n, j] ),
+ *   t[m, j] = sum_c x_m[c] * lora_a[e, j, c]   (fp32; t_workspace is [M, rank] fp32),
+ * x_m = x[sorted_flat[m] / gather_k] when gather_k > 0 (token rows, as for gate_up), else x[m].
+ * lora_a is [E, rank, in_features], lora_b [E, out_features, rank], both in adapter_dtype (bf16,
+ * fp16 or fp32); x is in x_dtype (bf16 or fp16); out is [M, out_features] fp32; rank <= 64,
+ * in_features a multiple of 8, num_experts <= 1024. Rows past offsets[E] are untouched.
+ * Replaces: the per-expert Python loop of `up[s:t] += _lora(a_cat[s:t], A[e], B[e])` at
+ * engines/fast.py:229-233 and 249-253 (lora.py:251-256 `_lora`), and its host sync on the
+ * group sizes. */
+int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
+                   int32_t num_experts, const void* lora_a, const void* lora_b, int32_t adapter_dtype,
+                   int32_t rank, int64_t in_features, int64_t out_features, float scaling,
+                   int32_t delta_dtype, float* t_workspace, float* out, hipStream_t stream);
+
 /* Decode path, first half: routing of top_k_index recomputed on the device (no route launch),
  * gate_up GEMV with the fused epilogue. h is [tokens * top_k, h_cols] in act_dtype, row
  * t * top_k + s holding token t's activation for slot s (flat order, not expert order).

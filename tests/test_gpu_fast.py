@@ -249,6 +249,24 @@ def test_lora_fused_matches_reference(n_tok):
     assert got.dtype == ref.dtype and rel < 2e-2, rel
 
 
+def test_lora_fused_forward_never_syncs():
+    """The LoRA deltas of every expert group are added on the device (e4b_lora_delta), so the
+    fused LoRA forward needs no group sizes on the host: no device synchronisation at all
+    (the reference slices its groups after a .tolist(), fast.py:209-216)."""
+    _announce("lora sync-free")
+    mod = _lora()
+    hs, idx, wts = _lora_inputs(12)
+    assert e4b.enable_fast(mod) == 1
+    with torch.no_grad():
+        mod(hs, idx, wts)  # warm the caching allocator
+        torch.cuda.synchronize()
+        torch.cuda.set_sync_debug_mode("error")
+        try:
+            mod(hs, idx, wts)
+        finally:
+            torch.cuda.set_sync_debug_mode("default")
+
+
 def test_lora_training_and_grad_fall_back_exactly():
     _announce("lora fallback")
     mod = _lora()

@@ -361,6 +361,52 @@ def test_combine_bit_exact(wdt, H):
     assert np.array_equal(_bits(out16), numerics.f32_to_bf16_bits(acc))
 
 
+# ------------------------------------------------------------------------ LoRA delta
+
+
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("adt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("gather", [True, False])
+def test_lora_delta_matches_per_group_reference(xdt, adt, gather):
+    """e4b_lora_delta adds scaling * (x_m @ A[e].T) @ B[e].T, rounded to the compute dtype, to
+    every expert-sorted row of an fp32 projection in one pass -- the per-group `_lora` of
+    lora.py:251-256 as fast.py:229-233 applies it, here checked per group against an fp64
+    product (the kernel keeps t and the sums in fp32: the bar is the delta's own rounding).
+    Empty experts, an out-of-range id (a dropped row left untouched) and rank 16 included."""
+    _announce(f"lora delta xdt={xdt} adt={adt} gather={gather}")
+    E, T, top, K, Nout, r, scaling = 12, 37, 2, 256, 200, 16, 0.75
+    g = torch.Generator().manual_seed(60)
+    idx = torch.stack([torch.randperm(E - 3, generator=g)[:top] for _ in range(T)]).to(torch.int64)
+    idx[5, 1] = E + 4  # dropped
+    x = (torch.randn(T if gather else T * top, K, generator=g)).to(xdt)
+    A = (torch.randn(E, r, K, generator=g) * 0.05).to(adt)
+    B = (torch.randn(E, Nout, r, generator=g) * 0.05).to(adt)
+    M = T * top
+    rb = ops.route(idx.to(DEV), E)
+    base = torch.randn(M, Nout, generator=g)
+    out = base.clone().to(DEV)
+    ops.lora_delta(x.to(DEV), rb, M, E, A.to(DEV), B.to(DEV), scaling, out, gather_k=top if gather else 0)
+    flat = idx.numpy().reshape(-1)
+    valid = np.flatnonzero((flat >= 0) & (flat < E))
+    order = valid[np.argsort(flat[valid], kind="stable")]  # the routing's stable sort, dropped ids out
+    offs = np.concatenate([[0], np.cumsum(np.bincount(flat[valid], minlength=E))])
+    want = base.double().clone()
+    for e in range(E):
+        s, t = int(offs[e]), int(offs[e + 1])
+        if s == t:
+            continue
+        rows = torch.from_numpy(order[s:t]) // top if gather else torch.arange(s, t)
+        xm = x[rows].double()
+        d = scaling * (xm @ A[e].double().T) @ B[e].double().T
+        want[s:t] += d
+    got = out.cpu().double()
+    n_valid = int(offs[E])
+    assert torch.equal(got[n_valid:], base.double()[n_valid:])  # rows past the routed ones untouched
+    err = (got[:n_valid] - want[:n_valid]).abs()
+    tol = (want[:n_valid] - base.double()[:n_valid]).abs() * 2.0 ** -7 + 1e-6
+    assert bool((err <= tol).all()), float((err - tol).max())
+
+
 # ------------------------------------------------------------------- decode halves
 
 
