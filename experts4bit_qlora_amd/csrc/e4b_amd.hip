@@ -360,31 +360,44 @@ int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_r
   if (M == 0) return E4B_OK;
   if (!x || !lora_a || !lora_b || !t_workspace || !out) return fail(E4B_EINVAL, "NULL pointer");
   if (!aligned16(x) || !aligned16(lora_a)) return fail(E4B_EINVAL, "x and lora_a must be 16-byte aligned");
-  constexpr int kRowsPerBlock = e4b::kLoraThreads / e4b::kWave;
-  const dim3 ga(static_cast<unsigned>(cdiv(M, kRowsPerBlock)));
-#define E4B_LA(XD, AD)                                                                                       \
-  if (x_dtype == XD && adapter_dtype == AD)                                                                  \
-    hipLaunchKernelGGL((e4b::lora_a_kernel<XD, AD>), ga, dim3(e4b::kLoraThreads), 0, stream,                 \
-                       static_cast<const uint16_t*>(x), gather_k, rt->sorted_flat, rt->offsets, num_experts, \
-                       lora_a, rank, in_features, t_workspace, M);
+  // lora_a: 8-row tiles once there are enough rows to fill the chip with them, else 1-row tiles.
+  const int rgroups = static_cast<int>(cdiv(rank, e4b::kLoraRanksPerBlock));
+  const bool big = M > 2048;
+  const dim3 ga(static_cast<unsigned>(cdiv(M, big ? 8 : 1) * rgroups));
+#define E4B_LA(XD, AD)                                                                                         \
+  if (x_dtype == XD && adapter_dtype == AD) {                                                                  \
+    if (big)                                                                                                   \
+      hipLaunchKernelGGL((e4b::lora_a_kernel<XD, AD, 8>), ga, dim3(e4b::kLoraThreads), 0, stream,              \
+                         static_cast<const uint16_t*>(x), gather_k, rt->sorted_flat, rt->offsets, num_experts, \
+                         lora_a, rank, in_features, t_workspace, M, rgroups);                                  \
+    else                                                                                                       \
+      hipLaunchKernelGGL((e4b::lora_a_kernel<XD, AD, 1>), ga, dim3(e4b::kLoraThreads), 0, stream,              \
+                         static_cast<const uint16_t*>(x), gather_k, rt->sorted_flat, rt->offsets, num_experts, \
+                         lora_a, rank, in_features, t_workspace, M, rgroups);                                  \
+  }
   E4B_LA(E4B_BF16, E4B_BF16) E4B_LA(E4B_BF16, E4B_FP16) E4B_LA(E4B_BF16, E4B_FP32)
   E4B_LA(E4B_FP16, E4B_BF16) E4B_LA(E4B_FP16, E4B_FP16) E4B_LA(E4B_FP16, E4B_FP32)
 #undef E4B_LA
-  const unsigned nx = static_cast<unsigned>(cdiv(out_features, e4b::kLoraThreads));
-  for (int64_t m0 = 0; m0 < M; m0 += 65535) {  // grid y holds at most 65535 rows per launch
-    const int64_t mc = std::min<int64_t>(65535, M - m0);
-    const dim3 gb(nx, static_cast<unsigned>(mc));
-    const float* t0 = t_workspace + m0 * rank;
-    float* o0 = out + m0 * out_features;
-#define E4B_LB(AD, OD)                                                                                    \
-    if (adapter_dtype == AD && delta_dtype == OD)                                                         \
-      hipLaunchKernelGGL((e4b::lora_b_add_kernel<AD, OD>), gb, dim3(e4b::kLoraThreads), 0, stream, t0, rt->offsets, \
-                         num_experts, lora_b, rank, out_features, scaling, o0, mc, m0);
-    E4B_LB(E4B_BF16, E4B_BF16) E4B_LB(E4B_BF16, E4B_FP16) E4B_LB(E4B_BF16, E4B_FP32)
-    E4B_LB(E4B_FP16, E4B_BF16) E4B_LB(E4B_FP16, E4B_FP16) E4B_LB(E4B_FP16, E4B_FP32)
-    E4B_LB(E4B_FP32, E4B_BF16) E4B_LB(E4B_FP32, E4B_FP16) E4B_LB(E4B_FP32, E4B_FP32)
-#undef E4B_LB
+  // lora_b_add: row tiles sized so that small batches still spread over many blocks.
+  const int64_t ncb = cdiv(out_features, e4b::kLoraThreads);
+  const int tile_rows = M <= 512 ? 1 : (M <= 8192 ? 8 : e4b::kLoraMaxTileRows);
+  if (cdiv(M, tile_rows) * ncb > 0x7fffffffLL) return fail(E4B_EUNSUPPORTED, "LoRA delta grid too large");
+  const dim3 gb(static_cast<unsigned>(cdiv(M, tile_rows) * ncb));
+#define E4B_LB(AD, OD)                                                                                          \
+  if (adapter_dtype == AD && delta_dtype == OD) {                                                               \
+    if (rank <= 16)                                                                                             \
+      hipLaunchKernelGGL((e4b::lora_b_add_kernel<AD, OD, 16>), gb, dim3(e4b::kLoraThreads), 0, stream,          \
+                         t_workspace, rt->offsets, num_experts, lora_b, rank, out_features, scaling, out, M,   \
+                         tile_rows, ncb);                                                                       \
+    else                                                                                                        \
+      hipLaunchKernelGGL((e4b::lora_b_add_kernel<AD, OD, e4b::kLoraMaxRank>), gb, dim3(e4b::kLoraThreads), 0,   \
+                         stream, t_workspace, rt->offsets, num_experts, lora_b, rank, out_features, scaling,   \
+                         out, M, tile_rows, ncb);                                                               \
   }
+  E4B_LB(E4B_BF16, E4B_BF16) E4B_LB(E4B_BF16, E4B_FP16) E4B_LB(E4B_BF16, E4B_FP32)
+  E4B_LB(E4B_FP16, E4B_BF16) E4B_LB(E4B_FP16, E4B_FP16) E4B_LB(E4B_FP16, E4B_FP32)
+  E4B_LB(E4B_FP32, E4B_BF16) E4B_LB(E4B_FP32, E4B_FP16) E4B_LB(E4B_FP32, E4B_FP32)
+#undef E4B_LB
   return check_launch("lora kernels");
 }
 

@@ -8,9 +8,10 @@
 // `(scaling * F.linear(F.linear(x, A), B)).to(x.dtype)` of lora.py:251-256 applied per expert
 // group as fast.py:229-233 / 249-253 do, in one pass over all groups: no group sizes on the host.
 //
-//   lora_a_kernel      one wave per sorted row: the r dot products of length `in`, 8 values per
-//                      lane per step, then one wave reduction per rank.
-//   lora_b_add_kernel  one thread per (row, output column): r multiply-adds, rounded once, added.
+//   lora_a_kernel      tiles of 1 or 8 sorted rows x 16 ranks per block: each A value loaded is
+//                      used for every row of the tile that shares its expert.
+//   lora_b_add_kernel  tiles of up to 32 rows x 256 output columns per block: t rows in LDS, the
+//                      column's B slice in registers, r multiply-adds, rounded once, added.
 #pragma once
 
 #include "common.h"
@@ -55,78 +56,155 @@ E4B_DEV float wave_sum(float v) {
   return v;
 }
 
+// Rows of one launch tile that share an expert form a segment; sorted rows make every segment
+// one contiguous run, found from the LDS-staged offsets: [s, end) with end = min(tile end,
+// offsets[e + 1]).
+E4B_DEV int64_t segment_end(const int* offs, int e, int64_t mend) {
+  return offs[e + 1] < mend ? static_cast<int64_t>(offs[e + 1]) : mend;
+}
+
+constexpr int kLoraRanksPerWave = 4;
+constexpr int kLoraRanksPerBlock = kLoraRanksPerWave * (kLoraThreads / kWave);  // 16
+
 // t[m, :r] for every sorted row m < offsets[E] (rows past it, dropped ids, are left alone).
-// `in` is a multiple of 8.
-template <int XDT, int ADT>
+// Block b covers rank group b % rgroups (16 ranks, 4 per wave) of the TR-row tile b / rgroups.
+// Per segment, each lane loads 8 values of each of its wave's 4 rank rows of A[e] once per
+// step and applies them to every row of the segment, so A is read once per tile, not per row;
+// the `in` dimension is spread over the 64 lanes (8 values each, coalesced) and reduced across
+// the wave at the end. `in` is a multiple of 8.
+template <int XDT, int ADT, int TR>
 __global__ void __launch_bounds__(kLoraThreads) lora_a_kernel(const uint16_t* __restrict__ x, int gather_k,
                                                               const int32_t* __restrict__ sorted_flat,
                                                               const int32_t* __restrict__ offsets, int E,
                                                               const void* __restrict__ A, int r, int64_t in,
-                                                              float* __restrict__ t, int64_t M) {
+                                                              float* __restrict__ t, int64_t M, int rgroups) {
   __shared__ int offs[1025];
   for (int i = threadIdx.x; i <= E; i += blockDim.x) offs[i] = offsets[i];
   __syncthreads();
+  constexpr int kEs = ADT == E4B_FP32 ? 4 : 2;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t m = int64_t(blockIdx.x) * (kLoraThreads / kWave) + threadIdx.x / kWave;
-  if (m >= M || m >= offs[E]) return;  // whole wave; no barrier follows
-  const int e = row_expert(offs, E, static_cast<int>(m));
-  const int64_t src = gather_k > 0 ? sorted_flat[m] / gather_k : m;
-  const uint16_t* xr = x + src * in;
-  const int64_t a_row = in;  // elements per rank row of A
-  const char* Ae = static_cast<const char*>(A) + int64_t(e) * r * in * (ADT == E4B_FP32 ? 4 : 2);
-  float acc[kLoraMaxRank];
+  const int64_t tile = blockIdx.x / rgroups;
+  const int j0 = static_cast<int>(blockIdx.x % rgroups) * kLoraRanksPerBlock +
+                 static_cast<int>(threadIdx.x / kWave) * kLoraRanksPerWave;
+  if (j0 >= r) return;  // whole wave; no barrier follows
+  const int64_t mbeg = tile * TR;
+  int64_t mend = mbeg + TR < M ? mbeg + TR : M;
+  if (offs[E] < mend) mend = offs[E];
+  for (int64_t s = mbeg; s < mend;) {
+    const int e = row_expert(offs, E, static_cast<int>(s));
+    const int64_t send = segment_end(offs, e, mend);
+    const int nr = static_cast<int>(send - s);  // 1..TR, uniform
+    const uint16_t* xr[TR];
 #pragma unroll
-  for (int j = 0; j < kLoraMaxRank; ++j) acc[j] = 0.0f;
-  for (int64_t c = int64_t(lane) * 8; c < in; c += kWave * 8) {
-    float xv[8];
-    load8<XDT>(xr, c, xv);
+    for (int i = 0; i < TR; ++i) {
+      const int64_t m = s + (i < nr ? i : nr - 1);
+      xr[i] = x + (gather_k > 0 ? static_cast<int64_t>(sorted_flat[m] / gather_k) : m) * in;
+    }
+    const char* Ae = static_cast<const char*>(A) + (int64_t(e) * r + j0) * in * kEs;
+    float acc[TR][kLoraRanksPerWave];
 #pragma unroll
-    for (int j = 0; j < kLoraMaxRank; ++j) {
-      if (j < r) {
-        float av[8];
-        load8<ADT>(Ae + j * a_row * (ADT == E4B_FP32 ? 4 : 2), c, av);
+    for (int i = 0; i < TR; ++i)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[j] = __builtin_fmaf(xv[i], av[i], acc[j]);
+      for (int q = 0; q < kLoraRanksPerWave; ++q) acc[i][q] = 0.0f;
+    for (int64_t c = int64_t(lane) * 8; c < in; c += kWave * 8) {
+      float av[kLoraRanksPerWave][8];
+#pragma unroll
+      for (int q = 0; q < kLoraRanksPerWave; ++q) {
+        if (j0 + q < r) {
+          load8<ADT>(Ae + int64_t(q) * in * kEs, c, av[q]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) av[q][u] = 0.0f;
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TR; ++i) {
+        if (i < nr) {
+          float xv[8];
+          load8<XDT>(xr[i], c, xv);
+#pragma unroll
+          for (int q = 0; q < kLoraRanksPerWave; ++q)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc[i][q] = __builtin_fmaf(xv[u], av[q][u], acc[i][q]);
+        }
       }
     }
-  }
 #pragma unroll
-  for (int j = 0; j < kLoraMaxRank; ++j) {
-    if (j < r) {
-      const float s = wave_sum(acc[j]);
-      if (lane == 0) t[m * r + j] = s;
+    for (int i = 0; i < TR; ++i) {
+      if (i < nr) {
+#pragma unroll
+        for (int q = 0; q < kLoraRanksPerWave; ++q) {
+          if (j0 + q < r) {
+            const float v = wave_sum(acc[i][q]);
+            if (lane == 0) t[(s + i) * r + j0 + q] = v;
+          }
+        }
+      }
     }
+    s = send;
   }
 }
 
-// out[m, n] += odt(scaling * t[m, :] . B[e, n, :]) for the sorted rows m = m0 + blockIdx.y below
-// offsets[E]; t and out point at row m0, and `rows` bounds this launch's rows.
-template <int ADT, int ODT>
+constexpr int kLoraMaxTileRows = 32;
+
+// out[m, n] += odt(scaling * t[m, :] . B[e, n, :]) for the sorted rows below offsets[E].
+// Block b covers the 256 output columns of column block b % ncb over the `tile_rows` rows of
+// tile b / ncb: the tile's t rows are staged in LDS (zero-padded to RB ranks), and per segment
+// each thread holds its column's B[e, n, :r] in registers and applies it to every row, so B is
+// read once per tile and every access to `out` is coalesced. The rank sum runs in rank order.
+template <int ADT, int ODT, int RB>
 __global__ void __launch_bounds__(kLoraThreads) lora_b_add_kernel(const float* __restrict__ t,
                                                                   const int32_t* __restrict__ offsets, int E,
                                                                   const void* __restrict__ B, int r, int64_t nout,
-                                                                  float scaling, float* __restrict__ out,
-                                                                  int64_t rows, int64_t m0) {
+                                                                  float scaling, float* __restrict__ out, int64_t M,
+                                                                  int tile_rows, int64_t ncb) {
   __shared__ int offs[1025];
+  __shared__ float4 ts[kLoraMaxTileRows][RB / 4];
   for (int i = threadIdx.x; i <= E; i += blockDim.x) offs[i] = offsets[i];
-  __syncthreads();
-  const int64_t ml = blockIdx.y;
-  const int64_t m = m0 + ml;
-  const int64_t n = int64_t(blockIdx.x) * kLoraThreads + threadIdx.x;
-  if (ml >= rows || m >= offs[E] || n >= nout) return;
-  const int e = row_expert(offs, E, static_cast<int>(m));
-  const float* tm = t + ml * r;
-  float s = 0.0f;
-  if constexpr (ADT == E4B_FP32) {
-    const float* b = static_cast<const float*>(B) + (int64_t(e) * nout + n) * r;
-    for (int j = 0; j < r; ++j) s = __builtin_fmaf(tm[j], b[j], s);
-  } else {
-    const uint16_t* b = static_cast<const uint16_t*>(B) + (int64_t(e) * nout + n) * r;
-    for (int j = 0; j < r; ++j) s = __builtin_fmaf(tm[j], to_f<ADT>(b[j]), s);
+  const int64_t tile = blockIdx.x / ncb;
+  const int64_t n = (blockIdx.x % ncb) * kLoraThreads + threadIdx.x;
+  const int64_t mbeg = tile * tile_rows;
+  float* tsf = reinterpret_cast<float*>(&ts[0][0]);
+  for (int i = threadIdx.x; i < tile_rows * RB; i += blockDim.x) {
+    const int row = i / RB, j = i % RB;
+    const int64_t m = mbeg + row;
+    tsf[i] = (m < M && j < r) ? t[m * r + j] : 0.0f;
   }
-  float d = scaling * s;
-  if constexpr (ODT != E4B_FP32) d = rnd<ODT>(d);  // the delta's own rounding, then the fp32 add
-  out[ml * nout + n] += d;
+  __syncthreads();
+  int64_t mend = mbeg + tile_rows < M ? mbeg + tile_rows : M;
+  if (offs[E] < mend) mend = offs[E];
+  if (n >= nout) return;  // no barrier follows
+  for (int64_t s = mbeg; s < mend;) {
+    const int e = row_expert(offs, E, static_cast<int>(s));
+    const int64_t send = segment_end(offs, e, mend);
+    float bv[RB];
+    const int64_t bo = (int64_t(e) * nout + n) * r;
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+      if (j < r) {
+        if constexpr (ADT == E4B_FP32) bv[j] = static_cast<const float*>(B)[bo + j];
+        else bv[j] = to_f<ADT>(static_cast<const uint16_t*>(B)[bo + j]);
+      } else {
+        bv[j] = 0.0f;
+      }
+    }
+    for (int64_t m = s; m < send; ++m) {
+      const float4* tr = ts[m - mbeg];
+      float acc = 0.0f;
+#pragma unroll
+      for (int q = 0; q < RB / 4; ++q) {
+        const float4 tv = tr[q];
+        acc = __builtin_fmaf(tv.x, bv[4 * q], acc);
+        acc = __builtin_fmaf(tv.y, bv[4 * q + 1], acc);
+        acc = __builtin_fmaf(tv.z, bv[4 * q + 2], acc);
+        acc = __builtin_fmaf(tv.w, bv[4 * q + 3], acc);
+      }
+      float d = scaling * acc;
+      if constexpr (ODT != E4B_FP32) d = rnd<ODT>(d);  // the delta's own rounding, then the fp32 add
+      out[m * nout + n] += d;
+    }
+    s = send;
+  }
 }
 
 }  // namespace e4b

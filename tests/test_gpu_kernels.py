@@ -364,18 +364,37 @@ def test_combine_bit_exact(wdt, H):
 # ------------------------------------------------------------------------ LoRA delta
 
 
-@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("adt", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("gather", [True, False])
-def test_lora_delta_matches_per_group_reference(xdt, adt, gather):
+_LORA_CASES = [
+    # (x dtype, adapter dtype, gather, E, tokens, rank, out features): the small cases run the
+    # 1-row tiles; 800 rows run 8-row output tiles; 3072 rows (200 experts: about 15 rows each, so
+    # most tiles hold several expert segments) run 8-row tiles in both kernels and a partial rank
+    # group; 9000 rows run 32-row output tiles at the largest rank.
+    (torch.bfloat16, torch.bfloat16, True, 12, 37, 16, 200),
+    (torch.bfloat16, torch.float32, True, 12, 37, 16, 200),
+    (torch.bfloat16, torch.bfloat16, False, 12, 37, 16, 200),
+    (torch.bfloat16, torch.float32, False, 12, 37, 16, 200),
+    (torch.float16, torch.bfloat16, True, 12, 37, 16, 200),
+    (torch.float16, torch.float32, True, 12, 37, 16, 200),
+    (torch.float16, torch.float16, False, 12, 37, 16, 200),
+    (torch.float16, torch.float32, False, 12, 37, 16, 200),
+    (torch.bfloat16, torch.float32, True, 12, 400, 5, 300),
+    (torch.bfloat16, torch.bfloat16, True, 200, 1536, 40, 300),
+    (torch.float16, torch.float32, False, 200, 1536, 40, 260),
+    (torch.bfloat16, torch.float32, True, 64, 4500, 64, 520),
+]
+
+
+@pytest.mark.parametrize("xdt,adt,gather,E,T,r,Nout", _LORA_CASES)
+def test_lora_delta_matches_per_group_reference(xdt, adt, gather, E, T, r, Nout):
     """e4b_lora_delta adds scaling * (x_m @ A[e].T) @ B[e].T, rounded to the compute dtype, to
     every expert-sorted row of an fp32 projection in one pass -- the per-group `_lora` of
     lora.py:251-256 as fast.py:229-233 applies it, here checked per group against an fp64
-    product (the kernel keeps t and the sums in fp32: the bar is the delta's own rounding).
-    Empty experts, an out-of-range id (a dropped row left untouched) and rank 16 included."""
-    _announce(f"lora delta xdt={xdt} adt={adt} gather={gather}")
-    E, T, top, K, Nout, r, scaling = 12, 37, 2, 256, 200, 16, 0.75
-    g = torch.Generator().manual_seed(60)
+    product. The bar is the delta's own rounding (2^-7 of it) plus the fp32 summation bound
+    (2^-14 of the same product over absolute values: K + r = 320 terms at 2^-24 each, with room).
+    Empty experts and an out-of-range id (a dropped row left untouched) are included."""
+    _announce(f"lora delta xdt={xdt} adt={adt} gather={gather} E={E} T={T} r={r} Nout={Nout}")
+    top, K, scaling = 2, 256, 0.75
+    g = torch.Generator().manual_seed(60 + T + r)
     idx = torch.stack([torch.randperm(E - 3, generator=g)[:top] for _ in range(T)]).to(torch.int64)
     idx[5, 1] = E + 4  # dropped
     x = (torch.randn(T if gather else T * top, K, generator=g)).to(xdt)
@@ -391,19 +410,21 @@ def test_lora_delta_matches_per_group_reference(xdt, adt, gather):
     order = valid[np.argsort(flat[valid], kind="stable")]  # the routing's stable sort, dropped ids out
     offs = np.concatenate([[0], np.cumsum(np.bincount(flat[valid], minlength=E))])
     want = base.double().clone()
+    bound = torch.zeros(M, Nout, dtype=torch.float64)
     for e in range(E):
         s, t = int(offs[e]), int(offs[e + 1])
         if s == t:
             continue
         rows = torch.from_numpy(order[s:t]) // top if gather else torch.arange(s, t)
         xm = x[rows].double()
-        d = scaling * (xm @ A[e].double().T) @ B[e].double().T
-        want[s:t] += d
+        Ae, Be = A[e].double(), B[e].double()
+        want[s:t] += scaling * (xm @ Ae.T) @ Be.T
+        bound[s:t] = scaling * (xm.abs() @ Ae.abs().T) @ Be.abs().T
     got = out.cpu().double()
     n_valid = int(offs[E])
     assert torch.equal(got[n_valid:], base.double()[n_valid:])  # rows past the routed ones untouched
     err = (got[:n_valid] - want[:n_valid]).abs()
-    tol = (want[:n_valid] - base.double()[:n_valid]).abs() * 2.0 ** -7 + 1e-6
+    tol = (want[:n_valid] - base.double()[:n_valid]).abs() * 2.0 ** -7 + bound[:n_valid] * 2.0 ** -14 + 1e-9
     assert bool((err <= tol).all()), float((err - tol).max())
 
 
