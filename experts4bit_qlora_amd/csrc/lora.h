@@ -50,11 +50,31 @@ E4B_DEV void load8(const void* base, int64_t c, float (&v)[8]) {
   }
 }
 
-E4B_DEV float wave_sum(float v) {
+// Wave sums of N per-lane values (N a power of two, <= 64) in N - 1 + log2(64 / N) shuffles:
+// each step folds the half of the values that lane bit BIT does not keep into the partner lane's
+// kept half. Afterwards v[0] of lane l is the wave sum of value l >> (6 - log2 N).
+template <int N, int BIT>
+struct WaveFold {
+  static E4B_DEV void run(float* v, int lane) {
+    if constexpr (N > 1) {
+      constexpr int H = N / 2;
+      const bool hi = (lane & BIT) != 0;
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
+      for (int k = 0; k < H; ++k) {
+        const float mine = hi ? v[k + H] : v[k];
+        const float other = hi ? v[k] : v[k + H];
+        v[k] = mine + __shfl_xor(other, BIT);
+      }
+      WaveFold<H, BIT / 2>::run(v, lane);
+    } else if constexpr (BIT >= 1) {
+      v[0] += __shfl_xor(v[0], BIT);
+      WaveFold<1, BIT / 2>::run(v, lane);
+    }
+  }
+};
+
+template <int N>
+constexpr int ilog2() { return N <= 1 ? 0 : 1 + ilog2<N / 2>(); }
 
 // Rows of one launch tile that share an expert form a segment; sorted rows make every segment
 // one contiguous run, found from the LDS-staged offsets: [s, end) with end = min(tile end,
@@ -101,11 +121,11 @@ __global__ void __launch_bounds__(kLoraThreads) lora_a_kernel(const uint16_t* __
       xr[i] = x + (gather_k > 0 ? static_cast<int64_t>(sorted_flat[m] / gather_k) : m) * in;
     }
     const char* Ae = static_cast<const char*>(A) + (int64_t(e) * r + j0) * in * kEs;
-    float acc[TR][kLoraRanksPerWave];
+    constexpr int kN = TR * kLoraRanksPerWave;  // value i * 4 + q: row i, rank j0 + q
+    float acc[kN];
 #pragma unroll
-    for (int i = 0; i < TR; ++i)
-#pragma unroll
-      for (int q = 0; q < kLoraRanksPerWave; ++q) acc[i][q] = 0.0f;
+    for (int f = 0; f < kN; ++f) acc[f] = 0.0f;
+#pragma unroll 2
     for (int64_t c = int64_t(lane) * 8; c < in; c += kWave * 8) {
       float av[kLoraRanksPerWave][8];
 #pragma unroll
@@ -125,27 +145,23 @@ __global__ void __launch_bounds__(kLoraThreads) lora_a_kernel(const uint16_t* __
 #pragma unroll
           for (int q = 0; q < kLoraRanksPerWave; ++q)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc[i][q] = __builtin_fmaf(xv[u], av[q][u], acc[i][q]);
+            for (int u = 0; u < 8; ++u)
+              acc[i * kLoraRanksPerWave + q] = __builtin_fmaf(xv[u], av[q][u], acc[i * kLoraRanksPerWave + q]);
         }
       }
     }
-#pragma unroll
-    for (int i = 0; i < TR; ++i) {
-      if (i < nr) {
-#pragma unroll
-        for (int q = 0; q < kLoraRanksPerWave; ++q) {
-          if (j0 + q < r) {
-            const float v = wave_sum(acc[i][q]);
-            if (lane == 0) t[(s + i) * r + j0 + q] = v;
-          }
-        }
-      }
+    WaveFold<kN, kWave / 2>::run(acc, lane);
+    constexpr int kSh = 6 - ilog2<kN>();
+    if ((lane & ((1 << kSh) - 1)) == 0) {
+      const int f = lane >> kSh, i = f / kLoraRanksPerWave, q = f % kLoraRanksPerWave;
+      if (i < nr && j0 + q < r) t[(s + i) * r + j0 + q] = acc[0];
     }
     s = send;
   }
 }
 
 constexpr int kLoraMaxTileRows = 32;
+constexpr int kLoraRowBatch = 8;
 
 // out[m, n] += odt(scaling * t[m, :] . B[e, n, :]) for the sorted rows below offsets[E].
 // Block b covers the 256 output columns of column block b % ncb over the `tile_rows` rows of
@@ -188,7 +204,7 @@ __global__ void __launch_bounds__(kLoraThreads) lora_b_add_kernel(const float* _
         bv[j] = 0.0f;
       }
     }
-    for (int64_t m = s; m < send; ++m) {
+    auto delta = [&](int64_t m) {
       const float4* tr = ts[m - mbeg];
       float acc = 0.0f;
 #pragma unroll
@@ -201,8 +217,17 @@ __global__ void __launch_bounds__(kLoraThreads) lora_b_add_kernel(const float* _
       }
       float d = scaling * acc;
       if constexpr (ODT != E4B_FP32) d = rnd<ODT>(d);  // the delta's own rounding, then the fp32 add
-      out[m * nout + n] += d;
+      return d;
+    };
+    int64_t m = s;
+    for (; m + kLoraRowBatch <= send; m += kLoraRowBatch) {  // the batch's loads go out together
+      float o[kLoraRowBatch];
+#pragma unroll
+      for (int u = 0; u < kLoraRowBatch; ++u) o[u] = out[(m + u) * nout + n];
+#pragma unroll
+      for (int u = 0; u < kLoraRowBatch; ++u) out[(m + u) * nout + n] = o[u] + delta(m + u);
     }
+    for (; m < send; ++m) out[m * nout + n] += delta(m);
     s = send;
   }
 }
