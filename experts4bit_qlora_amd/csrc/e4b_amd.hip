@@ -343,10 +343,13 @@ int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e
                                : launch_gemm_dt<E4B_FP16>(args, gemv, max_active, stream);
 }
 
-int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
-                   int32_t num_experts, const void* lora_a, const void* lora_b, int32_t adapter_dtype,
-                   int32_t rank, int64_t in_features, int64_t out_features, float scaling,
-                   int32_t delta_dtype, float* t_workspace, float* out, hipStream_t stream) {
+namespace {
+
+// Validation shared by the two LoRA entry points, then t = x . A^T for every routed row.
+int lora_a_pass(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
+                int32_t num_experts, const void* lora_a, const void* lora_b, int32_t adapter_dtype, int32_t rank,
+                int64_t in_features, int64_t out_features, int32_t delta_dtype, float* t_workspace,
+                const void* out, hipStream_t stream) {
   if (!act_dtype_ok(x_dtype)) return fail(E4B_EINVAL, "x_dtype must be bf16 or fp16 (got %d)", x_dtype);
   if (!any_dtype_ok(adapter_dtype) || !any_dtype_ok(delta_dtype)) return fail(E4B_EINVAL, "bad adapter/delta dtype");
   if (M < 0 || M > 0x7fffffffLL) return fail(E4B_EINVAL, "bad row count %lld", (long long)M);
@@ -378,9 +381,23 @@ int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_r
   E4B_LA(E4B_BF16, E4B_BF16) E4B_LA(E4B_BF16, E4B_FP16) E4B_LA(E4B_BF16, E4B_FP32)
   E4B_LA(E4B_FP16, E4B_BF16) E4B_LA(E4B_FP16, E4B_FP16) E4B_LA(E4B_FP16, E4B_FP32)
 #undef E4B_LA
+  return check_launch("lora_a_kernel");
+}
+
+int lora_tile_rows(int64_t M) { return M <= 512 ? 1 : (M <= 8192 ? 8 : e4b::kLoraMaxTileRows); }
+
+}  // namespace
+
+int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
+                   int32_t num_experts, const void* lora_a, const void* lora_b, int32_t adapter_dtype,
+                   int32_t rank, int64_t in_features, int64_t out_features, float scaling,
+                   int32_t delta_dtype, float* t_workspace, float* out, hipStream_t stream) {
+  const int st = lora_a_pass(x, x_dtype, gather_k, rt, M, num_experts, lora_a, lora_b, adapter_dtype, rank,
+                             in_features, out_features, delta_dtype, t_workspace, out, stream);
+  if (st != E4B_OK || M == 0) return st;
   // lora_b_add: row tiles sized so that small batches still spread over many blocks.
   const int64_t ncb = cdiv(out_features, e4b::kLoraThreads);
-  const int tile_rows = M <= 512 ? 1 : (M <= 8192 ? 8 : e4b::kLoraMaxTileRows);
+  const int tile_rows = lora_tile_rows(M);
   if (cdiv(M, tile_rows) * ncb > 0x7fffffffLL) return fail(E4B_EUNSUPPORTED, "LoRA delta grid too large");
   const dim3 gb(static_cast<unsigned>(cdiv(M, tile_rows) * ncb));
 #define E4B_LB(AD, OD)                                                                                          \
@@ -399,6 +416,46 @@ int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_r
   E4B_LB(E4B_FP32, E4B_BF16) E4B_LB(E4B_FP32, E4B_FP16) E4B_LB(E4B_FP32, E4B_FP32)
 #undef E4B_LB
   return check_launch("lora kernels");
+}
+
+int e4b_lora_delta_epilogue(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
+                            int32_t num_experts, const void* lora_a, const void* lora_b, int32_t adapter_dtype,
+                            int32_t rank, int64_t in_features, int64_t out_features, float scaling,
+                            float* t_workspace, const float* proj, int32_t epilogue, float limit, void* h,
+                            int32_t h_dtype, hipStream_t stream) {
+  if (!act_dtype_ok(h_dtype)) return fail(E4B_EINVAL, "h_dtype must be bf16 or fp16 (got %d)", h_dtype);
+  const bool gated_epi = epilogue == E4B_EPI_SWIGLU || epilogue == E4B_EPI_CLAMP_SWIGLU;
+  if (!gated_epi && epilogue != E4B_EPI_ACT)
+    return fail(E4B_EUNSUPPORTED, "epilogue %d: only SWIGLU, CLAMP_SWIGLU and ACT", epilogue);
+  if (gated_epi && out_features % 2 != 0) return fail(E4B_EINVAL, "gated epilogue needs an even out_features");
+  const int st = lora_a_pass(x, x_dtype, gather_k, rt, M, num_experts, lora_a, lora_b, adapter_dtype, rank,
+                             in_features, out_features, h_dtype, t_workspace, proj, stream);
+  if (st != E4B_OK || M == 0) return st;
+  if (!h) return fail(E4B_EINVAL, "NULL pointer");
+  const int64_t nh = gated_epi ? out_features / 2 : out_features;
+  const int64_t ncb = cdiv(nh, e4b::kLoraThreads);
+  const int tile_rows = lora_tile_rows(M);
+  if (cdiv(M, tile_rows) * ncb > 0x7fffffffLL) return fail(E4B_EUNSUPPORTED, "LoRA delta grid too large");
+  const dim3 gb(static_cast<unsigned>(cdiv(M, tile_rows) * ncb));
+#define E4B_LE(AD, HD, RB, G)                                                                                      \
+  hipLaunchKernelGGL((e4b::lora_b_epilogue_kernel<AD, HD, HD, RB, G>), gb, dim3(e4b::kLoraThreads), 0, stream,     \
+                     t_workspace, rt->offsets, num_experts, lora_b, rank, nh, out_features, scaling, proj, epilogue, \
+                     limit, static_cast<uint16_t*>(h), M, tile_rows, ncb)
+#define E4B_LE_R(AD, HD, G)                                 \
+  if (rank <= 16) E4B_LE(AD, HD, 16, G);                    \
+  else E4B_LE(AD, HD, e4b::kLoraMaxRank, G);
+#define E4B_LE_DT(AD, HD)                                   \
+  if (adapter_dtype == AD && h_dtype == HD) {               \
+    if (gated_epi) { E4B_LE_R(AD, HD, true) }               \
+    else { E4B_LE_R(AD, HD, false) }                        \
+  }
+  E4B_LE_DT(E4B_BF16, E4B_BF16) E4B_LE_DT(E4B_BF16, E4B_FP16)
+  E4B_LE_DT(E4B_FP16, E4B_BF16) E4B_LE_DT(E4B_FP16, E4B_FP16)
+  E4B_LE_DT(E4B_FP32, E4B_BF16) E4B_LE_DT(E4B_FP32, E4B_FP16)
+#undef E4B_LE_DT
+#undef E4B_LE_R
+#undef E4B_LE
+  return check_launch("lora_b_epilogue_kernel");
 }
 
 int e4b_combine(const void* down, int32_t down_dtype, const int32_t* inv, const void* top_k_weights,

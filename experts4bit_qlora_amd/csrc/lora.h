@@ -232,4 +232,75 @@ __global__ void __launch_bounds__(kLoraThreads) lora_b_add_kernel(const float* _
   }
 }
 
+// The gate_up projection's delta fused with the activation: for the sorted rows below
+// offsets[E], g = proj[m, n] + odt(delta[m, n]) and, when gated, u = proj[m, n + nh] +
+// odt(delta[m, n + nh]) (the two halves of lora.py's `_epilogue`, `proj.chunk(2, -1)`), then
+// h[m, n] = hdt(gated(epi, g, u) or single(epi, g)) for the nh = h columns. Same tiling as
+// lora_b_add_kernel; the fp32 projection is read once and never written back.
+template <int ADT, int ODT, int HDT, int RB, bool GATED>
+__global__ void __launch_bounds__(kLoraThreads) lora_b_epilogue_kernel(
+    const float* __restrict__ t, const int32_t* __restrict__ offsets, int E, const void* __restrict__ B, int r,
+    int64_t nh, int64_t nout, float scaling, const float* __restrict__ proj, int epi, float limit,
+    uint16_t* __restrict__ h, int64_t M, int tile_rows, int64_t ncb) {
+  __shared__ int offs[1025];
+  __shared__ float4 ts[kLoraMaxTileRows][RB / 4];
+  for (int i = threadIdx.x; i <= E; i += blockDim.x) offs[i] = offsets[i];
+  const int64_t tile = blockIdx.x / ncb;
+  const int64_t n = (blockIdx.x % ncb) * kLoraThreads + threadIdx.x;
+  const int64_t mbeg = tile * tile_rows;
+  float* tsf = reinterpret_cast<float*>(&ts[0][0]);
+  for (int i = threadIdx.x; i < tile_rows * RB; i += blockDim.x) {
+    const int row = i / RB, j = i % RB;
+    const int64_t m = mbeg + row;
+    tsf[i] = (m < M && j < r) ? t[m * r + j] : 0.0f;
+  }
+  __syncthreads();
+  int64_t mend = mbeg + tile_rows < M ? mbeg + tile_rows : M;
+  if (offs[E] < mend) mend = offs[E];
+  if (n >= nh) return;  // no barrier follows
+  constexpr int kHalves = GATED ? 2 : 1;
+  for (int64_t s = mbeg; s < mend;) {
+    const int e = row_expert(offs, E, static_cast<int>(s));
+    const int64_t send = segment_end(offs, e, mend);
+    float bv[kHalves][RB];
+#pragma unroll
+    for (int hf = 0; hf < kHalves; ++hf) {
+      const int64_t bo = (int64_t(e) * nout + n + hf * nh) * r;
+#pragma unroll
+      for (int j = 0; j < RB; ++j) {
+        if (j < r) {
+          if constexpr (ADT == E4B_FP32) bv[hf][j] = static_cast<const float*>(B)[bo + j];
+          else bv[hf][j] = to_f<ADT>(static_cast<const uint16_t*>(B)[bo + j]);
+        } else {
+          bv[hf][j] = 0.0f;
+        }
+      }
+    }
+    for (int64_t m = s; m < send; ++m) {
+      const float4* tr = ts[m - mbeg];
+      float v[kHalves];
+#pragma unroll
+      for (int hf = 0; hf < kHalves; ++hf) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int q = 0; q < RB / 4; ++q) {
+          const float4 tv = tr[q];
+          acc = __builtin_fmaf(tv.x, bv[hf][4 * q], acc);
+          acc = __builtin_fmaf(tv.y, bv[hf][4 * q + 1], acc);
+          acc = __builtin_fmaf(tv.z, bv[hf][4 * q + 2], acc);
+          acc = __builtin_fmaf(tv.w, bv[hf][4 * q + 3], acc);
+        }
+        float d = scaling * acc;
+        if constexpr (ODT != E4B_FP32) d = rnd<ODT>(d);
+        v[hf] = proj[m * nout + n + hf * nh] + d;
+      }
+      float o;
+      if constexpr (GATED) o = gated(epi, v[0], v[1], 1.0f, limit, 0.0f, 0.0f);
+      else o = single(epi, v[0], 0.0f);
+      h[m * nh + n] = from_f<HDT>(o);
+    }
+    s = send;
+  }
+}
+
 }  // namespace e4b

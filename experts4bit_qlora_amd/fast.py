@@ -151,7 +151,8 @@ def fused_experts_forward(mod, hidden_states, top_k_index, top_k_weights):
 def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
     """Fused inference forward of an ``ExpertsLoRA`` (``fast.py:163-257``): grouped GEMMs over the
     expert-sorted rows with the low-rank delta of every expert group added on the device
-    (``e4b_lora_delta``) before the base's epilogue, so no group size comes to the host (the
+    (``e4b_lora_delta``; for the gate_up projection fused with the activation,
+    ``e4b_lora_delta_epilogue``), so no group size comes to the host (the
     reference slices the groups in Python after a ``.tolist()``). The GEMM outputs stay fp32
     until the activation is rounded for the down projection."""
     base = mod.base
@@ -180,8 +181,13 @@ def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
     rb = ops.route(top_k_index, E)
     up = ops.grouped_gemm(x, w1, rb, tokens, M, N.EPI_NONE, gather_k=k, path=_kernel_path, out_dtype=torch.float32)
-    ops.lora_delta(x, rb, M, E, mod.gate_up_lora_A, mod.gate_up_lora_B, mod.scaling, up, gather_k=k)
-    h = _epilogue(base, up).to(compute_dtype).contiguous()
+    epi = _fused_epilogue(base)
+    if epi is not None:  # delta + activation in one pass over the fp32 rows
+        h = ops.lora_delta_epilogue(x, rb, M, E, mod.gate_up_lora_A, mod.gate_up_lora_B, mod.scaling, up, epi[0],
+                                    limit=epi[1], gather_k=k, h_dtype=compute_dtype)
+    else:  # a custom activation: the base's own Python epilogue
+        ops.lora_delta(x, rb, M, E, mod.gate_up_lora_A, mod.gate_up_lora_B, mod.scaling, up, gather_k=k)
+        h = _epilogue(base, up).to(compute_dtype).contiguous()
     down = ops.grouped_gemm(h, w2, rb, tokens, M, N.EPI_NONE, path=_kernel_path, out_dtype=torch.float32)
     ops.lora_delta(h, rb, M, E, mod.down_lora_A, mod.down_lora_B, mod.scaling, down)
     return ops.combine(down, rb, top_k_weights, tokens, k, input_dtype)

@@ -238,6 +238,36 @@ def lora_delta(x: torch.Tensor, rb: RoutingBuffers, M: int, num_experts: int, lo
     return out
 
 
+def lora_delta_epilogue(x: torch.Tensor, rb: RoutingBuffers, M: int, num_experts: int, lora_a: torch.Tensor,
+                        lora_b: torch.Tensor, scaling: float, proj: torch.Tensor, epilogue: int, limit: float = 0.0,
+                        gather_k: int = 0, h_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """The gate_up projection's LoRA delta fused with the activation: returns ``h`` ``[M, n']``
+    (``n' = out_features / 2`` for ``EPI_SWIGLU`` / ``EPI_CLAMP_SWIGLU``, else ``out_features``)
+    in ``h_dtype`` (default ``x.dtype``), ``h[m] = epilogue(proj[m] + h_dtype(scaling * (x_m @
+    A[e].T) @ B[e].T))`` for every routed row; ``proj`` (fp32, expert-sorted rows) is not written.
+    Rows past the routed ones are left unset."""
+    _require_cuda(x, lora_a, lora_b, proj)
+    if proj.dtype != torch.float32 or not proj.is_contiguous():
+        raise ValueError("proj must be a contiguous fp32 tensor")
+    L = N.lib()
+    xc = x.contiguous()
+    a = lora_a.contiguous()
+    b = lora_b.to(a.dtype).contiguous()
+    E, r, k_in = a.shape
+    n_out = b.shape[1]
+    gated = epilogue in (N.EPI_SWIGLU, N.EPI_CLAMP_SWIGLU)
+    hd = h_dtype or xc.dtype
+    h = torch.empty(M, n_out // 2 if gated else n_out, dtype=hd, device=x.device)
+    t = torch.empty(max(M, 1), r, dtype=torch.float32, device=x.device)
+    rt = rb.struct()
+    N.check("e4b_lora_delta_epilogue",
+            L.e4b_lora_delta_epilogue(xc.data_ptr(), dtype_code(xc.dtype), gather_k, ctypes.byref(rt), M, num_experts,
+                                      a.data_ptr(), b.data_ptr(), dtype_code(a.dtype), r, k_in, n_out, float(scaling),
+                                      t.data_ptr(), proj.data_ptr(), int(epilogue), float(limit), h.data_ptr(),
+                                      dtype_code(hd), _stream(x.device)))
+    return h
+
+
 def decode_gate_up(hidden: torch.Tensor, top_k_index: torch.Tensor, w1: QW, epilogue: int, alpha: float = 1.702,
                    limit: float = 7.0) -> torch.Tensor:
     """Decode-path gate_up (routing recomputed on the device): ``h [tokens * k, h_cols]`` in flat

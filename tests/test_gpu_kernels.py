@@ -428,6 +428,44 @@ def test_lora_delta_matches_per_group_reference(xdt, adt, gather, E, T, r, Nout)
     assert bool((err <= tol).all()), float((err - tol).max())
 
 
+@pytest.mark.parametrize("epi,adt,T,r", [("swiglu", torch.float32, 37, 16), ("swiglu", torch.bfloat16, 1536, 40),
+                                         ("clamp_swiglu", torch.float32, 400, 8), ("act", torch.bfloat16, 37, 16),
+                                         ("swiglu", torch.float32, 4500, 16)])
+def test_lora_delta_epilogue_matches_delta_then_epilogue(epi, adt, T, r):
+    """e4b_lora_delta_epilogue == e4b_lora_delta on the fp32 rows followed by the activation in
+    fp32 (the base's `_epilogue`, lora.py:102-128, on proj.chunk(2, -1)) and one rounding to the
+    compute dtype; they differ only by the sigmoid's few fp32 ulp, so within 2^-7 relative."""
+    _announce(f"lora delta epilogue epi={epi} adt={adt} T={T} r={r}")
+    E, top, K, n_out, scaling, limit = 40, 2, 256, 384, 0.5, 7.0
+    code = {"swiglu": N.EPI_SWIGLU, "clamp_swiglu": N.EPI_CLAMP_SWIGLU, "act": N.EPI_ACT}[epi]
+    g = torch.Generator().manual_seed(70 + T + r)
+    idx = torch.stack([torch.randperm(E - 2, generator=g)[:top] for _ in range(T)]).to(torch.int64)
+    idx[3, 0] = -1  # dropped
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16).to(DEV)
+    A = (torch.randn(E, r, K, generator=g) * 0.05).to(adt).to(DEV)
+    B = (torch.randn(E, n_out, r, generator=g) * 0.05).to(adt).to(DEV)
+    M = T * top
+    rb = ops.route(idx.to(DEV), E)
+    proj = (torch.randn(M, n_out, generator=g) * 4.0).to(DEV)
+    proj0 = proj.clone()
+    h = ops.lora_delta_epilogue(x, rb, M, E, A, B, scaling, proj, code, limit=limit, gather_k=top)
+    ref = proj.clone()
+    ops.lora_delta(x, rb, M, E, A, B, scaling, ref, gather_k=top)
+    if code == N.EPI_ACT:
+        want = torch.nn.functional.silu(ref)
+    else:
+        gte, up = ref.chunk(2, dim=-1)
+        if code == N.EPI_CLAMP_SWIGLU:
+            gte, up = gte.clamp(max=limit), up.clamp(-limit, limit)
+        want = torch.nn.functional.silu(gte) * up
+    n_valid = int(rb.offsets[E].item())
+    got, want = h[:n_valid].float().cpu(), want[:n_valid].to(torch.bfloat16).float().cpu()
+    assert got.shape == want.shape
+    err = (got - want).abs()
+    assert bool((err <= want.abs() * 2.0 ** -7 + 1e-6).all()), float(err.max())
+    assert torch.equal(proj, proj0)  # the fp32 rows are only read
+
+
 # ------------------------------------------------------------------- decode halves
 
 
