@@ -406,6 +406,10 @@ int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_r
       hipLaunchKernelGGL((e4b::lora_b_add_kernel<AD, OD, 16>), gb, dim3(e4b::kLoraThreads), 0, stream,          \
                          t_workspace, rt->offsets, num_experts, lora_b, rank, out_features, scaling, out, M,   \
                          tile_rows, ncb);                                                                       \
+    else if (rank <= 32)                                                                                        \
+      hipLaunchKernelGGL((e4b::lora_b_add_kernel<AD, OD, 32>), gb, dim3(e4b::kLoraThreads), 0, stream,          \
+                         t_workspace, rt->offsets, num_experts, lora_b, rank, out_features, scaling, out, M,   \
+                         tile_rows, ncb);                                                                       \
     else                                                                                                        \
       hipLaunchKernelGGL((e4b::lora_b_add_kernel<AD, OD, e4b::kLoraMaxRank>), gb, dim3(e4b::kLoraThreads), 0,   \
                          stream, t_workspace, rt->offsets, num_experts, lora_b, rank, out_features, scaling,   \
@@ -443,6 +447,7 @@ int e4b_lora_delta_epilogue(const void* x, int32_t x_dtype, int32_t gather_k, co
                      limit, static_cast<uint16_t*>(h), M, tile_rows, ncb)
 #define E4B_LE_R(AD, HD, G)                                 \
   if (rank <= 16) E4B_LE(AD, HD, 16, G);                    \
+  else if (rank <= 32) E4B_LE(AD, HD, 32, G);               \
   else E4B_LE(AD, HD, e4b::kLoraMaxRank, G);
 #define E4B_LE_DT(AD, HD)                                   \
   if (adapter_dtype == AD && h_dtype == HD) {               \

@@ -380,6 +380,7 @@ _LORA_CASES = [
     (torch.bfloat16, torch.float32, True, 12, 400, 5, 300),
     (torch.bfloat16, torch.bfloat16, True, 200, 1536, 40, 300),
     (torch.float16, torch.float32, False, 200, 1536, 40, 260),
+    (torch.bfloat16, torch.float32, True, 64, 1200, 32, 300),
     (torch.bfloat16, torch.float32, True, 64, 4500, 64, 520),
 ]
 
@@ -430,7 +431,7 @@ def test_lora_delta_matches_per_group_reference(xdt, adt, gather, E, T, r, Nout)
 
 @pytest.mark.parametrize("epi,adt,T,r", [("swiglu", torch.float32, 37, 16), ("swiglu", torch.bfloat16, 1536, 40),
                                          ("clamp_swiglu", torch.float32, 400, 8), ("act", torch.bfloat16, 37, 16),
-                                         ("swiglu", torch.float32, 4500, 16)])
+                                         ("swiglu", torch.float32, 4500, 16), ("swiglu", torch.float32, 1200, 32)])
 def test_lora_delta_epilogue_matches_delta_then_epilogue(epi, adt, T, r):
     """e4b_lora_delta_epilogue == e4b_lora_delta on the fp32 rows followed by the activation in
     fp32 (the base's `_epilogue`, lora.py:102-128, on proj.chunk(2, -1)) and one rounding to the
