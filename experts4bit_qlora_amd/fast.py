@@ -80,8 +80,27 @@ def _eligible_mxfp4(mod) -> Optional[str]:
 # ------------------------------------------------------------------- kernel descriptors
 
 
+def _qweight_sources(mod):
+    srcs = [mod.gate_up_proj, mod.gate_up_absmax, mod.down_proj, mod.down_absmax, mod.code]
+    if getattr(mod, "compress_statistics", False):
+        srcs += [mod.gate_up_absmax2, mod.gate_up_absmax_offset, mod.down_absmax2, mod.down_absmax_offset, mod.code2]
+    return srcs
+
+
 def _qweights(mod):
-    """(gate_up, down) kernel descriptors of an NF4 ``ExpertsNbit`` (fp32 or double-quant absmax)."""
+    """(gate_up, down) kernel descriptors of an NF4 ``ExpertsNbit``, cached on the module. The key
+    is every source tensor's storage address and in-place version counter, so a replaced buffer
+    or an in-place update (``load_state_dict`` copies) rebuilds them, including any dtype copy."""
+    key = tuple((t.data_ptr(), t._version) for t in _qweight_sources(mod))
+    hit = mod.__dict__.get("_e4b_qw_cache")
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    qws = _build_qweights(mod)
+    mod.__dict__["_e4b_qw_cache"] = (key, qws)
+    return qws
+
+
+def _build_qweights(mod):
     E = mod.num_experts
     n1, k1 = mod._gate_up_shape
     n2, k2 = mod._down_shape

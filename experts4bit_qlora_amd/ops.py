@@ -55,6 +55,10 @@ class QW:
     bias: torch.Tensor | None = None
 
     def struct(self) -> N.QWeight:
+        """The C descriptor, built once: the tensors it points at are held by this object."""
+        cached = self.__dict__.get("_struct")
+        if cached is not None:
+            return cached
         s = N.QWeight()
         s.format = self.fmt
         s.num_experts = self.num_experts
@@ -67,6 +71,7 @@ class QW:
         s.code = _ptr(self.code)
         s.code2 = _ptr(self.code2)
         s.bias = _ptr(self.bias)
+        self.__dict__["_struct"] = s
         return s
 
 

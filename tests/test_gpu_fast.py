@@ -206,6 +206,23 @@ def test_bare_fused_forward_never_syncs():
             torch.cuda.set_sync_debug_mode("default")
 
 
+def test_weight_descriptor_cache_follows_in_place_updates():
+    """The kernel descriptors are cached per module; an in-place update of a weight buffer (what
+    load_state_dict does) must reach the next fused forward."""
+    _announce("descriptor cache + in-place update")
+    mod, hs, top_i, top_w = _make(seed=11)
+    e4b.enable_fast(mod)
+    with torch.no_grad():
+        first = mod(hs, top_i, top_w)
+        mod.gate_up_absmax.mul_(2.0)
+        mod.down_absmax.mul_(0.5)
+        second = mod(hs, top_i, top_w)
+        e4b.disable_fast(mod)
+        ref = mod(hs, top_i, top_w)
+    assert not torch.equal(first, second)
+    assert _b_rel(second, ref) < 1.5e-2
+
+
 # ----------------------------------------------------------------------- ExpertsLoRA
 
 
