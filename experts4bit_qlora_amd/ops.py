@@ -54,8 +54,13 @@ class QW:
     code2: torch.Tensor | None = None
     bias: torch.Tensor | None = None
 
+    def __setattr__(self, name, value):  # a changed field invalidates the cached descriptor
+        self.__dict__.pop("_struct", None)
+        object.__setattr__(self, name, value)
+
     def struct(self) -> N.QWeight:
-        """The C descriptor, built once: the tensors it points at are held by this object."""
+        """The C descriptor, built once per field state: the tensors it points at are held by this
+        object, and assigning any field drops it."""
         cached = self.__dict__.get("_struct")
         if cached is not None:
             return cached
@@ -145,8 +150,14 @@ class RoutingBuffers:
         return r
 
 
+_TILE_M: list[int] = []
+
+
 def mfma_tile_m() -> int:
-    return int(N.lib().e4b_mfma_tile_m())
+    """Rows per MFMA tile of the library (a constant of the build; queried once)."""
+    if not _TILE_M:
+        _TILE_M.append(int(N.lib().e4b_mfma_tile_m()))
+    return _TILE_M[0]
 
 
 def route(top_k_index: torch.Tensor, num_experts: int, tile_m: int | None = None) -> RoutingBuffers:

@@ -168,3 +168,19 @@ def test_native_error_raises_with_message():
     with pytest.raises(N.NativeError, match="status -1"):
         N.lib().e4b_dequant(None, 0, 1, N.FP32, 4096, None)
         N.check("e4b_dequant", -1)
+
+
+def test_descriptor_structs_follow_field_changes():
+    """QW caches its C struct; assigning a field (a bias added after a first call, say) must
+    rebuild the struct, never hand the library a stale pointer."""
+    import torch
+    from experts4bit_qlora_amd import ops
+
+    qw = ops.QW(N.FMT_MXFP4, 2, 64, 64, torch.zeros(2 * 64 * 32, dtype=torch.uint8),
+                torch.zeros(2 * 64 * 2, dtype=torch.uint8))
+    s1 = qw.struct()
+    assert qw.struct() is s1 and not s1.bias
+    bias = torch.ones(2, 64)
+    qw.bias = bias
+    s2 = qw.struct()
+    assert s2 is not s1 and s2.bias == bias.data_ptr()
