@@ -110,8 +110,8 @@ def _bind(L):
     L.e4b_lora_delta.argtypes = [P, I32, I32, RT, I64, I32, P, P, I32, I32, I64, I64, F32, I32,
                                  P, P, P]
     L.e4b_lora_delta_epilogue.restype = ctypes.c_int
-    L.e4b_lora_delta_epilogue.argtypes = [P, I32, I32, RT, I64, I32, P, P, I32, I32, I64, I64, F32, P, P, I32,
-                                          F32, P, I32, P]
+    L.e4b_lora_delta_epilogue.argtypes = [P, I32, I32, RT, I64, I32, P, P, I32, I32, I64, I64, F32, I32, P, P,
+                                          I32, F32, P, I32, P]
     L.e4b_decode_gate_up.restype = ctypes.c_int
     L.e4b_decode_gate_up.argtypes = [P, I32, I64, P, I32, QW, I32, F32, F32, P, P]
     L.e4b_decode_down_combine.restype = ctypes.c_int

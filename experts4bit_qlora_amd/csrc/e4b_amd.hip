@@ -425,9 +425,11 @@ int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_r
 int e4b_lora_delta_epilogue(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
                             int32_t num_experts, const void* lora_a, const void* lora_b, int32_t adapter_dtype,
                             int32_t rank, int64_t in_features, int64_t out_features, float scaling,
-                            float* t_workspace, const float* proj, int32_t epilogue, float limit, void* h,
-                            int32_t h_dtype, hipStream_t stream) {
+                            int32_t delta_dtype, float* t_workspace, const float* proj, int32_t epilogue,
+                            float limit, void* h, int32_t h_dtype, hipStream_t stream) {
   if (!act_dtype_ok(h_dtype)) return fail(E4B_EINVAL, "h_dtype must be bf16 or fp16 (got %d)", h_dtype);
+  if (delta_dtype != h_dtype && delta_dtype != E4B_FP32)
+    return fail(E4B_EINVAL, "delta_dtype must be h_dtype or fp32 (got %d)", delta_dtype);
   const bool gated_epi = epilogue == E4B_EPI_SWIGLU || epilogue == E4B_EPI_CLAMP_SWIGLU;
   if (!gated_epi && epilogue != E4B_EPI_ACT)
     return fail(E4B_EUNSUPPORTED, "epilogue %d: only SWIGLU, CLAMP_SWIGLU and ACT", epilogue);
@@ -441,23 +443,27 @@ int e4b_lora_delta_epilogue(const void* x, int32_t x_dtype, int32_t gather_k, co
   const int tile_rows = lora_tile_rows(M);
   if (cdiv(M, tile_rows) * ncb > 0x7fffffffLL) return fail(E4B_EUNSUPPORTED, "LoRA delta grid too large");
   const dim3 gb(static_cast<unsigned>(cdiv(M, tile_rows) * ncb));
-#define E4B_LE(AD, HD, RB, G)                                                                                      \
-  hipLaunchKernelGGL((e4b::lora_b_epilogue_kernel<AD, HD, HD, RB, G>), gb, dim3(e4b::kLoraThreads), 0, stream,     \
+#define E4B_LE(AD, OD, HD, RB, G)                                                                                  \
+  hipLaunchKernelGGL((e4b::lora_b_epilogue_kernel<AD, OD, HD, RB, G>), gb, dim3(e4b::kLoraThreads), 0, stream,     \
                      t_workspace, rt->offsets, num_experts, lora_b, rank, nh, out_features, scaling, proj, epilogue, \
                      limit, static_cast<uint16_t*>(h), M, tile_rows, ncb)
-#define E4B_LE_R(AD, HD, G)                                 \
-  if (rank <= 16) E4B_LE(AD, HD, 16, G);                    \
-  else if (rank <= 32) E4B_LE(AD, HD, 32, G);               \
-  else E4B_LE(AD, HD, e4b::kLoraMaxRank, G);
+#define E4B_LE_R(AD, OD, HD, G)                             \
+  if (rank <= 16) E4B_LE(AD, OD, HD, 16, G);                \
+  else if (rank <= 32) E4B_LE(AD, OD, HD, 32, G);           \
+  else E4B_LE(AD, OD, HD, e4b::kLoraMaxRank, G);
+#define E4B_LE_OD(AD, OD, HD)                               \
+  if (gated_epi) { E4B_LE_R(AD, OD, HD, true) }             \
+  else { E4B_LE_R(AD, OD, HD, false) }
 #define E4B_LE_DT(AD, HD)                                   \
   if (adapter_dtype == AD && h_dtype == HD) {               \
-    if (gated_epi) { E4B_LE_R(AD, HD, true) }               \
-    else { E4B_LE_R(AD, HD, false) }                        \
+    if (delta_dtype == E4B_FP32) { E4B_LE_OD(AD, E4B_FP32, HD) } \
+    else { E4B_LE_OD(AD, HD, HD) }                          \
   }
   E4B_LE_DT(E4B_BF16, E4B_BF16) E4B_LE_DT(E4B_BF16, E4B_FP16)
   E4B_LE_DT(E4B_FP16, E4B_BF16) E4B_LE_DT(E4B_FP16, E4B_FP16)
   E4B_LE_DT(E4B_FP32, E4B_BF16) E4B_LE_DT(E4B_FP32, E4B_FP16)
 #undef E4B_LE_DT
+#undef E4B_LE_OD
 #undef E4B_LE_R
 #undef E4B_LE
   return check_launch("lora_b_epilogue_kernel");

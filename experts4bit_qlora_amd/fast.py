@@ -22,6 +22,7 @@ ONE library call (route, gate_up + epilogue, down, combine) with no host sync.
 """
 from __future__ import annotations
 
+import weakref
 from typing import Optional
 
 import torch
@@ -87,17 +88,36 @@ def _qweight_sources(mod):
     return srcs
 
 
-def _qweights(mod):
-    """(gate_up, down) kernel descriptors of an NF4 ``ExpertsNbit``, cached on the module. The key
-    is every source tensor's storage address and in-place version counter, so a replaced buffer
-    or an in-place update (``load_state_dict`` copies) rebuilds them, including any dtype copy."""
-    key = tuple((t.data_ptr(), t._version) for t in _qweight_sources(mod))
-    hit = mod.__dict__.get("_e4b_qw_cache")
+# Kernel descriptors per module, outside the module itself: a module's own state must stay
+# deep-copyable and picklable (the descriptors hold ctypes structs with raw pointers), and an
+# entry disappears with its module.
+_DESC_CACHE: "weakref.WeakKeyDictionary[torch.nn.Module, dict]" = weakref.WeakKeyDictionary()
+
+
+def _cached_descriptors(mod, tag, sources, build):
+    """``build()``'s result for ``mod``, rebuilt whenever a source tensor is replaced (storage
+    address) or updated in place (version counter, which ``load_state_dict`` copies bump).
+    Inference tensors carry no version counter: with any among the sources nothing is cached."""
+    if any(t.is_inference() for t in sources):
+        return build()
+    key = tuple((t.data_ptr(), t._version, t.dtype) for t in sources)
+    per_mod = _DESC_CACHE.setdefault(mod, {})
+    hit = per_mod.get(tag)
     if hit is not None and hit[0] == key:
         return hit[1]
-    qws = _build_qweights(mod)
-    mod.__dict__["_e4b_qw_cache"] = (key, qws)
-    return qws
+    value = build()
+    per_mod[tag] = (key, value)
+    return value
+
+
+def _drop_descriptors(mod) -> None:
+    """Forget ``mod``'s cached descriptors (and the weight tensors they keep alive)."""
+    _DESC_CACHE.pop(mod, None)
+
+
+def _qweights(mod):
+    """(gate_up, down) kernel descriptors of an NF4 ``ExpertsNbit``, cached per module."""
+    return _cached_descriptors(mod, "nf4", _qweight_sources(mod), lambda: _build_qweights(mod))
 
 
 def _build_qweights(mod):
@@ -113,6 +133,23 @@ def _build_qweights(mod):
         w1 = ops.nf4_qweight(mod.gate_up_proj, mod.gate_up_absmax, mod.code, n1, k1, num_experts=E)
         w2 = ops.nf4_qweight(mod.down_proj, mod.down_absmax, mod.code, n2, k2, num_experts=E)
     return w1, w2
+
+
+def _mxfp4_qweights(mod, cd):
+    """(gate_up, down) descriptors of a ``GptOssExpertsMxfp4`` with its biases in the compute
+    dtype ``cd``, cached per module like the NF4 ones (the bias casts included)."""
+    E = mod.num_experts
+    n1, k1 = mod._gate_up_shape
+    n2, k2 = mod._down_shape
+
+    def build():
+        w1 = ops.mxfp4_qweight(mod.gate_up_proj, mod.gate_up_absmax, n1, k1, num_experts=E,
+                               bias=mod.gate_up_bias.to(cd))
+        w2 = ops.mxfp4_qweight(mod.down_proj, mod.down_absmax, n2, k2, num_experts=E, bias=mod.down_bias.to(cd))
+        return w1, w2
+
+    srcs = [mod.gate_up_proj, mod.gate_up_absmax, mod.gate_up_bias, mod.down_proj, mod.down_absmax, mod.down_bias]
+    return _cached_descriptors(mod, ("mxfp4", cd), srcs, build)
 
 
 def _fused_epilogue(base):
@@ -143,6 +180,7 @@ def fused_experts_forward(mod, hidden_states, top_k_index, top_k_weights):
     if compute_dtype not in (torch.bfloat16, torch.float16):
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
     if mod.gate_up_proj.numel() == 0 or mod.down_proj.numel() == 0:
+        _drop_descriptors(mod)  # the evicted weights must not stay alive through the cache
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
 
     input_dtype = hidden_states.dtype
@@ -183,6 +221,7 @@ def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
     if compute_dtype not in (torch.bfloat16, torch.float16):
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
     if base.gate_up_proj.numel() == 0 or base.down_proj.numel() == 0:
+        _drop_descriptors(base)  # the evicted weights must not stay alive through the cache
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
 
     input_dtype = hidden_states.dtype
@@ -201,14 +240,17 @@ def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
     rb = ops.route(top_k_index, E)
     up = ops.grouped_gemm(x, w1, rb, tokens, M, N.EPI_NONE, gather_k=k, path=_kernel_path, out_dtype=torch.float32)
     epi = _fused_epilogue(base)
+    # the deltas stay fp32 until the single rounding of h / of the combined output: fewer
+    # rounding points than the reference's compute-dtype casts (lora.py:256), as for the base path
     if epi is not None:  # delta + activation in one pass over the fp32 rows
         h = ops.lora_delta_epilogue(x, rb, M, E, mod.gate_up_lora_A, mod.gate_up_lora_B, mod.scaling, up, epi[0],
-                                    limit=epi[1], gather_k=k, h_dtype=compute_dtype)
+                                    limit=epi[1], gather_k=k, h_dtype=compute_dtype, delta_dtype=torch.float32)
     else:  # a custom activation: the base's own Python epilogue
-        ops.lora_delta(x, rb, M, E, mod.gate_up_lora_A, mod.gate_up_lora_B, mod.scaling, up, gather_k=k)
+        ops.lora_delta(x, rb, M, E, mod.gate_up_lora_A, mod.gate_up_lora_B, mod.scaling, up, gather_k=k,
+                       delta_dtype=torch.float32)
         h = _epilogue(base, up).to(compute_dtype).contiguous()
     down = ops.grouped_gemm(h, w2, rb, tokens, M, N.EPI_NONE, path=_kernel_path, out_dtype=torch.float32)
-    ops.lora_delta(h, rb, M, E, mod.down_lora_A, mod.down_lora_B, mod.scaling, down)
+    ops.lora_delta(h, rb, M, E, mod.down_lora_A, mod.down_lora_B, mod.scaling, down, delta_dtype=torch.float32)
     return ops.combine(down, rb, top_k_weights, tokens, k, input_dtype)
 
 
@@ -219,18 +261,16 @@ def fused_mxfp4_forward(mod, hidden_states, top_k_index, top_k_weights):
     if _wants_reference(mod, hidden_states):
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
     cd = mod.compute_dtype if mod.compute_dtype is not None else hidden_states.dtype
-    if cd not in (torch.bfloat16, torch.float16) or mod.gate_up_proj.numel() == 0:
+    if mod.gate_up_proj.numel() == 0 or mod.down_proj.numel() == 0:
+        _drop_descriptors(mod)
+        return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+    if cd not in (torch.bfloat16, torch.float16):
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
     input_dtype = hidden_states.dtype
     x = hidden_states.to(cd)
     if x.shape[0] == 0:
         return torch.zeros(0, mod.hidden_dim, dtype=input_dtype, device=x.device)
-    E = mod.num_experts
-    n1, k1 = mod._gate_up_shape
-    n2, k2 = mod._down_shape
-    w1 = ops.mxfp4_qweight(mod.gate_up_proj, mod.gate_up_absmax, n1, k1, num_experts=E,
-                           bias=mod.gate_up_bias.to(cd))
-    w2 = ops.mxfp4_qweight(mod.down_proj, mod.down_absmax, n2, k2, num_experts=E, bias=mod.down_bias.to(cd))
+    w1, w2 = _mxfp4_qweights(mod, cd)
     return ops.moe_forward(x, top_k_index, top_k_weights, w1, w2, N.EPI_GPTOSS, input_dtype, alpha=mod.alpha,
                            limit=mod.limit, path=_kernel_path)
 
@@ -339,4 +379,5 @@ def disable_fast(model) -> int:
             mod.forward = mod._e4b_fast_ref
             del mod._e4b_fast_ref
             restored += 1
+        _drop_descriptors(mod)
     return restored

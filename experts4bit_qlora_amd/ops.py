@@ -256,12 +256,14 @@ def lora_delta(x: torch.Tensor, rb: RoutingBuffers, M: int, num_experts: int, lo
 
 def lora_delta_epilogue(x: torch.Tensor, rb: RoutingBuffers, M: int, num_experts: int, lora_a: torch.Tensor,
                         lora_b: torch.Tensor, scaling: float, proj: torch.Tensor, epilogue: int, limit: float = 0.0,
-                        gather_k: int = 0, h_dtype: torch.dtype | None = None) -> torch.Tensor:
+                        gather_k: int = 0, h_dtype: torch.dtype | None = None,
+                        delta_dtype: torch.dtype | None = None) -> torch.Tensor:
     """The gate_up projection's LoRA delta fused with the activation: returns ``h`` ``[M, n']``
     (``n' = out_features / 2`` for ``EPI_SWIGLU`` / ``EPI_CLAMP_SWIGLU``, else ``out_features``)
-    in ``h_dtype`` (default ``x.dtype``), ``h[m] = epilogue(proj[m] + h_dtype(scaling * (x_m @
-    A[e].T) @ B[e].T))`` for every routed row; ``proj`` (fp32, expert-sorted rows) is not written.
-    Rows past the routed ones are left unset."""
+    in ``h_dtype`` (default ``x.dtype``), ``h[m] = epilogue(proj[m] + delta_dtype(scaling * (x_m @
+    A[e].T) @ B[e].T))`` for every routed row (``delta_dtype``: ``h_dtype`` by default, as the
+    reference's ``_lora`` casts it back, or ``torch.float32`` to leave it unrounded); ``proj``
+    (fp32, expert-sorted rows) is not written. Rows past the routed ones are left unset."""
     _require_cuda(x, lora_a, lora_b, proj)
     if proj.dtype != torch.float32 or not proj.is_contiguous():
         raise ValueError("proj must be a contiguous fp32 tensor")
@@ -279,8 +281,8 @@ def lora_delta_epilogue(x: torch.Tensor, rb: RoutingBuffers, M: int, num_experts
     N.check("e4b_lora_delta_epilogue",
             L.e4b_lora_delta_epilogue(xc.data_ptr(), dtype_code(xc.dtype), gather_k, ctypes.byref(rt), M, num_experts,
                                       a.data_ptr(), b.data_ptr(), dtype_code(a.dtype), r, k_in, n_out, float(scaling),
-                                      t.data_ptr(), proj.data_ptr(), int(epilogue), float(limit), h.data_ptr(),
-                                      dtype_code(hd), _stream(x.device)))
+                                      dtype_code(delta_dtype or hd), t.data_ptr(), proj.data_ptr(), int(epilogue),
+                                      float(limit), h.data_ptr(), dtype_code(hd), _stream(x.device)))
     return h
 
 

@@ -149,7 +149,8 @@ int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_r
 
 // The gate_up projection's LoRA delta fused with the activation, for the fused LoRA forward's
 // first projection: the same t = x . A^T pass as e4b_lora_delta (same arguments and limits,
-// the delta rounded to h_dtype), then for every routed row g = proj[m, n] + delta[m, n] and,
+// the delta rounded to delta_dtype: h_dtype as the reference's `_lora` casts it back, or E4B_FP32
+// to keep it unrounded), then for every routed row g = proj[m, n] + delta[m, n] and,
 // for the gated epilogues, u = proj[m, n + out/2] + delta[m, n + out/2] (the `proj.chunk(2, -1)`
 // halves), h[m, n] = h_dtype(SWIGLU / CLAMP_SWIGLU(g, u; limit) or ACT(g)). `proj` (fp32
 // [M, out_features]) is only read; h is [M, out_features / 2] (gated) or [M, out_features].
@@ -157,8 +158,8 @@ int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_r
 int e4b_lora_delta_epilogue(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
                             int32_t num_experts, const void* lora_a, const void* lora_b, int32_t adapter_dtype,
                             int32_t rank, int64_t in_features, int64_t out_features, float scaling,
-                            float* t_workspace, const float* proj, int32_t epilogue, float limit, void* h,
-                            int32_t h_dtype, hipStream_t stream);
+                            int32_t delta_dtype, float* t_workspace, const float* proj, int32_t epilogue,
+                            float limit, void* h, int32_t h_dtype, hipStream_t stream);
 
 /* Decode path, first half: routing of top_k_index recomputed on the device (no route launch),
  * gate_up GEMV with the fused epilogue. h is [tokens * top_k, h_cols] in act_dtype, row

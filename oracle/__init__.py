@@ -29,10 +29,19 @@ Pinning status (what checks each function, so a plausible mistake fails one of t
 * NF4 dequant         -- pinned: hand-computed golden vectors, brute-force loop on tiny
                          inputs, whole-stack == per-expert invariant.
 * double-quant absmax -- dequant given (codes, absmax2, offset, code2) pinned by closed
-                         form on hand vectors; the 256-entry ``code2`` table and the
-                         quantizer's exact byte choices are PARITY UNPINNED (bitsandbytes
-                         is not importable here; only structural invariants are checked).
-* FP4 (bnb) table     -- PARITY UNPINNED (structural checks only; not on the fast path).
+                         form on hand vectors; the 256-entry ``code2`` table pinned against
+                         its exact rational construction (every entry within 2 fp32 ulp)
+                         and hand-derived fp32 bits of every decade's first and last cell,
+                         with negative controls (a grid one point short, a decade off).
+                         The quantizer's byte choices only generate inputs: parity is per
+                         given bytes.
+* FP4 (bnb) table     -- pinned bit for bit against bitsandbytes' published CUDA decode tree.
+* LoRA forward        -- ``moe.forward_lora_fp32`` (exact) and ``moe.reference_lora_loop``
+                         (the reference's rounding points): pinned by closed forms on small
+                         inputs (zero adapter == base oracle; rank-1 adapter == hand sum) and
+                         a negative control (delta added after the activation fails).
+* routers             -- ``routing.router_topk``: pinned by brute force on small inputs
+                         (sorted logits, ties to the lower expert index).
 * MXFP4 dequant       -- pinned: the reference's hand-checkable golden vector and golden
                          fixtures written by transformers' ``convert_moe_packed_tensors``.
 * routing             -- pinned: brute force on tiny inputs and the reference's special

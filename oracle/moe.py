@@ -9,6 +9,12 @@ Three restatements, all over the SAME dequantized weights:
                         bf16 gate_up output, the base epilogue in bf16 (``lora.py:102-128``), bf16
                         down output, fp32 router weight, ``buf[order] = down * w`` then a
                         fixed-axis k-sum (``fast.py:260-278``), cast back.
+``forward_lora_fp32``   the same fp32 oracle for an ``ExpertsLoRA`` (``lora.py:329-407``): each
+                        projection plus its low-rank delta ``scaling * (x A^T) B^T``
+                        (``_lora``, ``lora.py:251-256``) before the activation, exact (fp64).
+``reference_lora_loop`` ``ExpertsLoRA.forward`` itself in torch on the CPU, with its rounding
+                        points (compute-dtype projections, the delta in the adapter dtype then
+                        cast back, ``lora.py:251-256, 329-460``): the LoRA error anchor.
 ``reference_loop``      the reference per-expert loop ``ExpertsNbit.forward``
                         (``_vendor/experts.py:468-516``) in torch on the CPU: per hit expert,
                         dequantize to the compute dtype, ``F.linear``, ``act(gate) * up``,
@@ -82,6 +88,82 @@ def forward_fp32(x, top_k_index, top_k_weights, w1, w2, epilogue="swiglu", b1=No
             y = y + np.asarray(b2[e], dtype=np.float64)
         np.add.at(out, tok, y * wts[tok, pos][:, None])
     return out.astype(np.float32)
+
+
+def forward_lora_fp32(x, top_k_index, top_k_weights, w1, w2, lora1, lora2, scaling, epilogue="swiglu"):
+    """fp32 oracle of ``ExpertsLoRA.forward`` (``lora.py:329-407``), accumulated in fp64.
+
+    ``lora1 = (A1 [E, r, K1], B1 [E, N1, r])`` and ``lora2 = (A2 [E, r, K2], B2 [E, N2, r])``.
+    Per routed expert ``e`` with rows ``x_e``:
+    ``proj = x_e W1[e]^T + scaling * (x_e A1[e]^T) B1[e]^T`` (``lora.py:373-382``: base
+    projection plus ``_lora``), ``h = epilogue(proj)`` (``:384``, ``_epilogue`` at ``:102-128``),
+    ``y = h W2[e]^T + scaling * (h A2[e]^T) B2[e]^T`` (``:386-399``), then ``y * w`` summed into the
+    token (``:401-402``). No intermediate rounding. ``w1[e]`` / ``w2[e]`` may be any object
+    indexable by expert (only the routed experts are read).
+    """
+    x = np.asarray(x, dtype=np.float64)
+    idx = np.asarray(top_k_index, dtype=np.int64)
+    wts = np.asarray(top_k_weights, dtype=np.float64)
+    A1, B1 = (np.asarray(t, np.float64) for t in lora1)
+    A2, B2 = (np.asarray(t, np.float64) for t in lora2)
+    n_half = B1.shape[1] // 2
+    out = np.zeros((x.shape[0], B2.shape[1]), dtype=np.float64)
+    for e in sorted(set(idx.reshape(-1).tolist())):
+        tok, pos = np.nonzero(idx == e)
+        xe = x[tok]
+        p = xe @ np.asarray(w1[e], np.float64).T + scaling * ((xe @ A1[e].T) @ B1[e].T)
+        h = _glu_exact(p, epilogue, n_half)
+        y = h @ np.asarray(w2[e], np.float64).T + scaling * ((h @ A2[e].T) @ B2[e].T)
+        np.add.at(out, tok, y * wts[tok, pos][:, None])
+    return out.astype(np.float32)
+
+
+def reference_lora_loop(x, top_k_index, top_k_weights, w1_dq, w2_dq, lora1, lora2, scaling, num_experts,
+                        compute_dtype=None, has_gate=True):
+    """``ExpertsLoRA.forward`` (``lora.py:329-407``; one token: ``_forward_decode``, ``:409-460``) in
+    torch on the CPU with the reference's rounding points: base projections in the compute dtype
+    (``F.linear`` against the dequantized expert), ``_lora`` in the adapter dtype and cast back
+    (``:251-256``), the SwiGLU in the compute dtype, the router weight multiplied in the compute
+    dtype and accumulated in fp32. ``w1_dq`` / ``w2_dq`` are ``(e, dtype) -> [out, in]`` callables;
+    ``lora1`` / ``lora2`` are ``(A, B)`` torch tensors. Returns ``x``'s dtype."""
+    import torch
+    import torch.nn.functional as F
+
+    def _lora(v, A, B):
+        return (scaling * F.linear(F.linear(v.to(A.dtype), A), B)).to(v.dtype)
+
+    def _act(proj):
+        if has_gate:
+            g, u = proj.chunk(2, dim=-1)
+            return F.silu(g) * u
+        return F.silu(proj)
+
+    input_dtype = x.dtype
+    cd = compute_dtype if compute_dtype is not None else x.dtype
+    hs = x.to(cd)
+    A1, B1 = lora1
+    A2, B2 = lora2
+    final = torch.zeros_like(hs, dtype=torch.float32)
+    with torch.no_grad():
+        if hs.shape[0] == 1:  # _forward_decode: the token's slots in routing order
+            for j in range(top_k_index.shape[1]):
+                e = int(top_k_index[0, j])
+                proj = F.linear(hs, w1_dq(e, cd)) + _lora(hs, A1[e], B1[e])
+                h = _act(proj)
+                h = F.linear(h, w2_dq(e, cd)) + _lora(h, A2[e], B2[e])
+                final += (h * top_k_weights[0, j]).to(final.dtype)
+            return final.to(input_dtype)
+        mask = F.one_hot(top_k_index, num_classes=num_experts).permute(2, 1, 0)
+        hit = torch.greater(mask.sum(dim=(-1, -2)), 0).nonzero(as_tuple=False).view(-1)
+        for e in hit.tolist():
+            pos, tok = torch.where(mask[e])
+            cur = hs[tok]
+            proj = F.linear(cur, w1_dq(e, cd)) + _lora(cur, A1[e], B1[e])
+            h = _act(proj)
+            h = F.linear(h, w2_dq(e, cd)) + _lora(h, A2[e], B2[e])
+            h = h * top_k_weights[tok, pos, None]
+            final.index_add_(0, tok, h.to(final.dtype))
+    return final.to(input_dtype)
 
 
 def epilogue_rounded(proj_r, epilogue, n_half, dt="bf16", b1=None):
@@ -199,11 +281,27 @@ def dequant_torch_expert(packed_e, absmax_e, code, n, k, dtype):
 
 
 def rel_errors(got, want):
-    """(rel-Frobenius, max-abs on oracle-RMS-normalised outputs, max-abs / max|want|)."""
+    """(rel-Frobenius, max-abs on unit-scale outputs, max-abs / max|want|) of ``[tokens, hidden]``
+    outputs. "Unit-scale" puts every token's output row at unit RMS (the oracle row's RMS), so a
+    token whose routing weights make its output several times larger than another's is not
+    judged on that scale; ``max-abs / max|want|`` is the reference's own ``_b_rel``
+    (``tests/test_fast.py:43-46``)."""
     g = np.asarray(got, np.float64)
     w = np.asarray(want, np.float64)
+    if not w.size:
+        return 0.0, 0.0, 0.0
     fro = np.linalg.norm(g - w) / max(np.linalg.norm(w), 1e-30)
-    rms = max(np.sqrt(np.mean(w * w)) if w.size else 0.0, 1e-30)
-    maxabs = np.max(np.abs(g - w)) / rms if w.size else 0.0
-    brel = np.max(np.abs(g - w)) / max(np.max(np.abs(w)), 1e-30) if w.size else 0.0
+    w2 = w.reshape(-1, w.shape[-1])
+    rms = np.maximum(np.sqrt(np.mean(w2 * w2, axis=-1, keepdims=True)), 1e-30)
+    maxabs = np.max(np.abs(g.reshape(w2.shape) - w2) / rms)
+    brel = np.max(np.abs(g - w)) / max(np.max(np.abs(w)), 1e-30)
     return float(fro), float(maxabs), float(brel)
+
+
+def maxabs_global_rms(got, want):
+    """max-abs over the whole output divided by the whole output's RMS (one scale for all
+    tokens): a stricter figure than ``rel_errors``' per-token one, reported beside it."""
+    g = np.asarray(got, np.float64)
+    w = np.asarray(want, np.float64)
+    rms = max(np.sqrt(np.mean(w * w)) if w.size else 0.0, 1e-30)
+    return float(np.max(np.abs(g - w)) / rms) if w.size else 0.0

@@ -13,6 +13,9 @@ Restates ``experts4bit_qlora/engines/fast.py:125-133`` (and the identical block 
 
 plus the inverse permutation ``inv[order[r]] = r`` that the combine uses to find the sorted
 row of a ``(token, slot)`` pair, and the exclusive prefix ``offsets`` of ``counts``.
+
+The routers that produce ``top_k_index`` / ``top_k_weights`` (inputs of the path, not on it)
+are restated by ``router_topk`` from ``experts4bit_qlora/engines/cpu_router.py:100-120``.
 """
 from __future__ import annotations
 
@@ -66,3 +69,32 @@ def m_tiles(counts, tile_m: int):
         for t in range(-(-int(c) // tile_m)):
             out.append((e, int(off[e]) + t * tile_m))
     return out
+
+
+SOFTMAX_THEN_TOPK = "softmax_then_topk"  # OLMoE / Qwen3-MoE (cpu_router.py:63-67)
+TOPK_THEN_SOFTMAX = "topk_then_softmax"  # gpt-oss
+
+
+def router_topk(logits, k: int, kind: str = SOFTMAX_THEN_TOPK, renorm: bool = False):
+    """The routing epilogue in fp32 (``cpu_router.py:100-120``): top-k by a stable descending
+    sort (ties to the lower expert index, ``deterministic_topk`` at ``:100-105``); for
+    ``softmax_then_topk`` the weights are the softmax over ALL logits gathered at the top-k
+    (renormalised over the k when ``renorm``), for ``topk_then_softmax`` the softmax over the k
+    selected logits. Returns ``(weights [T, k] fp32, indices [T, k] int64)``."""
+    z = np.asarray(logits, dtype=np.float32)
+    order = np.argsort(-z, axis=-1, kind="stable")[:, :k].astype(np.int64)
+    top = np.take_along_axis(z, order, axis=-1)
+
+    def softmax(v):
+        e = np.exp((v - v.max(axis=-1, keepdims=True)).astype(np.float32)).astype(np.float32)
+        return (e / e.sum(axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32)
+
+    if kind == SOFTMAX_THEN_TOPK:
+        w = np.take_along_axis(softmax(z), order, axis=-1)
+        if renorm:
+            w = (w / w.sum(axis=-1, keepdims=True, dtype=np.float32)).astype(np.float32)
+    elif kind == TOPK_THEN_SOFTMAX:
+        w = softmax(top)
+    else:
+        raise ValueError(f"unknown router kind {kind!r}")
+    return w.astype(np.float32), order

@@ -17,6 +17,7 @@ from experts4bit_qlora_amd import fast as F
 from experts4bit_qlora_amd import ops
 from oracle import moe
 from oracle import quant as oq
+from oracle_weights import oracle_weights
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -43,7 +44,7 @@ def _make(E=4, H=128, inter=64, k=2, tokens=16, seed=0, has_gate=True, scale=1.0
     gate_up = torch.randn(E, 2 * inter if has_gate else inter, H) * scale
     down = torch.randn(E, H, inter) * scale
     mod = e4b.Experts4bit.from_float(gate_up.to(DEV), down.to(DEV), compute_dtype=torch.bfloat16, has_gate=has_gate,
-                                     compress_statistics=dq)
+                                     compress_statistics=dq).eval()
     hs = torch.randn(tokens, H, dtype=torch.bfloat16, device=DEV)
     logits = torch.randn(tokens, E, device=DEV)
     top_w, top_i = torch.topk(torch.softmax(logits, -1), k=k, dim=-1)
@@ -51,12 +52,9 @@ def _make(E=4, H=128, inter=64, k=2, tokens=16, seed=0, has_gate=True, scale=1.0
 
 
 def _oracle(mod, hs, top_i, top_w):
-    """fp32 forward over the same dequantized NF4 values (test_fast.py:49-68), CPU oracle."""
-    E = mod.num_experts
-    w1 = np.stack([mod._dequantize_expert(mod.gate_up_proj, mod.gate_up_absmax, mod._gate_up_shape, e,
-                                          torch.float32).cpu().numpy() for e in range(E)])
-    w2 = np.stack([mod._dequantize_expert(mod.down_proj, mod.down_absmax, mod._down_shape, e,
-                                          torch.float32).cpu().numpy() for e in range(E)])
+    """fp32 forward over the same NF4 values (test_fast.py:49-68), CPU oracle; the weights are
+    the module's bytes decoded by the oracle, not by the kernel under test."""
+    w1, w2 = oracle_weights(mod)
     epi = "swiglu" if mod.has_gate else "act"
     return moe.forward_fp32(hs.float().cpu().numpy(), top_i.cpu().numpy(), top_w.float().cpu().numpy(), w1, w2, epi)
 
@@ -64,8 +62,11 @@ def _oracle(mod, hs, top_i, top_w):
 def _assert_fidelity(fast, ref, oracle, label=""):
     fro, maxabs, brel = moe.rel_errors(fast.float().cpu().numpy(), oracle)
     fro_ref, maxabs_ref, brel_ref = moe.rel_errors(ref.float().cpu().numpy(), oracle)
-    print(f"[fidelity] {label}: fused rel-fro {fro:.2e} max-abs/rms {maxabs:.2e} max-abs/max {brel:.2e} | "
-          f"reference loop rel-fro {fro_ref:.2e} max-abs/rms {maxabs_ref:.2e} max-abs/max {brel_ref:.2e}", flush=True)
+    g_fast = moe.maxabs_global_rms(fast.float().cpu().numpy(), oracle)
+    g_ref = moe.maxabs_global_rms(ref.float().cpu().numpy(), oracle)
+    print(f"[fidelity] {label}: fused rel-fro {fro:.2e} max-abs/row-rms {maxabs:.2e} (global rms {g_fast:.2e}) "
+          f"max-abs/max {brel:.2e} | reference loop rel-fro {fro_ref:.2e} max-abs/row-rms {maxabs_ref:.2e} "
+          f"(global rms {g_ref:.2e}) max-abs/max {brel_ref:.2e}", flush=True)
     assert fro <= 1e-2 and maxabs <= 2e-2, (label, fro, maxabs)
     assert fro <= max(2 * fro_ref, 5e-3), (label, fro, fro_ref)
 
@@ -266,6 +267,49 @@ def test_lora_fused_matches_reference(n_tok):
     assert got.dtype == ref.dtype and rel < 2e-2, rel
 
 
+def _olmoe_lora(r, adapter_dtype, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    E, H, I = 64, 2048, 1024
+    base = e4b.Experts4bit.from_float(torch.randn(E, 2 * I, H, generator=g, device=DEV) * 0.02,
+                                      torch.randn(E, H, I, generator=g, device=DEV) * 0.02,
+                                      compute_dtype=torch.bfloat16).eval()
+    mod = e4b.ExpertsLoRA(base, r=r, alpha=2 * r, dtype=adapter_dtype).to(DEV).eval()
+    with torch.no_grad():
+        # B ~ N(0, 0.02): the delta is of the order of the base projection, not a rounding error
+        for p in (mod.gate_up_lora_B, mod.down_lora_B):
+            p.copy_(torch.randn(p.shape, generator=g, device=DEV) * 0.02)
+    return mod
+
+
+@pytest.mark.parametrize("T,r,adt", [(1, 8, torch.bfloat16), (1, 16, torch.float32), (8, 16, torch.bfloat16),
+                                     (8, 20, torch.float32), (8, 32, torch.bfloat16), (8, 64, torch.float32),
+                                     (64, 8, torch.float32), (64, 16, torch.bfloat16)])
+def test_lora_fused_matches_the_lora_oracle_at_olmoe_geometry(T, r, adt):
+    """The fused LoRA forward against the fp64 restatement of ExpertsLoRA.forward
+    (lora.py:251-256, 329-407) over the oracle-decoded NF4 weights, at the layer bars, and no
+    worse than max(2 x the reference loop's own error, 5e-3)."""
+    _announce(f"lora vs oracle OLMoE T={T} r={r} adapters={adt}")
+    mod = _olmoe_lora(r, adt, seed=7000 + 10 * T + r)
+    x, idx, w = _cfg_inputs(T, 64, 2048, 8, seed=7100 + T, renorm=False)
+    assert e4b.enable_fast(mod) == 1
+    with torch.no_grad():
+        got = mod(x, idx, w)
+    w1, w2 = oracle_weights(mod.base)
+    lo1 = tuple(t.detach().float().cpu().numpy() for t in (mod.gate_up_lora_A, mod.gate_up_lora_B))
+    lo2 = tuple(t.detach().float().cpu().numpy() for t in (mod.down_lora_A, mod.down_lora_B))
+    xs, ids, ws = x.float().cpu().numpy(), idx.cpu().numpy(), w.float().cpu().numpy()
+    want = moe.forward_lora_fp32(xs, ids, ws, w1, w2, lo1, lo2, mod.scaling)
+    base_only = moe.forward_fp32(xs, ids, ws, w1, w2)
+    delta = np.linalg.norm(want - base_only) / np.linalg.norm(want)
+    assert delta > 0.05, delta  # the adapter moves the output well past the bars below
+    lt1 = tuple(t.detach().cpu() for t in (mod.gate_up_lora_A, mod.gate_up_lora_B))
+    lt2 = tuple(t.detach().cpu() for t in (mod.down_lora_A, mod.down_lora_B))
+    ref = moe.reference_lora_loop(x.cpu(), idx.cpu(), w.cpu(), lambda e, dt: torch.from_numpy(w1[e]).to(dt),
+                                  lambda e, dt: torch.from_numpy(w2[e]).to(dt), lt1, lt2, mod.scaling,
+                                  num_experts=64, compute_dtype=torch.bfloat16)
+    _assert_fidelity(got, ref, want, f"lora T={T} r={r} {adt}")
+
+
 def test_lora_fused_forward_never_syncs():
     """The LoRA deltas of every expert group are added on the device (e4b_lora_delta), so the
     fused LoRA forward needs no group sizes on the host: no device synchronisation at all
@@ -418,12 +462,39 @@ def test_gptoss_mxfp4_fused_matches_reference_and_oracle(T):
         ref = mod(x, idx, w)
         assert e4b.enable_fast(mod) == 1
         got = mod(x, idx, w)
-    w1 = np.stack([mod._dequantize_expert("gate_up", e, torch.float32).cpu().numpy() for e in range(E)])
-    w2 = np.stack([mod._dequantize_expert("down", e, torch.float32).cpu().numpy() for e in range(E)])
+    w1, w2 = oracle_weights(mod)
     oracle = moe.forward_fp32(x.float().cpu().numpy(), idx.cpu().numpy(), w.float().cpu().numpy(), w1, w2,
                               ("gptoss", 1.702, 7.0), b1=mod.gate_up_bias.float().cpu().numpy(),
                               b2=mod.down_bias.float().cpu().numpy())
     _assert_fidelity(got, ref, oracle, f"gptoss T={T}")
+
+
+@pytest.mark.parametrize("sizes", [[1, 1, 1], [6, 0, 9, 1]])
+def test_gemm_mxfp4_grouped_drop_in(sizes):
+    """ops.gemm_mxfp4_grouped keeps mxfp4_grouped.gemm_mxfp4_grouped's call shape
+    (nvme_experts.py:852-865): a[M, K] rows grouped by expert, blocks [E, N, K/2], scales
+    [E, N, K/32]; checked against the oracle-decoded weights per group, for the all-size-1 (GEMV)
+    and mixed (GEMM) cases the reference distinguishes (test_mxfp4_arena_train.py:669-673)."""
+    _announce(f"gemm_mxfp4_grouped sizes={sizes}")
+    g = torch.Generator().manual_seed(len(sizes))
+    E, N, K = 4, 96, 256
+    blocks = torch.randint(0, 256, (E, N, K // 2), generator=g, dtype=torch.uint8)
+    scales = torch.randint(118, 130, (E, N, K // 32), generator=g, dtype=torch.uint8)
+    ids = [e for e, n_e in enumerate(sizes) if n_e > 0]  # one group per expert, ascending
+    sz = [n_e for n_e in sizes if n_e > 0]
+    M = sum(sz)
+    a = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    got = ops.gemm_mxfp4_grouped(a.to(DEV), blocks.to(DEV), scales.to(DEV), sz, ids).float().cpu().numpy()
+    from oracle import c_oracle
+
+    want = np.zeros((M, N), np.float64)
+    r0 = 0
+    for e, n_e in zip(ids, sz):
+        wdense = c_oracle.dequant_mxfp4(blocks[e].numpy(), scales[e].numpy(), N, K).astype(np.float64)
+        want[r0:r0 + n_e] = a[r0:r0 + n_e].double().numpy() @ wdense.T
+        r0 += n_e
+    rel = np.abs(got - want).max() / np.abs(want).max()
+    assert rel < 2e-2, rel  # the reference's kernel bar (test_mxfp4_arena_train.py:704-722)
 
 
 def test_mxfp4_checkpoint_layout_is_deinterleaved_losslessly():
@@ -463,16 +534,10 @@ def _cfg_inputs(T, E, H, k, seed, renorm):
 
 
 def _oracle_rows(mod, x, idx, w, rows):
-    """CPU fp64 oracle on a subset of tokens (only the experts those tokens hit are decoded)."""
+    """CPU fp64 oracle on a subset of tokens; only the experts those tokens hit are decoded, by the
+    oracle's C restatement from the module's stored bytes (never by the kernel under test)."""
     sub_idx = idx[rows].cpu().numpy()
-    hit = sorted(set(sub_idx.reshape(-1).tolist()))
-    E = mod.num_experts
-    w1 = np.zeros((E,) + mod._gate_up_shape, np.float32)
-    w2 = np.zeros((E,) + mod._down_shape, np.float32)
-    for e in hit:
-        w1[e] = mod._dequantize_expert(mod.gate_up_proj, mod.gate_up_absmax, mod._gate_up_shape, e,
-                                       torch.float32).cpu().numpy()
-        w2[e] = mod._dequantize_expert(mod.down_proj, mod.down_absmax, mod._down_shape, e, torch.float32).cpu().numpy()
+    w1, w2 = oracle_weights(mod)
     return moe.forward_fp32(x[rows].float().cpu().numpy(), sub_idx, w[rows].float().cpu().numpy(), w1, w2)
 
 
@@ -490,7 +555,8 @@ def test_baseline_configs_decode(cfg, T):
         ref = mod(x, idx, w)
         assert e4b.enable_fast(mod) == 1
         got = mod(x, idx, w)
-    rows = list(range(min(T, 8)))
+    # every token up to 64; beyond that 64 tokens spread over the batch
+    rows = list(range(T)) if T <= 64 else sorted(set(np.linspace(0, T - 1, 64).astype(int).tolist()))
     oracle = _oracle_rows(mod, x, idx, w, rows)
     _assert_fidelity(got[rows], ref[rows], oracle, f"{cfg} T={T}")
 
@@ -509,9 +575,20 @@ def test_qwen3_zipf_prefill_4096():
     with torch.no_grad():
         got = mod(x, idx, w)
     assert torch.isfinite(got).all()
-    rows = [0, 1, 2, 1000, 2047, 4095]
+    # the first and the last token routed to every active expert: every expert's first tile and
+    # its last (the 32-row tail tiles of the split tiling included) is checked
+    flat = idx.reshape(-1).cpu().numpy()
+    rows = set()
+    for e in np.unique(flat):
+        hits = np.nonzero(flat == e)[0] // k
+        rows.update([int(hits[0]), int(hits[-1])])
+    rows = sorted(rows)
+    _announce(f"qwen3 prefill oracle on {len(rows)} tokens covering {len(np.unique(flat))} experts")
     oracle = _oracle_rows(mod, x, idx, w, rows)
-    fro, maxabs, _ = moe.rel_errors(got[rows].float().cpu().numpy(), oracle)
+    fro, maxabs, brel = moe.rel_errors(got[rows].float().cpu().numpy(), oracle)
+    g_rms = moe.maxabs_global_rms(got[rows].float().cpu().numpy(), oracle)
+    print(f"[fidelity] qwen3 prefill: rel-fro {fro:.2e} max-abs/row-rms {maxabs:.2e} (global rms {g_rms:.2e}) "
+          f"max-abs/max {brel:.2e}", flush=True)
     assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
     # the GEMV and MFMA families agree on the same prefill (size-independent cross-check)
     F.set_kernel_path("gemv")
@@ -544,11 +621,7 @@ def test_gptoss_config_shapes(T):
         ref = mod._e4b_fast_ref(x[:4], idx[:4], w[:4])
     rows = list(range(min(T, 4)))
     sub = idx[rows].cpu().numpy()
-    w1 = np.zeros((E, 2 * I, H), np.float32)
-    w2 = np.zeros((E, H, I), np.float32)
-    for e in sorted(set(sub.reshape(-1).tolist())):
-        w1[e] = mod._dequantize_expert("gate_up", e, torch.float32).cpu().numpy()
-        w2[e] = mod._dequantize_expert("down", e, torch.float32).cpu().numpy()
+    w1, w2 = oracle_weights(mod)
     oracle = moe.forward_fp32(x[rows].float().cpu().numpy(), sub, w[rows].float().cpu().numpy(), w1, w2,
                               ("gptoss", 1.702, 7.0), b1=mod.gate_up_bias.float().cpu().numpy(),
                               b2=mod.down_bias.float().cpu().numpy())

@@ -174,8 +174,25 @@ def test_chunked_route_boundaries_and_dropped_ids(M, E):
 # --------------------------------------------------------------------------------- GEMMs
 
 
-def _dense_from_kernel(qw) -> np.ndarray:
-    return ops.dequant(qw, 0, qw.num_experts, dtype=torch.float32).cpu().numpy()
+def _dense_from_oracle(qw) -> np.ndarray:
+    """``[E, n, k]`` fp32 weights of a descriptor, decoded from its bytes by the oracle's C
+    restatement -- not by the dequant kernel, whose parity is tested on its own."""
+    from oracle import c_oracle
+
+    E, n, k = qw.num_experts, qw.n, qw.k
+    packed = qw.packed.cpu().numpy().reshape(E, -1)
+    absmax = qw.absmax.cpu().numpy().reshape(E, -1)
+    out = np.empty((E, n, k), np.float32)
+    for e in range(E):
+        if qw.fmt == N.FMT_MXFP4:
+            out[e] = c_oracle.dequant_mxfp4(packed[e], absmax[e], n, k)
+            continue
+        am = absmax[e]
+        if qw.fmt == N.FMT_NF4_DQ:
+            am = c_oracle.dequant_absmax_dq(am, qw.absmax2.cpu().numpy().reshape(E, -1)[e],
+                                            float(qw.offset.cpu().numpy().reshape(E)[e]), qw.code2.cpu().numpy())
+        out[e] = c_oracle.dequant_4bit(packed[e], am, qw.code.cpu().numpy()).reshape(n, k)
+    return out
 
 
 def _weights_for(path, W):
@@ -225,7 +242,7 @@ def test_grouped_gemm_plain(path, fmt, T):
         qw = ops.mxfp4_qweight(b.reshape(E, -1).to(DEV), s.reshape(E, -1).to(DEV), n, k, num_experts=E)
     else:
         qw, _, _ = _nf4_stack(E, n, k, seed=6, dq=(fmt == "nf4_dq"))
-    W = _dense_from_kernel(qw)
+    W = _dense_from_oracle(qw)
     rng = np.random.default_rng(T)
     idx = np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)
     x = torch.randn(T, k, generator=torch.Generator().manual_seed(T)).to(torch.bfloat16)
@@ -283,7 +300,7 @@ def test_grouped_gemm_fused_epilogues(path, epi):
     if epi == "gptoss":
         bias = (torch.randn(E, n, generator=g) * 0.5).to(torch.bfloat16)
         qw.bias = bias.to(DEV)
-    W = _dense_from_kernel(qw)
+    W = _dense_from_oracle(qw)
     rng = np.random.default_rng(9)
     idx = np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)
     x = (torch.randn(T, H, generator=g) * 3).to(torch.bfloat16)
@@ -305,7 +322,7 @@ def test_grouped_gemm_fp16_activations():
     _announce("grouped gemm fp16")
     E, n, k, top, T = 4, 128, 256, 2, 20
     qw, _, _ = _nf4_stack(E, n, k, seed=10)
-    W = _dense_from_kernel(qw)
+    W = _dense_from_oracle(qw)
     rng = np.random.default_rng(11)
     idx = np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)
     x = torch.randn(T, k, generator=torch.Generator().manual_seed(12)).to(torch.float16)
@@ -325,7 +342,7 @@ def test_gemm_4bit_grouped_api_shape():
     _announce("gemm_4bit_grouped API")
     E, n, k = 5, 64, 128
     qw, packed, absmax = _nf4_stack(E, n, k, seed=13)
-    W = _dense_from_kernel(qw)
+    W = _dense_from_oracle(qw)
     sizes, ids = [3, 1, 7], [0, 2, 4]
     a = torch.randn(sum(sizes), k, generator=torch.Generator().manual_seed(14)).to(torch.bfloat16)
     out = ops.gemm_4bit_grouped(a.to(DEV), qw.packed.view(E, n, k // 2), qw.absmax.view(E, n, k // 64), sizes, ids)
@@ -382,6 +399,10 @@ _LORA_CASES = [
     (torch.float16, torch.float32, False, 200, 1536, 40, 260),
     (torch.bfloat16, torch.float32, True, 64, 1200, 32, 300),
     (torch.bfloat16, torch.float32, True, 64, 4500, 64, 520),
+    # ranks 17-31 inside the 32-rank register slice (the j < r masking), 1-row and 8-row tiles
+    (torch.bfloat16, torch.float32, True, 12, 37, 20, 200),
+    (torch.bfloat16, torch.bfloat16, True, 64, 1200, 24, 300),
+    (torch.float16, torch.float16, False, 64, 1200, 20, 260),
 ]
 
 
@@ -431,7 +452,8 @@ def test_lora_delta_matches_per_group_reference(xdt, adt, gather, E, T, r, Nout)
 
 @pytest.mark.parametrize("epi,adt,T,r", [("swiglu", torch.float32, 37, 16), ("swiglu", torch.bfloat16, 1536, 40),
                                          ("clamp_swiglu", torch.float32, 400, 8), ("act", torch.bfloat16, 37, 16),
-                                         ("swiglu", torch.float32, 4500, 16), ("swiglu", torch.float32, 1200, 32)])
+                                         ("swiglu", torch.float32, 4500, 16), ("swiglu", torch.float32, 1200, 32),
+                                         ("swiglu", torch.float32, 37, 20), ("swiglu", torch.bfloat16, 1200, 24)])
 def test_lora_delta_epilogue_matches_delta_then_epilogue(epi, adt, T, r):
     """e4b_lora_delta_epilogue == e4b_lora_delta on the fp32 rows followed by the activation in
     fp32 (the base's `_epilogue`, lora.py:102-128, on proj.chunk(2, -1)) and one rounding to the
@@ -449,9 +471,11 @@ def test_lora_delta_epilogue_matches_delta_then_epilogue(epi, adt, T, r):
     rb = ops.route(idx.to(DEV), E)
     proj = (torch.randn(M, n_out, generator=g) * 4.0).to(DEV)
     proj0 = proj.clone()
-    h = ops.lora_delta_epilogue(x, rb, M, E, A, B, scaling, proj, code, limit=limit, gather_k=top)
+    # the delta rounded to the compute dtype (the reference's `_lora` cast) or kept in fp32
+    ddt = torch.float32 if r in (8, 20, 32) else None
+    h = ops.lora_delta_epilogue(x, rb, M, E, A, B, scaling, proj, code, limit=limit, gather_k=top, delta_dtype=ddt)
     ref = proj.clone()
-    ops.lora_delta(x, rb, M, E, A, B, scaling, ref, gather_k=top)
+    ops.lora_delta(x, rb, M, E, A, B, scaling, ref, gather_k=top, delta_dtype=ddt)
     if code == N.EPI_ACT:
         want = torch.nn.functional.silu(ref)
     else:
@@ -477,9 +501,9 @@ def _stack(fmt, E, n, k, seed):
         w = torch.randn(E, n, k, generator=g) * 0.05
         b, s = Q.quantize_mxfp4(w)
         qw = ops.mxfp4_qweight(b.reshape(E, -1).to(DEV), s.reshape(E, -1).to(DEV), n, k, num_experts=E)
-        return qw, _dense_from_kernel(qw).astype(np.float64)
+        return qw, _dense_from_oracle(qw).astype(np.float64)
     qw, _, _ = _nf4_stack(E, n, k, seed=seed, dq=(fmt == "nf4_dq"))
-    return qw, _dense_from_kernel(qw).astype(np.float64)  # the exact fp32 code * absmax
+    return qw, _dense_from_oracle(qw).astype(np.float64)  # the exact fp32 code * absmax
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
@@ -609,7 +633,7 @@ def test_mfma_output_columns_not_a_multiple_of_eight(gated):
     E, H, cols, top, T = 4, 256, 100, 2, 40
     n = 2 * cols if gated else cols
     qw, _, _ = _nf4_stack(E, n, H, seed=50)
-    W = _dense_from_kernel(qw)
+    W = _dense_from_oracle(qw)
     rng = np.random.default_rng(51)
     idx = np.stack([rng.permutation(E)[:top] for _ in range(T)]).astype(np.int64)
     x = torch.randn(T, H, generator=torch.Generator().manual_seed(52)).to(torch.bfloat16)

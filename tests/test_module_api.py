@@ -228,3 +228,69 @@ def test_gptoss_mxfp4_cpu_reference_forward():
     want = moe.forward_fp32(x.numpy(), idx.numpy(), w.numpy(), w1, w2, ("gptoss", 1.702, 7.0), b1=b1.numpy(),
                             b2=b2.numpy())
     assert np.linalg.norm(got - want) / np.linalg.norm(want) < 1e-5
+
+
+# ------------------------------------------------------------- kernel descriptor cache
+
+
+def _nf4_module(E=4, H=128, inter=64, dq=False):
+    gu, dn = _weights(E=E, H=H, inter=inter)
+    return e4b.Experts4bit.from_float(gu, dn, compute_dtype=torch.bfloat16, compress_statistics=dq)
+
+
+def test_descriptor_cache_works_for_inference_tensors():
+    """Weights built under inference_mode carry no version counter: the descriptors are then
+    rebuilt per call instead of raising."""
+    with torch.inference_mode():
+        mod = _nf4_module()
+    w1, w2 = F._qweights(mod)
+    assert w1.struct().n == mod._gate_up_shape[0] and w2.struct().k == mod._down_shape[1]
+    assert F._build_qweights(mod)[0].n == w1.n
+
+
+def test_descriptor_cache_keeps_the_module_copyable_and_picklable():
+    import copy
+
+    mod = _nf4_module()
+    w1, w2 = F._qweights(mod)
+    w1.struct(), w2.struct()  # what a fused forward builds
+    assert F._qweights(mod)[0] is w1  # cached
+    clone = copy.deepcopy(mod)
+    assert torch.equal(clone.gate_up_proj, mod.gate_up_proj)
+    buf = io.BytesIO()
+    torch.save(mod, buf)
+    assert len(buf.getvalue()) > 0
+    # an in-place update (what load_state_dict does) rebuilds the descriptors
+    with torch.no_grad():
+        mod.gate_up_absmax.mul_(2)
+    assert F._qweights(mod)[0] is not w1
+
+
+def test_evicted_storage_frees_the_cached_weights():
+    """Swapping in a 0-element placeholder (offload eviction) and taking the fused forward's
+    fallback must not keep the old weight stack alive through the descriptor cache; nor must
+    disable_fast."""
+    import gc
+    import weakref
+
+    mod = _nf4_module()
+    F._qweights(mod)[0].struct()
+    old = weakref.ref(mod.gate_up_proj)
+    mod._e4b_fast_ref = lambda *a: "reference"
+    mod.gate_up_proj = torch.nn.Parameter(torch.empty(0, dtype=torch.uint8), requires_grad=False)
+    x = torch.randn(2, 128, dtype=torch.bfloat16)
+    idx = torch.zeros(2, 2, dtype=torch.long)
+    w = torch.ones(2, 2, dtype=torch.bfloat16)
+    with torch.no_grad():
+        assert F.fused_experts_forward(mod, x, idx, w) == "reference"
+    gc.collect()
+    assert old() is None
+    # disable_fast forgets the descriptors of the modules it walks
+    mod2 = _nf4_module()
+    F._qweights(mod2)
+    old2 = weakref.ref(mod2.down_proj)
+    mod2._e4b_fast_ref = mod2.forward
+    F.disable_fast(mod2)
+    mod2.down_proj = torch.nn.Parameter(torch.empty(0, dtype=torch.uint8), requires_grad=False)
+    gc.collect()
+    assert old2() is None

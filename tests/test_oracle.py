@@ -64,6 +64,15 @@ def test_fp4_table_structure():
     assert sorted(np.abs(c[:8]) * 12) == [0.0, 0.0625, 2.0, 3.0, 4.0, 6.0, 8.0, 12.0]
 
 
+def test_fp4_table_matches_published_decode_tree_bit_for_bit():
+    tree = np.array([codes.fp4_tree_value(n) for n in range(16)], np.float32)
+    assert np.array_equal(tree.view(np.uint32), codes.FP4_CODE.view(np.uint32))
+    # a plausible transcription slip (two magnitudes swapped) fails the check
+    bad = codes.FP4_CODE.copy()
+    bad[[4, 6]] = bad[[6, 4]]
+    assert not np.array_equal(tree.view(np.uint32), bad.view(np.uint32))
+
+
 def test_dynamic_map_structure():
     m = codes.dynamic_map_signed()
     assert m.shape == (256,) and np.all(np.diff(m) >= 0)
@@ -72,8 +81,81 @@ def test_dynamic_map_structure():
     assert pos.size == 128 and neg.size == 127
     # every negative entry mirrors a positive one; 1.0 is the unmatched extra
     assert np.allclose(np.sort(-neg), np.sort(pos[:-1]))
-    # 7 decades of resolution: smallest magnitude ~ 0.55e-6 * ... (0.1 + 1)/2 * 1e-6
-    assert np.isclose(pos.min(), 0.55e-6, rtol=1e-5)
+
+
+def _within_ulps_of_exact(table, exact, ulps=2.0):
+    """Every fp32 entry within ``ulps`` of its exact rational value (same sorted position)."""
+    from fractions import Fraction
+
+    t = np.asarray(table, np.float32)
+    if t.shape != (len(exact),):
+        return False
+    for v, ex in zip(t, exact):
+        if ex == 0:
+            if v != 0:
+                return False
+            continue
+        if abs(Fraction(float(v)) - ex) > Fraction(ulps) * Fraction(float(np.spacing(np.abs(v)))):
+            return False
+    return True
+
+
+def _dynamic_map_variant(points=lambda i: 2 ** i + 1, decade=lambda i: i - 6):
+    """The fp32 construction with a swappable grid size / decade: the negative controls."""
+    data = []
+    for i in range(7):
+        b = torch.linspace(0.1, 1, points(i), dtype=torch.float32)
+        means = (b[:-1] + b[1:]) / 2.0
+        data += ((10 ** decade(i)) * means).tolist() + ((-(10 ** decade(i))) * means).tolist()
+    data += [0.0, 1.0]
+    data += [0.0] * (256 - len(data))
+    return np.array(sorted(data), np.float32)
+
+
+def test_dynamic_map_within_two_ulps_of_its_exact_construction():
+    exact = codes.dynamic_map_exact()
+    assert len(exact) == 256 and exact[127] == 0 and exact[255] == 1
+    assert _within_ulps_of_exact(codes.dynamic_map_signed(), exact)
+
+
+def test_dynamic_map_negative_controls_fail_the_exact_check():
+    exact = codes.dynamic_map_exact()
+    assert _within_ulps_of_exact(_dynamic_map_variant(), exact)  # the construction itself passes
+    # a grid one point short in every decade (2**i points instead of 2**i + 1)
+    assert not _within_ulps_of_exact(_dynamic_map_variant(points=lambda i: max(2 ** i, 2)), exact)
+    # every decade one power of ten too small
+    assert not _within_ulps_of_exact(_dynamic_map_variant(decade=lambda i: i - 7), exact)
+
+
+def _hand_derived_cell(i, j):
+    """fp32 value of decade ``i``'s cell ``j`` in the construction's own fp32 steps, for the first
+    (j = 0) and last (j = 2**i - 1) cell of a decade: boundaries ``start, start + step`` or
+    ``1 - step, 1`` (``step = fl32(1 - 0.1f) / 2**i``, exact), midpoint ``fl32(a + b) / 2``,
+    value ``fl32(fl32(10**(i-6)) * midpoint)``."""
+    f = np.float32
+    start, end = f(0.1), f(1.0)
+    step = f(f(end - start) / f(2 ** i))
+    if j == 0:
+        a, b = start, f(start + step)
+    else:
+        assert j == 2 ** i - 1
+        a, b = f(end - step), end
+    mid = f(f(a + b) / f(2))
+    return f(f(10.0 ** (i - 6)) * mid)
+
+
+def test_dynamic_map_hand_derived_bits():
+    m = codes.dynamic_map_signed().view(np.uint32)
+    for idx, bits in codes.DYNAMIC_MAP_PINS.items():
+        assert int(m[idx]) == bits, (idx, hex(int(m[idx])), hex(bits))
+    # the pins are the fp32 steps of the construction, repeated here in numpy
+    for i in range(7):
+        for j in {0, 2 ** i - 1}:
+            pos = 128 + (2 ** i - 1) + j
+            want = _hand_derived_cell(i, j)
+            assert int(np.array([want], np.float32).view(np.uint32)[0]) == codes.DYNAMIC_MAP_PINS[pos], (i, j)
+            # the mirrored negative entry
+            assert m[254 - pos] == np.array([-want], np.float32).view(np.uint32)[0]
 
 
 # ------------------------------------------------------------------------------ NF4 decode
@@ -342,3 +424,106 @@ def test_reference_loop_port_matches_oracle():
                              lambda e, dt: w1t[e].to(dt), lambda e, dt: w2t[e].to(dt), num_experts=6)
     want = moe.forward_fp32(x, idx, wts, w1, w2)
     assert np.linalg.norm(got.numpy() - want) / np.linalg.norm(want) < 1e-5
+
+
+
+# ------------------------------------------------------------------------------- LoRA oracle
+
+
+def _tiny_lora(seed=3, E=6, H=128, I=64, r=4):
+    rng = np.random.default_rng(seed)
+    A1 = rng.standard_normal((E, r, H)).astype(np.float32) * 0.2
+    B1 = rng.standard_normal((E, 2 * I, r)).astype(np.float32) * 0.2
+    A2 = rng.standard_normal((E, r, I)).astype(np.float32) * 0.2
+    B2 = rng.standard_normal((E, H, r)).astype(np.float32) * 0.2
+    return (A1, B1), (A2, B2)
+
+
+def test_lora_oracle_zero_adapter_is_the_base_oracle():
+    x, idx, wts, w1, w2 = _tiny_problem(seed=4)
+    (A1, B1), (A2, B2) = _tiny_lora()
+    got = moe.forward_lora_fp32(x, idx, wts, w1, w2, (A1, 0 * B1), (A2, 0 * B2), 2.0)
+    want = moe.forward_fp32(x, idx, wts, w1, w2)
+    assert np.allclose(got, want, rtol=1e-6, atol=1e-7)
+
+
+def test_lora_oracle_closed_form_and_negative_control():
+    """One token, one expert, rank 1: the delta is scaling * (x.a) * b, added BEFORE the
+    activation; the same delta added after the activation (a plausible bug) must differ."""
+    x, idx, wts, w1, w2 = _tiny_problem(seed=5, T=1, k=1)
+    E, N1, H = w1.shape
+    rng = np.random.default_rng(6)
+    a1, b1 = rng.standard_normal(H), rng.standard_normal(N1)
+    a2, b2 = rng.standard_normal(w2.shape[2]), rng.standard_normal(w2.shape[1])
+    A1 = np.zeros((E, 1, H)); B1 = np.zeros((E, N1, 1))
+    A2 = np.zeros((E, 1, w2.shape[2])); B2 = np.zeros((E, w2.shape[1], 1))
+    e = int(idx[0, 0])
+    A1[e, 0], B1[e, :, 0], A2[e, 0], B2[e, :, 0] = a1, b1, a2, b2
+    s = 0.5
+    got = moe.forward_lora_fp32(x, idx, wts, w1, w2, (A1, B1), (A2, B2), s)
+    xd = x[0].astype(np.float64)
+    proj = w1[e].astype(np.float64) @ xd + s * (xd @ a1) * b1
+    g, u = proj[: N1 // 2], proj[N1 // 2:]
+    h = g / (1 + np.exp(-g)) * u
+    y = w2[e].astype(np.float64) @ h + s * (h @ a2) * b2
+    want = y * wts[0, 0]
+    assert np.allclose(got[0], want, rtol=1e-5, atol=1e-6)
+    # negative control: the gate_up delta after the SwiGLU
+    p0 = w1[e].astype(np.float64) @ xd
+    h_bad = p0[: N1 // 2] / (1 + np.exp(-p0[: N1 // 2])) * p0[N1 // 2:] + (s * (xd @ a1) * b1)[: N1 // 2]
+    bad = (w2[e].astype(np.float64) @ h_bad + s * (h_bad @ a2) * b2) * wts[0, 0]
+    assert np.linalg.norm(got[0] - bad) / np.linalg.norm(want) > 0.05
+
+
+@pytest.mark.parametrize("T", [1, 12])
+def test_reference_lora_loop_matches_the_lora_oracle(T):
+    """The reference's own loop (both its decode and its mask path) against the exact form,
+    in fp32 (tight) and bf16 compute (the reference's rounding, loose)."""
+    x, idx, wts, w1, w2 = _tiny_problem(seed=7, T=T)
+    (A1, B1), (A2, B2) = _tiny_lora(seed=8)
+    want = moe.forward_lora_fp32(x, idx, wts, w1, w2, (A1, B1), (A2, B2), 2.0)
+    t = torch.from_numpy
+    w1t, w2t = t(w1), t(w2)
+    lo1, lo2 = (t(A1), t(B1)), (t(A2), t(B2))
+    for cd, tol in ((torch.float32, 1e-5), (torch.bfloat16, 3e-2)):
+        got = moe.reference_lora_loop(t(x), t(idx), t(wts), lambda e, dt: w1t[e].to(dt), lambda e, dt: w2t[e].to(dt),
+                                      lo1, lo2, 2.0, num_experts=6, compute_dtype=cd)
+        fro = np.linalg.norm(got.float().numpy() - want) / np.linalg.norm(want)
+        assert fro < tol, (cd, fro)
+
+
+# ----------------------------------------------------------------------------------- routers
+
+
+def _router_bruteforce(logits_row, k, kind, renorm):
+    """Pure-Python routing epilogue: rank experts by (-logit, index), softmax in fp64."""
+    import math
+
+    z = [float(v) for v in logits_row]
+    ranked = sorted(range(len(z)), key=lambda e: (-z[e], e))[:k]
+    if kind == routing.SOFTMAX_THEN_TOPK:
+        mx = max(z)
+        den = sum(math.exp(v - mx) for v in z)
+        w = [math.exp(z[e] - mx) / den for e in ranked]
+        if renorm:
+            tot = sum(w)
+            w = [v / tot for v in w]
+    else:
+        mx = max(z[e] for e in ranked)
+        den = sum(math.exp(z[e] - mx) for e in ranked)
+        w = [math.exp(z[e] - mx) / den for e in ranked]
+    return w, ranked
+
+
+@pytest.mark.parametrize("kind,renorm", [(routing.SOFTMAX_THEN_TOPK, False), (routing.SOFTMAX_THEN_TOPK, True),
+                                         (routing.TOPK_THEN_SOFTMAX, False)])
+def test_router_matches_bruteforce(kind, renorm):
+    rng = np.random.default_rng(9)
+    logits = rng.standard_normal((20, 16)).astype(np.float32)
+    logits[3, [2, 7, 11]] = 5.0  # ties resolve to the lower expert index
+    w, i = routing.router_topk(logits, 4, kind, renorm)
+    for t in range(20):
+        bw, bi = _router_bruteforce(logits[t], 4, kind, renorm)
+        assert list(i[t]) == bi
+        assert np.allclose(w[t], bw, rtol=1e-6)
+    assert list(i[3][:3]) == [2, 7, 11]
