@@ -28,6 +28,7 @@ EXPORTS = (
     "e4b_last_error",
     "e4b_mfma_tile_m",
     "e4b_dequant",
+    "e4b_weight_shift",
     "e4b_route_scratch_ints",
     "e4b_route",
     "e4b_grouped_gemm",
@@ -66,6 +67,7 @@ class QWeight(ctypes.Structure):
         ("code", ctypes.c_void_p),
         ("code2", ctypes.c_void_p),
         ("bias", ctypes.c_void_p),
+        ("shift", ctypes.c_void_p),
     ]
 
 
@@ -98,6 +100,8 @@ def _bind(L):
     L.e4b_mfma_tile_m.argtypes = []
     L.e4b_dequant.restype = ctypes.c_int
     L.e4b_dequant.argtypes = [QW, I32, I32, I32, P, P]
+    L.e4b_weight_shift.restype = ctypes.c_int
+    L.e4b_weight_shift.argtypes = [QW, P, P]
     L.e4b_route_scratch_ints.restype = I64
     L.e4b_route_scratch_ints.argtypes = [I64, I32]
     L.e4b_route.restype = ctypes.c_int

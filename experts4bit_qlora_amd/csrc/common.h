@@ -64,6 +64,29 @@ E4B_DEV uint32_t pack2(uint16_t lo, uint16_t hi) {
   return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
 }
 
+// ------------------------------------------------------------- fp16 operands of bf16 data
+// Power-of-two shift that puts values whose largest biased exponent (fp32 / bf16 field) is e
+// into [2^14, 2^15): below fp16's largest finite value, with fp16's 11 significant bits for
+// everything down to 2^-28 of that maximum. Exponents below 20 (|v| < 2^-107) count as 20, so
+// the shift and its inverse stay normal fp32 powers of two.
+__host__ __device__ inline int exp_shift(int e) { return 141 - (e > 20 ? e : 20); }
+
+// Largest biased exponent among the 8 bf16 values of a 16-byte piece, in bits 7..14.
+E4B_DEV uint32_t bf16_exp_max(const uint4& v) {
+  auto m2 = [](uint32_t w) { return max(w & 0x7f80u, (w >> 16) & 0x7f80u); };
+  return max(max(m2(v.x), m2(v.y)), max(m2(v.z), m2(v.w)));
+}
+
+// Two bf16 values times 2^d as an fp16 pair: exact for results of at least 2^-14 (bf16's 8
+// significant bits fit fp16's 11) when the results stay below 2^15, which exp_shift of their
+// row's (or chunk's) largest exponent guarantees. Round-toward-zero only touches results below
+// 2^-14 (at least 2^-28 under the row maximum).
+E4B_DEV uint32_t bf16x2_to_f16x2(uint32_t w, int d) {
+  const float lo = __builtin_amdgcn_ldexpf(__uint_as_float(w << 16), d);
+  const float hi = __builtin_amdgcn_ldexpf(__uint_as_float(w & 0xffff0000u), d);
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+}
+
 // ------------------------------------------------------------------------------ epilogues
 // sigmoid(x) = 1 / (1 + 2^(-x log2 e)) on the hardware exp2 and reciprocal (each within 1 ulp):
 // a few ulp of fp32 error, far below the bf16 / fp16 rounding every result goes through, for a

@@ -390,13 +390,8 @@ E4B_DEV void pair_chunk_dots(const uint4 (&qa)[CPL], const uint4 (&qb)[CPL], con
   }
 }
 
-// bf16 -> scaled fp16 restaging of activations (up kernel, NF4 weights).
-// Largest biased exponent among the 8 bf16 values of a 16-byte piece, in bits 7..14.
-E4B_DEV uint32_t bf16_exp_max(const uint4& v) {
-  auto m2 = [](uint32_t w) { return max(w & 0x7f80u, (w >> 16) & 0x7f80u); };
-  return max(max(m2(v.x), m2(v.y)), max(m2(v.z), m2(v.w)));
-}
-
+// bf16 -> scaled fp16 restaging of activations (up kernel, NF4 weights): bf16_exp_max gives a
+// 16-byte piece's largest exponent field.
 // Maximum over the aligned quad of lanes (the four pieces of one 32-value chunk).
 E4B_DEV uint32_t quad_max(uint32_t v) {
   v = max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), 0xb1, 0xf, 0xf, false)));
@@ -404,17 +399,8 @@ E4B_DEV uint32_t quad_max(uint32_t v) {
   return v;
 }
 
-// Shift that puts a chunk whose largest biased exponent is e into [2^14, 2^15); exponents below
-// 20 (|x| < 2^-107) count as 20, so both the shift and its inverse stay normal fp32 powers of two.
-E4B_DEV int chunk_shift(uint32_t exp_bits) { return 141 - max(static_cast<int>(exp_bits >> 7), 20); }
-
-// Two bf16 values times 2^d as an fp16 pair (exact for results of at least 2^-14; the values
-// carry 8 significant bits and the results stay below 2^15).
-E4B_DEV uint32_t bf16x2_to_f16x2(uint32_t w, int d) {
-  const float lo = __builtin_amdgcn_ldexpf(__uint_as_float(w << 16), d);
-  const float hi = __builtin_amdgcn_ldexpf(__uint_as_float(w & 0xffff0000u), d);
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
-}
+// Shift that puts a chunk whose largest biased exponent is e into [2^14, 2^15).
+E4B_DEV int chunk_shift(uint32_t exp_bits) { return exp_shift(static_cast<int>(exp_bits >> 7)); }
 
 E4B_DEV uint4 piece_to_f16(const uint4& v, int d) {
   return make_uint4(bf16x2_to_f16x2(v.x, d), bf16x2_to_f16x2(v.y, d), bf16x2_to_f16x2(v.z, d),

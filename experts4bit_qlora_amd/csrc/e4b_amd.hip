@@ -18,6 +18,7 @@
 #include "gemv.h"
 #include "lora.h"
 #include "route.h"
+#include "scale.h"
 
 namespace {
 
@@ -126,6 +127,22 @@ void launch_gemv_fmt(const e4b::GemmArgs& a, int64_t max_active, hipStream_t s) 
   }
 }
 
+// One tile height; the fp16 mode (a.a_exp set) exists for bf16 activations with NF4 weights.
+template <int DT, int FMT, int BM>
+void launch_mfma_bm(const e4b::GemmArgs& a, dim3 grid, hipStream_t s) {
+  if constexpr (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4) {
+    if (a.a_exp && a.a_f16) {
+      hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, BM, 2>), grid, dim3(e4b::gemm_threads(BM)), 0, s, a);
+      return;
+    }
+    if (a.a_exp) {
+      hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, BM, 1>), grid, dim3(e4b::gemm_threads(BM)), 0, s, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, BM, 0>), grid, dim3(e4b::gemm_threads(BM)), 0, s, a);
+}
+
 template <int DT, int FMT>
 void launch_mfma_fmt(const e4b::GemmArgs& a, hipStream_t s) {
   const bool pair = a.epi == E4B_EPI_SWIGLU || a.epi == E4B_EPI_CLAMP_SWIGLU || a.epi == E4B_EPI_GPTOSS;
@@ -134,16 +151,9 @@ void launch_mfma_fmt(const e4b::GemmArgs& a, hipStream_t s) {
   // 8 XCDs x ceil(max_tiles / 8) M tiles x n_tiles blocks, mapped to tiles in the kernel
   const int64_t n_tiles = cdiv(a.n_out, cols);
   dim3 grid(static_cast<unsigned>(e4b::kXcds * cdiv(a.rt.max_tiles, e4b::kXcds) * n_tiles));
-  if (a.rt.tile_m == e4b::kTileMSmall) {
-    hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, e4b::kTileMSmall>), grid,
-                       dim3(e4b::gemm_threads(e4b::kTileMSmall)), 0, s, a);
-  } else if (a.rt.tile_m == e4b::kTileMBig) {
-    hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, e4b::kTileMBig>), grid,
-                       dim3(e4b::gemm_threads(e4b::kTileMBig)), 0, s, a);
-  } else {
-    hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, e4b::kTileM>), grid, dim3(e4b::gemm_threads(e4b::kTileM)), 0,
-                       s, a);
-  }
+  if (a.rt.tile_m == e4b::kTileMSmall) launch_mfma_bm<DT, FMT, e4b::kTileMSmall>(a, grid, s);
+  else if (a.rt.tile_m == e4b::kTileMBig) launch_mfma_bm<DT, FMT, e4b::kTileMBig>(a, grid, s);
+  else launch_mfma_bm<DT, FMT, e4b::kTileM>(a, grid, s);
 }
 
 template <int DT>
@@ -298,9 +308,12 @@ int64_t e4b_route_scratch_ints(int64_t M, int32_t num_experts) {
   return cdiv(M, e4b::kRouteChunk) * (int64_t(num_experts) + 1);
 }
 
-int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e4b_qweight* w, const e4b_routing* rt,
-                     int64_t tokens, int64_t M, int32_t epilogue, float alpha, float limit, int32_t flags, void* out,
-                     int32_t out_dtype, hipStream_t stream) {
+// e4b_grouped_gemm, plus the fp16 matrix-core mode of the fused forward: a_exp (the A rows'
+// largest exponents) selects it on the MFMA path, out_exp collects the h rows' exponents.
+static int grouped_gemm_impl(const void* a, int32_t act_dtype, int32_t gather_k, const e4b_qweight* w,
+                             const e4b_routing* rt, int64_t tokens, int64_t M, int32_t epilogue, float alpha,
+                             float limit, int32_t flags, void* out, int32_t out_dtype, const int32_t* a_exp,
+                             int a_f16, int32_t* out_exp, hipStream_t stream) {
   int rc = check_weight(w);
   if (rc) return rc;
   rc = check_routing(rt, M);
@@ -338,9 +351,36 @@ int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e
   args.out = out;
   args.n_out = pair ? w->n / 2 : w->n;
   args.out_f32 = out_dtype == E4B_FP32;
+  const bool f16c = a_exp != nullptr;
+  if (f16c && (gemv || act_dtype != E4B_BF16 || w->format == E4B_FMT_MXFP4 || !w->shift))
+    return fail(E4B_EINVAL, "the fp16 matrix-core mode needs the MFMA path, bf16 activations and NF4 weight shifts");
+  args.a_exp = a_exp;
+  args.a_f16 = a_exp != nullptr && a_f16;
+  args.out_exp = out_exp;
   const int64_t max_active = std::min<int64_t>(w->num_experts, M);
   return act_dtype == E4B_BF16 ? launch_gemm_dt<E4B_BF16>(args, gemv, max_active, stream)
                                : launch_gemm_dt<E4B_FP16>(args, gemv, max_active, stream);
+}
+
+int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e4b_qweight* w, const e4b_routing* rt,
+                     int64_t tokens, int64_t M, int32_t epilogue, float alpha, float limit, int32_t flags, void* out,
+                     int32_t out_dtype, hipStream_t stream) {
+  return grouped_gemm_impl(a, act_dtype, gather_k, w, rt, tokens, M, epilogue, alpha, limit, flags, out, out_dtype,
+                           nullptr, 0, nullptr, stream);
+}
+
+int e4b_weight_shift(const e4b_qweight* w, int32_t* shift, hipStream_t stream) {
+  int rc = check_weight(w);
+  if (rc) return rc;
+  if (w->format == E4B_FMT_MXFP4) return fail(E4B_EUNSUPPORTED, "MXFP4 weights need no shift (exact in bf16)");
+  if (!shift) return fail(E4B_EINVAL, "shift is NULL");
+  if (w->format == E4B_FMT_NF4)
+    hipLaunchKernelGGL((e4b::weight_shift_kernel<E4B_FMT_NF4>), dim3(w->num_experts), dim3(e4b::kScaleThreads), 0,
+                       stream, *w, shift);
+  else
+    hipLaunchKernelGGL((e4b::weight_shift_kernel<E4B_FMT_NF4_DQ>), dim3(w->num_experts), dim3(e4b::kScaleThreads),
+                       0, stream, *w, shift);
+  return check_launch("weight_shift_kernel");
 }
 
 namespace {
@@ -578,6 +618,8 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
   }
   b += align256(sizeof(uint16_t) * M * h_cols);                        // h
   b += align256(sizeof(float) * M * n2);                               // down rows (fp32)
+  b += align256(sizeof(int32_t) * tokens) + align256(sizeof(int32_t) * M);  // fp16 mode row exponents
+  b += align256(sizeof(uint16_t) * tokens * n2);  // fp16 mode: scaled tokens (hidden = w1->k = w2->n)
   return b;
 }
 
@@ -595,6 +637,9 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   if (h_cols != w2->k)
     return fail(E4B_EINVAL, "gate_up output (%lld) does not match down k (%lld)", (long long)h_cols,
                 (long long)w2->k);
+  if (w1->k != w2->n)
+    return fail(E4B_EINVAL, "gate_up input (%lld) and down output (%lld) must both be the hidden size",
+                (long long)w1->k, (long long)w2->n);
   if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "bad tokens/top_k");
   if (tokens == 0) return E4B_OK;
   const int E = w1->num_experts;
@@ -656,30 +701,47 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   }
   void* h = take(sizeof(uint16_t) * M * h_cols);
   void* down = take(sizeof(float) * M * w2->n);
+  int32_t* xexp = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * tokens));
+  int32_t* hexp = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));
+  uint16_t* x16 = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * tokens * w1->k));
+  // fp16 matrix-core mode: both GEMMs on the MFMA path, bf16 activations, NF4 weight shifts
+  const bool gemv_path = flags == E4B_PATH_GEMV || (flags == E4B_PATH_AUTO && tokens <= 4);
+  const bool f16c = !gemv_path && act_dtype == E4B_BF16 && w1->format != E4B_FMT_MXFP4 && w1->shift && w2->shift;
+  const int32_t* up_exp = f16c ? xexp : nullptr;
+  int32_t* h_exp = f16c ? hexp : nullptr;
+  // the gate_up GEMM reads the tokens as scaled fp16 rows in fp16 mode
+  const void* up_a = f16c ? static_cast<const void*>(x16) : hidden;
 
   rc = e4b_route(top_k_index, tokens, top_k, E, &rt, stream);
   if (rc) return rc;
+  if (f16c) {  // token row exponents and scaled fp16 rows; the h row exponents zeroed
+    const int64_t blocks = cdiv(tokens, e4b::kScaleThreads / e4b::kWave);
+    hipLaunchKernelGGL(e4b::row_exp_kernel, dim3(static_cast<unsigned>(blocks)), dim3(e4b::kScaleThreads), 0, stream,
+                       static_cast<const uint16_t*>(hidden), tokens, w1->k, xexp, x16, hexp, M);
+    rc = check_launch("row_exp_kernel");
+    if (rc) return rc;
+  }
   if (split) {
     hipLaunchKernelGGL(e4b::split_tiles_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, rt.offsets, rt.meta, E,
                        rbig, rsmall);
     rc = check_launch("split_tiles_kernel");
     if (rc) return rc;
     for (const e4b_routing* r : {&rbig, &rsmall}) {
-      rc = e4b_grouped_gemm(hidden, act_dtype, top_k, w1, r, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
-                            stream);
+      rc = grouped_gemm_impl(up_a, act_dtype, top_k, w1, r, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
+                             up_exp, 1, h_exp, stream);
       if (rc) return rc;
     }
     for (const e4b_routing* r : {&rbig, &rsmall}) {
-      rc = e4b_grouped_gemm(h, act_dtype, 0, w2, r, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
-                            stream);
+      rc = grouped_gemm_impl(h, act_dtype, 0, w2, r, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
+                             h_exp, 0, nullptr, stream);
       if (rc) return rc;
     }
   } else {
-    rc = e4b_grouped_gemm(hidden, act_dtype, top_k, w1, &rt, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
-                          stream);
+    rc = grouped_gemm_impl(up_a, act_dtype, top_k, w1, &rt, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
+                           up_exp, 1, h_exp, stream);
     if (rc) return rc;
-    rc = e4b_grouped_gemm(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
-                          stream);
+    rc = grouped_gemm_impl(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
+                           h_exp, 0, nullptr, stream);
     if (rc) return rc;
   }
   return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,

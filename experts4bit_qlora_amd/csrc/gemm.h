@@ -24,6 +24,14 @@
 // the gate rows of BN/2 output columns and rows BN/2..BN-1 their up rows, and a wave's gate and up
 // accumulators sit in the same lanes, so the activation runs on registers (fp32) before the
 // only store.
+//
+// fp16 mode (F16C, bf16 activations with NF4 weights): the MFMAs multiply fp16 operands. The
+// weights are decoded as fp16(fl32(code * absmax) * 2^shift[e]) -- one rounding, 2^-11 relative
+// where the bf16 weight carries 2^-8 -- and each A row is staged as its bf16 values times
+// 2^exp_shift(row exponent), exact in fp16. The accumulators are scaled back by
+// 2^-(row shift + expert shift) before the epilogue, so the results are those of the exact
+// weights to within fp16's rounding of each weight. The gate_up GEMM also collects every h
+// row's largest exponent (an order-independent atomicMax) for the down GEMM's row scales.
 #pragma once
 
 #include "common.h"
@@ -76,11 +84,13 @@ E4B_DEV uint32_t cvt_pair(float a, float b) {
   }
 }
 
-// fp32 product code * scale. For fp16 the product is kept away from the conversion (mul_f32),
-// which instruction selection could otherwise fuse into one rounding of the exact product.
-template <int DT>
+// fp32 product code * scale. To reproduce the dequantized fp16 weight bit for bit (REF) the
+// product is kept away from the conversion (mul_f32), which instruction selection could otherwise
+// fuse into one rounding of the exact product; the fp16 matrix-core mode takes that fusion (one
+// rounding instead of two, and fewer instructions).
+template <int DT, bool REF = true>
 E4B_DEV float code_times_scale(float c, float s) {
-  if constexpr (DT == E4B_FP16) return mul_f32(c, s);
+  if constexpr (DT == E4B_FP16 && REF) return mul_f32(c, s);
   else return c * s;
 }
 
@@ -110,7 +120,7 @@ E4B_DEV uint32_t fp4_scaled_pair(uint32_t w, float scale) {
   }
 }
 
-template <int DT, int FMT, int NB>
+template <int DT, int FMT, int NB, bool REF = true>
 E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float (&code)[16], float scale, uint32_t (&wv)[NB]) {
   if constexpr (FMT == E4B_FMT_MXFP4) {
 #pragma unroll
@@ -125,7 +135,7 @@ E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float (&code)[
   uint32_t q[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
-    q[i] = cvt_pair<DT>(code_times_scale<DT>(code[2 * i], scale), code_times_scale<DT>(code[2 * i + 1], scale));
+    q[i] = cvt_pair<DT>(code_times_scale<DT, REF>(code[2 * i], scale), code_times_scale<DT, REF>(code[2 * i + 1], scale));
   uint32_t lo[4], hi[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
@@ -168,8 +178,13 @@ E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float (&code)[
 constexpr int gemm_tile_nw(int bm) { return bm == kTileM ? kTileNWWide : kTileNW; }
 constexpr int gemm_threads(int bm) { return bm >= kTileM ? 512 : 256; }
 
-template <int DT, int FMT, int BM>
+// F16: 0 = operands in the activation dtype; fp16 mode with A rows converted while staged (1)
+// or already stored as scaled fp16 by row_exp_kernel (2).
+template <int DT, int FMT, int BM, int F16 = 0>
 __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p) {
+  constexpr bool F16C = F16 != 0;
+  static_assert(!F16C || (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4), "fp16 mode: bf16 activations, NF4 weights");
+  constexpr int CT = F16C ? E4B_FP16 : DT;  // MFMA operand type
   constexpr int NT = gemm_threads(BM);
   constexpr int BN = gemm_tile_nw(BM);
   constexpr int WAVES = NT / kWave;
@@ -187,6 +202,8 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLdsPitch];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kLdsPitch];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
+  __shared__ int row_shift_s[F16C ? BM : 1];  // fp16 mode: each tile row's activation shift
+  __shared__ int hexp_s[F16C ? BM : 1];       // fp16 mode, gate_up: each tile row's h exponent
 
   // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so linear
   // block L runs on XCD L % 8. XCD x takes the contiguous run of M tiles
@@ -231,6 +248,16 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   const int r = row0 + ar;
   const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
   const uint16_t* aptr = p.a + src * k + aseg;
+  // fp16 mode: this thread's A-row shift and the tile expert's weight shift
+  int ash = 0, wsh = 0;
+  if constexpr (F16C) {
+    ash = exp_shift(p.a_exp[src]);
+    wsh = p.w.shift[e];
+    if (tid % TPR == 0) {
+      row_shift_s[ar] = ash;
+      hexp_s[ar] = 0;
+    }
+  }
 
   // W assignment: LDS row tid / TPW (0..BN-1), 2 * WB values of the 64-deep step at
   // (tid % TPW) * 2 * WB.
@@ -309,14 +336,23 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
       const float prod = code2_s[sq[set]] * sa[set];
       scale = prod + offset;
     }
+    if constexpr (F16C) scale = __builtin_amdgcn_ldexpf(scale, wsh);  // exact: a power of two
     uint32_t wv[WB];
-    dequant_bytes<DT, FMT, WB>(wq[set], code, scale, wv);
+    dequant_bytes<CT, FMT, WB, !F16C>(wq[set], code, scale, wv);
     uint4* ws = reinterpret_cast<uint4*>(&Ws[buf][lrow * kLdsPitch + half * 2 * WB]);
 #pragma unroll
     for (int i = 0; i < WB / 4; ++i) ws[i] = make_uint4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
     u32x4_t* as = reinterpret_cast<u32x4_t*>(&As[buf][ar * kLdsPitch + aseg]);
 #pragma unroll
-    for (int i = 0; i < AV; ++i) as[i] = areg[set][i];
+    for (int i = 0; i < AV; ++i) {
+      if constexpr (F16 == 1) {
+        const u32x4_t v = areg[set][i];
+        as[i] = u32x4_t{bf16x2_to_f16x2(v[0], ash), bf16x2_to_f16x2(v[1], ash), bf16x2_to_f16x2(v[2], ash),
+                        bf16x2_to_f16x2(v[3], ash)};
+      } else {
+        as[i] = areg[set][i];
+      }
+    }
   };
   // MFMA operands of one 32-deep half step (ks) of LDS buffer buf, and the MFMAs on them
   auto read_frags = [&](int buf, int ks, uint4 (&av)[MS], uint4 (&bv)[NS]) {
@@ -334,7 +370,7 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-      for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = mfma_16x16x32<DT>(av[ms], bv[ns], acc[ms][ns]);
+      for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = mfma_16x16x32<CT>(av[ms], bv[ns], acc[ms][ns]);
   };
 
   // Step indices past the last step are clamped (a cached re-read nobody uses), for the same
@@ -392,6 +428,40 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   }
 
   // Epilogue: lane holds D[4*(lane/16) + i][lane % 16] of each 16x16 sub-tile.
+  if constexpr (F16C) {
+    // the operand scales come off first: 2^-(row shift + expert shift), exact
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = -(row_shift_s[wave_m * WM + ms * 16 + 4 * (lane >> 4) + i] + wsh);
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns) acc[ms][ns][i] = __builtin_amdgcn_ldexpf(acc[ms][ns][i], d);
+      }
+  }
+  // fp16 mode, gate_up: hm is the largest exponent of the h values this lane stored in tile row
+  // lr; the 16 lanes holding that row reduce it, one of them folds it into the block's row
+  // maximum, and after the epilogue the block folds those into out_exp (atomicMax: the result
+  // does not depend on the order)
+  const bool collect = F16C && p.out_exp != nullptr;
+  // (a DPP max over each 16-lane row of the wave: VALU moves, not LDS permutes, so the 16 rows'
+  // reductions of a lane do not queue behind LDS round trips)
+  auto note_row_exp = [&](int lr, uint32_t hm) {
+    auto dpp_max = [](uint32_t v, auto ctrl) {
+      return max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), decltype(ctrl)::value,
+                                                                       0xf, 0xf, false)));
+    };
+    hm = dpp_max(hm, std::integral_constant<int, 0xb1>{});   // quad_perm [1,0,3,2]
+    hm = dpp_max(hm, std::integral_constant<int, 0x4e>{});   // quad_perm [2,3,0,1]
+    hm = dpp_max(hm, std::integral_constant<int, 0x141>{});  // row_half_mirror
+    hm = dpp_max(hm, std::integral_constant<int, 0x140>{});  // row_mirror
+    if ((lane & 15) == 0 && hm != 0) atomicMax(&hexp_s[lr], static_cast<int>(hm));
+  };
+  auto flush_row_exps = [&]() {
+    __syncthreads();
+    for (int t = tid; t < BM; t += NT)
+      if (row0 + t < row_end && hexp_s[t] != 0) atomicMax(&p.out_exp[row0 + t], hexp_s[t]);
+  };
   const bool has_bias = p.w.bias != nullptr;
   const uint16_t* bias = static_cast<const uint16_t*>(p.w.bias);
   // The two prefill projections take a branch-free path: epilogue kind, bias and output type
@@ -403,15 +473,22 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
     for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int rr = row0 + wave_m * WM + ms * 16 + 4 * (lane >> 4) + i;
+        const int lr = wave_m * WM + ms * 16 + 4 * (lane >> 4) + i;
+        const int rr = row0 + lr;
         uint16_t* const orow = out + int64_t(rr) * p.n_out + cbase;
+        uint32_t hm = 0;
 #pragma unroll
         for (int ns = 0; ns < NS / 2; ++ns) {
           const float v = silu_f32(acc[ms][ns][i]) * acc[ms][ns + NS / 2][i];
-          if (rr < row_end && cbase + ns * 16 < p.n_out) orow[ns * 16] = from_f<DT>(v);
+          const uint16_t hb = from_f<DT>(v);
+          const bool st = rr < row_end && cbase + ns * 16 < p.n_out;
+          if (st) orow[ns * 16] = hb;
+          if (collect && st) hm = max(hm, (static_cast<uint32_t>(hb) >> 7) & 0xffu);
         }
+        if (collect) note_row_exp(lr, hm);
       }
     }
+    if (collect) flush_row_exps();
     return;
   }
   if (!pair && p.epi == E4B_EPI_NONE && !has_bias && p.out_f32) {  // down: fp32 rows
@@ -431,34 +508,48 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
     }
     return;
   }
+  // general path; in fp16 mode a gate_up output (never fp32 there) also notes its exponents
+  auto put = [&](int64_t i, float v, uint32_t& hm) {
+    if (collect) {
+      const uint16_t hb = from_f<DT>(v);
+      static_cast<uint16_t*>(p.out)[i] = hb;
+      hm = max(hm, (static_cast<uint32_t>(hb) >> 7) & 0xffu);
+    } else {
+      store_elem<DT>(p, i, v);
+    }
+  };
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int rr = row0 + wave_m * WM + ms * 16 + 4 * (lane >> 4) + i;
-      if (rr >= row_end) continue;
-      const int64_t orow = int64_t(rr) * p.n_out;
-      if (pair) {
+      const int lr = wave_m * WM + ms * 16 + 4 * (lane >> 4) + i;
+      const int rr = row0 + lr;
+      uint32_t hm = 0;
+      if (rr < row_end) {  // the 16 lanes of a row agree, so the reduction below is not split
+        const int64_t orow = int64_t(rr) * p.n_out;
+        if (pair) {
 #pragma unroll
-        for (int ns = 0; ns < NS / 2; ++ns) {
-          const int64_t jj = col0 + wave_n * (WN / 2) + ns * 16 + (lane & 15);
-          if (jj >= p.n_out) continue;
-          const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + jj]) : 0.0f;
-          const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + n / 2 + jj]) : 0.0f;
-          store_elem<DT>(p, orow + jj,
-                         gated(p.epi, acc[ms][ns][i], acc[ms][ns + NS / 2][i], p.alpha, p.limit, bg, bu));
-        }
-      } else {
+          for (int ns = 0; ns < NS / 2; ++ns) {
+            const int64_t jj = col0 + wave_n * (WN / 2) + ns * 16 + (lane & 15);
+            if (jj >= p.n_out) continue;
+            const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + jj]) : 0.0f;
+            const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + n / 2 + jj]) : 0.0f;
+            put(orow + jj, gated(p.epi, acc[ms][ns][i], acc[ms][ns + NS / 2][i], p.alpha, p.limit, bg, bu), hm);
+          }
+        } else {
 #pragma unroll
-        for (int ns = 0; ns < NS; ++ns) {
-          const int64_t nn = col0 + wave_n * WN + ns * 16 + (lane & 15);
-          if (nn >= p.n_out) continue;
-          const float b = has_bias ? to_f<DT>(bias[int64_t(e) * n + nn]) : 0.0f;
-          store_elem<DT>(p, orow + nn, single(p.epi, acc[ms][ns][i], b));
+          for (int ns = 0; ns < NS; ++ns) {
+            const int64_t nn = col0 + wave_n * WN + ns * 16 + (lane & 15);
+            if (nn >= p.n_out) continue;
+            const float b = has_bias ? to_f<DT>(bias[int64_t(e) * n + nn]) : 0.0f;
+            put(orow + nn, single(p.epi, acc[ms][ns][i], b), hm);
+          }
         }
       }
+      if (collect) note_row_exp(lr, hm);
     }
   }
+  if (collect) flush_row_exps();
 }
 
 }  // namespace e4b

@@ -1,0 +1,89 @@
+// Power-of-two scales of the fp16 matrix-core mode of the fused forward.
+//
+// With bf16 activations the MFMA GEMMs can run on fp16 operands instead: three more significant
+// bits for the dequantized weights (the largest error term of the bf16 GEMM against an fp32
+// reference) at the same matrix-core rate. fp16's range is narrower than bf16's, so operands
+// are scaled by powers of two, which is exact and removed from the fp32 sums afterwards:
+//   row_exp_kernel       the largest biased exponent of every activation row (one wave per
+//                        row), and the zeroing of the h-row exponents the gate_up GEMM collects;
+//   weight_shift_kernel  per expert, the shift that brings its largest block scale (decoded, for
+//                        double quantization) into [2^14, 2^15): computed once per weight version.
+#pragma once
+
+#include "common.h"
+
+namespace e4b {
+
+constexpr int kScaleThreads = 256;
+
+E4B_DEV uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) v = max(v, static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), o)));
+  return v;
+}
+
+// row_exp[r] = the largest biased exponent over row r of x [rows, k] (bf16, k % 8 == 0), and
+// x16[r] = fp16(x[r] * 2^exp_shift(row_exp[r])) (exact; see bf16x2_to_f16x2), the gate_up
+// GEMM's operand staged once instead of once per output tile; zero[0 .. nzero) = 0 (grid-stride:
+// the grid has rows / 4 blocks of 256 threads). One wave per row; a row's pieces stay in
+// registers between the two passes when k <= 64 * 8 * kRowPieces.
+constexpr int kRowPieces = 8;  // 16-byte pieces per lane held across the passes (k <= 4096)
+
+__global__ void __launch_bounds__(kScaleThreads) row_exp_kernel(const uint16_t* __restrict__ x, int64_t rows,
+                                                                int64_t k, int32_t* __restrict__ row_exp,
+                                                                uint16_t* __restrict__ x16,
+                                                                int32_t* __restrict__ zero, int64_t nzero) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nzero; i += int64_t(gridDim.x) * blockDim.x)
+    zero[i] = 0;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = int64_t(blockIdx.x) * (kScaleThreads / kWave) + threadIdx.x / kWave;
+  if (row >= rows) return;  // whole waves; no barrier follows
+  const uint4* xr = reinterpret_cast<const uint4*>(x + row * k);
+  uint4* yr = reinterpret_cast<uint4*>(x16 + row * k);
+  const int64_t pieces = k / 8;
+  uint32_t m = 0;
+  uint4 v[kRowPieces];
+#pragma unroll
+  for (int j = 0; j < kRowPieces; ++j) {
+    const int64_t i = lane + int64_t(j) * kWave;
+    v[j] = xr[i < pieces ? i : 0];
+    m = max(m, bf16_exp_max(v[j]));
+  }
+  for (int64_t i = lane + int64_t(kRowPieces) * kWave; i < pieces; i += kWave) m = max(m, bf16_exp_max(xr[i]));
+  m = wave_max_u32(m);
+  if (lane == 0) row_exp[row] = static_cast<int32_t>(m >> 7);
+  const int d = exp_shift(static_cast<int>(m >> 7));
+  auto conv = [&](const uint4& a) {
+    return make_uint4(bf16x2_to_f16x2(a.x, d), bf16x2_to_f16x2(a.y, d), bf16x2_to_f16x2(a.z, d),
+                      bf16x2_to_f16x2(a.w, d));
+  };
+#pragma unroll
+  for (int j = 0; j < kRowPieces; ++j) {
+    const int64_t i = lane + int64_t(j) * kWave;
+    if (i < pieces) yr[i] = conv(v[j]);
+  }
+  for (int64_t i = lane + int64_t(kRowPieces) * kWave; i < pieces; i += kWave) yr[i] = conv(xr[i]);
+}
+
+// shift[e] = exp_shift(largest biased fp32 exponent of expert e's block scales), one block per
+// expert (blockIdx.x), NF4 (fp32 absmax) or NF4_DQ (decoded absmax).
+template <int FMT>
+__global__ void __launch_bounds__(kScaleThreads) weight_shift_kernel(e4b_qweight w, int32_t* __restrict__ shift) {
+  __shared__ uint32_t wm[kScaleThreads / kWave];
+  const int e = blockIdx.x;
+  const int64_t nb = w.n * (w.k / 64);
+  uint32_t m = 0;
+  for (int64_t b = threadIdx.x; b < nb; b += blockDim.x)
+    m = max(m, (__float_as_uint(nf4_block_scale<FMT>(w, e, b)) >> 23) & 0xffu);
+  m = wave_max_u32(m);
+  if ((threadIdx.x & (kWave - 1)) == 0) wm[threadIdx.x / kWave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t t = 0;
+#pragma unroll
+    for (int i = 0; i < kScaleThreads / kWave; ++i) t = max(t, wm[i]);
+    shift[e] = exp_shift(static_cast<int>(t));
+  }
+}
+
+}  // namespace e4b

@@ -132,7 +132,8 @@ def _build_qweights(mod):
     else:
         w1 = ops.nf4_qweight(mod.gate_up_proj, mod.gate_up_absmax, mod.code, n1, k1, num_experts=E)
         w2 = ops.nf4_qweight(mod.down_proj, mod.down_absmax, mod.code, n2, k2, num_experts=E)
-    return w1, w2
+    # per-expert exponents: the fused forward's matrix-core GEMMs then run on fp16 operands
+    return ops.with_weight_shift(w1), ops.with_weight_shift(w2)
 
 
 def _mxfp4_qweights(mod, cd):

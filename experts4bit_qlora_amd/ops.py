@@ -53,6 +53,7 @@ class QW:
     code: torch.Tensor | None = None
     code2: torch.Tensor | None = None
     bias: torch.Tensor | None = None
+    shift: torch.Tensor | None = None  # NF4: per-expert exponents of the fp16 matrix-core mode
 
     def __setattr__(self, name, value):  # a changed field invalidates the cached descriptor
         self.__dict__.pop("_struct", None)
@@ -76,8 +77,22 @@ class QW:
         s.code = _ptr(self.code)
         s.code2 = _ptr(self.code2)
         s.bias = _ptr(self.bias)
+        s.shift = _ptr(self.shift)
         self.__dict__["_struct"] = s
         return s
+
+
+def with_weight_shift(qw: QW) -> QW:
+    """Attach the per-expert exponents (``e4b_weight_shift``) that let the fused forward run its
+    matrix-core GEMMs on fp16 operands; computed on the device, no synchronisation. A no-op for
+    MXFP4 (exact in bf16) and for weights off the device."""
+    if qw.fmt == N.FMT_MXFP4 or not qw.packed.is_cuda:
+        return qw
+    shift = torch.empty(qw.num_experts, dtype=torch.int32, device=qw.packed.device)
+    s = qw.struct()
+    N.check("e4b_weight_shift", N.lib().e4b_weight_shift(ctypes.byref(s), shift.data_ptr(), _stream(shift.device)))
+    qw.shift = shift
+    return qw
 
 
 def nf4_qweight(packed, absmax, code, n, k, num_experts=None, bias=None) -> QW:

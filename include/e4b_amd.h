@@ -65,6 +65,9 @@ typedef struct e4b_qweight {
   const float* code;     /* NF4 / NF4_DQ: fp32 [16] 4-bit code (the module's `code` buffer) */
   const float* code2;    /* NF4_DQ only: fp32 [256] second-level code */
   const void* bias;      /* optional [E, n] in the activation dtype (gpt-oss), else NULL */
+  const int32_t* shift;  /* optional, NF4 / NF4_DQ: [E] per-expert power-of-two exponents from
+                            e4b_weight_shift. When both projections carry them, e4b_moe_forward
+                            runs its bf16 matrix-core GEMMs in fp16 (see there); NULL: not */
 } e4b_qweight;
 
 /* Device-side routing of M = tokens * top_k (token, slot) assignments. */
@@ -97,6 +100,14 @@ int32_t e4b_mfma_tile_m(void);
  * MXFP4, formats/mxfp4.py:35-105 dequantize_mxfp4 before its final transpose. */
 int e4b_dequant(const e4b_qweight* w, int32_t expert_begin, int32_t expert_count, int32_t out_dtype,
                 void* out, hipStream_t stream);
+
+/* Per-expert weight exponents for the fp16 matrix-core mode of e4b_moe_forward: shift[e] =
+ * 141 - max(E_e, 20), E_e the largest biased fp32 exponent of expert e's block scales (the
+ * decoded ones for NF4_DQ), so every |code * absmax| * 2^shift[e] is below 2^15 and the scaled
+ * weights sit in fp16's normal range. shift is [E] int32 on the device. NF4 / NF4_DQ only.
+ * Has no counterpart in the reference: it is derived data of the weights, computed once per
+ * weight version (the Python layer caches it with the kernel descriptors). */
+int e4b_weight_shift(const e4b_qweight* w, int32_t* shift, hipStream_t stream);
 
 /* int32 scratch the route needs for M = tokens * top_k routed rows over E experts: 0 up to
  * 4096 rows (one workgroup routes them), else ceil(M / 256) * (E + 1) (three launches over
@@ -190,6 +201,13 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
  * [tokens, top_k] in weight_dtype; out [tokens, w2->n] in out_dtype.
  * Small batches (tokens <= 8, or flags == E4B_PATH_GEMV within the decode limits) take the
  * two-launch decode path; larger ones route once and run the grouped GEMMs.
+ * fp16 matrix-core mode (bf16 activations, NF4 / NF4_DQ weights whose descriptors both carry
+ * `shift`): the GEMMs multiply fp16 operands -- every weight fp16(fl32(code * absmax) *
+ * 2^shift[e]) (one rounding of the fp32 product, 2^-11 relative, where bf16 weights carry
+ * 2^-8), every activation row scaled by a power of two that puts its largest value in
+ * [2^14, 2^15) (exact for bf16 values), the scales removed from the fp32 sums before the
+ * epilogue -- so the layer keeps the decode path's accuracy at any batch. h is still rounded
+ * once to act_dtype. Without `shift` the GEMMs use the bf16 dequantized weights themselves.
  * Replaces: engines/fast.py:100-160 fused_experts_forward (the bare-module forward that
  * enable_fast binds, fast.py:371-372), with no device->host synchronisation. */
 int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,

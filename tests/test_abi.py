@@ -46,8 +46,20 @@ def test_enums_match_header():
 
 
 def test_struct_layouts():
-    assert ctypes.sizeof(N.QWeight) == 4 + 4 + 8 + 8 + 7 * 8
+    assert ctypes.sizeof(N.QWeight) == 4 + 4 + 8 + 8 + 8 * 8
+    assert N.QWeight.shift.offset == 4 + 4 + 8 + 8 + 7 * 8  # the last field, after bias
     assert ctypes.sizeof(N.Routing) == 6 * 8 + 4 + 4 + 8
+
+
+def test_weight_shift_rejects_bad_arguments():
+    """Validation happens before any launch, so it runs without a device."""
+    L = N.lib()
+    s = _qw(format=N.FMT_MXFP4)
+    assert L.e4b_weight_shift(ctypes.byref(s), 4096, None) == -2
+    assert "MXFP4" in _err()
+    s = _qw()
+    assert L.e4b_weight_shift(ctypes.byref(s), None, None) == -1
+    assert "NULL" in _err()
 
 
 def _qw(**kw):

@@ -650,6 +650,52 @@ def test_decode_path_forced_up_to_its_row_limit(T):
     assert fro <= 1e-2
 
 
+@pytest.mark.parametrize("xscale,wscale,dq", [(2.0 ** 20, 1.0, False), (2.0 ** -20, 1.0, False),
+                                              (1.0, 2.0 ** -24, False), (1.0, 2.0 ** 12, True), (2.0 ** -8, 2.0 ** 8, True)])
+def test_fp16_matrix_core_mode_keeps_the_bf16_range(xscale, wscale, dq):
+    """The MFMA path (T=32) runs fp16 operands under power-of-two row and expert scales: with
+    activations and weights far outside fp16's own range the layer still meets the bars against
+    the oracle (an unscaled fp16 operand would overflow to inf or flush to zero here)."""
+    _announce(f"fp16 mode range xscale={xscale} wscale={wscale} dq={dq}")
+    E, H, I, k, T = 16, 256, 128, 4, 32
+    g = torch.Generator().manual_seed(int(abs(np.log2(xscale * wscale))) + 17)
+    gu = torch.randn(E, 2 * I, H, generator=g) * 0.05 * wscale
+    dn = torch.randn(E, H, I, generator=g) * 0.05 * wscale
+    mod = e4b.Experts4bit.from_float(gu.to(DEV), dn.to(DEV), compute_dtype=torch.bfloat16,
+                                     compress_statistics=dq).eval()
+    x = (torch.randn(T, H, generator=g) * xscale).to(torch.bfloat16).to(DEV)
+    val, idx = torch.topk(torch.randn(T, E, generator=g), k, dim=-1)
+    w = torch.softmax(val, -1).to(torch.bfloat16).to(DEV)
+    idx = idx.to(DEV)
+    with torch.no_grad():
+        ref = mod(x, idx, w)
+        assert e4b.enable_fast(mod) == 1
+        w1, w2 = F._qweights(mod)
+        assert w1.shift is not None and w2.shift is not None  # the fp16 mode is on
+        got = mod(x, idx, w)
+    assert torch.isfinite(got).all()
+    _assert_fidelity(got, ref, _oracle(mod, x, idx, w), f"fp16 mode x*{xscale} w*{wscale} dq={dq}")
+
+
+def test_weight_shift_matches_the_oracle_exponents():
+    """e4b_weight_shift: 141 - max(E, 20), E the largest biased exponent of each expert's block
+    scales (decoded ones for double quantization), from the oracle's decode of the same bytes."""
+    _announce("weight shift")
+    for dq in (False, True):
+        mod, *_ = _make(E=6, seed=20 + dq, dq=dq, scale=0.05)
+        w1, _ = F._qweights(mod)
+        got = w1.shift.cpu().numpy()
+        ow, _ = oracle_weights(mod)
+        for e in range(6):
+            am = ow.absmax[e]
+            if dq:
+                from oracle import c_oracle
+
+                am = c_oracle.dequant_absmax_dq(am, ow.absmax2[e], ow.offset[e], ow.code2)
+            E_ = int(((np.abs(am).astype(np.float32).view(np.uint32) >> 23) & 0xFF).max())
+            assert got[e] == 141 - max(E_, 20), (dq, e, got[e], E_)
+
+
 def test_out_of_range_ids_contribute_nothing():
     _announce("dropped ids")
     mod, hs, top_i, top_w = _make(E=8, tokens=6, k=2, seed=11)
