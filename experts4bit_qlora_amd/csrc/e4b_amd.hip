@@ -1,7 +1,8 @@
 // C-ABI entry points of libe4b_amd.so (declared in include/e4b_amd.h).
 //
 // Host code only validates, picks a kernel instantiation and launches on the caller's stream.
-// No device memory is allocated here and no call synchronises the device.
+// No device memory is allocated here and no call but the e4b_decode_sync_errors diagnostic
+// synchronises the device.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -10,8 +11,12 @@
 #include <cstring>
 #include <string>
 
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 #include "decode.h"
+#include "decode_fused.h"
 #include "decode_launch.h"
 #include "dequant.h"
 #include "gemm.h"
@@ -42,6 +47,70 @@ int check_launch(const char* what) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// State of the single-launch decode (decode_fused.h) per stream slot: kSyncCounters launch
+// counters (zero when the library loads, never reset) and two h exchange buffers of
+// kFusedMaxH values (zero when the library loads; each launch zeroes the one the next launch
+// uses), 4 MB for all slots; and the sticky flag a wait that ran out of time raises. Each device
+// holds its own copy; host code reaches it through the addresses hipGetSymbolAddress gives on
+// that device.
+__device__ unsigned g_decode_sync[e4b::kSyncSlots * e4b::kSyncCounters * e4b::kSyncStride];
+__device__ __align__(256) uint16_t g_decode_h[e4b::kSyncSlots * 2 * e4b::kFusedMaxH];
+__device__ unsigned g_decode_sync_errors;
+
+constexpr int kMaxDevices = 64;
+struct DecodeSync {
+  bool init = false, ok = false;
+  unsigned* ctr = nullptr;     // device address of g_decode_sync
+  uint16_t* hx = nullptr;      // device address of g_decode_h
+  unsigned* errors = nullptr;  // device address of g_decode_sync_errors
+  hipStream_t streams[e4b::kSyncSlots] = {};
+  int used = 0;
+};
+std::mutex g_sync_mu;
+DecodeSync g_sync[kMaxDevices];
+std::atomic<unsigned long long> g_wait_ticks{10000000ull};  // 100 ms at the 100 MHz real-time clock
+
+// The device addresses of the current device's counters, set up on first use.
+DecodeSync* decode_sync_device() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  DecodeSync& s = g_sync[dev];
+  if (!s.init) {
+    s.init = true;
+    void* c = nullptr;
+    void* h = nullptr;
+    void* e = nullptr;
+    s.ok = hipGetSymbolAddress(&c, HIP_SYMBOL(g_decode_sync)) == hipSuccess &&
+           hipGetSymbolAddress(&h, HIP_SYMBOL(g_decode_h)) == hipSuccess &&
+           hipGetSymbolAddress(&e, HIP_SYMBOL(g_decode_sync_errors)) == hipSuccess && c && h && e;
+    if (!s.ok) (void)hipGetLastError();  // no single-launch decode on this device; nothing left pending
+    s.ctr = static_cast<unsigned*>(c);
+    s.hx = static_cast<uint16_t*>(h);
+    s.errors = static_cast<unsigned*>(e);
+  }
+  return s.ok ? &s : nullptr;
+}
+
+// The counters and exchange buffers of `stream`'s slot (a stream keeps its slot for the life of
+// the process); false when every slot is taken or the state is unavailable.
+bool decode_sync_slot(hipStream_t stream, unsigned** ctr, uint16_t** hx, unsigned** errors) {
+  std::lock_guard<std::mutex> lk(g_sync_mu);
+  DecodeSync* s = decode_sync_device();
+  if (!s) return false;
+  int slot = -1;
+  for (int i = 0; i < s->used; ++i)
+    if (s->streams[i] == stream) slot = i;
+  if (slot < 0) {
+    if (s->used == e4b::kSyncSlots) return false;
+    slot = s->used++;
+    s->streams[slot] = stream;
+  }
+  *ctr = s->ctr + size_t(slot) * e4b::kSyncCounters * e4b::kSyncStride;
+  *hx = s->hx + size_t(slot) * 2 * e4b::kFusedMaxH;
+  *errors = s->errors;
+  return true;
+}
 
 bool act_dtype_ok(int dt) { return dt == E4B_BF16 || dt == E4B_FP16; }
 bool any_dtype_ok(int dt) { return dt == E4B_BF16 || dt == E4B_FP16 || dt == E4B_FP32; }
@@ -238,6 +307,46 @@ int64_t max_small_tiles(int64_t M, int E) { return std::max<int64_t>(1, std::min
 
 bool is_gated_epi(int epi) {
   return epi == E4B_EPI_SWIGLU || epi == E4B_EPI_CLAMP_SWIGLU || epi == E4B_EPI_GPTOSS;
+}
+
+// Shapes the single-launch decode takes: one token, a gated epilogue, the decode limits, down
+// rows of at most 3072 values, the routed experts' h within one exchange buffer.
+bool fused_supported(int64_t tokens, int64_t M, int E, const e4b_qweight* w1, const e4b_qweight* w2, int epi) {
+  return tokens == 1 && is_gated_epi(epi) && decode_supported(M, E, w1, true) && decode_supported(M, E, w2, false) &&
+         e4b::decode_fused_cpld(w2->k) > 0 && std::min<int64_t>(M, E) * w2->k <= e4b::kFusedMaxH;
+}
+
+// The single-launch decode on `stream`'s slot; E4B_EUNSUPPORTED when no slot is free or the
+// device holds too few blocks at once (the caller then takes the two-launch path).
+int launch_fused(const void* hidden, int act_dtype, const int64_t* top_k_index, const void* top_k_weights,
+                 int weight_dtype, int top_k, const e4b_qweight* w1, const e4b_qweight* w2, int epilogue, float alpha,
+                 float limit, void* out, int out_dtype, hipStream_t stream) {
+  e4b::FusedArgs a{};
+  if (!decode_sync_slot(stream, &a.ctr, &a.hx, &a.errors)) return E4B_EUNSUPPORTED;
+  a.x = static_cast<const uint16_t*>(hidden);
+  a.topk = top_k_index;
+  a.topk_w = top_k_weights;
+  a.wdt = weight_dtype;
+  a.k = top_k;
+  a.E = w1->num_experts;
+  a.w1 = *w1;
+  a.w2 = *w2;
+  a.epi = epilogue;
+  a.alpha = alpha;
+  a.limit = limit;
+  a.n_out = w2->k;
+  a.out = out;
+  a.odt = out_dtype;
+  a.timeout = g_wait_ticks.load(std::memory_order_relaxed);
+#define E4B_FUSED(DT, FMT)                                                    \
+  if (act_dtype == DT && w1->format == FMT) {                                 \
+    if (!e4b::launch_decode_fused<DT, FMT>(a, stream)) return E4B_EUNSUPPORTED; \
+    return check_launch("decode_fused_kernel");                               \
+  }
+  E4B_FUSED(E4B_BF16, E4B_FMT_NF4) E4B_FUSED(E4B_BF16, E4B_FMT_NF4_DQ) E4B_FUSED(E4B_BF16, E4B_FMT_MXFP4)
+  E4B_FUSED(E4B_FP16, E4B_FMT_NF4) E4B_FUSED(E4B_FP16, E4B_FMT_NF4_DQ) E4B_FUSED(E4B_FP16, E4B_FMT_MXFP4)
+#undef E4B_FUSED
+  return fail(E4B_EINVAL, "no single-launch decode for act_dtype %d / format %d", act_dtype, w1->format);
 }
 
 }  // namespace
@@ -656,11 +765,19 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   if (!top_k_index || !top_k_weights || !hidden || !out) return fail(E4B_EINVAL, "NULL pointer");
   if (!aligned16(hidden)) return fail(E4B_EINVAL, "hidden must be 16-byte aligned");
 
-  // Decode path: two launches, routing recomputed in LDS, combine fused into the down kernel.
+  if (flags < E4B_PATH_AUTO || flags > E4B_PATH_DECODE_FUSED) return fail(E4B_EINVAL, "bad flags %d", flags);
+  // Decode path: routing recomputed in LDS, combine fused into the down projection; two
+  // launches, or one for a single token when asked for.
   const bool decode_ok = decode_supported(M, E, w1, true) && decode_supported(M, E, w2, false);
-  const bool use_decode = decode_ok && ((flags == E4B_PATH_AUTO && tokens <= 8) || flags == E4B_PATH_GEMV);
+  const bool use_decode =
+      decode_ok && (((flags == E4B_PATH_AUTO || flags == E4B_PATH_DECODE_FUSED) && tokens <= 8) || flags == E4B_PATH_GEMV);
   if (use_decode) {
     void* h = workspace;
+    if (flags == E4B_PATH_DECODE_FUSED && fused_supported(tokens, M, E, w1, w2, epilogue)) {
+      rc = launch_fused(hidden, act_dtype, top_k_index, top_k_weights, weight_dtype, top_k, w1, w2, epilogue, alpha,
+                        limit, out, out_dtype, stream);
+      if (rc != E4B_EUNSUPPORTED) return rc;  // no free slot or too small a device: two launches instead
+    }
     rc = e4b_decode_gate_up(hidden, act_dtype, tokens, top_k_index, top_k, w1, epilogue, alpha, limit, h, stream);
     if (rc) return rc;
     return e4b_decode_down_combine(h, act_dtype, tokens, top_k_index, top_k_weights, weight_dtype, top_k, w2, out,
@@ -746,6 +863,24 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   }
   return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
                      stream);
+}
+
+int e4b_decode_sync_errors(uint32_t* errors, int32_t reset) {
+  if (!errors) return fail(E4B_EINVAL, "NULL pointer");
+  std::lock_guard<std::mutex> lk(g_sync_mu);
+  DecodeSync* s = decode_sync_device();
+  if (!s) return fail(E4B_EUNSUPPORTED, "single-launch decode counters are not available on this device");
+  unsigned v = 0;
+  if (hipMemcpy(&v, s->errors, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess)
+    return check_launch("e4b_decode_sync_errors");
+  *errors = v;
+  if (reset && hipMemset(s->errors, 0, sizeof(unsigned)) != hipSuccess) return check_launch("e4b_decode_sync_errors");
+  return E4B_OK;
+}
+
+int e4b_decode_wait_limit(uint64_t ticks) {
+  g_wait_ticks.store(ticks ? ticks : 10000000ull, std::memory_order_relaxed);
+  return E4B_OK;
 }
 
 }  // extern "C"

@@ -50,8 +50,10 @@ enum e4b_epilogue {
                                after adding the per-expert gate_up bias */
 };
 
-/* Kernel-path selection flags for the grouped GEMMs (0 = automatic by token count). */
-enum e4b_flags { E4B_PATH_AUTO = 0, E4B_PATH_GEMV = 1, E4B_PATH_MFMA = 2 };
+/* Kernel-path selection flags for the grouped GEMMs (0 = automatic by token count).
+ * E4B_PATH_DECODE_FUSED (e4b_moe_forward only): a single token runs the decode path in one
+ * launch (see e4b_moe_forward); otherwise as E4B_PATH_AUTO. */
+enum e4b_flags { E4B_PATH_AUTO = 0, E4B_PATH_GEMV = 1, E4B_PATH_MFMA = 2, E4B_PATH_DECODE_FUSED = 3 };
 
 typedef struct e4b_qweight {
   int32_t format;        /* e4b_format */
@@ -200,7 +202,18 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
  * hidden [tokens, w1->k] in act_dtype; top_k_index [tokens, top_k] int64; top_k_weights
  * [tokens, top_k] in weight_dtype; out [tokens, w2->n] in out_dtype.
  * Small batches (tokens <= 8, or flags == E4B_PATH_GEMV within the decode limits) take the
- * two-launch decode path; larger ones route once and run the grouped GEMMs.
+ * decode path, two launches (gate_up, then down + combine); larger ones route once and run the
+ * grouped GEMMs.
+ * flags == E4B_PATH_DECODE_FUSED runs a single token (gated epilogue, w2->k <= 3072, routed
+ * experts * w2->k <= 16384) in ONE launch: its blocks hand h to one another through exchange
+ * buffers the library owns (4 MB per device), so the launch assumes that its blocks (up to 512,
+ * those that fit on the device at once) all run concurrently -- true when nothing else occupies
+ * the device's compute units. Each stream gets its own buffers (64 streams per device; further
+ * streams take the two-launch form); two launches that overlap on one stream's buffers, e.g. the
+ * same captured graph replayed on two streams at once, race. A wait that runs out (see
+ * e4b_decode_wait_limit) raises the flag e4b_decode_sync_errors reads instead of hanging, and
+ * leaves that call's output undefined. On MI355X it is slower than the two launches (the h
+ * hand-off across the device costs more than a kernel boundary), hence not the default.
  * fp16 matrix-core mode (bf16 activations, NF4 / NF4_DQ weights whose descriptors both carry
  * `shift`): the GEMMs multiply fp16 operands -- every weight fp16(fl32(code * absmax) *
  * 2^shift[e]) (one rounding of the fp32 product, 2^-11 relative, where bf16 weights carry
@@ -215,6 +228,17 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
                     const e4b_qweight* w2, int32_t epilogue, float alpha, float limit, int32_t flags,
                     void* workspace, size_t workspace_bytes, void* out, int32_t out_dtype,
                     hipStream_t stream);
+
+/* Sticky flag of the single-token decode launch on the current device: non-zero once a launch
+ * gave up waiting for its other blocks (its output is then undefined). reset != 0 clears it.
+ * Synchronises the device (a diagnostic, not for the decode loop).
+ * No counterpart in the reference (its decode runs as separate launches). */
+int e4b_decode_sync_errors(uint32_t* errors, int32_t reset);
+
+/* Wait bound of the single-token decode launch, in ticks of the device's 100 MHz real-time
+ * clock, for launches made after this call (0: the default, 10^7 = 100 ms).
+ * No counterpart in the reference. */
+int e4b_decode_wait_limit(uint64_t ticks);
 
 #ifdef __cplusplus
 }
