@@ -884,3 +884,55 @@ int e4b_decode_wait_limit(uint64_t ticks) {
 }
 
 }  // extern "C"
+
+namespace {
+
+// The workspace of e4b_moe_forward_noalloc: a file-scope device array, one per device for the
+// life of the process. Host code uses the address hipGetSymbolAddress gives on each device,
+// never the array's name.
+__device__ __align__(256) unsigned char scratch[E4B_NOALLOC_WORKSPACE_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's `scratch`, taken on the first call on that device.
+int scratch_address(void** ptr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return check_launch("hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(E4B_EUNSUPPORTED, "device %d beyond %d devices", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p) {
+      (void)hipGetLastError();
+      return fail(E4B_ELAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(err));
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return E4B_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int e4b_moe_forward_noalloc(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                            const void* top_k_weights, int32_t weight_dtype, int32_t top_k, const e4b_qweight* w1,
+                            const e4b_qweight* w2, int32_t epilogue, float alpha, float limit, int32_t flags,
+                            void* out, int32_t out_dtype, hipStream_t stream) {
+  if (!w1 || !w2) return fail(E4B_EINVAL, "weight descriptor is NULL");
+  if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "bad tokens/top_k");
+  const size_t need = e4b_moe_workspace_bytes(tokens, top_k, w1->num_experts, w1->n, w2->n, epilogue, act_dtype);
+  if (need > size_t(E4B_NOALLOC_WORKSPACE_BYTES))
+    return fail(E4B_ESPACE, "this call needs %zu bytes of workspace; e4b_moe_forward_noalloc holds %zu",
+                need, size_t(E4B_NOALLOC_WORKSPACE_BYTES));
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc) return rc;
+  return e4b_moe_forward(hidden, act_dtype, tokens, top_k_index, top_k_weights, weight_dtype, top_k, w1, w2, epilogue,
+                         alpha, limit, flags, ws, size_t(E4B_NOALLOC_WORKSPACE_BYTES), out, out_dtype, stream);
+}
+
+}  // extern "C"

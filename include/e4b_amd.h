@@ -229,6 +229,21 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
                     void* workspace, size_t workspace_bytes, void* out, int32_t out_dtype,
                     hipStream_t stream);
 
+/* e4b_moe_forward without a workspace argument and without any allocation: the workspace is a
+ * device array of E4B_NOALLOC_WORKSPACE_BYTES that the library holds on every device it runs on
+ * until the process ends. Calls whose e4b_moe_workspace_bytes exceeds it fail with E4B_ESPACE
+ * (at Qwen3-30B-A3B geometry that allows 800 tokens at top-8). All calls on one device share the array:
+ * calls that overlap in time on one device (e.g. on two streams) race; calls in one stream's
+ * order do not. The array is not cleared between calls (nothing the forward reads from it
+ * has to start at zero).
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+#define E4B_NOALLOC_WORKSPACE_BYTES (64u << 20)
+int e4b_moe_forward_noalloc(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                            const void* top_k_weights, int32_t weight_dtype, int32_t top_k, const e4b_qweight* w1,
+                            const e4b_qweight* w2, int32_t epilogue, float alpha, float limit, int32_t flags,
+                            void* out, int32_t out_dtype, hipStream_t stream);
+
 /* Sticky flag of the single-token decode launch on the current device: non-zero once a launch
  * gave up waiting for its other blocks (its output is then undefined). reset != 0 clears it.
  * Synchronises the device (a diagnostic, not for the decode loop).
