@@ -10,10 +10,12 @@ and weights are resident in HBM when the timed region starts.
 ``value`` = routed-expert HBM bytes per step / step time (GB/s): each distinct routed expert's
 3,538,944 bytes (packed NF4 + fp32 absmax, both projections) counted once per layer. The line
 also carries us/layer and tok/s at batches 1, 8 and 64, the Qwen3-30B-A3B-geometry 4096-token
-Zipf prefill in TFLOP/s, the dominant kernel's roofline measured with HIP events
-on the launch stream, and the reference per-expert loop timed on the host CPU.
+Zipf prefill in TFLOP/s, the Qwen3-geometry double-quant decode at batches 1, 32
+and 256 and the gpt-oss MXFP4 layer at 1 and 2048 tokens, the
+dominant kernel's roofline measured with HIP events on the launch stream, and the reference
+per-expert loop timed on the host CPU.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--extra]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--no-prefill] [--no-extra]
 """
 from __future__ import annotations
 
@@ -374,7 +376,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--extra", action="store_true", help="also run configs[2] and configs[4]")
+    ap.add_argument("--no-extra", action="store_true", help="skip configs[2] (Qwen3 double-quant decode) and "
+                    "configs[4] (gpt-oss MXFP4)")
     ap.add_argument("--kernel-only", action="store_true", help="only the dominant-kernel loop (for profiling)")
     ap.add_argument("--prefill-only", action="store_true", help="only the configs[3] prefill (for profiling)")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -426,7 +429,10 @@ def main():
         log("Qwen3 4096-token Zipf prefill")
         prefill = prefill_bench(args.steps, args.warmup)
 
-    extra = extra_benches(args.steps, args.warmup) if args.extra else None
+    extra = None
+    if not args.no_extra:
+        log("configs[2] Qwen3 double-quant decode and configs[4] gpt-oss MXFP4")
+        extra = extra_benches(args.steps, args.warmup)
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -183,7 +183,11 @@ def fused_experts_forward(mod, hidden_states, top_k_index, top_k_weights):
     if mod.gate_up_proj.numel() == 0 or mod.down_proj.numel() == 0:
         _drop_descriptors(mod)  # the evicted weights must not stay alive through the cache
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+    return _bare_forward(mod, hidden_states, top_k_index, top_k_weights, compute_dtype)
 
+
+def _bare_forward(mod, hidden_states, top_k_index, top_k_weights, compute_dtype):
+    """The fused forward of a bare NF4 base once the fallbacks are ruled out."""
     input_dtype = hidden_states.dtype
     x = hidden_states.to(compute_dtype)
     tokens = x.shape[0]
@@ -224,6 +228,11 @@ def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
     if base.gate_up_proj.numel() == 0 or base.down_proj.numel() == 0:
         _drop_descriptors(base)  # the evicted weights must not stay alive through the cache
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+    if mod._adapter_is_zero():
+        # the adapter contributes exactly nothing (both B zero): the base's own fused forward,
+        # one call, as the reference's delegation to an accelerated base (lora.py:181-214). The
+        # verdict costs one sync on the first call and is cached until train() / a state load.
+        return _bare_forward(base, hidden_states, top_k_index, top_k_weights, compute_dtype)
 
     input_dtype = hidden_states.dtype
     x = hidden_states.to(compute_dtype)

@@ -246,6 +246,32 @@ def _lora_inputs(n_tok, E=8, H=128, seed=1):
     return hs, idx, wts
 
 
+@pytest.mark.parametrize("n_tok", [1, 12])
+def test_lora_zero_adapter_is_the_bare_fused_forward(n_tok):
+    """An untrained adapter (both B zero) contributes exactly nothing: the patched wrapper then
+    runs the base's own fused forward (one e4b_moe_forward call), equal to it bit for bit, as
+    the reference delegates to an accelerated base (lora.py:181-214). Once the adapter is
+    trained (and the cached verdict reset, as train() / a state load do) the LoRA path runs."""
+    from experts4bit_qlora_amd import fast as F
+
+    _announce(f"lora zero adapter n_tok={n_tok}")
+    mod = _lora()
+    with torch.no_grad():
+        mod.gate_up_lora_B.zero_()
+        mod.down_lora_B.zero_()
+    mod._delegate_ok = None
+    hs, idx, wts = _lora_inputs(n_tok)
+    assert e4b.enable_fast(mod) == 1
+    with torch.no_grad():
+        got = mod(hs, idx, wts)
+        bare = F.fused_experts_forward(mod.base, hs, idx, wts)
+        assert torch.equal(got, bare)
+        mod.down_lora_B.normal_(0, 0.02)
+        mod._delegate_ok = None
+        trained = mod(hs, idx, wts)
+    assert not torch.equal(trained, bare)
+
+
 def test_lora_patches_wrapper_and_skips_wrapped_base():
     mod = _lora()
     assert e4b.enable_fast(mod) == 1
