@@ -51,11 +51,19 @@ constexpr int kTileMSmall = 32;  // rows per tile for mid-size batches
 constexpr int kTileNW = 128;     // weight rows per tile of the 32- and 256-row shapes
 constexpr int kTileNWWide = 256; // weight rows per tile of the 128-row (prefill) shape
 constexpr int kTileK = 64;
-constexpr int kLdsPitch = kTileK + 8;  // elements; 144-byte rows keep 16-byte alignment
+
+// LDS tile layout: 128-byte rows of 64 elements, the row's eight 16-byte groups stored in the
+// order group ^ (row & 7). gfx950 serves ds_read_b128 at 256 bytes per clock and ds_write_b128
+// at 128: the MFMA fragment reads (16 consecutive rows, one group each) and the staging stores
+// (consecutive groups of a few rows) then fall in distinct banks, both conflict-free. (A
+// 144-byte padded row costs the fragment reads a 2-way conflict, a 160-byte one the stores:
+// measured with SQ_LDS_BANK_CONFLICT on single-instruction patterns.) Element offset of the
+// 16-byte group holding column col (a multiple of 8) of a row:
+E4B_DEV int lds_at(int row, int col) { return row * kTileK + ((((col >> 3) ^ row) & 7) << 3); }
 // K steps of global loads in flight ahead of the MFMAs (6 for the 32-row tiles was measured:
 // no change at bs=64, whose blocks are bound by their decode and LDS work, not by latency).
-// The 256-row tiles hold two: their activation sets are twice as large and a third spills.
-constexpr int gemm_stages(int bm) { return bm == kTileMBig ? 2 : 3; }
+// The 128- and 256-row tiles hold two: a third set spills at their 256-register budget.
+constexpr int gemm_stages(int bm) { return bm >= kTileM ? 2 : 3; }
 constexpr int kXcds = 8;    // accelerator dies of an MI355X; blocks go round-robin over them
 
 template <int DT>
@@ -199,8 +207,8 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   constexpr int WB = kTileK / 2 / TPW;    // packed weight bytes per thread per step
   static_assert(AV >= 1 && NS % 2 == 0 && (WB == 16 || WB == 8), "tile shape");
   constexpr int ST = gemm_stages(BM);
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kLdsPitch];
-  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kLdsPitch];
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kTileK];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kTileK];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
   __shared__ int row_shift_s[F16C ? BM : 1];  // fp16 mode: each tile row's activation shift
   __shared__ int hexp_s[F16C ? BM : 1];       // fp16 mode, gate_up: each tile row's h exponent
@@ -339,31 +347,42 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
     if constexpr (F16C) scale = __builtin_amdgcn_ldexpf(scale, wsh);  // exact: a power of two
     uint32_t wv[WB];
     dequant_bytes<CT, FMT, WB, !F16C>(wq[set], code, scale, wv);
-    uint4* ws = reinterpret_cast<uint4*>(&Ws[buf][lrow * kLdsPitch + half * 2 * WB]);
+    // the swizzled store addresses are recomputed every step (a few integer ops): held across
+    // the loop they would take registers the pipeline needs
+    int wr = lrow, arow = ar;
+    asm volatile("" : "+v"(wr), "+v"(arow));
 #pragma unroll
-    for (int i = 0; i < WB / 4; ++i) ws[i] = make_uint4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
-    u32x4_t* as = reinterpret_cast<u32x4_t*>(&As[buf][ar * kLdsPitch + aseg]);
+    for (int i = 0; i < WB / 4; ++i)
+      *reinterpret_cast<uint4*>(&Ws[buf][lds_at(wr, half * 2 * WB + 8 * i)]) =
+          make_uint4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
 #pragma unroll
     for (int i = 0; i < AV; ++i) {
+      u32x4_t* as = reinterpret_cast<u32x4_t*>(&As[buf][lds_at(arow, aseg + 8 * i)]);
       if constexpr (F16 == 1) {
         const u32x4_t v = areg[set][i];
-        as[i] = u32x4_t{bf16x2_to_f16x2(v[0], ash), bf16x2_to_f16x2(v[1], ash), bf16x2_to_f16x2(v[2], ash),
-                        bf16x2_to_f16x2(v[3], ash)};
+        *as = u32x4_t{bf16x2_to_f16x2(v[0], ash), bf16x2_to_f16x2(v[1], ash), bf16x2_to_f16x2(v[2], ash),
+                      bf16x2_to_f16x2(v[3], ash)};
       } else {
-        as[i] = areg[set][i];
+        *as = areg[set][i];
       }
     }
   };
-  // MFMA operands of one 32-deep half step (ks) of LDS buffer buf, and the MFMAs on them
+  // MFMA operands of one 32-deep half step (ks) of LDS buffer buf, and the MFMAs on them. Every
+  // fragment row is a multiple of 16 plus (lane & 15), so its swizzle term is lane & 7: the
+  // lane's column offset for half step 0 is ((lane >> 4) ^ (lane & 7)) * 8 and for half step 1
+  // that XOR 32 (group 4 + lane >> 4), and the rows add compile-time offsets to one base.
+  const int fcol0 = ((lane >> 4) ^ (lane & 7)) << 3;
+  const int a_frag = (wave_m * WM + (lane & 15)) * kTileK;
+  const int w_frag = (lane & 15) * kTileK;
   auto read_frags = [&](int buf, int ks, uint4 (&av)[MS], uint4 (&bv)[NS]) {
-    const int kcol = ks * 32 + (lane >> 4) * 8;
+    const int fcol = ks ? fcol0 ^ 32 : fcol0;
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) {
-      av[ms] = *reinterpret_cast<const uint4*>(&As[buf][(wave_m * WM + ms * 16 + (lane & 15)) * kLdsPitch + kcol]);
+      av[ms] = *reinterpret_cast<const uint4*>(&As[buf][a_frag + ms * 16 * kTileK + fcol]);
     }
 #pragma unroll
     for (int ns = 0; ns < NS; ++ns) {
-      bv[ns] = *reinterpret_cast<const uint4*>(&Ws[buf][(nbase[ns] + (lane & 15)) * kLdsPitch + kcol]);
+      bv[ns] = *reinterpret_cast<const uint4*>(&Ws[buf][w_frag + nbase[ns] * kTileK + fcol]);
     }
   };
   auto mfmas = [&](const uint4 (&av)[MS], const uint4 (&bv)[NS]) {
