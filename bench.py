@@ -39,12 +39,14 @@ QWEN3 = dict(E=128, H=2048, I=768, k=8, renorm=True)
 GPTOSS = dict(E=32, H=2880, I=2880, k=4)
 
 
-# HBM bytes per launch of the dominant kernel, from the two counter runs summarised in
-# profiles/decode_up_kernel_olmoe_bs1.txt (FETCH_SIZE and WRITE_SIZE, scaled by what a 256 MiB
-# device copy reads for each in the same runs). Keyed by the kernel it was measured on, so a
-# changed kernel reports null until it is measured again.
+# HBM bytes per launch, from the two counter runs summarised in profiles/ (FETCH_SIZE and
+# WRITE_SIZE, scaled by what a 256 MiB device copy reads for each in the same runs). Keyed by
+# the kernel it was measured on, so a changed kernel reports null until it is measured again.
 MEASURED_TRAFFIC = {
-    "decode_up_kernel<bf16, nf4, G=16, CPL=4, full, gated>": 19_055_000,
+    "decode_up_kernel<bf16, nf4, G=16, CPL=4, full, gated>": 18_881_000,
+    "decode_down_kernel<bf16, nf4, G=32, CPL=1, JOBS=1, full>": 9_707_000,
+    # profiles/prefill_qwen3_4096_zipf.txt: 296.81 MB read + 50.18 MB written per dispatch
+    "void e4b::gemm_mfma_kernel<0, 1, 128, 2>": 346_990_000,
 }
 
 
@@ -172,7 +174,8 @@ def decode_bench(mods, cfg, T, steps, warmup, seed0):
 def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
     """The decode gate_up kernel (routing + gate_up GEMV + SwiGLU) at bs=1 alone, 16 layers per
     graph replay, timed with HIP events on the launch stream: achieved = routed gate_up bytes
-    per launch / average launch duration."""
+    per launch / average launch duration. The second decode kernel (down GEMV + k-slot combine)
+    is timed the same way, on the h the first one wrote; it is reported beside the roofline."""
     import torch
 
     from experts4bit_qlora_amd import _native as N
@@ -180,19 +183,27 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
     from experts4bit_qlora_amd import ops
 
     inputs = [make_inputs(cfg, 1, seed0 + 10 * l) for l in range(len(mods))]
-    qws = [F._qweights(m)[0] for m in mods]
+    qws = [F._qweights(m) for m in mods]
     torch.cuda.synchronize()
 
     def launches():
-        return [ops.decode_gate_up(x, idx, qw, N.EPI_SWIGLU) for (x, idx, _), qw in zip(inputs, qws)]
+        return [ops.decode_gate_up(x, idx, qw[0], N.EPI_SWIGLU) for (x, idx, _), qw in zip(inputs, qws)]
 
-    g, _ = graph_of(launches)
+    g, hs = graph_of(launches)
     ms = time_graph(g, steps * 4, warmup)
     per_launch_us = ms * 1e3 / len(mods)
-    gu_b, _ = nf4_expert_bytes(cfg["H"], cfg["I"])
+    gu_b, dn_b = nf4_expert_bytes(cfg["H"], cfg["I"])
     bytes_per_launch = cfg["k"] * gu_b  # 8 distinct routed experts at bs=1
     achieved = bytes_per_launch / (per_launch_us * 1e-6) / 1e9
     kernel = "decode_up_kernel<bf16, nf4, G=16, CPL=4, full, gated>"
+
+    def down_launches():
+        return [ops.decode_down_combine(h, idx, w, qw[1], x.dtype) for h, (x, idx, w), qw in zip(hs, inputs, qws)]
+
+    g2, _ = graph_of(down_launches)
+    ms2 = time_graph(g2, steps * 4, warmup)
+    down_us = ms2 * 1e3 / len(mods)
+    down_bytes = cfg["k"] * dn_b
     return {
         "bound": "hbm",
         "kernel": kernel + " (routing + gate_up + SwiGLU, bs=1)",
@@ -203,7 +214,64 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
         "traffic": MEASURED_TRAFFIC.get(kernel),
         "bytes_per_launch": bytes_per_launch,
         "avg_launch_us": round(per_launch_us, 3),
+        "second_kernel": {
+            "kernel": "decode_down_kernel<bf16, nf4, G=32, CPL=1, JOBS=1, full> (down + k-slot combine, bs=1)",
+            "avg_launch_us": round(down_us, 3),
+            "bytes_per_launch": down_bytes,
+            "achieved": round(down_bytes / (down_us * 1e-6) / 1e9, 1),
+            "frac": round(down_bytes / (down_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": MEASURED_TRAFFIC.get("decode_down_kernel<bf16, nf4, G=32, CPL=1, JOBS=1, full>"),
+        },
     }
+
+
+def prefill_gemm_roofline(mod, x, idx, w, cfg):
+    """The prefill's GEMM launches (fp16 matrix-core mode) timed by the device tracer over five
+    eager forwards: algorithmic FLOP of each launch (the rows its tiles hold, both gate_up halves)
+    / its average duration, against the dense bf16/fp16 peak. The 128-row tiles carry every
+    expert's rows except a last tile of at most 32 rows, which the 32-row launch takes."""
+    import collections
+
+    import torch
+    from torch.profiler import ProfilerActivity, profile
+
+    H, I = cfg["H"], cfg["I"]
+    counts = torch.bincount(idx.reshape(-1), minlength=cfg["E"]).cpu().tolist()
+    tail = [c % 128 if 0 < c % 128 <= 32 else 0 for c in counts]
+    rows = {128: sum(counts) - sum(tail), 32: sum(tail)}
+    flop = {(128, "gate_up"): 2 * rows[128] * 2 * I * H, (128, "down"): 2 * rows[128] * H * I,
+            (32, "gate_up"): 2 * rows[32] * 2 * I * H, (32, "down"): 2 * rows[32] * H * I}
+    with torch.no_grad():
+        mod(x, idx, w)
+        torch.cuda.synchronize()
+        with profile(activities=[ProfilerActivity.CUDA]) as prof:
+            for _ in range(5):
+                mod(x, idx, w)
+            torch.cuda.synchronize()
+    durs = collections.defaultdict(list)
+    for ev in prof.events():
+        if ev.device_type == torch.autograd.DeviceType.CUDA and "gemm_mfma_kernel" in ev.name:
+            t = getattr(ev, "device_time", None)
+            durs[ev.name.split("(")[0]].append(t if t is not None else ev.cuda_time)
+    out = {}
+    for name, d in durs.items():
+        # gemm_mfma_kernel<DT, FMT, BM, F16>: F16 2 = gate_up (tokens staged as scaled fp16), 1 = down
+        args = name[name.index("<") + 1:name.index(">")].split(",")
+        bm, f16 = int(args[2]), int(args[3])
+        proj = "gate_up" if f16 == 2 else "down"
+        us = sum(d) / len(d)
+        tf = flop[(bm, proj)] / (us * 1e-6) / 1e12
+        out[f"{proj}_{bm}row"] = {"kernel": name, "avg_launch_us": round(us, 2), "calls": len(d),
+                                  "flop_per_launch": flop[(bm, proj)], "achieved": round(tf, 1),
+                                  "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+    if not out:
+        return None
+    dom = max(out.values(), key=lambda v: v["avg_launch_us"])
+    return {"bound": "mfma", "kernel": dom["kernel"] + " (dominant prefill GEMM)", "achieved": dom["achieved"],
+            "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"],
+            "traffic": MEASURED_TRAFFIC.get(dom["kernel"]),
+            "flop_per_launch": dom["flop_per_launch"], "avg_launch_us": dom["avg_launch_us"],
+            "timer": "device tracer (torch.profiler), 5 eager forwards", "launches": out}
 
 
 def pmc_pass(mods, cfg, seed0):
@@ -254,7 +322,9 @@ def prefill_bench(steps, warmup):
     ms = time_graph(g, max(steps, 10), warmup)
     flops = 2 * cfg["k"] * 4096 * (2 * cfg["I"] * cfg["H"] + cfg["H"] * cfg["I"])
     tflops = flops / (ms / 1e3) / 1e12
+    roof = prefill_gemm_roofline(mod, x, idx, w, cfg)
     return {
+        "roofline": roof,
         "workload": "Qwen3-30B-A3B geometry, 1 layer, 4096-token prefill, Zipf(1.1), NF4 double-quant",
         "ms": ms,
         "tflops": tflops,
@@ -265,56 +335,65 @@ def prefill_bench(steps, warmup):
     }
 
 
-def extra_benches(steps, warmup):
-    """configs[2] (Qwen3 decode, double-quant) and configs[4] (gpt-oss MXFP4 + biases)."""
+def extra_benches(steps, warmup, qwen_layers=8, gptoss_layers=4):
+    """configs[2] (Qwen3 decode, double-quant) and configs[4] (gpt-oss MXFP4 + biases): a stack of
+    layers (independent weights and inputs) per graph replay, as for the OLMoE decode step, so the
+    per-layer time does not carry a whole graph launch; us = replay time / layers."""
     import torch
 
     import experts4bit_qlora_amd as e4b
 
     out = {}
     cfg = QWEN3
-    mod = make_layer(cfg, seed=1000 + 200, dq=True)
-    e4b.enable_fast(mod)
+    mods = [make_layer(cfg, seed=1000 + 200 + l, dq=True) for l in range(qwen_layers)]
+    for m in mods:
+        e4b.enable_fast(m)
     per_expert = dq_expert_bytes(cfg["H"], cfg["I"])
     for T in (1, 32, 256):
-        x, idx, w = make_inputs(cfg, T, seed=1000 + 210 + T)
+        inputs = [make_inputs(cfg, T, seed=1000 + 210 + T + 7 * l) for l in range(qwen_layers)]
 
         def step():
             with torch.no_grad():
-                return mod(x, idx, w)
+                return [m(x, idx, w) for m, (x, idx, w) in zip(mods, inputs)]
 
         g, _ = graph_of(step)
-        ms = time_graph(g, steps * 4, warmup)
-        nbytes = int(torch.unique(idx).numel()) * per_expert
-        out[f"qwen3_dq_bs{T}"] = {"us": ms * 1e3, "hbm_gbs": nbytes / (ms / 1e3) / 1e9}
-    del mod
+        ms = time_graph(g, steps * 2, warmup) / qwen_layers
+        nbytes = sum(int(torch.unique(idx).numel()) for _, idx, _ in inputs) / qwen_layers * per_expert
+        out[f"qwen3_dq_bs{T}"] = {"us": ms * 1e3, "hbm_gbs": nbytes / (ms / 1e3) / 1e9, "layers": qwen_layers}
+    del mods
+    torch.cuda.empty_cache()
     cfg = GPTOSS
-    g0 = torch.Generator(device="cuda").manual_seed(1400)
     E, H, I = cfg["E"], cfg["H"], cfg["I"]
-    gu = torch.randn(E, 2 * I, H, generator=g0, device="cuda") * 0.02
-    dn = torch.randn(E, H, I, generator=g0, device="cuda") * 0.02
-    b1 = torch.randn(E, 2 * I, generator=g0, device="cuda") * 0.02
-    b2 = torch.randn(E, H, generator=g0, device="cuda") * 0.02
-    mod = e4b.GptOssExpertsMxfp4.from_float(gu, b1, dn, b2).eval()
-    del gu, dn
-    e4b.enable_fast(mod)
+    mods = []
+    for l in range(gptoss_layers):
+        g0 = torch.Generator(device="cuda").manual_seed(1400 + l)
+        gu = torch.randn(E, 2 * I, H, generator=g0, device="cuda") * 0.02
+        dn = torch.randn(E, H, I, generator=g0, device="cuda") * 0.02
+        b1 = torch.randn(E, 2 * I, generator=g0, device="cuda") * 0.02
+        b2 = torch.randn(E, H, generator=g0, device="cuda") * 0.02
+        mod = e4b.GptOssExpertsMxfp4.from_float(gu, b1, dn, b2).eval()
+        del gu, dn
+        e4b.enable_fast(mod)
+        mods.append(mod)
     per_expert = (2 * I * H + H * I) // 2 + (2 * I * H + H * I) // 32 + (2 * I + H) * 2
     for T in (1, 2048):
-        gi = torch.Generator(device="cuda").manual_seed(1410 + T)
-        x = torch.randn(T, H, generator=gi, device="cuda").to(torch.bfloat16)
-        val, idx = torch.topk(torch.randn(T, E, generator=gi, device="cuda"), cfg["k"], dim=-1)
-        w = torch.softmax(val, -1).to(torch.bfloat16)
+        inputs = []
+        for l in range(gptoss_layers):
+            gi = torch.Generator(device="cuda").manual_seed(1410 + T + 13 * l)
+            x = torch.randn(T, H, generator=gi, device="cuda").to(torch.bfloat16)
+            val, idx = torch.topk(torch.randn(T, E, generator=gi, device="cuda"), cfg["k"], dim=-1)
+            inputs.append((x, idx, torch.softmax(val, -1).to(torch.bfloat16)))
 
         def step():
             with torch.no_grad():
-                return mod(x, idx, w)
+                return [m(x, idx, w) for m, (x, idx, w) in zip(mods, inputs)]
 
         g, _ = graph_of(step)
-        ms = time_graph(g, steps * 2, warmup)
-        nbytes = int(torch.unique(idx).numel()) * per_expert
+        ms = time_graph(g, steps, warmup) / gptoss_layers
+        nbytes = sum(int(torch.unique(idx).numel()) for _, idx, _ in inputs) / gptoss_layers * per_expert
         flops = 2 * cfg["k"] * T * (2 * I * H + H * I)
         out[f"gptoss_mxfp4_bs{T}"] = {"us": ms * 1e3, "hbm_gbs": nbytes / (ms / 1e3) / 1e9,
-                                      "tflops": flops / (ms / 1e3) / 1e12}
+                                      "tflops": flops / (ms / 1e3) / 1e12, "layers": gptoss_layers}
     return out
 
 
