@@ -32,6 +32,8 @@ EXPORTS = (
     "e4b_weight_shift",
     "e4b_route_scratch_ints",
     "e4b_route",
+    "e4b_route_groups",
+    "e4b_gather_rows",
     "e4b_grouped_gemm",
     "e4b_combine",
     "e4b_lora_delta",
@@ -110,6 +112,10 @@ def _bind(L):
     L.e4b_route_scratch_ints.argtypes = [I64, I32]
     L.e4b_route.restype = ctypes.c_int
     L.e4b_route.argtypes = [P, I64, I32, I32, RT, P]
+    L.e4b_route_groups.restype = ctypes.c_int
+    L.e4b_route_groups.argtypes = [ctypes.POINTER(ctypes.c_int64), I32, P, I32, RT, P]
+    L.e4b_gather_rows.restype = ctypes.c_int
+    L.e4b_gather_rows.argtypes = [P, I64, I64, P, P, P, I32, I64, P, P]
     L.e4b_grouped_gemm.restype = ctypes.c_int
     L.e4b_grouped_gemm.argtypes = [P, I32, I32, QW, RT, I64, I64, I32, F32, F32, I32, P, I32, P]
     L.e4b_combine.restype = ctypes.c_int

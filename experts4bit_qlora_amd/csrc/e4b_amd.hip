@@ -19,6 +19,7 @@
 #include "decode_fused.h"
 #include "decode_launch.h"
 #include "dequant.h"
+#include "gather.h"
 #include "gemm.h"
 #include "gemv.h"
 #include "lora.h"
@@ -410,6 +411,49 @@ int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t
   hipLaunchKernelGGL(e4b::route_place_kernel, dim3(static_cast<unsigned>(nchunks)), dim3(e4b::kRouteChunk), 0, stream,
                      top_k_index, M, num_experts, rt->scratch, *rt);
   return check_launch("route_count/scan/place kernels");
+}
+
+int e4b_route_groups(const int64_t* sizes, int32_t groups, const int64_t* expert_ids, int32_t num_experts,
+                     const e4b_routing* rt, hipStream_t stream) {
+  if (groups < 0 || groups > e4b::kGroupsMax)
+    return fail(E4B_EUNSUPPORTED, "groups=%d outside [0, %d]", groups, e4b::kGroupsMax);
+  if (num_experts <= 0 || num_experts > e4b::kRouteMaxExperts)
+    return fail(E4B_EUNSUPPORTED, "num_experts=%d outside [1, %d]", num_experts, e4b::kRouteMaxExperts);
+  if (groups > 0 && (!sizes || !expert_ids)) return fail(E4B_EINVAL, "NULL pointer");
+  e4b::GroupOffsets go{};
+  int64_t M = 0;
+  for (int g = 0; g < groups; ++g) {
+    if (sizes[g] < 0) return fail(E4B_EINVAL, "group %d has a negative size", g);
+    go.off[g] = static_cast<int32_t>(M);
+    M += sizes[g];
+    if (M > 0x7fffffffLL) return fail(E4B_EUNSUPPORTED, "groups hold more than 2^31 - 1 rows");
+  }
+  go.off[groups] = static_cast<int32_t>(M);
+  int rc = check_routing(rt, M);
+  if (rc) return rc;
+  // every expert's rows are whole tiles but its last: at most ceil(M / tile_m) + min(E, groups)
+  const int64_t need = cdiv(M, rt->tile_m) + std::min<int64_t>(num_experts, groups);
+  if (M > 0 && rt->max_tiles < need)
+    return fail(E4B_ESPACE, "max_tiles=%d < %lld needed", rt->max_tiles, (long long)need);
+  hipLaunchKernelGGL(e4b::route_groups_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, go, groups, expert_ids,
+                     num_experts, *rt);
+  return check_launch("route_groups_kernel");
+}
+
+int e4b_gather_rows(void* dst, int64_t row_bytes, int64_t dst_off, const int64_t* src_addr, const int64_t* ident,
+                    const int64_t* have, int32_t slots, int64_t n_bytes, unsigned long long* bytes_copied,
+                    hipStream_t stream) {
+  if (slots < 0 || n_bytes < 0 || row_bytes < 0 || dst_off < 0) return fail(E4B_EINVAL, "negative sizes");
+  if (slots == 0 || n_bytes == 0) return E4B_OK;
+  if (!dst || !src_addr || !ident || !have) return fail(E4B_EINVAL, "NULL pointer");
+  if (dst_off + n_bytes > row_bytes)
+    return fail(E4B_EINVAL, "segment [%lld, %lld) runs past the %lld-byte slot row", (long long)dst_off,
+                (long long)(dst_off + n_bytes), (long long)row_bytes);
+  if (slots > 65535) return fail(E4B_EUNSUPPORTED, "slots=%d > 65535", slots);
+  const dim3 grid(static_cast<unsigned>(cdiv(n_bytes, e4b::kGatherChunk)), static_cast<unsigned>(slots));
+  hipLaunchKernelGGL(e4b::gather_rows_kernel, grid, dim3(e4b::kGatherThreads), 0, stream, static_cast<uint8_t*>(dst),
+                     row_bytes, dst_off, src_addr, ident, have, n_bytes, bytes_copied);
+  return check_launch("gather_rows_kernel");
 }
 
 int64_t e4b_route_scratch_ints(int64_t M, int32_t num_experts) {

@@ -405,6 +405,70 @@ E4B_DEV float load_weight(const void* w, int64_t i) {
   }
 }
 
+// Routing of host-described row groups whose expert ids are on the device (the grouped call of
+// engines/pipelined.py:502-508: fixed group sizes, device ids, no host read-back). Group g holds
+// input rows [off[g], off[g + 1]) for expert ids[g]; the rows of an expert's groups go to its
+// segment in group order (sorted_flat: sorted row -> input row, inv: input row -> sorted row, -1
+// for a group whose id is outside [0, E)). The offsets come as a kernel argument, so no host
+// data travels through memory. One 512-thread block; groups <= kGroupsMax.
+constexpr int kGroupsMax = 512;
+struct GroupOffsets {
+  int32_t off[kGroupsMax + 1];
+};
+
+__global__ void __launch_bounds__(kRouteThreads) route_groups_kernel(GroupOffsets go, int G,
+                                                                     const int64_t* __restrict__ ids, int E,
+                                                                     e4b_routing rt) {
+  __shared__ int goff[kGroupsMax + 1];
+  __shared__ int gid[kGroupsMax];
+  __shared__ int gpos[kGroupsMax];
+  __shared__ int cnt[kRouteMaxExperts];
+  __shared__ int start[kRouteMaxExperts];
+  __shared__ int wsum[kRouteWaves];
+  __shared__ int dropped;
+  const int tid = threadIdx.x;
+  for (int i = tid; i < E; i += kRouteThreads) cnt[i] = 0;
+  for (int i = tid; i <= G; i += kRouteThreads) goff[i] = go.off[i];
+  if (tid == 0) dropped = 0;
+  int e = -1;
+  if (tid < G) {
+    const int64_t v = ids[tid];
+    e = (v >= 0 && v < E) ? static_cast<int>(v) : -1;
+    gid[tid] = e;
+  }
+  __syncthreads();
+  if (tid < G) {
+    const int sz = goff[tid + 1] - goff[tid];
+    if (e >= 0) atomicAdd(&cnt[e], sz);
+    else atomicAdd(&dropped, sz);
+  }
+  __syncthreads();
+  const int ea = 2 * tid, eb = 2 * tid + 1;
+  int offa, offb;
+  emit_expert_tables(ea < E ? cnt[ea] : 0, eb < E ? cnt[eb] : 0, E, dropped, rt, wsum, offa, offb);
+  if (ea < E) start[ea] = offa;
+  if (eb < E) start[eb] = offb;
+  __syncthreads();
+  // a group's first sorted row: its expert's first row plus the rows of earlier groups of it
+  if (tid < G && e >= 0) {
+    int before = 0;
+    for (int g = 0; g < tid; ++g) before += (gid[g] == e) ? goff[g + 1] - goff[g] : 0;
+    gpos[tid] = start[e] + before;
+  }
+  __syncthreads();
+  for (int g = 0; g < G; ++g) {
+    const int r0 = goff[g], n = goff[g + 1] - r0, eg = gid[g];
+    for (int i = tid; i < n; i += kRouteThreads) {
+      if (eg >= 0) {
+        rt.sorted_flat[gpos[g] + i] = r0 + i;
+        rt.inv[r0 + i] = gpos[g] + i;
+      } else {
+        rt.inv[r0 + i] = -1;
+      }
+    }
+  }
+}
+
 // Two tile lists from the routed offsets, for grouped GEMMs run at two tile heights. A tile
 // costs about the same whatever its height until its MFMA work catches up with its weight
 // decoding (the whole expert matrix per tile), so every expert keeps big tiles

@@ -412,29 +412,108 @@ def _routing_from_sizes(sizes, expert_ids, num_experts: int, device) -> tuple[Ro
     return rb, M
 
 
+def route_groups(sizes, expert_ids: torch.Tensor, num_experts: int, tile_m: int | None = None) -> RoutingBuffers:
+    """Routing of row groups with host ``sizes`` and device ``expert_ids`` (``e4b_route_groups``):
+    no host read-back of the ids, nothing copied between host and device."""
+    _require_cuda(expert_ids)
+    L = N.lib()
+    ids = expert_ids.to(torch.int64).contiguous()
+    G = len(sizes)
+    if ids.numel() != G:
+        raise ValueError("sizes and expert_ids differ in length")
+    M = int(sum(int(s) for s in sizes))
+    tm = tile_m or mfma_tile_m()
+    max_tiles = max(1, -(-M // tm) + min(num_experts, G))
+    i32 = dict(dtype=torch.int32, device=ids.device)
+    rb = RoutingBuffers(
+        sorted_flat=torch.empty(max(M, 1), **i32),
+        inv=torch.empty(max(M, 1), **i32),
+        offsets=torch.empty(num_experts + 1, **i32),
+        active=torch.empty(num_experts, **i32),
+        tiles=torch.empty(2 * max_tiles, **i32),
+        meta=torch.empty(4, **i32),
+        max_tiles=max_tiles,
+        tile_m=tm,
+    )
+    host_sizes = (ctypes.c_int64 * max(G, 1))(*[int(s) for s in sizes])
+    rs = rb.struct()
+    N.check("e4b_route_groups", L.e4b_route_groups(host_sizes, G, ids.data_ptr(), num_experts, ctypes.byref(rs),
+                                                   _stream(ids.device)))
+    return rb
+
+
+def _grouped_call(a: torch.Tensor, qw: QW, sizes, expert_ids) -> torch.Tensor:
+    """The reference grouped call on ``qw``: host id lists route on the host side as before; a
+    device id tensor routes on the device and the rows come back in group order through ``inv``
+    (rows of an out-of-range id are zero), all without a synchronisation."""
+    if torch.is_tensor(expert_ids) and expert_ids.is_cuda:
+        M = int(sum(int(s) for s in sizes))
+        if a.shape[0] != M:
+            raise ValueError(f"a has {a.shape[0]} rows but sizes sum to {M}")
+        rb = route_groups(sizes, expert_ids, qw.num_experts)
+        tokens = max((int(s) for s in sizes), default=0)
+        out = grouped_gemm(a, qw, rb, tokens, M, gather_k=1)
+        inv = rb.inv[:M].long()
+        return out.index_select(0, inv.clamp(min=0)).masked_fill_((inv < 0).unsqueeze(1), 0)
+    rb, M = _routing_from_sizes(sizes, expert_ids, qw.num_experts, qw.packed.device)
+    if a.shape[0] != M:
+        raise ValueError(f"a has {a.shape[0]} rows but sizes sum to {M}")
+    tokens = max(sizes) if len(sizes) else 0
+    return grouped_gemm(a, qw, rb, tokens, M)
+
+
 def gemm_4bit_grouped(a: torch.Tensor, w: torch.Tensor, absmax: torch.Tensor, sizes, expert_ids,
                       code: torch.Tensor | None = None) -> torch.Tensor:
     """Drop-in for ``nf4_grouped.gemm_4bit_grouped(a, w[E,N,K/2], absmax[E,N,K/64], sizes, ids)``
-    (the call shape at engines/fast.py:137-156): ``[M, N]`` in ``a``'s dtype."""
+    (the call shapes at engines/fast.py:137-156 -- host ids -- and engines/pipelined.py:502-508 --
+    device ids, no synchronisation): ``[M, N]`` in ``a``'s dtype."""
+    E, n, kh = w.shape
+    c = code if code is not None else _nf4_code_on(w.device)
+    qw = nf4_qweight(w, absmax, c, n, kh * 2, num_experts=E)
+    return _grouped_call(a, qw, sizes, expert_ids)
+
+
+_NF4_CODE: dict = {}
+
+
+def _nf4_code_on(device) -> torch.Tensor:
+    """The NF4 code table on ``device``, made once (a host-to-device copy per call would
+    synchronise)."""
     from .quant import code_4bit
 
-    E, n, kh = w.shape
-    c = code if code is not None else code_4bit("nf4", device=w.device)
-    rb, M = _routing_from_sizes(sizes, expert_ids, E, w.device)
-    if a.shape[0] != M:
-        raise ValueError(f"a has {a.shape[0]} rows but sizes sum to {M}")
-    qw = nf4_qweight(w, absmax, c, n, kh * 2, num_experts=E)
-    tokens = max(sizes) if len(sizes) else 0
-    return grouped_gemm(a, qw, rb, tokens, M)
+    key = torch.device(device)
+    t = _NF4_CODE.get(key)
+    if t is None:
+        t = _NF4_CODE[key] = code_4bit("nf4", device=key)
+    return t
 
 
 def gemm_mxfp4_grouped(a: torch.Tensor, blocks: torch.Tensor, scales: torch.Tensor, sizes, expert_ids) -> torch.Tensor:
     """Drop-in for ``mxfp4_grouped.gemm_mxfp4_grouped(a, blocks[E,N,K/2], scales[E,N,K/32], sizes, ids)``
-    (engines/nvme_experts.py:852-865)."""
+    (engines/nvme_experts.py:852-865); host or device ids as for gemm_4bit_grouped."""
     E, n, kh = blocks.shape
-    rb, M = _routing_from_sizes(sizes, expert_ids, E, blocks.device)
-    if a.shape[0] != M:
-        raise ValueError(f"a has {a.shape[0]} rows but sizes sum to {M}")
     qw = mxfp4_qweight(blocks, scales, n, kh * 2, num_experts=E)
-    tokens = max(sizes) if len(sizes) else 0
-    return grouped_gemm(a, qw, rb, tokens, M)
+    return _grouped_call(a, qw, sizes, expert_ids)
+
+
+def gather_rows(dst: torch.Tensor, src_addr: torch.Tensor, ident: torch.Tensor, have: torch.Tensor, n_bytes: int,
+                dst_off: int = 0, bytes_copied: torch.Tensor | None = None) -> None:
+    """Address-table row gather (``e4b_gather_rows``): slot s of ``dst`` (``[slots, row]``, any
+    dtype, contiguous) receives ``n_bytes`` read at the absolute address ``src_addr[s]`` at byte
+    ``dst_off`` of its row, unless ``ident[s] == have[s]``. ``bytes_copied`` (a device int64 scalar)
+    accumulates the bytes moved. Enqueued on the current stream; nothing is read back."""
+    _require_cuda(dst, src_addr, ident, have)
+    if not dst.is_contiguous() or dst.dim() < 2:
+        raise ValueError("dst must be a contiguous [slots, row...] tensor")
+    for t in (src_addr, ident, have):
+        if t.dtype != torch.int64 or not t.is_contiguous() or t.numel() != dst.shape[0]:
+            raise ValueError("src_addr, ident and have must be contiguous int64 with one entry per slot")
+    row_bytes = dst[0].numel() * dst.element_size()
+    cp = None
+    if bytes_copied is not None:
+        if bytes_copied.dtype != torch.int64 or not bytes_copied.is_cuda or bytes_copied.numel() != 1:
+            raise ValueError("bytes_copied must be a one-element int64 device tensor")
+        cp = bytes_copied.data_ptr()
+    N.check("e4b_gather_rows",
+            N.lib().e4b_gather_rows(dst.data_ptr(), row_bytes, int(dst_off), src_addr.data_ptr(), ident.data_ptr(),
+                                    have.data_ptr(), dst.shape[0], int(n_bytes), cp, _stream(dst.device)))

@@ -122,6 +122,28 @@ int64_t e4b_route_scratch_ints(int64_t M, int32_t num_experts);
 int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t num_experts,
               const e4b_routing* rt, hipStream_t stream);
 
+/* Routing of row groups with host sizes and device expert ids: group g holds the input rows
+ * [sum(sizes[:g]), sum(sizes[:g+1])) for expert expert_ids[g] (int64, on the device, read only
+ * there). An expert's groups are concatenated in group order; sorted_flat maps each sorted row to
+ * its input row, inv each input row to its sorted row (-1 when the id is outside [0, E): those
+ * rows are dropped and counted in meta[2]). The sizes travel as kernel arguments: nothing is
+ * copied to or from host memory, so a decode loop with fixed sizes never synchronises.
+ * groups <= 512; rt->max_tiles >= ceil(M / tile_m) + min(E, groups).
+ * Replaces: the device-id grouped call of engines/pipelined.py:502-508 (gemm_4bit_grouped with
+ * `sizes` on the host and the ids as a device tensor). */
+int e4b_route_groups(const int64_t* sizes, int32_t groups, const int64_t* expert_ids, int32_t num_experts,
+                     const e4b_routing* rt, hipStream_t stream);
+
+/* Address-table row gather: for each slot s < slots, unless ident[s] == have[s] (the slot
+ * already holds that row), copies n_bytes from the absolute address src_addr[s] (device memory
+ * or host memory mapped into the device's address space) to dst + s * row_bytes + dst_off.
+ * ident, have and src_addr are int64 device arrays. bytes_copied (optional, device) accumulates
+ * the bytes moved. Replaces: _gather_rows_addr and its launch in engines/pipelined.py:117-151,
+ * 408-417, with the traffic accounting of :471-487. */
+int e4b_gather_rows(void* dst, int64_t row_bytes, int64_t dst_off, const int64_t* src_addr, const int64_t* ident,
+                    const int64_t* have, int32_t slots, int64_t n_bytes, unsigned long long* bytes_copied,
+                    hipStream_t stream);
+
 /* Grouped GEMM over the expert-sorted rows: out[r, :] = epilogue(a_row(r) @ deq(W[e(r)]).T).
  * a_row(r) = a[sorted_flat[r] / gather_k] when gather_k > 0 (the gather of fast.py:135 fused
  * into the A loads), else a[r]. out is [M, n] (E4B_EPI_NONE, E4B_EPI_ACT) or [M, n/2] (gated
