@@ -171,6 +171,42 @@ def decode_bench(mods, cfg, T, steps, warmup, seed0):
     }
 
 
+def lora_bench(mods, cfg, steps, warmup, seed0, bare, rank=16):
+    """The 16-layer decode step through ExpertsLoRA wrappers (the module load_moe_4bit_streaming
+    builds) over the same bases: rank-16 fp32 adapters with nonzero B (a trained adapter, so the
+    LoRA path runs), graph-replayed like the bare step; us per layer and the ratio to the bare
+    layer at the same batch."""
+    import torch
+
+    import experts4bit_qlora_amd as e4b
+
+    wrappers = []
+    for l, m in enumerate(mods):
+        w = e4b.ExpertsLoRA(m, r=rank, alpha=2 * rank, dtype=torch.float32).to("cuda").eval()
+        g = torch.Generator(device="cuda").manual_seed(seed0 + 50 + l)
+        with torch.no_grad():
+            for p in (w.gate_up_lora_B, w.down_lora_B):
+                p.copy_(torch.randn(p.shape, generator=g, device="cuda") * 0.02)
+        assert e4b.enable_fast(w) == 1
+        wrappers.append(w)
+    out = {}
+    for T in (1, 8):
+        inputs = [make_inputs(cfg, T, seed0 + 10 * l) for l in range(len(mods))]
+
+        def step():
+            with torch.no_grad():
+                return [m(x, idx, w) for m, (x, idx, w) in zip(wrappers, inputs)]
+
+        g, _ = graph_of(step)
+        ms = time_graph(g, steps, warmup)
+        us = ms * 1e3 / len(mods)
+        out[f"bs{T}"] = {"us_per_layer": round(us, 3), "vs_bare_layer": round(us / bare[T]["us_per_layer"], 3),
+                         "rank": rank}
+    for w in wrappers:
+        e4b.disable_fast(w)
+    return out
+
+
 def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
     """The decode gate_up kernel (routing + gate_up GEMV + SwiGLU) at bs=1 alone, 16 layers per
     graph replay, timed with HIP events on the launch stream: achieved = routed gate_up bytes
@@ -502,6 +538,8 @@ def main():
         log(f"decode step, batch {T}")
         decode[T] = decode_bench(mods, cfg, T, args.steps, args.warmup, seed0=1000 + 100)
     main_line = decode[1]
+    log("ExpertsLoRA decode step, batches 1 and 8")
+    lora = lora_bench(mods, cfg, args.steps, args.warmup, 1000 + 100, decode)
 
     prefill = None
     if not args.no_prefill:
@@ -544,6 +582,7 @@ def main():
                    for T, d in decode.items()},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "lora_decode": lora,
     }
     if prefill is not None:
         line["prefill"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in prefill.items()}
