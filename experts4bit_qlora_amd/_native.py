@@ -43,6 +43,8 @@ EXPORTS = (
     "e4b_moe_workspace_bytes",
     "e4b_moe_forward",
     "e4b_moe_forward_noalloc",
+    "e4b_moe_lora_workspace_bytes",
+    "e4b_moe_lora_forward",
     "e4b_decode_sync_errors",
     "e4b_decode_wait_limit",
 )
@@ -74,6 +76,19 @@ class QWeight(ctypes.Structure):
         ("code2", ctypes.c_void_p),
         ("bias", ctypes.c_void_p),
         ("shift", ctypes.c_void_p),
+    ]
+
+
+class Lora(ctypes.Structure):
+    """``e4b_lora``: the four adapter matrices of an ExpertsLoRA, their dtype, rank and scaling."""
+    _fields_ = [
+        ("a1", ctypes.c_void_p),
+        ("b1", ctypes.c_void_p),
+        ("a2", ctypes.c_void_p),
+        ("b2", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("rank", ctypes.c_int32),
+        ("scaling", ctypes.c_float),
     ]
 
 
@@ -137,6 +152,11 @@ def _bind(L):
                                   I32, P]
     L.e4b_moe_forward_noalloc.restype = ctypes.c_int
     L.e4b_moe_forward_noalloc.argtypes = [P, I32, I64, P, P, I32, I32, QW, QW, I32, F32, F32, I32, P, I32, P]
+    L.e4b_moe_lora_workspace_bytes.restype = ctypes.c_size_t
+    L.e4b_moe_lora_workspace_bytes.argtypes = [I64, I32, I32, I64, I64, I32, I32, I32]
+    L.e4b_moe_lora_forward.restype = ctypes.c_int
+    L.e4b_moe_lora_forward.argtypes = [P, I32, I64, P, P, I32, I32, QW, QW, ctypes.POINTER(Lora), I32, F32, I32, P,
+                                       ctypes.c_size_t, P, I32, P]
     L.e4b_decode_sync_errors.restype = ctypes.c_int
     L.e4b_decode_sync_errors.argtypes = [ctypes.POINTER(ctypes.c_uint32), I32]
     L.e4b_decode_wait_limit.restype = ctypes.c_int

@@ -47,6 +47,12 @@
 // Chunk c (16 packed bytes = 32 values) of a row goes to lane gl = c % G of the row's group,
 // as its (c / G)-th chunk. When the row's chunk count is not a multiple of G the spare slots
 // load chunk 0 and their products are dropped by a select, so no load is behind a branch.
+//
+// LoRA variants (template LR > 0, ranks up to LR): every routed row f carries t[f, :] = x_f .
+// A[e]^T from a small preceding launch; a weight row's fp32 sum gains lscale * t[f, :] . B[e,
+// row, :] before the epilogue (up) or the combine (down). The G lanes of the row's group split
+// the rank, so the delta costs one fused multiply-add per rank slot and rides the existing
+// group reduction; B is loaded with the weights, t with the row's activations.
 #pragma once
 
 #include "common.h"
@@ -97,7 +103,73 @@ struct DecodeArgs {
   void* out;                  // gate_up: h [T*k, n_out] act dtype; down: out [T, n] in odt
   int odt;
   int64_t n_out;
+  // LoRA delta (the LORA kernel variants): lt [T*k, lr] fp32 holds t = x . A[e]^T of every flat
+  // row; lb is B [E, w.n, lr] in lbdt; weight row `row` of flat row f gains
+  // lscale * sum_q lt[f, q] * B[e, row, q] in fp32 before its epilogue / combine.
+  const float* lt;
+  const void* lb;
+  int lbdt, lr;
+  float lscale;
 };
+
+// LoRA inside the decode GEMVs: lane gl of a G-lane column group takes ranks q = gl + G * i
+// (i < lora_slots<G, LR>()), so its partial delta rides the group's existing reduction. B entries
+// are loaded as raw bits with the weights and converted when used. Every slot is loaded (a slot
+// past the rank re-reads rank 0 and is zeroed by a select) and the adapter dtype is applied by
+// selects: branches here, even uniform ones, measured ~100 more VGPRs in the up kernel and
+// spills in the items kernel.
+constexpr int kDecLoraMaxRank = 64;
+
+// Rank slots per lane for LoRA variants built for ranks up to LR (LR = 0: no LoRA, one unused slot).
+template <int G, int LR>
+constexpr int lora_slots() {
+  return LR > 0 ? (LR + G - 1) / G : 1;
+}
+
+// Raw bits of B[e, row, gl + G * i] for the lane's slots (0 past the rank).
+template <int G, int LR>
+E4B_DEV void load_lora_b(const DecodeArgs& p, int e, int64_t row, int gl, uint32_t (&b)[lora_slots<G, LR>()]) {
+  const int64_t base = (int64_t(e) * p.w.n + row) * p.lr;
+  // two 16-bit loads per entry (the second re-reads the first for 16-bit adapters), no branch
+  const char* bp = static_cast<const char*>(p.lb);
+  const int es = p.lbdt == E4B_FP32 ? 4 : 2;
+#pragma unroll
+  for (int i = 0; i < lora_slots<G, LR>(); ++i) {
+    const int q = gl + G * i;
+    const int64_t o = (base + (q < p.lr ? q : 0)) * es;
+    const uint32_t lo = *reinterpret_cast<const uint16_t*>(bp + o);
+    const uint32_t hi = *reinterpret_cast<const uint16_t*>(bp + o + es - 2);
+    b[i] = q < p.lr ? (es == 4 ? lo | (hi << 16) : lo) : 0u;
+  }
+}
+
+// t[f, gl + G * i] for the lane's slots (0 past the rank).
+template <int G, int LR>
+E4B_DEV void load_lora_t(const DecodeArgs& p, int f, int gl, float (&t)[lora_slots<G, LR>()]) {
+#pragma unroll
+  for (int i = 0; i < lora_slots<G, LR>(); ++i) {
+    const int q = gl + G * i;
+    const float v = p.lt[int64_t(f) * p.lr + (q < p.lr ? q : 0)];
+    t[i] = q < p.lr ? v : 0.0f;
+  }
+}
+
+E4B_DEV float lora_b_value(uint32_t bits, int bdt) {
+  const uint16_t h = static_cast<uint16_t>(bits);
+  const float f16 = to_f<E4B_FP16>(h), bf16 = to_f<E4B_BF16>(h), f32 = __uint_as_float(bits);
+  return bdt == E4B_FP32 ? f32 : (bdt == E4B_BF16 ? bf16 : f16);
+}
+
+// The lane's share of lscale * t . B[e, row, :] (summed over the group by its reduction).
+template <int G, int LR>
+E4B_DEV float lora_partial(const DecodeArgs& p, const float (&t)[lora_slots<G, LR>()],
+                           const uint32_t (&b)[lora_slots<G, LR>()]) {
+  float d = 0.0f;
+#pragma unroll
+  for (int i = 0; i < lora_slots<G, LR>(); ++i)
+    d = __builtin_fmaf(t[i], lora_b_value(b[i], p.lbdt), d);
+  return p.lscale * d;
+}
 
 // The first round trip of both kernels loads raw values without branching on them (lanes
 // beyond M read row 0) and decodes them only after every load of the round trip is issued: a
@@ -448,8 +520,9 @@ E4B_DEV uint4 load_chunk_w(const e4b_qweight& w, int e, int64_t row, int c) {
 }
 
 // gate_up GEMV + fused epilogue for the a-th routed expert (blockIdx.y), G lanes per column.
-template <int DT, int FMT, int G, int CPL, bool FULL, bool PAIR>
+template <int DT, int FMT, int G, int CPL, bool FULL, bool PAIR, int LR>
 __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
+  constexpr bool LORA = LR > 0;
   // NF4 codes as fp16 single entries; e2m1 codes in the activation dtype
   constexpr int CDT = FMT == E4B_FMT_MXFP4 ? DT : E4B_FP16;
   constexpr bool kConv = CDT != DT;  // bf16 activations restaged as scaled fp16
@@ -538,6 +611,14 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
   const uint32_t bg_bits = bias[has_bias ? row_a : 0];
   const uint32_t bu_bits = bias[has_bias ? row_b : 0];
   const float off = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
+  // LoRA: the column's B entries (once per block) and the row's t entries, after the weights
+  uint32_t lba[lora_slots<G, LR>()], lbb[lora_slots<G, LR>()];
+  float ltv[lora_slots<G, LR>()];
+  if constexpr (LORA) {
+    load_lora_b<G, LR>(p, e, row_a, gl, lba);
+    if constexpr (pair) load_lora_b<G, LR>(p, e, row_b, gl, lbb);
+    load_lora_t<G, LR>(p, f, gl, ltv);
+  }
 
   // the activation row while the weights are in flight; the chunk loop then waits for each
   // chunk's weights only
@@ -573,6 +654,10 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
           if constexpr (kConv) d = __builtin_amdgcn_ldexpf(d, sh);
           acc_b += valid[i] ? d * sb[i] : 0.0f;
         });
+    if constexpr (LORA) {
+      acc_a += lora_partial<G, LR>(p, ltv, lba);
+      if constexpr (pair) acc_b += lora_partial<G, LR>(p, ltv, lbb);
+    }
     acc_a = group_reduce<G>(acc_a);
     if constexpr (pair) acc_b = group_reduce<G>(acc_b);
     if (live && gl == 0) {
@@ -590,6 +675,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
     // next routed row of this expert (the same for the whole block): restage its activations
     f = __ffsll(static_cast<long long>(rows)) - 1;
     load_x(f);
+    if constexpr (LORA) load_lora_t<G, LR>(p, f, gl, ltv);
     __syncthreads();  // every wave is done with the current row
     store_x();
     __syncthreads();
@@ -607,8 +693,9 @@ constexpr int kItemThreads = 512;
 constexpr int kItemWaves = kItemThreads / kWave;
 constexpr int kItemMaxX = 16384;  // tokens * k1 activation elements staged (32 KB)
 
-template <int DT, int FMT, int G, int CPL, bool FULL, bool PAIR>
+template <int DT, int FMT, int G, int CPL, bool FULL, bool PAIR, int LR>
 __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArgs p) {
+  constexpr bool LORA = LR > 0;
   constexpr int CDT = FMT == E4B_FMT_MXFP4 ? DT : E4B_FP16;
   constexpr bool kConv = CDT != DT;
   constexpr int kXU = kItemMaxX / 8 / kItemThreads;  // 16-byte activation pieces per thread
@@ -617,6 +704,7 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
   __shared__ int xsh[kConv ? kItemMaxX / 32 + 1 : 1];     // per chunk: the inverse restaging shift
   __shared__ WaveRoute route[kItemWaves];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
+  __shared__ float lts[LR > 0 ? kDecMaxRows * LR : 1];  // LoRA: t of every flat row
   const int tid = static_cast<int>(threadIdx.x);
   const int lane = tid & (kWave - 1);
   const int wid = tid / kWave;
@@ -636,9 +724,27 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
   float cf, cs;
   load_pair_codes<FMT>(w, cf, cs);
   const float c2 = (FMT == E4B_FMT_NF4_DQ) ? w.code2[tid & 255] : 0.0f;
+  // LoRA: the t entries of every flat row (M * lr <= 64 * LR), staged beside the activations
+  constexpr int kTU = LORA ? kDecMaxRows * LR / kItemThreads : 1;
+  const int nt = M * p.lr;
+  float tv[kTU];
+  if constexpr (LORA) {
+#pragma unroll
+    for (int u = 0; u < kTU; ++u) {
+      const int i = tid + u * kItemThreads;
+      tv[u] = p.lt[i < nt ? i : 0];
+    }
+  }
 
   WaveRoute& r = route[wid];
   const int nact = wave_route(row_id(p, M, id_raw), r);
+  if constexpr (LORA) {
+#pragma unroll
+    for (int u = 0; u < kTU; ++u) {
+      const int i = tid + u * kItemThreads;
+      if (i < nt) lts[i] = tv[u];
+    }
+  }
   if (tid < 256) {
     if constexpr (FMT != E4B_FMT_MXFP4) store_pair_entry<false>(lut, pair_entry<CDT, false>(cf, cs));
     if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[tid] = c2;
@@ -690,6 +796,7 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
     RawScale ra[CPL], rb[CPL];
     uint32_t bg, bu;
     float off;
+    uint32_t lba[lora_slots<G, LR>()], lbb[lora_slots<G, LR>()];  // LoRA B entries of the two rows
   };
   auto load = [&](int it, Buf& b) {
     const int a = it / ncg;
@@ -707,6 +814,10 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
     b.bg = bias[has_bias ? row_a : 0];
     b.bu = bias[has_bias ? row_b : 0];
     b.off = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
+    if constexpr (LORA) {
+      load_lora_b<G, LR>(p, e, row_a, gl, b.lba);
+      if constexpr (pair) load_lora_b<G, LR>(p, e, row_b, gl, b.lbb);
+    }
   };
   auto compute = [&](int it, const Buf& b) {
     const int a = it / ncg;
@@ -727,8 +838,9 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
       const int tok = f / p.k;
       asm volatile("" : "+v"(lane_off));  // table addresses recomputed per row, not held
       float acc_a = 0.0f, acc_b = 0.0f;
-      // (no look-ahead past four chunks per lane: with two weight buffers it spills)
-      pair_chunk_dots<CDT, FMT, CPL, pair, (CPL <= 4)>(
+      // (no look-ahead past four chunks per lane, nor beside more than two LoRA rank slots per
+      // lane: with two weight buffers it spills)
+      pair_chunk_dots<CDT, FMT, CPL, pair, (CPL <= 4 && !(LORA && lora_slots<G, LR>() > 2))>(
           b.qa, b.qb, lut_bytes, lane_off,
           [&](int i, uint4 (&xv)[4]) {
 #pragma unroll
@@ -743,6 +855,17 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
             if constexpr (kConv) d = __builtin_amdgcn_ldexpf(d, sh);
             acc_b += valid[i] ? d * sb[i] : 0.0f;
           });
+      if constexpr (LORA) {
+        float ltv[lora_slots<G, LR>()];
+#pragma unroll
+        for (int i = 0; i < lora_slots<G, LR>(); ++i) {
+          const int q = gl + G * i;
+          const float v = lts[f * p.lr + (q < p.lr ? q : 0)];  // no branch around the read
+          ltv[i] = q < p.lr ? v : 0.0f;
+        }
+        acc_a += lora_partial<G, LR>(p, ltv, b.lba);
+        if constexpr (pair) acc_b += lora_partial<G, LR>(p, ltv, b.lbb);
+      }
       acc_a = group_reduce<G>(acc_a);
       if constexpr (pair) acc_b = group_reduce<G>(acc_b);
       if (live && gl == 0) {
@@ -775,8 +898,9 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
 
 // down GEMV over every routed row for kDownCols output columns, then the k-slot combine.
 // Jobs (one routed expert, all kDownCols columns) go to G-lane groups, JOBS per group in flight.
-template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL>
+template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL, int LR>
 __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) {
+  constexpr bool LORA = LR > 0;
   __shared__ __align__(16) uint4 lut[FMT == E4B_FMT_MXFP4 ? 1 : 256 * kLutRowBytes / 16];  // none for e2m1
   __shared__ WaveRoute route[kDecWaves];
   __shared__ float res[kDecMaxRows * kDownCols];
@@ -822,6 +946,8 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
     uint4 q[JOBS][CPL][C], xv[JOBS][CPL][4];
     RawScale rs[JOBS][CPL][C];
     uint16_t bb[JOBS][C];  // raw bias bits, converted when the job runs
+    uint32_t lbw[JOBS][C][lora_slots<G, LR>()];  // LoRA: B entries of the job's columns
+    float ltv[JOBS][lora_slots<G, LR>()];        // LoRA: t entries of the job's current row
     bool valid[CPL];
     int je[JOBS], jf[JOBS];
     unsigned long long jrows[JOBS];
@@ -849,6 +975,13 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
       const uint16_t* bp = has_bias ? bias + int64_t(e) * n : p.x;
 #pragma unroll
       for (int cl = 0; cl < C; ++cl) bb[t][cl] = bp[has_bias ? cols[cl] : 0];
+      if constexpr (LORA) {
+        if (ok) {
+#pragma unroll
+          for (int cl = 0; cl < C; ++cl) load_lora_b<G, LR>(p, e, cols[cl], gl, lbw[t][cl]);
+          load_lora_t<G, LR>(p, jf[t], gl, ltv[t]);
+        }
+      }
     }
     if (!table_ready) {
       if constexpr (FMT != E4B_FMT_MXFP4) store_pair_entry<kSplit>(lut, pair_entry<DT, kSplit>(cf, cs));
@@ -901,6 +1034,10 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
             }
           }
         }
+        if constexpr (LORA) {
+#pragma unroll
+          for (int cl = 0; cl < C; ++cl) acc[cl] += lora_partial<G, LR>(p, ltv[t], lbw[t][cl]);
+        }
 #pragma unroll
         for (int cl = 0; cl < C; ++cl) {
           const float v = group_reduce<G>(acc[cl]);
@@ -909,6 +1046,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
         rows &= rows - 1;
         if (!rows) break;
         f = __ffsll(static_cast<long long>(rows)) - 1;
+        if constexpr (LORA) load_lora_t<G, LR>(p, f, gl, ltv[t]);
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
           bool v;

@@ -34,29 +34,33 @@ int device_cus() {
   return c;
 }
 
-template <int DT, int FMT, int G, int CPL, bool FULL>
+template <int DT, int FMT, int G, int CPL, bool FULL, int LR>
 void up_gc(const DecodeArgs& a, int64_t max_active, hipStream_t s) {
   constexpr int cols_per_block = kDecWaves * (kWave / G);
   dim3 grid(static_cast<unsigned>((a.n_out + cols_per_block - 1) / cols_per_block), static_cast<unsigned>(max_active));
-  if (is_gated(a.epi)) hipLaunchKernelGGL((decode_up_kernel<DT, FMT, G, CPL, FULL, true>), grid, dim3(kDecThreads), 0, s, a);
-  else hipLaunchKernelGGL((decode_up_kernel<DT, FMT, G, CPL, FULL, false>), grid, dim3(kDecThreads), 0, s, a);
+  if (is_gated(a.epi))
+    hipLaunchKernelGGL((decode_up_kernel<DT, FMT, G, CPL, FULL, true, LR>), grid, dim3(kDecThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_up_kernel<DT, FMT, G, CPL, FULL, false, LR>), grid, dim3(kDecThreads), 0, s, a);
 }
 
 // item kernel: one block per CU (its LDS holds one block), no more blocks than items / waves
-template <int DT, int FMT, int G, int CPL, bool FULL>
+template <int DT, int FMT, int G, int CPL, bool FULL, int LR>
 void up_items_gc(const DecodeArgs& a, int64_t max_active, hipStream_t s) {
   constexpr int cols_per_item = kWave / G;
   const int64_t items = max_active * ((a.n_out + cols_per_item - 1) / cols_per_item);
   const int64_t blocks = std::min<int64_t>(device_cus(), (items + kItemWaves - 1) / kItemWaves);
   dim3 grid(static_cast<unsigned>(std::max<int64_t>(blocks, 1)));
-  if (is_gated(a.epi)) hipLaunchKernelGGL((decode_up_items_kernel<DT, FMT, G, CPL, FULL, true>), grid, dim3(kItemThreads), 0, s, a);
-  else hipLaunchKernelGGL((decode_up_items_kernel<DT, FMT, G, CPL, FULL, false>), grid, dim3(kItemThreads), 0, s, a);
+  if (is_gated(a.epi))
+    hipLaunchKernelGGL((decode_up_items_kernel<DT, FMT, G, CPL, FULL, true, LR>), grid, dim3(kItemThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((decode_up_items_kernel<DT, FMT, G, CPL, FULL, false, LR>), grid, dim3(kItemThreads), 0, s, a);
 }
 
-template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL>
+template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL, int LR>
 void down_gc(const DecodeArgs& a, hipStream_t s) {
   dim3 grid(static_cast<unsigned>((a.w.n + kDownCols - 1) / kDownCols));
-  hipLaunchKernelGGL((decode_down_kernel<DT, FMT, G, CPL, JOBS, FULL>), grid, dim3(kDecThreads), 0, s, a);
+  hipLaunchKernelGGL((decode_down_kernel<DT, FMT, G, CPL, JOBS, FULL, LR>), grid, dim3(kDecThreads), 0, s, a);
 }
 
 // The fused kernel's grid: the largest power of two <= min(kFusedMaxGrid, blocks resident at
@@ -87,32 +91,50 @@ bool fused_gc(FusedArgs& a, hipStream_t s) {
 
 }  // namespace
 
-template <int DT, int FMT>
-void launch_decode_up(const DecodeArgs& a, DecShape d, int64_t max_active, hipStream_t s) {
+template <int DT, int FMT, int LR>
+void launch_decode_up_l(const DecodeArgs& a, DecShape d, int64_t max_active, hipStream_t s) {
   const bool items = decode_up_items(a.tokens, a.w.k);
-#define E4B_UP(g, c)                                                          \
-  if (d.G == g && d.CPL == c) {                                               \
-    if (items && d.full) up_items_gc<DT, FMT, g, c, true>(a, max_active, s);  \
-    else if (items) up_items_gc<DT, FMT, g, c, false>(a, max_active, s);      \
-    else if (d.full) up_gc<DT, FMT, g, c, true>(a, max_active, s);            \
-    else up_gc<DT, FMT, g, c, false>(a, max_active, s);                       \
-    return;                                                                   \
+#define E4B_UP(g, c)                                                                \
+  if (d.G == g && d.CPL == c) {                                                     \
+    if (items && d.full) up_items_gc<DT, FMT, g, c, true, LR>(a, max_active, s);  \
+    else if (items) up_items_gc<DT, FMT, g, c, false, LR>(a, max_active, s);      \
+    else if (d.full) up_gc<DT, FMT, g, c, true, LR>(a, max_active, s);            \
+    else up_gc<DT, FMT, g, c, false, LR>(a, max_active, s);                       \
+    return;                                                                         \
   }
   E4B_UP(4, 2) E4B_UP(4, 4) E4B_UP(8, 4) E4B_UP(16, 4) E4B_UP(16, 6) E4B_UP(32, 4)
 #undef E4B_UP
 }
 
 template <int DT, int FMT>
-void launch_decode_down(const DecodeArgs& a, DecShape d, hipStream_t s) {
+void launch_decode_up(const DecodeArgs& a, DecShape d, int64_t max_active, hipStream_t s) {
+  if constexpr (FMT != E4B_FMT_MXFP4) {  // LoRA wraps the NF4 bases only
+    if (a.lt && a.lr <= 16) return launch_decode_up_l<DT, FMT, 16>(a, d, max_active, s);
+    if (a.lt) return launch_decode_up_l<DT, FMT, kDecLoraMaxRank>(a, d, max_active, s);
+  }
+  launch_decode_up_l<DT, FMT, 0>(a, d, max_active, s);
+}
+
+template <int DT, int FMT, int LR>
+void launch_decode_down_l(const DecodeArgs& a, DecShape d, hipStream_t s) {
 #define E4B_DOWN(g, c, j)                                               \
   if (d.G == g && d.CPL == c && d.JOBS == j) {                          \
-    if (d.full) down_gc<DT, FMT, g, c, j, true>(a, s);                  \
-    else down_gc<DT, FMT, g, c, j, false>(a, s);                        \
+    if (d.full) down_gc<DT, FMT, g, c, j, true, LR>(a, s);            \
+    else down_gc<DT, FMT, g, c, j, false, LR>(a, s);                  \
     return;                                                             \
   }
   E4B_DOWN(16, 1, 2) E4B_DOWN(32, 1, 1) E4B_DOWN(32, 2, 1) E4B_DOWN(32, 3, 1)
   E4B_DOWN(32, 4, 1)
 #undef E4B_DOWN
+}
+
+template <int DT, int FMT>
+void launch_decode_down(const DecodeArgs& a, DecShape d, hipStream_t s) {
+  if constexpr (FMT != E4B_FMT_MXFP4) {  // LoRA wraps the NF4 bases only
+    if (a.lt && a.lr <= 16) return launch_decode_down_l<DT, FMT, 16>(a, d, s);
+    if (a.lt) return launch_decode_down_l<DT, FMT, kDecLoraMaxRank>(a, d, s);
+  }
+  launch_decode_down_l<DT, FMT, 0>(a, d, s);
 }
 
 template <int DT, int FMT>

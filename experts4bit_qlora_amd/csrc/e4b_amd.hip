@@ -909,6 +909,162 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
                      stream);
 }
 
+static_assert(e4b::kDecLoraMaxRank == e4b::kLoraMaxRank, "one rank limit for both LoRA paths");
+
+size_t e4b_moe_lora_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts, int64_t n1, int64_t n2,
+                                    int32_t epilogue, int32_t act_dtype, int32_t rank) {
+  (void)act_dtype;
+  const int64_t M = tokens * top_k;
+  const int64_t h_cols = is_gated_epi(epilogue) ? n1 / 2 : n1;
+  const size_t t = align256(sizeof(float) * M * std::max(rank, 1));
+  const size_t h = align256(sizeof(uint16_t) * M * h_cols);
+  const size_t dec = h + 2 * t;  // h, t of the gate_up and of the down projection
+  size_t g = 0;
+  g += 2 * align256(sizeof(int32_t) * M);                               // sorted_flat, inv
+  g += align256(sizeof(int32_t) * (num_experts + 1)) + align256(sizeof(int32_t) * num_experts);
+  g += align256(sizeof(int32_t) * 2 * max_tiles_for(M, num_experts, mfma_tile_for(M, num_experts)));
+  g += align256(sizeof(int32_t) * 4) + align256(sizeof(int32_t) * e4b_route_scratch_ints(M, num_experts));
+  g += align256(sizeof(float) * M * n1) + h + align256(sizeof(float) * M * n2) + t;  // up, h, down, t
+  return std::max(dec, g);
+}
+
+int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                         const void* top_k_weights, int32_t weight_dtype, int32_t top_k, const e4b_qweight* w1,
+                         const e4b_qweight* w2, const e4b_lora* lora, int32_t epilogue, float limit, int32_t flags,
+                         void* workspace, size_t workspace_bytes, void* out, int32_t out_dtype, hipStream_t stream) {
+  int rc = check_weight(w1);
+  if (rc) return rc;
+  rc = check_weight(w2);
+  if (rc) return rc;
+  if (!lora) return fail(E4B_EINVAL, "lora is NULL");
+  if (w1->num_experts != w2->num_experts) return fail(E4B_EINVAL, "w1/w2 expert counts differ");
+  if (w1->format != w2->format) return fail(E4B_EINVAL, "w1 and w2 use different formats");
+  if (w1->format == E4B_FMT_MXFP4) return fail(E4B_EUNSUPPORTED, "LoRA adapters wrap the NF4 formats only");
+  const bool pair = epilogue == E4B_EPI_SWIGLU || epilogue == E4B_EPI_CLAMP_SWIGLU;
+  if (!pair && epilogue != E4B_EPI_ACT)
+    return fail(E4B_EUNSUPPORTED, "epilogue %d: the LoRA forward takes SWIGLU, CLAMP_SWIGLU and ACT", epilogue);
+  if (pair && (w1->n % 2)) return fail(E4B_EINVAL, "gated epilogue needs an even n");
+  const int64_t h_cols = pair ? w1->n / 2 : w1->n;
+  if (h_cols != w2->k || w1->k != w2->n)
+    return fail(E4B_EINVAL, "w1 [%lld, %lld] and w2 [%lld, %lld] do not chain", (long long)w1->n, (long long)w1->k,
+                (long long)w2->n, (long long)w2->k);
+  const int r = lora->rank;
+  if (r <= 0 || r > e4b::kLoraMaxRank) return fail(E4B_EUNSUPPORTED, "rank=%d outside [1, %d]", r, e4b::kLoraMaxRank);
+  if (!any_dtype_ok(lora->dtype)) return fail(E4B_EINVAL, "bad adapter dtype %d", lora->dtype);
+  if (!act_dtype_ok(act_dtype)) return fail(E4B_EINVAL, "act_dtype must be bf16 or fp16 (got %d)", act_dtype);
+  if (!any_dtype_ok(weight_dtype) || !any_dtype_ok(out_dtype)) return fail(E4B_EINVAL, "bad weight/out dtype");
+  if (flags < E4B_PATH_AUTO || flags > E4B_PATH_DECODE_FUSED) return fail(E4B_EINVAL, "bad flags %d", flags);
+  if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "bad tokens/top_k");
+  if (tokens == 0) return E4B_OK;
+  const int E = w1->num_experts;
+  const int64_t M = tokens * top_k;
+  const size_t need = e4b_moe_lora_workspace_bytes(tokens, top_k, E, w1->n, w2->n, epilogue, act_dtype, r);
+  if (!workspace || workspace_bytes < need)
+    return fail(E4B_ESPACE, "workspace %zu bytes < %zu needed", workspace_bytes, need);
+  if (!hidden || !top_k_index || !top_k_weights || !out || !lora->a1 || !lora->b1 || !lora->a2 || !lora->b2)
+    return fail(E4B_EINVAL, "NULL pointer");
+  if (!aligned16(hidden) || !aligned16(workspace) || !aligned16(lora->a1) || !aligned16(lora->a2))
+    return fail(E4B_EINVAL, "hidden, workspace and the A matrices must be 16-byte aligned");
+  if (flags == E4B_PATH_DECODE_FUSED) flags = E4B_PATH_AUTO;  // no single-launch form with adapters
+
+  char* p = static_cast<char*>(workspace);
+  auto take = [&](size_t bytes) {
+    char* q = p;
+    p += align256(bytes);
+    return q;
+  };
+  const bool decode_ok = decode_supported(M, E, w1, true) && decode_supported(M, E, w2, false);
+  if (decode_ok && ((flags == E4B_PATH_AUTO && tokens <= 8) || flags == E4B_PATH_GEMV)) {
+    // t1 = A1 . x per flat row -> gate_up GEMV + delta + epilogue -> t2 = A2 . h -> down GEMV +
+    // delta + combine: four launches, no routing tables.
+    void* h = take(sizeof(uint16_t) * M * h_cols);
+    float* t1 = reinterpret_cast<float*>(take(sizeof(float) * M * r));
+    float* t2 = reinterpret_cast<float*>(take(sizeof(float) * M * r));
+    auto t_rows = [&](const void* x, int gather_k, const void* A, int64_t in, float* t) {
+      const dim3 grid(static_cast<unsigned>(M), static_cast<unsigned>(cdiv(r, e4b::kLoraThreads / e4b::kWave)));
+#define E4B_LT(XD, AD)                                                                                            \
+  if (act_dtype == XD && lora->dtype == AD)                                                                       \
+    hipLaunchKernelGGL((e4b::lora_t_rows_kernel<XD, AD>), grid, dim3(e4b::kLoraThreads), 0, stream,               \
+                       static_cast<const uint16_t*>(x), gather_k, top_k_index, E, A, r, in, t);
+      E4B_LT(E4B_BF16, E4B_BF16) E4B_LT(E4B_BF16, E4B_FP16) E4B_LT(E4B_BF16, E4B_FP32)
+      E4B_LT(E4B_FP16, E4B_BF16) E4B_LT(E4B_FP16, E4B_FP16) E4B_LT(E4B_FP16, E4B_FP32)
+#undef E4B_LT
+      return check_launch("lora_t_rows_kernel");
+    };
+    e4b::DecodeArgs a{};
+    a.topk = top_k_index;
+    a.tokens = static_cast<int>(tokens);
+    a.k = top_k;
+    a.E = E;
+    a.lbdt = lora->dtype;
+    a.lr = r;
+    a.lscale = lora->scaling;
+    rc = t_rows(hidden, top_k, lora->a1, w1->k, t1);
+    if (rc) return rc;
+    a.x = static_cast<const uint16_t*>(hidden);
+    a.w = *w1;
+    a.epi = epilogue;
+    a.alpha = 1.0f;
+    a.limit = limit;
+    a.out = h;
+    a.odt = act_dtype;
+    a.n_out = h_cols;
+    a.lt = t1;
+    a.lb = lora->b1;
+    launch_decode<true>(a, act_dtype, std::min<int64_t>(E, M), M, stream);
+    rc = check_launch("decode_up_kernel (LoRA)");
+    if (rc) return rc;
+    rc = t_rows(h, 0, lora->a2, w2->k, t2);
+    if (rc) return rc;
+    a.x = static_cast<const uint16_t*>(h);
+    a.topk_w = top_k_weights;
+    a.wdt = weight_dtype;
+    a.w = *w2;
+    a.epi = E4B_EPI_NONE;
+    a.out = out;
+    a.odt = out_dtype;
+    a.n_out = w2->n;
+    a.lt = t2;
+    a.lb = lora->b2;
+    launch_decode<false>(a, act_dtype, 0, M, stream);
+    return check_launch("decode_down_kernel (LoRA)");
+  }
+
+  // Grouped path: route once; gate_up GEMM to fp32 rows, its delta fused with the activation,
+  // down GEMM to fp32 rows plus its delta, combine. The deltas stay fp32 until h / out are
+  // rounded.
+  e4b_routing rt;
+  rt.sorted_flat = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));
+  rt.inv = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));
+  rt.offsets = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (E + 1)));
+  rt.active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
+  rt.tile_m = mfma_tile_for(M, E);
+  rt.max_tiles = static_cast<int32_t>(max_tiles_for(M, E, rt.tile_m));
+  rt.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rt.max_tiles));
+  rt.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
+  rt.scratch = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * e4b_route_scratch_ints(M, E)));
+  float* up = reinterpret_cast<float*>(take(sizeof(float) * M * w1->n));
+  void* h = take(sizeof(uint16_t) * M * h_cols);
+  float* down = reinterpret_cast<float*>(take(sizeof(float) * M * w2->n));
+  float* t = reinterpret_cast<float*>(take(sizeof(float) * M * r));
+  rc = e4b_route(top_k_index, tokens, top_k, E, &rt, stream);
+  if (rc) return rc;
+  rc = grouped_gemm_impl(hidden, act_dtype, top_k, w1, &rt, tokens, M, E4B_EPI_NONE, 1.0f, limit, flags, up, E4B_FP32,
+                         nullptr, 0, nullptr, stream);
+  if (rc) return rc;
+  rc = e4b_lora_delta_epilogue(hidden, act_dtype, top_k, &rt, M, E, lora->a1, lora->b1, lora->dtype, r, w1->k, w1->n,
+                               lora->scaling, E4B_FP32, t, up, epilogue, limit, h, act_dtype, stream);
+  if (rc) return rc;
+  rc = grouped_gemm_impl(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, 1.0f, limit, flags, down, E4B_FP32,
+                         nullptr, 0, nullptr, stream);
+  if (rc) return rc;
+  rc = e4b_lora_delta(h, act_dtype, 0, &rt, M, E, lora->a2, lora->b2, lora->dtype, r, w2->k, w2->n, lora->scaling,
+                      E4B_FP32, t, down, stream);
+  if (rc) return rc;
+  return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
+                     stream);
+}
+
 int e4b_decode_sync_errors(uint32_t* errors, int32_t reset) {
   if (!errors) return fail(E4B_EINVAL, "NULL pointer");
   std::lock_guard<std::mutex> lk(g_sync_mu);

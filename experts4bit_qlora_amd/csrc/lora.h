@@ -160,6 +160,40 @@ __global__ void __launch_bounds__(kLoraThreads) lora_a_kernel(const uint16_t* __
   }
 }
 
+// t[f, j] = sum_c x_f[c] * A[e_f, j, c] over the flat rows f of the decode path, in flat order
+// (no routing tables): e_f = ids[f], x_f = row f / gather_k of x (gather_k > 0) or row f; a row
+// whose id is outside [0, E) gets t = 0. Block (f, rank quad): wave w takes rank
+// 4 * blockIdx.y + w, its lanes spread over `in` 8 values at a time (coalesced), and the wave
+// sums at the end. The decode GEMVs add t . B[e, n, :] to their fp32 sums themselves.
+template <int XDT, int ADT>
+__global__ void __launch_bounds__(kLoraThreads) lora_t_rows_kernel(const uint16_t* __restrict__ x, int gather_k,
+                                                                   const int64_t* __restrict__ ids, int E,
+                                                                   const void* __restrict__ A, int r, int64_t in,
+                                                                   float* __restrict__ t) {
+  constexpr int kEs = ADT == E4B_FP32 ? 4 : 2;
+  const int f = static_cast<int>(blockIdx.x);
+  const int j = static_cast<int>(blockIdx.y) * (kLoraThreads / kWave) + static_cast<int>(threadIdx.x / kWave);
+  if (j >= r) return;  // whole wave; no barrier follows
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t id = ids[f];
+  float acc = 0.0f;
+  if (id >= 0 && id < E) {
+    const char* Ar = static_cast<const char*>(A) + (id * r + j) * in * kEs;
+    const uint16_t* xr = x + (gather_k > 0 ? f / gather_k : f) * in;
+#pragma unroll 4
+    for (int64_t c = int64_t(lane) * 8; c < in; c += kWave * 8) {
+      float av[8], xv[8];
+      load8<ADT>(Ar, c, av);
+      load8<XDT>(xr, c, xv);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = __builtin_fmaf(xv[u], av[u], acc);
+    }
+  }
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if (lane == 0) t[int64_t(f) * r + j] = acc;
+}
+
 constexpr int kLoraMaxTileRows = 32;
 constexpr int kLoraRowBatch = 8;
 

@@ -211,12 +211,16 @@ def _bare_forward(mod, hidden_states, top_k_index, top_k_weights, compute_dtype)
 
 
 def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
-    """Fused inference forward of an ``ExpertsLoRA`` (``fast.py:163-257``): grouped GEMMs over the
-    expert-sorted rows with the low-rank delta of every expert group added on the device
-    (``e4b_lora_delta``; for the gate_up projection fused with the activation,
-    ``e4b_lora_delta_epilogue``), so no group size comes to the host (the
-    reference slices the groups in Python after a ``.tolist()``). The GEMM outputs stay fp32
-    until the activation is rounded for the down projection."""
+    """Fused inference forward of an ``ExpertsLoRA`` (``fast.py:163-257``), with no device->host
+    synchronisation (the reference slices its expert groups in Python after a ``.tolist()``).
+
+    With a kernel epilogue (SwiGLU, clamped SwiGLU, SiLU) the whole layer is one C-ABI call,
+    ``e4b_moe_lora_forward``: up to 8 tokens add the low-rank deltas inside the decode GEMVs
+    (four launches), larger batches run the grouped GEMMs with every expert group's delta added
+    on the device. A custom activation keeps the base's own Python epilogue between the grouped
+    GEMMs, the deltas applied by ``e4b_lora_delta``. Either way the deltas stay fp32 until h and
+    the combined output are rounded (fewer rounding points than the reference's compute-dtype
+    casts, ``lora.py:256``, as for the base path)."""
     base = mod.base
     if _wants_reference(mod, hidden_states):
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
@@ -247,18 +251,17 @@ def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
     r = mod.gate_up_lora_A.shape[1]
     if r > 64 or x.shape[1] % 8 or base._down_shape[1] % 8:  # beyond the delta kernel's limits
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)
+    epi = _fused_epilogue(base)
+    if epi is not None:
+        return ops.moe_lora_forward(x, top_k_index, top_k_weights, w1, w2,
+                                    (mod.gate_up_lora_A, mod.gate_up_lora_B), (mod.down_lora_A, mod.down_lora_B),
+                                    mod.scaling, epi[0], input_dtype, limit=epi[1], path=_kernel_path)
+    # a custom activation: the base's own Python epilogue between the grouped GEMMs
     rb = ops.route(top_k_index, E)
     up = ops.grouped_gemm(x, w1, rb, tokens, M, N.EPI_NONE, gather_k=k, path=_kernel_path, out_dtype=torch.float32)
-    epi = _fused_epilogue(base)
-    # the deltas stay fp32 until the single rounding of h / of the combined output: fewer
-    # rounding points than the reference's compute-dtype casts (lora.py:256), as for the base path
-    if epi is not None:  # delta + activation in one pass over the fp32 rows
-        h = ops.lora_delta_epilogue(x, rb, M, E, mod.gate_up_lora_A, mod.gate_up_lora_B, mod.scaling, up, epi[0],
-                                    limit=epi[1], gather_k=k, h_dtype=compute_dtype, delta_dtype=torch.float32)
-    else:  # a custom activation: the base's own Python epilogue
-        ops.lora_delta(x, rb, M, E, mod.gate_up_lora_A, mod.gate_up_lora_B, mod.scaling, up, gather_k=k,
-                       delta_dtype=torch.float32)
-        h = _epilogue(base, up).to(compute_dtype).contiguous()
+    ops.lora_delta(x, rb, M, E, mod.gate_up_lora_A, mod.gate_up_lora_B, mod.scaling, up, gather_k=k,
+                   delta_dtype=torch.float32)
+    h = _epilogue(base, up).to(compute_dtype).contiguous()
     down = ops.grouped_gemm(h, w2, rb, tokens, M, N.EPI_NONE, path=_kernel_path, out_dtype=torch.float32)
     ops.lora_delta(h, rb, M, E, mod.down_lora_A, mod.down_lora_B, mod.scaling, down, delta_dtype=torch.float32)
     return ops.combine(down, rb, top_k_weights, tokens, k, input_dtype)

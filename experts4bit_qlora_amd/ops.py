@@ -357,6 +357,39 @@ def moe_forward(hidden: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: 
     return out
 
 
+def moe_lora_forward(hidden: torch.Tensor, top_k_index: torch.Tensor, top_k_weights: torch.Tensor, w1: QW, w2: QW,
+                     lora1: tuple[torch.Tensor, torch.Tensor], lora2: tuple[torch.Tensor, torch.Tensor],
+                     scaling: float, epilogue: int, out_dtype: torch.dtype, limit: float = 7.0,
+                     path: int = N.PATH_AUTO) -> torch.Tensor:
+    """The fused ExpertsLoRA forward in one C-ABI call (``e4b_moe_lora_forward``): ``lora1 =
+    (A1 [E, r, H], B1 [E, n1, r])`` of the gate_up projection, ``lora2 = (A2 [E, r, I],
+    B2 [E, H, r])`` of the down projection, all in one dtype (B is converted to A's if not)."""
+    _require_cuda(hidden, top_k_index, top_k_weights, w1.packed, w2.packed, *lora1, *lora2)
+    L = N.lib()
+    x = hidden.contiguous()
+    idx = top_k_index.to(torch.int64).contiguous()
+    w = top_k_weights.contiguous()
+    T, k = idx.shape
+    a1 = lora1[0].contiguous()
+    adt = a1.dtype
+    b1 = lora1[1].to(adt).contiguous()
+    a2 = lora2[0].to(adt).contiguous()
+    b2 = lora2[1].to(adt).contiguous()
+    r = int(a1.shape[1])
+    ws_bytes = int(L.e4b_moe_lora_workspace_bytes(T, k, w1.num_experts, w1.n, w2.n, epilogue, dtype_code(x.dtype), r))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    out = torch.empty(T, w2.n, dtype=out_dtype, device=x.device)
+    s1, s2 = w1.struct(), w2.struct()
+    lo = N.Lora(a1=a1.data_ptr(), b1=b1.data_ptr(), a2=a2.data_ptr(), b2=b2.data_ptr(), dtype=dtype_code(adt), rank=r,
+                scaling=float(scaling))
+    N.check("e4b_moe_lora_forward",
+            L.e4b_moe_lora_forward(x.data_ptr(), dtype_code(x.dtype), T, idx.data_ptr(), w.data_ptr(),
+                                   dtype_code(w.dtype), k, ctypes.byref(s1), ctypes.byref(s2), ctypes.byref(lo),
+                                   epilogue, float(limit), path, ws.data_ptr(), ws_bytes, out.data_ptr(),
+                                   dtype_code(out_dtype), _stream(x.device)))
+    return out
+
+
 def decode_sync_errors(device=None, reset: bool = False) -> int:
     """The sticky give-up flag of the single-token decode launch on ``device`` (non-zero: a
     launch stopped waiting for its other blocks and its output was undefined). Synchronises."""

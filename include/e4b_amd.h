@@ -266,6 +266,40 @@ int e4b_moe_forward_noalloc(const void* hidden, int32_t act_dtype, int64_t token
                             const e4b_qweight* w2, int32_t epilogue, float alpha, float limit, int32_t flags,
                             void* out, int32_t out_dtype, hipStream_t stream);
 
+/* Per-expert low-rank adapters of both projections (the ExpertsLoRA parameters, lora.py:172-175):
+ * gate_up gains scaling * (x . A1[e]^T) . B1[e]^T, down gains scaling * (h . A2[e]^T) . B2[e]^T. */
+typedef struct e4b_lora {
+  const void* a1;  /* [E, rank, w1->k]  gate_up_lora_A */
+  const void* b1;  /* [E, w1->n, rank]  gate_up_lora_B */
+  const void* a2;  /* [E, rank, w2->k]  down_lora_A */
+  const void* b2;  /* [E, w2->n, rank]  down_lora_B */
+  int32_t dtype;   /* e4b_dtype of all four (bf16, fp16 or fp32) */
+  int32_t rank;    /* 1..64 */
+  float scaling;   /* alpha / rank */
+} e4b_lora;
+
+/* Bytes of workspace e4b_moe_lora_forward needs for these sizes (either path). */
+size_t e4b_moe_lora_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts, int64_t n1, int64_t n2,
+                                    int32_t epilogue, int32_t act_dtype, int32_t rank);
+
+/* The whole frozen-expert forward with per-expert LoRA deltas, in one call: arguments as
+ * e4b_moe_forward plus `lora`; epilogue SWIGLU, CLAMP_SWIGLU or ACT; NF4 / NF4_DQ weights.
+ * Both deltas stay fp32 until h (act_dtype) and out (out_dtype) are rounded, as the base's
+ * projections do.
+ * Decode path (tokens <= 8 within the decode limits, or flags == E4B_PATH_GEMV): four
+ * launches -- t1 = x . A1^T per routed row; the gate_up GEMV with scaling * t1 . B1[e, n, :]
+ * added to each column's fp32 sum before the epilogue; t2 = h . A2^T; the down GEMV with its
+ * delta added the same way, then the combine. Otherwise: route, grouped GEMMs to fp32 rows,
+ * the deltas of every expert group added on the device (as e4b_lora_delta_epilogue and
+ * e4b_lora_delta), combine. No device->host synchronisation on either path. flags ==
+ * E4B_PATH_DECODE_FUSED is taken as E4B_PATH_AUTO.
+ * Replaces: engines/fast.py:163-257 fused_experts_lora_forward (the ExpertsLoRA forward that
+ * enable_fast binds, fast.py:328-329), whose groups are sliced on the host after a .tolist(). */
+int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                         const void* top_k_weights, int32_t weight_dtype, int32_t top_k, const e4b_qweight* w1,
+                         const e4b_qweight* w2, const e4b_lora* lora, int32_t epilogue, float limit, int32_t flags,
+                         void* workspace, size_t workspace_bytes, void* out, int32_t out_dtype, hipStream_t stream);
+
 /* Sticky flag of the single-token decode launch on the current device: non-zero once a launch
  * gave up waiting for its other blocks (its output is then undefined). reset != 0 clears it.
  * Synchronises the device (a diagnostic, not for the decode loop).

@@ -169,6 +169,54 @@ def test_moe_forward_checks_shapes_and_workspace():
                              N.EPI_SWIGLU, 1.0, 7.0, 0, 4096, 0, 8192, N.BF16, None) == 0
 
 
+def _lora(rank=16, dtype=N.FP32, scaling=2.0):
+    return N.Lora(a1=4096, b1=4096, a2=4096, b2=4096, dtype=dtype, rank=rank, scaling=scaling)
+
+
+def test_lora_struct_layout():
+    assert ctypes.sizeof(N.Lora) == 4 * 8 + 4 + 4 + 4 + 4  # 4 pointers, dtype, rank, scaling, padding
+    assert N.Lora.scaling.offset == 4 * 8 + 8
+
+
+def test_moe_lora_forward_rejects_bad_arguments():
+    """e4b_moe_lora_forward validates everything before its first launch: formats, epilogues,
+    ranks, shapes, dtypes and the workspace size."""
+    L = N.lib()
+    w1, w2 = _qw(n=128, k=64), _qw(n=64, k=64)
+    lo = _lora()
+    need = L.e4b_moe_lora_workspace_bytes(2, 2, 2, 128, 64, N.EPI_SWIGLU, N.BF16, 16)
+    assert need >= L.e4b_moe_lora_workspace_bytes(2, 2, 2, 128, 64, N.EPI_SWIGLU, N.BF16, 1) > 0
+
+    def call(w1=w1, w2=w2, lo=lo, epi=N.EPI_SWIGLU, ws=need, tokens=2, act=N.BF16, flags=0):
+        return L.e4b_moe_lora_forward(4096, act, tokens, 4096, 4096, N.BF16, 2, ctypes.byref(w1), ctypes.byref(w2),
+                                      ctypes.byref(lo) if lo is not None else None, epi, 7.0, flags, 4096, ws, 8192,
+                                      N.BF16, None)
+
+    assert call(lo=None) == -1 and "lora is NULL" in _err()
+    m1, m2 = _qw(n=128, k=64, format=N.FMT_MXFP4), _qw(n=64, k=64, format=N.FMT_MXFP4)
+    assert call(w1=m1, w2=m2) == -2 and "NF4" in _err()
+    assert call(epi=N.EPI_GPTOSS) == -2 and "epilogue" in _err()
+    assert call(epi=N.EPI_NONE) == -2 and "epilogue" in _err()
+    assert call(lo=_lora(rank=0)) == -2 and "rank" in _err()
+    assert call(lo=_lora(rank=65)) == -2 and "rank" in _err()
+    assert call(lo=_lora(dtype=7)) == -1 and "adapter dtype" in _err()
+    assert call(w2=_qw(n=64, k=128)) == -1 and "chain" in _err()
+    assert call(act=N.FP32) == -1 and "act_dtype" in _err()
+    assert call(flags=9) == -1 and "flags" in _err()
+    assert call(ws=need - 1) == -4 and "workspace" in _err()
+    assert call(tokens=0, ws=0) == 0  # no tokens: a valid no-op
+
+
+def test_lora_workspace_covers_both_paths():
+    L = N.lib()
+    for T in (1, 8, 64, 4096):
+        got = L.e4b_moe_lora_workspace_bytes(T, 8, 64, 2048, 2048, N.EPI_SWIGLU, N.BF16, 64)
+        M = T * 8
+        decode = M * 1024 * 2 + 2 * M * 64 * 4
+        grouped = M * (2048 * 4 + 1024 * 2 + 2048 * 4 + 64 * 4)
+        assert got >= max(decode, grouped), T
+
+
 def test_workspace_grows_with_tokens():
     L = N.lib()
     a = L.e4b_moe_workspace_bytes(1, 8, 64, 2048, 2048, N.EPI_SWIGLU, N.BF16)
