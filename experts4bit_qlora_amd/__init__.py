@@ -16,6 +16,7 @@ from .lora import ExpertsLoRA
 from .arch.deepseek_v4 import DeepseekV4Experts4bit, DeepseekV4ExpertsNbit
 from .arch.gptoss import GptOssExperts4bit, GptOssExpertsMxfp4, GptOssExpertsNbit
 from .ops import gemm_4bit_grouped, gemm_mxfp4_grouped
+from .train import disable_fast_train, enable_fast_train
 
 __version__ = "0.1.0"
 
@@ -30,7 +31,9 @@ __all__ = [
     "GptOssExpertsMxfp4",
     "dequantize_mxfp4",
     "disable_fast",
+    "disable_fast_train",
     "enable_fast",
+    "enable_fast_train",
     "fast_available",
     "gemm_4bit_grouped",
     "gemm_mxfp4_grouped",

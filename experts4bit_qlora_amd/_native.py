@@ -38,6 +38,10 @@ EXPORTS = (
     "e4b_combine",
     "e4b_lora_delta",
     "e4b_lora_delta_epilogue",
+    "e4b_lora_t",
+    "e4b_lora_t_add",
+    "e4b_lora_wgrad",
+    "e4b_grouped_dgrad",
     "e4b_decode_gate_up",
     "e4b_decode_down_combine",
     "e4b_moe_workspace_bytes",
@@ -141,6 +145,14 @@ def _bind(L):
     L.e4b_lora_delta_epilogue.restype = ctypes.c_int
     L.e4b_lora_delta_epilogue.argtypes = [P, I32, I32, RT, I64, I32, P, P, I32, I32, I64, I64, F32, I32, P, P,
                                           I32, F32, P, I32, P]
+    L.e4b_lora_t.restype = ctypes.c_int
+    L.e4b_lora_t.argtypes = [P, I32, I32, RT, I64, I32, P, I32, I32, I64, P, P]
+    L.e4b_lora_t_add.restype = ctypes.c_int
+    L.e4b_lora_t_add.argtypes = [P, RT, I64, I32, P, I32, I32, I64, F32, I32, P, P]
+    L.e4b_lora_wgrad.restype = ctypes.c_int
+    L.e4b_lora_wgrad.argtypes = [P, I32, P, I32, I32, RT, I64, I32, I64, F32, P, P]
+    L.e4b_grouped_dgrad.restype = ctypes.c_int
+    L.e4b_grouped_dgrad.argtypes = [P, I32, QW, RT, I64, P, P]
     L.e4b_decode_gate_up.restype = ctypes.c_int
     L.e4b_decode_gate_up.argtypes = [P, I32, I64, P, I32, QW, I32, F32, F32, P, P]
     L.e4b_decode_down_combine.restype = ctypes.c_int

@@ -25,6 +25,7 @@
 #include "lora.h"
 #include "route.h"
 #include "scale.h"
+#include "train.h"
 
 namespace {
 
@@ -538,23 +539,25 @@ int e4b_weight_shift(const e4b_qweight* w, int32_t* shift, hipStream_t stream) {
 
 namespace {
 
-// Validation shared by the two LoRA entry points, then t = x . A^T for every routed row.
+// Validation of the shared LoRA arguments (the B side's too when lora_b / out_features are
+// given: out_features >= 0), then, for M > 0, t = x . A^T for every routed row.
 int lora_a_pass(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
                 int32_t num_experts, const void* lora_a, const void* lora_b, int32_t adapter_dtype, int32_t rank,
                 int64_t in_features, int64_t out_features, int32_t delta_dtype, float* t_workspace,
                 const void* out, hipStream_t stream) {
+  const bool b_side = out_features >= 0;
   if (!act_dtype_ok(x_dtype)) return fail(E4B_EINVAL, "x_dtype must be bf16 or fp16 (got %d)", x_dtype);
   if (!any_dtype_ok(adapter_dtype) || !any_dtype_ok(delta_dtype)) return fail(E4B_EINVAL, "bad adapter/delta dtype");
   if (M < 0 || M > 0x7fffffffLL) return fail(E4B_EINVAL, "bad row count %lld", (long long)M);
   if (num_experts <= 0 || num_experts > 1024) return fail(E4B_EUNSUPPORTED, "num_experts=%d outside [1, 1024]", num_experts);
   if (rank <= 0 || rank > e4b::kLoraMaxRank) return fail(E4B_EUNSUPPORTED, "rank=%d outside [1, %d]", rank, e4b::kLoraMaxRank);
-  if (in_features <= 0 || in_features % 8 != 0 || out_features <= 0)
+  if (in_features <= 0 || in_features % 8 != 0 || (b_side && out_features <= 0))
     return fail(E4B_EINVAL, "in_features (%lld) must be a positive multiple of 8, out_features (%lld) positive",
                 (long long)in_features, (long long)out_features);
   if (gather_k < 0) return fail(E4B_EINVAL, "gather_k must be >= 0");
   if (!rt || !rt->offsets || (gather_k > 0 && !rt->sorted_flat)) return fail(E4B_EINVAL, "routing offsets / order are NULL");
   if (M == 0) return E4B_OK;
-  if (!x || !lora_a || !lora_b || !t_workspace || !out) return fail(E4B_EINVAL, "NULL pointer");
+  if (!x || !lora_a || !t_workspace || (b_side && (!lora_b || !out))) return fail(E4B_EINVAL, "NULL pointer");
   if (!aligned16(x) || !aligned16(lora_a)) return fail(E4B_EINVAL, "x and lora_a must be 16-byte aligned");
   // lora_a: 8-row tiles once there are enough rows to fill the chip with them, else 1-row tiles.
   const int rgroups = static_cast<int>(cdiv(rank, e4b::kLoraRanksPerBlock));
@@ -579,15 +582,11 @@ int lora_a_pass(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_rout
 
 int lora_tile_rows(int64_t M) { return M <= 512 ? 1 : (M <= 8192 ? 8 : e4b::kLoraMaxTileRows); }
 
-}  // namespace
-
-int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
-                   int32_t num_experts, const void* lora_a, const void* lora_b, int32_t adapter_dtype,
-                   int32_t rank, int64_t in_features, int64_t out_features, float scaling,
-                   int32_t delta_dtype, float* t_workspace, float* out, hipStream_t stream) {
-  const int st = lora_a_pass(x, x_dtype, gather_k, rt, M, num_experts, lora_a, lora_b, adapter_dtype, rank,
-                             in_features, out_features, delta_dtype, t_workspace, out, stream);
-  if (st != E4B_OK || M == 0) return st;
+// out[m, :] += delta_dtype(scaling * t[m, :] . B[e_m, :, :]^T) for the routed rows (M > 0, the
+// arguments validated).
+int lora_b_pass(const float* t_workspace, const e4b_routing* rt, int64_t M, int32_t num_experts, const void* lora_b,
+                int32_t adapter_dtype, int32_t rank, int64_t out_features, float scaling, int32_t delta_dtype,
+                float* out, hipStream_t stream) {
   // lora_b_add: row tiles sized so that small batches still spread over many blocks.
   const int64_t ncb = cdiv(out_features, e4b::kLoraThreads);
   const int tile_rows = lora_tile_rows(M);
@@ -613,6 +612,108 @@ int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_r
   E4B_LB(E4B_FP32, E4B_BF16) E4B_LB(E4B_FP32, E4B_FP16) E4B_LB(E4B_FP32, E4B_FP32)
 #undef E4B_LB
   return check_launch("lora kernels");
+}
+
+}  // namespace
+
+int e4b_lora_delta(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
+                   int32_t num_experts, const void* lora_a, const void* lora_b, int32_t adapter_dtype,
+                   int32_t rank, int64_t in_features, int64_t out_features, float scaling,
+                   int32_t delta_dtype, float* t_workspace, float* out, hipStream_t stream) {
+  const int st = lora_a_pass(x, x_dtype, gather_k, rt, M, num_experts, lora_a, lora_b, adapter_dtype, rank,
+                             in_features, out_features, delta_dtype, t_workspace, out, stream);
+  if (st != E4B_OK || M == 0) return st;
+  return lora_b_pass(t_workspace, rt, M, num_experts, lora_b, adapter_dtype, rank, out_features, scaling, delta_dtype,
+                     out, stream);
+}
+
+int e4b_lora_t(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
+               int32_t num_experts, const void* lora_a, int32_t adapter_dtype, int32_t rank, int64_t in_features,
+               float* t, hipStream_t stream) {
+  return lora_a_pass(x, x_dtype, gather_k, rt, M, num_experts, lora_a, nullptr, adapter_dtype, rank, in_features, -1,
+                     E4B_FP32, t, nullptr, stream);
+}
+
+int e4b_lora_t_add(const float* t, const e4b_routing* rt, int64_t M, int32_t num_experts, const void* lora_b,
+                   int32_t adapter_dtype, int32_t rank, int64_t out_features, float scaling, int32_t delta_dtype,
+                   float* out, hipStream_t stream) {
+  if (!any_dtype_ok(adapter_dtype) || !any_dtype_ok(delta_dtype)) return fail(E4B_EINVAL, "bad adapter/delta dtype");
+  if (M < 0 || M > 0x7fffffffLL) return fail(E4B_EINVAL, "bad row count %lld", (long long)M);
+  if (num_experts <= 0 || num_experts > 1024) return fail(E4B_EUNSUPPORTED, "num_experts=%d outside [1, 1024]", num_experts);
+  if (rank <= 0 || rank > e4b::kLoraMaxRank) return fail(E4B_EUNSUPPORTED, "rank=%d outside [1, %d]", rank, e4b::kLoraMaxRank);
+  if (out_features <= 0) return fail(E4B_EINVAL, "out_features must be positive");
+  if (!rt || !rt->offsets) return fail(E4B_EINVAL, "routing offsets are NULL");
+  if (M == 0) return E4B_OK;
+  if (!t || !lora_b || !out) return fail(E4B_EINVAL, "NULL pointer");
+  return lora_b_pass(t, rt, M, num_experts, lora_b, adapter_dtype, rank, out_features, scaling, delta_dtype, out,
+                     stream);
+}
+
+int e4b_lora_wgrad(const float* u, int32_t rank, const void* a, int32_t a_dtype, int32_t gather_k,
+                   const e4b_routing* rt, int64_t M, int32_t num_experts, int64_t cols, float scale, float* out,
+                   hipStream_t stream) {
+  if (!act_dtype_ok(a_dtype)) return fail(E4B_EINVAL, "a_dtype must be bf16 or fp16 (got %d)", a_dtype);
+  if (M < 0 || M > 0x7fffffffLL) return fail(E4B_EINVAL, "bad row count %lld", (long long)M);
+  if (num_experts <= 0 || num_experts > 65535) return fail(E4B_EUNSUPPORTED, "num_experts=%d outside [1, 65535]", num_experts);
+  if (rank <= 0 || rank > e4b::kLoraMaxRank) return fail(E4B_EUNSUPPORTED, "rank=%d outside [1, %d]", rank, e4b::kLoraMaxRank);
+  if (cols <= 0) return fail(E4B_EINVAL, "cols must be positive");
+  if (gather_k < 0) return fail(E4B_EINVAL, "gather_k must be >= 0");
+  if (!rt || !rt->offsets || (gather_k > 0 && !rt->sorted_flat)) return fail(E4B_EINVAL, "routing offsets / order are NULL");
+  if (!out || (M > 0 && (!u || !a))) return fail(E4B_EINVAL, "NULL pointer");
+  if (cdiv(cols, e4b::kWgradThreads) > 0x7fffffffLL) return fail(E4B_EUNSUPPORTED, "too many columns");
+  // every expert's block writes its rows of out (zeros for an expert without rows)
+  const dim3 grid(static_cast<unsigned>(cdiv(cols, e4b::kWgradThreads)), static_cast<unsigned>(num_experts));
+#define E4B_WG(XD, RB)                                                                                            \
+  hipLaunchKernelGGL((e4b::lora_wgrad_kernel<XD, RB>), grid, dim3(e4b::kWgradThreads), 0, stream, u, rank,       \
+                     static_cast<const uint16_t*>(a), gather_k, rt->sorted_flat, rt->offsets, cols, scale, out)
+#define E4B_WG_R(XD)                                     \
+  if (rank <= 16) E4B_WG(XD, 16);                        \
+  else if (rank <= 32) E4B_WG(XD, 32);                   \
+  else E4B_WG(XD, e4b::kLoraMaxRank);
+  if (a_dtype == E4B_BF16) { E4B_WG_R(E4B_BF16) }
+  else { E4B_WG_R(E4B_FP16) }
+#undef E4B_WG_R
+#undef E4B_WG
+  return check_launch("lora_wgrad_kernel");
+}
+
+int e4b_grouped_dgrad(const void* grad, int32_t grad_dtype, const e4b_qweight* w, const e4b_routing* rt, int64_t M,
+                      float* out, hipStream_t stream) {
+  int rc = check_weight(w);
+  if (rc) return rc;
+  rc = check_routing(rt, M);
+  if (rc) return rc;
+  if (!act_dtype_ok(grad_dtype)) return fail(E4B_EINVAL, "grad_dtype must be bf16 or fp16 (got %d)", grad_dtype);
+  if (w->format == E4B_FMT_MXFP4) return fail(E4B_EUNSUPPORTED, "the grouped dgrad takes NF4 / NF4_DQ weights");
+  if (w->n % 64 != 0) return fail(E4B_EUNSUPPORTED, "the grouped dgrad needs n (%lld) divisible by 64", (long long)w->n);
+  if (rt->tile_m != e4b::kTileM && rt->tile_m != e4b::kTileMSmall)
+    return fail(E4B_EINVAL, "routing tile_m=%d but the dgrad takes %d or %d", rt->tile_m, e4b::kTileM,
+                e4b::kTileMSmall);
+  if (M < 0) return fail(E4B_EINVAL, "negative row count");
+  if (M == 0) return E4B_OK;
+  if (!grad || !out) return fail(E4B_EINVAL, "NULL pointer");
+  if (!aligned16(grad)) return fail(E4B_EINVAL, "grad must be 16-byte aligned");
+  e4b::DgradArgs a;
+  a.g = static_cast<const uint16_t*>(grad);
+  a.w = *w;
+  a.rt = *rt;
+  a.out = out;
+  const int bm = rt->tile_m;
+  const int64_t grid = e4b::kXcds * cdiv(rt->max_tiles, e4b::kXcds) * cdiv(w->k, e4b::dgrad_cols(bm));
+  if (grid > 0x7fffffffLL) return fail(E4B_EUNSUPPORTED, "dgrad grid too large");
+#define E4B_DG(DT, FMT, BM)                                                                                       \
+  hipLaunchKernelGGL((e4b::dgrad_mfma_kernel<DT, FMT, BM>), dim3(static_cast<unsigned>(grid)),                   \
+                     dim3(e4b::dgrad_threads(BM)), 0, stream, a)
+#define E4B_DG_BM(DT, FMT)                                  \
+  if (bm == e4b::kTileM) E4B_DG(DT, FMT, e4b::kTileM);      \
+  else E4B_DG(DT, FMT, e4b::kTileMSmall);
+  if (grad_dtype == E4B_BF16 && w->format == E4B_FMT_NF4) { E4B_DG_BM(E4B_BF16, E4B_FMT_NF4) }
+  else if (grad_dtype == E4B_BF16) { E4B_DG_BM(E4B_BF16, E4B_FMT_NF4_DQ) }
+  else if (w->format == E4B_FMT_NF4) { E4B_DG_BM(E4B_FP16, E4B_FMT_NF4) }
+  else { E4B_DG_BM(E4B_FP16, E4B_FMT_NF4_DQ) }
+#undef E4B_DG_BM
+#undef E4B_DG
+  return check_launch("dgrad_mfma_kernel");
 }
 
 int e4b_lora_delta_epilogue(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,

@@ -269,6 +269,74 @@ def lora_delta(x: torch.Tensor, rb: RoutingBuffers, M: int, num_experts: int, lo
     return out
 
 
+def lora_t(x: torch.Tensor, rb: RoutingBuffers, M: int, num_experts: int, lora_a: torch.Tensor,
+           gather_k: int = 0) -> torch.Tensor:
+    """``t[m] = x_m @ A[e_m].T`` for the expert-sorted rows: fp32 ``[M, r]`` (``lora_a [E, r, in]``
+    in any dtype; ``x_m`` as for :func:`lora_delta`). Rows past the routed ones are left unset."""
+    _require_cuda(x, lora_a)
+    L = N.lib()
+    xc = x.contiguous()
+    a = lora_a.contiguous()
+    E, r, k_in = a.shape
+    t = torch.empty(max(M, 1), r, dtype=torch.float32, device=x.device)
+    rt = rb.struct()
+    N.check("e4b_lora_t",
+            L.e4b_lora_t(xc.data_ptr(), dtype_code(xc.dtype), gather_k, ctypes.byref(rt), M, num_experts, a.data_ptr(),
+                         dtype_code(a.dtype), r, k_in, t.data_ptr(), _stream(x.device)))
+    return t[:M]
+
+
+def lora_t_add(t: torch.Tensor, rb: RoutingBuffers, M: int, num_experts: int, lora_b: torch.Tensor, scaling: float,
+               out: torch.Tensor, delta_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """``out[m] += delta_dtype(scaling * t[m] @ B[e_m].T)`` in place for the routed rows (``t`` fp32
+    ``[M, r]``, ``lora_b [E, out_features, r]``, ``out`` fp32 ``[M, out_features]``)."""
+    _require_cuda(t, lora_b, out)
+    if out.dtype != torch.float32 or not out.is_contiguous() or t.dtype != torch.float32:
+        raise ValueError("t and out must be fp32, out contiguous")
+    L = N.lib()
+    tc = t.contiguous()
+    b = lora_b.contiguous()
+    E, n_out, r = b.shape
+    rt = rb.struct()
+    N.check("e4b_lora_t_add",
+            L.e4b_lora_t_add(tc.data_ptr(), ctypes.byref(rt), M, num_experts, b.data_ptr(), dtype_code(b.dtype), r,
+                             n_out, float(scaling), dtype_code(delta_dtype), out.data_ptr(), _stream(t.device)))
+    return out
+
+
+def lora_wgrad(u: torch.Tensor, a: torch.Tensor, rb: RoutingBuffers, M: int, num_experts: int, scale: float,
+               gather_k: int = 0) -> torch.Tensor:
+    """Per-expert ``out[e] = scale * u_e.T @ a_e`` over expert e's sorted rows: fp32 ``[E, r, cols]``
+    (``u`` fp32 ``[M, r]``; ``a_m`` = ``a[sorted_flat[m] // gather_k]`` or ``a[m]``)."""
+    _require_cuda(u, a)
+    L = N.lib()
+    uc = u.contiguous()
+    ac = a.contiguous()
+    r = uc.shape[1]
+    cols = ac.shape[1]
+    out = torch.empty(num_experts, r, cols, dtype=torch.float32, device=a.device)
+    rt = rb.struct()
+    N.check("e4b_lora_wgrad",
+            L.e4b_lora_wgrad(uc.data_ptr(), r, ac.data_ptr(), dtype_code(ac.dtype), gather_k, ctypes.byref(rt), M,
+                             num_experts, cols, float(scale), out.data_ptr(), _stream(a.device)))
+    return out
+
+
+def grouped_dgrad(g: torch.Tensor, qw: QW, rb: RoutingBuffers, M: int) -> torch.Tensor:
+    """Input gradient of a frozen grouped projection: ``out[m] = g[m] @ deq(W[e_m])`` over the
+    expert-sorted rows, fp32 ``[M, k]`` (``g [M, n]`` bf16 / fp16; ``rb.tile_m`` 128 or 32)."""
+    _require_cuda(g, qw.packed)
+    L = N.lib()
+    gc = g.contiguous()
+    out = torch.empty(max(M, 1), qw.k, dtype=torch.float32, device=g.device)
+    s = qw.struct()
+    rt = rb.struct()
+    N.check("e4b_grouped_dgrad",
+            L.e4b_grouped_dgrad(gc.data_ptr(), dtype_code(gc.dtype), ctypes.byref(s), ctypes.byref(rt), M,
+                                out.data_ptr(), _stream(g.device)))
+    return out[:M]
+
+
 def lora_delta_epilogue(x: torch.Tensor, rb: RoutingBuffers, M: int, num_experts: int, lora_a: torch.Tensor,
                         lora_b: torch.Tensor, scaling: float, proj: torch.Tensor, epilogue: int, limit: float = 0.0,
                         gather_k: int = 0, h_dtype: torch.dtype | None = None,

@@ -196,6 +196,41 @@ int e4b_lora_delta_epilogue(const void* x, int32_t x_dtype, int32_t gather_k, co
                             int32_t delta_dtype, float* t_workspace, const float* proj, int32_t epilogue,
                             float limit, void* h, int32_t h_dtype, hipStream_t stream);
 
+/* The two halves of e4b_lora_delta, for the training lane's backward (same arguments and
+ * limits): t[m, :] = x_m . A[e_m]^T for the routed rows (t fp32 [M, rank]), and
+ * out[m, :] += delta_dtype(scaling * t[m, :] . B[e_m]^T) (B [E, out_features, rank]).
+ * Replaces: the `F.linear(x, A)` and `F.linear(., B)` halves of lora.py:251-256 `_lora`, per
+ * expert group, inside nf4_qlora.fused_grouped_lora's forward and backward (grouped-nf4-gemm,
+ * external; called at engines/fast.py:509-518, 531-540). */
+int e4b_lora_t(const void* x, int32_t x_dtype, int32_t gather_k, const e4b_routing* rt, int64_t M,
+               int32_t num_experts, const void* lora_a, int32_t adapter_dtype, int32_t rank, int64_t in_features,
+               float* t, hipStream_t stream);
+int e4b_lora_t_add(const float* t, const e4b_routing* rt, int64_t M, int32_t num_experts, const void* lora_b,
+                   int32_t adapter_dtype, int32_t rank, int64_t out_features, float scaling, int32_t delta_dtype,
+                   float* out, hipStream_t stream);
+
+/* Per-expert LoRA weight gradient: out[e, j, c] = scale * sum over expert e's routed rows m (in
+ * sorted order) of u[m, j] * a_m[c], out fp32 [E, rank, cols] (every expert written, zeros
+ * where an expert has no rows). u fp32 [M, rank]; a_m = row sorted_flat[m] / gather_k of a
+ * (gather_k > 0) or row m, a [*, cols] in a_dtype. dL/dA[e] = scaling * (g . B[e])^T x and
+ * dL/dB[e]^T = scaling * t^T g of a projection's adapter.
+ * Replaces: the adapter gradients of nf4_qlora.fused_grouped_lora's backward (grouped-nf4-gemm,
+ * external; engines/fast.py:509-540), i.e. autograd through lora.py:251-256 per expert. */
+int e4b_lora_wgrad(const float* u, int32_t rank, const void* a, int32_t a_dtype, int32_t gather_k,
+                   const e4b_routing* rt, int64_t M, int32_t num_experts, int64_t cols, float scale, float* out,
+                   hipStream_t stream);
+
+/* Grouped input gradient of a frozen projection: out[m, :] = grad[m, :] . deq(W[e_m]) for the
+ * expert-sorted rows (grad [M, w->n] in grad_dtype, out fp32 [M, w->k]); the weights are the
+ * forward's dequantized values (one fp32 product code * absmax, one rounding to grad_dtype),
+ * fp32 accumulation on the matrix cores, nothing materialised. rt->tile_m 128 or 32 (the row
+ * tiles); NF4 / NF4_DQ; w->n a multiple of 64.
+ * Replaces: the `grad_out @ deq(W)` of nf4_qlora.fused_grouped_lora's backward -- its per-expert
+ * recompute-decode loop, or the single-launch dgrad kernel that engines/fast.py:426-452 selects
+ * with `dgrad_kernel=True` (grouped-nf4-gemm >= 0.7.0, external). */
+int e4b_grouped_dgrad(const void* grad, int32_t grad_dtype, const e4b_qweight* w, const e4b_routing* rt, int64_t M,
+                      float* out, hipStream_t stream);
+
 /* Decode path, first half: routing of top_k_index recomputed on the device (no route launch),
  * gate_up GEMV with the fused epilogue. h is [tokens * top_k, h_cols] in act_dtype, row
  * t * top_k + s holding token t's activation for slot s (flat order, not expert order).
