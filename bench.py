@@ -11,7 +11,8 @@ and weights are resident in HBM when the timed region starts.
 3,538,944 bytes (packed NF4 + fp32 absmax, both projections) counted once per layer. The line
 also carries us/layer and tok/s at batches 1, 8 and 64, the Qwen3-30B-A3B-geometry 4096-token
 Zipf prefill in TFLOP/s, the Qwen3-geometry double-quant decode at batches 1, 32
-and 256 and the gpt-oss MXFP4 layer at 1 and 2048 tokens, the
+and 256, the gpt-oss MXFP4 layer at 1 and 2048 tokens, the
+ExpertsLoRA decode step and training step (forward + backward, grouped dgrad TFLOP/s), the
 dominant kernel's roofline measured with HIP events on the launch stream, and the reference
 per-expert loop timed on the host CPU.
 
@@ -433,6 +434,83 @@ def extra_benches(steps, warmup, qwen_layers=8, gptoss_layers=4):
     return out
 
 
+def train_bench(steps, warmup, tokens=2048, rank=16, ref_steps=3):
+    """The training lane on one OLMoE-geometry layer (E=64, H=2048, I=1024, top-8): ExpertsLoRA
+    with rank-16 fp32 adapters (B nonzero), a 2048-token micro-batch, loss = sum(out * fixed
+    weights). Times the fused forward + backward (enable_fast_train) and the module's reference
+    per-expert loop (same GPU, same module) with events, and the grouped dgrad of each projection
+    alone: algorithmic FLOP 2 * M * n * k per launch / its average time, against the dense bf16
+    peak."""
+    import torch
+
+    import experts4bit_qlora_amd as e4b
+    from experts4bit_qlora_amd import fast as F
+    from experts4bit_qlora_amd import ops
+
+    cfg = OLMOE
+    base = make_layer(cfg, seed=4242)
+    mod = e4b.ExpertsLoRA(base, r=rank, alpha=2 * rank, dtype=torch.float32).to("cuda").train()
+    g = torch.Generator(device="cuda").manual_seed(4243)
+    with torch.no_grad():
+        for p in (mod.gate_up_lora_B, mod.down_lora_B):
+            p.copy_(torch.randn(p.shape, generator=g, device="cuda") * 0.02)
+    x, idx, w = make_inputs(cfg, tokens, seed=4244)
+    loss_w = torch.randn(tokens, cfg["H"], generator=g, device="cuda")
+
+    def step():
+        xs = x.detach().requires_grad_(True)
+        for p in mod.parameters():
+            p.grad = None
+        (mod(xs, idx, w).float() * loss_w).sum().backward()
+
+    def timed(n_steps, n_warm):
+        for _ in range(n_warm):
+            step()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(n_steps):
+            step()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / n_steps
+
+    ref_ms = timed(ref_steps, 1)
+    assert e4b.enable_fast_train(mod) == 1
+    fused_ms = timed(steps, warmup)
+
+    # the dgrad launches alone, on the routing the lane builds
+    E, H, I, k = cfg["E"], cfg["H"], cfg["I"], cfg["k"]
+    M = tokens * k
+    w1, w2 = F._qweights(base)
+    rb = ops.route(idx, E, tile_m=128 if M >= 64 * min(E, M) else 32)
+    dg = {}
+    for name, qw, n_, k_ in (("gate_up", w1, 2 * I, H), ("down", w2, H, I)):
+        gr = torch.randn(M, n_, generator=g, device="cuda").to(torch.bfloat16)
+        for _ in range(warmup):
+            ops.grouped_dgrad(gr, qw, rb, M)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            ops.grouped_dgrad(gr, qw, rb, M)
+        end.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1e3 / steps
+        flop = 2 * M * n_ * k_
+        tf = flop / (us * 1e-6) / 1e12
+        dg[name] = {"avg_launch_us": round(us, 1), "flop_per_launch": flop, "achieved": round(tf, 1),
+                    "unit": "TFLOP/s", "peak": BF16_PEAK_TFLOPS, "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+    e4b.disable_fast_train(mod)
+    return {"workload": f"1 OLMoE-geometry layer, {tokens} tokens x top-{k}, ExpertsLoRA r={rank} fp32 adapters, "
+                        "forward + backward (dL/dx and every adapter gradient)",
+            "fused_ms": round(fused_ms, 3), "reference_loop_ms": round(ref_ms, 3),
+            "speedup_vs_reference_loop": round(ref_ms / fused_ms, 2),
+            "reference": "the module's reference forward (per-expert dequantize + linear loop, torch autograd) on "
+                         f"the same GPU, {ref_steps} steps",
+            "dgrad": dg}
+
+
 def cpu_baseline(mod, cfg, budget_s=20.0):
     """The reference per-expert loop (the oracle's torch-CPU restatement of ExpertsNbit.forward)
     on the host cores, one OLMoE layer at batch 1, same weights and inputs."""
@@ -495,6 +573,7 @@ def main():
                     "configs[4] (gpt-oss MXFP4)")
     ap.add_argument("--kernel-only", action="store_true", help="only the dominant-kernel loop (for profiling)")
     ap.add_argument("--prefill-only", action="store_true", help="only the configs[3] prefill (for profiling)")
+    ap.add_argument("--train-only", action="store_true", help="only the training-lane leg (for profiling)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for counter runs: the dominant kernel eagerly once per layer, then a 256 MiB "
                          "device copy whose counter reading calibrates bytes per counted KiB")
@@ -515,6 +594,9 @@ def main():
     N.lib()  # fail loudly if the kernel library is missing
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_bench(args.steps, args.warmup)}), flush=True)
+        return
+    if args.train_only:
+        print(json.dumps({"train": train_bench(args.steps, args.warmup)}), flush=True)
         return
     cfg = OLMOE
     log("building 16 OLMoE-geometry NF4 layers")
@@ -547,9 +629,12 @@ def main():
         prefill = prefill_bench(args.steps, args.warmup)
 
     extra = None
+    train = None
     if not args.no_extra:
         log("configs[2] Qwen3 double-quant decode and configs[4] gpt-oss MXFP4")
         extra = extra_benches(args.steps, args.warmup)
+        log("training lane: ExpertsLoRA forward + backward, 2048 tokens")
+        train = train_bench(args.steps, args.warmup)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -588,6 +673,8 @@ def main():
         line["prefill"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in prefill.items()}
     if extra is not None:
         line["extra"] = extra
+    if train is not None:
+        line["train"] = train
     print(json.dumps(line), flush=True)
 
 
