@@ -9,6 +9,7 @@ static positional-signature contract (``tests/test_fast_staging_composition.py``
 import ast
 import inspect
 import io
+import os
 
 import numpy as np
 import pytest
@@ -91,6 +92,32 @@ def test_state_dict_round_trip(dq):
     idx = torch.randint(0, 4, (5, 2))
     w = torch.rand(5, 2).to(torch.bfloat16)
     assert torch.equal(m(x, idx, w), m2(x, idx, w))
+
+
+CHECKPOINT = os.path.join(os.path.dirname(__file__), "golden", "expertsnbit_nf4_checkpoint.pt")
+
+
+@pytest.mark.parametrize("tensors_only", [False, True])
+def test_reference_format_checkpoint_loads_and_decodes(tensors_only):
+    """A state_dict in the reference's on-disk format (tests/golden/make_checkpoint.py, written
+    from the format definition of _vendor/experts.py:236-327, not by this package) loads under
+    strict=True, with its _extra_state or without it (a tensors-only / safetensors save), and the
+    module's reference forward matches the fixture's fp64 expectation to bf16 accuracy."""
+    d = torch.load(CHECKPOINT, weights_only=True)
+    sd = dict(d["state_dict"])
+    if tensors_only:
+        sd = {k: v for k, v in sd.items() if not k.endswith("_extra_state")}
+    m = e4b.Experts4bit(4, 128, 64, quant_type="nf4", compute_dtype=torch.bfloat16)
+    m.load_state_dict(sd, strict=True)
+    assert torch.equal(m.gate_up_proj, d["state_dict"]["gate_up_proj"])
+    assert torch.equal(m.down_absmax, d["state_dict"]["down_absmax"])
+    with torch.no_grad():
+        out = m(d["x"], d["top_k_index"], d["top_k_weights"]).double()
+    exp = d["expected"]
+    assert ((out - exp).norm() / exp.norm()).item() < 1e-2
+    # a module of another construction refuses the metadata
+    with pytest.raises(ValueError, match="intermediate_dim|hidden_dim"):
+        e4b.Experts4bit(4, 128, 128, quant_type="nf4").set_extra_state(d["state_dict"]["_extra_state"])
 
 
 def test_extra_state_rejects_a_different_scheme_and_accepts_legacy():
