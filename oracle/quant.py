@@ -105,7 +105,10 @@ def double_quant_absmax(absmax, blocksize2: int = 256, code2=None):
 
     ``offset`` is the mean of the absmax (accumulated in fp64, stored fp32); the centred values
     are quantized blockwise (``blocksize2`` per block) to the nearest entry of the signed
-    dynamic map after scaling by ``1/absmax2``. PARITY UNPINNED vs bitsandbytes (not importable).
+    dynamic map after scaling by ``1/absmax2``. Input generation only: bitsandbytes' own double
+    quantizer (not importable here) may pick other bytes for the same absmax, which does not
+    matter for parity -- that is defined per given bytes, and the decode of (codes, absmax2,
+    offset, code2) is pinned.
     """
     if code2 is None:
         code2 = dynamic_map_signed()
