@@ -6,17 +6,21 @@
 //                      reduction runs over the weight's OUTPUT features, so the weights are read
 //                      along their rows' k axis and transposed while they are decoded into LDS:
 //                      each thread decodes a 4 (n) x 8 (k) block -- 4 row words of packed bytes,
-//                      one scale per row -- and stores it as 8 k-rows of 4 n-values, the layout
+//                      one scale per row, in registers -- pairs its rows per k column with
+//                      v_perm, and stores it as 8 k-rows of 4 n-values, the layout
 //                      the MFMA B fragments read (k-rows of 64 reduction values, the same XOR
 //                      swizzle as the forward GEMM). Every weight is dt(fp32(code * scale)), the
 //                      forward's dequantized value; the gradient rows are the A operand as loaded;
 //                      v_mfma_f32_16x16x32 with fp32 accumulators; two register stages of global
-//                      loads ahead of the MFMAs, double-buffered LDS, one barrier per 64-deep step.
+//                      loads ahead of the MFMAs, double-buffered LDS, one barrier per 64-deep step,
+//                      the decode of step s + 1 interleaved with the MFMAs of step s.
 //   lora_wgrad_kernel  out[e, j, c] = scale * sum over expert e's rows m of u[m, j] * a_m[c] (in
 //                      row order): dL/dA = scaling * (g . B)^T . x and dL/dB^T = scaling * t^T . g
 //                      of a LoRA projection, per expert. Block (expert, 256 columns); the rows'
 //                      u entries are staged in LDS 32 at a time and broadcast to the block.
 #pragma once
+
+#include <type_traits>
 
 #include "common.h"
 #include "gemm.h"
@@ -50,7 +54,6 @@ __global__ void __launch_bounds__(dgrad_threads(BM)) dgrad_mfma_kernel(DgradArgs
   constexpr int ST = 2;
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kTileK];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BC * kTileK];
-  __shared__ float code_s[16];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
 
   // XCD-aware order, as the forward GEMM: XCD x takes a contiguous run of row tiles and sweeps
@@ -74,7 +77,9 @@ __global__ void __launch_bounds__(dgrad_threads(BM)) dgrad_mfma_kernel(DgradArgs
   const int row0 = p.rt.tiles[2 * tile + 1];
   const int row_end = min(row0 + BM, p.rt.offsets[e + 1]);
 
-  if (tid < 16) code_s[tid] = p.w.code[tid];
+  float code[16];  // the same in every lane
+#pragma unroll
+  for (int i = 0; i < 16; ++i) code[i] = p.w.code[i];
   if constexpr (FMT == E4B_FMT_NF4_DQ) {
     if (tid < 256) code2_s[tid] = p.w.code2[tid];
   }
@@ -140,53 +145,93 @@ __global__ void __launch_bounds__(dgrad_threads(BM)) dgrad_mfma_kernel(DgradArgs
         sc[i] = prod + offset;
       }
     }
-    // column j of the block: byte j / 2 of each row word, the first element in the high nibble
+    // each row word decoded in registers (the forward's byte-plane decode: dt(fp32(code *
+    // scale)), pairs of consecutive k), then rows paired per k column by v_perm: k column 2b
+    // and 2b + 1 of the block take the low / high halves of byte b's pairs of rows (0, 1) and
+    // (2, 3), one 8-byte store each into the k-row's four n values
+    uint32_t wv[4][4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int sh = 8 * (j >> 1) + ((j & 1) ? 0 : 4);
-      float v[4];
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t word[1] = {wq[set][i]};
+      dequant_bytes<DT, FMT, 4>(word, code, sc[i], wv[i]);
+    }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = code_times_scale<DT>(code_s[(wq[set][i] >> sh) & 15u], sc[i]);
-      const int row = wrow + j;
-      const int at = row * kTileK + ((((nq >> 1) ^ row) & 7) << 3) + 4 * (nq & 1);
-      *reinterpret_cast<uint2*>(&Ws[buf][at]) = make_uint2(cvt_pair<DT>(v[0], v[1]), cvt_pair<DT>(v[2], v[3]));
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t lo01 = __builtin_amdgcn_perm(wv[1][b], wv[0][b], 0x05040100u);
+      const uint32_t hi01 = __builtin_amdgcn_perm(wv[1][b], wv[0][b], 0x07060302u);
+      const uint32_t lo23 = __builtin_amdgcn_perm(wv[3][b], wv[2][b], 0x05040100u);
+      const uint32_t hi23 = __builtin_amdgcn_perm(wv[3][b], wv[2][b], 0x07060302u);
+      const int r0 = wrow + 2 * b, r1 = r0 + 1;
+      const int g = 4 * (nq & 1);
+      *reinterpret_cast<uint2*>(&Ws[buf][r0 * kTileK + ((((nq >> 1) ^ r0) & 7) << 3) + g]) = make_uint2(lo01, lo23);
+      *reinterpret_cast<uint2*>(&Ws[buf][r1 * kTileK + ((((nq >> 1) ^ r1) & 7) << 3) + g]) = make_uint2(hi01, hi23);
     }
   };
   const int fcol0 = ((lane >> 4) ^ (lane & 7)) << 3;
   const int a_frag = (wave_m * 32 + (lane & 15)) * kTileK;
   const int w_frag = (wave_c * WC + (lane & 15)) * kTileK;
-  auto mfma_step = [&](int buf) {
+  // fragments of one 32-deep half step (ks) of LDS buffer buf, and the MFMAs on them
+  auto read_frags = [&](int buf, int ks, uint4 (&av)[MS], uint4 (&bv)[NS]) {
+    const int fcol = ks ? fcol0 ^ 32 : fcol0;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int fcol = ks ? fcol0 ^ 32 : fcol0;
-      uint4 av[MS], bv[NS];
+    for (int ms = 0; ms < MS; ++ms)
+      av[ms] = *reinterpret_cast<const uint4*>(&As[buf][a_frag + ms * 16 * kTileK + fcol]);
 #pragma unroll
-      for (int ms = 0; ms < MS; ++ms)
-        av[ms] = *reinterpret_cast<const uint4*>(&As[buf][a_frag + ms * 16 * kTileK + fcol]);
+    for (int ns = 0; ns < NS; ++ns)
+      bv[ns] = *reinterpret_cast<const uint4*>(&Ws[buf][w_frag + ns * 16 * kTileK + fcol]);
+  };
+  auto mfmas = [&](const uint4 (&av)[MS], const uint4 (&bv)[NS]) {
 #pragma unroll
-      for (int ns = 0; ns < NS; ++ns)
-        bv[ns] = *reinterpret_cast<const uint4*>(&Ws[buf][w_frag + ns * 16 * kTileK + fcol]);
+    for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-      for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-        for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = mfma_16x16x32<DT>(av[ms], bv[ns], acc[ms][ns]);
-    }
+      for (int ns = 0; ns < NS; ++ns) acc[ms][ns] = mfma_16x16x32<DT>(av[ms], bv[ns], acc[ms][ns]);
   };
 
+  // Step s (LDS buffer and register set u = s % 2, both compile-time in the unrolled loop), in
+  // two scheduling blocks around its one barrier, as the forward GEMM: the MFMAs of half step 0
+  // with the decode and staging of step s + 1 (into the other buffer) and the refill of set u
+  // with step s + 2 spread between them; after the barrier, the MFMAs of half step 1 while step
+  // s + 1's first fragments are read. Step indices past the last are clamped (unused re-reads).
   const int64_t steps = n / kTileK;
   const int64_t last = steps - 1;
+  constexpr int kMf = MS * NS;
+  constexpr int kDsRead = (MS + NS + kMf - 1) / kMf;  // fragment reads per MFMA
+  constexpr int kValu = 240 / kMf;
+  uint4 fa0[MS], fb0[NS], fa1[MS], fb1[NS];
   load_step(0, 0);
   load_step(1, min<int64_t>(1, last));
-  __syncthreads();  // code tables
+  __syncthreads();  // code2 table
   stage(0, 0);
   __syncthreads();
-  for (int64_t s = 0; s < steps; ++s) {
-    const int cur = static_cast<int>(s & 1);
-    load_step(cur, min<int64_t>(s + 2, last));  // set cur held step s, staged already
-    mfma_step(cur);
-    stage(cur ^ 1, cur ^ 1);  // step s + 1 (a stale re-read after the last step, unused)
+  read_frags(0, 0, fa0, fb0);
+  auto iteration = [&](auto uc, int64_t s) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+    read_frags(u, 1, fa1, fb1);
+    mfmas(fa0, fb0);
+    stage(u ^ 1, u ^ 1);
+#pragma unroll
+    for (int i = 0; i < kMf; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, kDsRead, 0);  // LDS reads
+      __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);    // VALU
+    }
+    load_step(u, min<int64_t>(s + 2, last));
     __syncthreads();
+    read_frags(u ^ 1, 0, fa0, fb0);
+    mfmas(fa1, fb1);
+#pragma unroll
+    for (int i = 0; i < kMf; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int64_t s = 0;
+  for (; s + 2 <= steps; s += 2) {
+    iteration(std::integral_constant<int, 0>{}, s);
+    iteration(std::integral_constant<int, 1>{}, s + 1);
   }
+  if (s < steps) iteration(std::integral_constant<int, 0>{}, s);
 
   // lane holds D[4 * (lane / 16) + i][lane % 16] of each 16 x 16 sub-tile
   const int64_t cbase = c0 + wave_c * WC + (lane & 15);
