@@ -93,13 +93,21 @@ __global__ void __launch_bounds__(dgrad_threads(BM)) dgrad_mfma_kernel(DgradArgs
 
   // weight block: rows 4 * nq .. 4 * nq + 3 of the step, columns c0 + 8 * cg .. + 7 (one packed
   // word per row, inside one 64-column scale block); columns past k read column 0 (never stored)
-  const int nq = tid % NQ;
-  const int cg = tid / NQ;
+  // lane l of wave w: column group (l & 7) + 8 * (w % CGW), row quad (l >> 3) + 8 * (w / CGW), so a
+  // load instruction reads 32 contiguous bytes of each of 8 rows
+  constexpr int CGW = BC / 64;  // waves across the column groups
+  const int cg = (lane & 7) + 8 * (wid % CGW);
+  const int nq = (lane >> 3) + 8 * (wid / CGW);
   const int64_t cc = (c0 + 8 * cg < K) ? c0 + 8 * cg : 0;
   const uint8_t* wbase = p.w.packed + int64_t(e) * n * (K / 2) + cc / 2;
   const int64_t nb = n * (K / 64);  // scale blocks per expert
   const int64_t cblk = cc / 64;
   const float offset = (FMT == E4B_FMT_NF4_DQ) ? p.w.offset[e] : 0.0f;
+  // The weight tile's LDS layout: k-rows of 64 n values, the 16-byte group of n-group ng stored
+  // at ng ^ (row & 7) ^ ((row >> 3) & 7). The extra term makes the staging stores -- eight
+  // column groups of one n-quad, rows 8 apart -- land in distinct banks, and the fragment reads
+  // (16 consecutive rows) stay conflict-free.
+  auto w_at = [](int row, int ng) { return row * kTileK + (((ng ^ row ^ (row >> 3)) & 7) << 3); };
 
   f32x4_t acc[MS][NS];
 #pragma unroll
@@ -163,13 +171,20 @@ __global__ void __launch_bounds__(dgrad_threads(BM)) dgrad_mfma_kernel(DgradArgs
       const uint32_t hi23 = __builtin_amdgcn_perm(wv[3][b], wv[2][b], 0x07060302u);
       const int r0 = wrow + 2 * b, r1 = r0 + 1;
       const int g = 4 * (nq & 1);
-      *reinterpret_cast<uint2*>(&Ws[buf][r0 * kTileK + ((((nq >> 1) ^ r0) & 7) << 3) + g]) = make_uint2(lo01, lo23);
-      *reinterpret_cast<uint2*>(&Ws[buf][r1 * kTileK + ((((nq >> 1) ^ r1) & 7) << 3) + g]) = make_uint2(hi01, hi23);
+      *reinterpret_cast<uint2*>(&Ws[buf][w_at(r0, nq >> 1) + g]) = make_uint2(lo01, lo23);
+      *reinterpret_cast<uint2*>(&Ws[buf][w_at(r1, nq >> 1) + g]) = make_uint2(hi01, hi23);
     }
   };
   const int fcol0 = ((lane >> 4) ^ (lane & 7)) << 3;
   const int a_frag = (wave_m * 32 + (lane & 15)) * kTileK;
+  // B fragment rows wave_c * WC + 16 * ns + (lane & 15): the swizzle term of row r is
+  // g ^ (r & 7) ^ ((r >> 3) & 7), and (r >> 3) & 7 = g1 ^ (2 * ns & 7) with the lane's
+  // g1 = ((wave_c * WC) / 8 + (lane & 15) / 8) & 7: for these tile shapes (WC a multiple of 32)
+  // g1 has no bit 1 and 2 * ns no bit 0, so their sum mod 8 is their XOR (a carry out of bit 2
+  // is dropped) -- four XOR terms per half step, not one address per fragment.
+  static_assert(WC % 32 == 0, "fragment swizzle terms");
   const int w_frag = (wave_c * WC + (lane & 15)) * kTileK;
+  const int g1 = (((wave_c * WC) >> 3) + ((lane & 15) >> 3)) & 7;
   // fragments of one 32-deep half step (ks) of LDS buffer buf, and the MFMAs on them
   auto read_frags = [&](int buf, int ks, uint4 (&av)[MS], uint4 (&bv)[NS]) {
     const int fcol = ks ? fcol0 ^ 32 : fcol0;
@@ -178,7 +193,8 @@ __global__ void __launch_bounds__(dgrad_threads(BM)) dgrad_mfma_kernel(DgradArgs
       av[ms] = *reinterpret_cast<const uint4*>(&As[buf][a_frag + ms * 16 * kTileK + fcol]);
 #pragma unroll
     for (int ns = 0; ns < NS; ++ns)
-      bv[ns] = *reinterpret_cast<const uint4*>(&Ws[buf][w_frag + ns * 16 * kTileK + fcol]);
+      bv[ns] = *reinterpret_cast<const uint4*>(
+          &Ws[buf][w_frag + ns * 16 * kTileK + ((((lane >> 4) + 4 * ks) ^ (lane & 7) ^ g1 ^ ((2 * ns) & 7)) << 3)]);
   };
   auto mfmas = [&](const uint4 (&av)[MS], const uint4 (&bv)[NS]) {
 #pragma unroll
