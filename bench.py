@@ -46,8 +46,8 @@ GPTOSS = dict(E=32, H=2880, I=2880, k=4)
 MEASURED_TRAFFIC = {
     "decode_up_kernel<bf16, nf4, G=16, CPL=4, full, gated>": 18_881_000,
     "decode_down_kernel<bf16, nf4, G=32, CPL=1, JOBS=1, full>": 9_707_000,
-    # profiles/prefill_qwen3_4096_zipf.txt: 296.81 MB read + 50.18 MB written per dispatch
-    "void e4b::gemm_mfma_kernel<0, 1, 128, 2>": 346_990_000,
+    # prefill: keyed by the kernel and the projection ("<kernel> gate_up_256row"); measured
+    # again for each kernel change (profiles/prefill_qwen3_4096_zipf.txt)
 }
 
 
@@ -265,8 +265,10 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
 def prefill_gemm_roofline(mod, x, idx, w, cfg):
     """The prefill's GEMM launches (fp16 matrix-core mode) timed by the device tracer over five
     eager forwards: algorithmic FLOP of each launch (the rows its tiles hold, both gate_up halves)
-    / its average duration, against the dense bf16/fp16 peak. The 128-row tiles carry every
-    expert's rows except a last tile of at most 32 rows, which the 32-row launch takes."""
+    / its average duration, against the dense bf16/fp16 peak. The 256-row tiles
+    (gemm_wide_kernel) carry every expert's rows except a last tile of at most 32 rows, which the
+    32-row launch (gemm_mfma_kernel) takes; each forward runs gate_up then down with each kernel,
+    so a kernel's calls alternate between the two projections in time order."""
     import collections
 
     import torch
@@ -274,10 +276,10 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg):
 
     H, I = cfg["H"], cfg["I"]
     counts = torch.bincount(idx.reshape(-1), minlength=cfg["E"]).cpu().tolist()
-    tail = [c % 128 if 0 < c % 128 <= 32 else 0 for c in counts]
-    rows = {128: sum(counts) - sum(tail), 32: sum(tail)}
-    flop = {(128, "gate_up"): 2 * rows[128] * 2 * I * H, (128, "down"): 2 * rows[128] * H * I,
-            (32, "gate_up"): 2 * rows[32] * 2 * I * H, (32, "down"): 2 * rows[32] * H * I}
+    tail = [c % 256 if 0 < c % 256 <= 32 else 0 for c in counts]
+    rows = {256: sum(counts) - sum(tail), 32: sum(tail)}
+    flop = {(bm, "gate_up"): 2 * r * 2 * I * H for bm, r in rows.items()}
+    flop.update({(bm, "down"): 2 * r * H * I for bm, r in rows.items()})
     with torch.no_grad():
         mod(x, idx, w)
         torch.cuda.synchronize()
@@ -285,17 +287,19 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg):
             for _ in range(5):
                 mod(x, idx, w)
             torch.cuda.synchronize()
-    durs = collections.defaultdict(list)
+    calls = collections.defaultdict(list)
     for ev in prof.events():
-        if ev.device_type == torch.autograd.DeviceType.CUDA and "gemm_mfma_kernel" in ev.name:
+        if ev.device_type == torch.autograd.DeviceType.CUDA and ("gemm_wide_kernel" in ev.name or
+                                                                 "gemm_mfma_kernel" in ev.name):
             t = getattr(ev, "device_time", None)
-            durs[ev.name.split("(")[0]].append(t if t is not None else ev.cuda_time)
+            calls[ev.name.split("(")[0]].append((ev.time_range.start, t if t is not None else ev.cuda_time))
+    durs = collections.defaultdict(list)
+    for name, cs in calls.items():
+        bm = 256 if "gemm_wide_kernel" in name else int(name[name.index("<") + 1:name.index(">")].split(",")[2])
+        for i, (_, d) in enumerate(sorted(cs)):
+            durs[(name, bm, "gate_up" if i % 2 == 0 else "down")].append(d)
     out = {}
-    for name, d in durs.items():
-        # gemm_mfma_kernel<DT, FMT, BM, F16>: F16 2 = gate_up (tokens staged as scaled fp16), 1 = down
-        args = name[name.index("<") + 1:name.index(">")].split(",")
-        bm, f16 = int(args[2]), int(args[3])
-        proj = "gate_up" if f16 == 2 else "down"
+    for (name, bm, proj), d in durs.items():
         us = sum(d) / len(d)
         tf = flop[(bm, proj)] / (us * 1e-6) / 1e12
         out[f"{proj}_{bm}row"] = {"kernel": name, "avg_launch_us": round(us, 2), "calls": len(d),
@@ -303,10 +307,11 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg):
                                   "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
     if not out:
         return None
-    dom = max(out.values(), key=lambda v: v["avg_launch_us"])
-    return {"bound": "mfma", "kernel": dom["kernel"] + " (dominant prefill GEMM)", "achieved": dom["achieved"],
-            "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"],
-            "traffic": MEASURED_TRAFFIC.get(dom["kernel"]),
+    dom_key = max(out, key=lambda key: out[key]["avg_launch_us"])
+    dom = out[dom_key]
+    return {"bound": "mfma", "kernel": f"{dom['kernel']} ({dom_key.rsplit('_', 1)[0]}, dominant prefill GEMM)",
+            "achieved": dom["achieved"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"],
+            "traffic": MEASURED_TRAFFIC.get(f"{dom['kernel']} {dom_key}"),
             "flop_per_launch": dom["flop_per_launch"], "avg_launch_us": dom["avg_launch_us"],
             "timer": "device tracer (torch.profiler), 5 eager forwards", "launches": out}
 

@@ -1,9 +1,9 @@
 """In-tree build of ``libe4b_amd.so`` for gfx950 with ``hipcc`` (no cmake, no JIT cache).
 
 ``python -m experts4bit_qlora_amd._build`` (or ``__graft_entry__.build()``) compiles
-``csrc/e4b_amd.hip`` (entry points and the routing / dequant / grouped-GEMM kernels) and
-``csrc/decode_inst.hip`` once per (activation dtype, weight format) pair, all in parallel, then
-links them into ``experts4bit_qlora_amd/libe4b_amd.so``. The output is written to a temporary
+``csrc/e4b_amd.hip`` (entry points and the routing / dequant / GEMV / LoRA / training kernels),
+and ``csrc/decode_inst.hip`` and ``csrc/gemm_inst.hip`` once per (activation dtype, weight format)
+pair, all in parallel, then links them into ``experts4bit_qlora_amd/libe4b_amd.so``. The output is written to a temporary
 name and renamed, so a failed build never leaves a half-written library behind.
 """
 from __future__ import annotations
@@ -18,6 +18,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(_HERE, "csrc")
 SRC = os.path.join(CSRC, "e4b_amd.hip")
 DECODE_SRC = os.path.join(CSRC, "decode_inst.hip")
+GEMM_SRC = os.path.join(CSRC, "gemm_inst.hip")
 INCLUDE = os.path.join(os.path.dirname(_HERE), "include")
 # (E4B_INST_DT, E4B_INST_FMT): bf16/fp16 x NF4/NF4_DQ/MXFP4
 DECODE_PAIRS = [(dt, fmt) for dt in (0, 1) for fmt in (0, 1, 2)]
@@ -72,6 +73,10 @@ def build(verbose: bool = False) -> str:
             obj = os.path.join(tmpdir, f"decode_{dt}_{fmt}.o")
             cmds.append([cc, *FLAGS, *inc, f"-DE4B_INST_DT={dt}", f"-DE4B_INST_FMT={fmt}", "-c", "-o", obj,
                          DECODE_SRC])
+            objs.append(obj)
+            obj = os.path.join(tmpdir, f"gemm_{dt}_{fmt}.o")
+            cmds.append([cc, *FLAGS, *inc, f"-DE4B_INST_DT={dt}", f"-DE4B_INST_FMT={fmt}", "-c", "-o", obj,
+                         GEMM_SRC])
             objs.append(obj)
         msgs = _run_all(cmds)
         tmp = OUT + ".tmp"

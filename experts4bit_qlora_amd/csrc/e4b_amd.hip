@@ -21,6 +21,7 @@
 #include "dequant.h"
 #include "gather.h"
 #include "gemm.h"
+#include "gemm_launch.h"
 #include "gemv.h"
 #include "lora.h"
 #include "route.h"
@@ -198,46 +199,17 @@ void launch_gemv_fmt(const e4b::GemmArgs& a, int64_t max_active, hipStream_t s) 
   }
 }
 
-// One tile height; the fp16 mode (a.a_exp set) exists for bf16 activations with NF4 weights.
-template <int DT, int FMT, int BM>
-void launch_mfma_bm(const e4b::GemmArgs& a, dim3 grid, hipStream_t s) {
-  if constexpr (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4) {
-    if (a.a_exp && a.a_f16) {
-      hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, BM, 2>), grid, dim3(e4b::gemm_threads(BM)), 0, s, a);
-      return;
-    }
-    if (a.a_exp) {
-      hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, BM, 1>), grid, dim3(e4b::gemm_threads(BM)), 0, s, a);
-      return;
-    }
-  }
-  hipLaunchKernelGGL((e4b::gemm_mfma_kernel<DT, FMT, BM, 0>), grid, dim3(e4b::gemm_threads(BM)), 0, s, a);
-}
-
-template <int DT, int FMT>
-void launch_mfma_fmt(const e4b::GemmArgs& a, hipStream_t s) {
-  const bool pair = a.epi == E4B_EPI_SWIGLU || a.epi == E4B_EPI_CLAMP_SWIGLU || a.epi == E4B_EPI_GPTOSS;
-  const int64_t nw = e4b::gemm_tile_nw(a.rt.tile_m);
-  const int64_t cols = pair ? nw / 2 : nw;
-  // 8 XCDs x ceil(max_tiles / 8) M tiles x n_tiles blocks, mapped to tiles in the kernel
-  const int64_t n_tiles = cdiv(a.n_out, cols);
-  dim3 grid(static_cast<unsigned>(e4b::kXcds * cdiv(a.rt.max_tiles, e4b::kXcds) * n_tiles));
-  if (a.rt.tile_m == e4b::kTileMSmall) launch_mfma_bm<DT, FMT, e4b::kTileMSmall>(a, grid, s);
-  else if (a.rt.tile_m == e4b::kTileMBig) launch_mfma_bm<DT, FMT, e4b::kTileMBig>(a, grid, s);
-  else launch_mfma_bm<DT, FMT, e4b::kTileM>(a, grid, s);
-}
-
 template <int DT>
 int launch_gemm_dt(const e4b::GemmArgs& a, bool gemv, int64_t max_active, hipStream_t s) {
   switch (a.w.format) {
     case E4B_FMT_NF4:
-      gemv ? launch_gemv_fmt<DT, E4B_FMT_NF4>(a, max_active, s) : launch_mfma_fmt<DT, E4B_FMT_NF4>(a, s);
+      gemv ? launch_gemv_fmt<DT, E4B_FMT_NF4>(a, max_active, s) : e4b::launch_mfma_gemm<DT, E4B_FMT_NF4>(a, s);
       break;
     case E4B_FMT_NF4_DQ:
-      gemv ? launch_gemv_fmt<DT, E4B_FMT_NF4_DQ>(a, max_active, s) : launch_mfma_fmt<DT, E4B_FMT_NF4_DQ>(a, s);
+      gemv ? launch_gemv_fmt<DT, E4B_FMT_NF4_DQ>(a, max_active, s) : e4b::launch_mfma_gemm<DT, E4B_FMT_NF4_DQ>(a, s);
       break;
     default:
-      gemv ? launch_gemv_fmt<DT, E4B_FMT_MXFP4>(a, max_active, s) : launch_mfma_fmt<DT, E4B_FMT_MXFP4>(a, s);
+      gemv ? launch_gemv_fmt<DT, E4B_FMT_MXFP4>(a, max_active, s) : e4b::launch_mfma_gemm<DT, E4B_FMT_MXFP4>(a, s);
       break;
   }
   return check_launch(gemv ? "gemv_kernel" : "gemm_mfma_kernel");
@@ -302,9 +274,9 @@ int mfma_tile_for(int64_t M, int E) {
   return M >= 64 * groups ? e4b::kTileM : e4b::kTileMSmall;
 }
 
-// Prefill re-tiling (split_tiles_kernel): 128-row tiles, except that an expert whose last
+// Prefill re-tiling (split_tiles_kernel): 256-row tiles, except that an expert whose last
 // tile would hold at most 32 rows runs those rows in one 32-row tile.
-int64_t max_big_tiles(int64_t M, int E) { return max_tiles_for(M, E, e4b::kTileM); }
+int64_t max_big_tiles(int64_t M, int E) { return max_tiles_for(M, E, e4b::kTileMBig); }
 int64_t max_small_tiles(int64_t M, int E) { return std::max<int64_t>(1, std::min<int64_t>(E, M)); }
 
 bool is_gated_epi(int epi) {
@@ -945,14 +917,14 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   rt.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rt.max_tiles));
   rt.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
   rt.scratch = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * e4b_route_scratch_ints(M, E)));
-  // Prefill-sized groups on the MFMA path run at two tile heights: 128-row tiles, and one
-  // 32-row tile for an expert whose last tile would hold at most 32 rows (the long Zipf tail
-  // of experts with a handful of rows each). A tile's cost is mostly the decoding of its
-  // expert's weights, which the smaller tile does with a quarter of the MFMA work beside it.
+  // Prefill-sized groups on the MFMA path run at two tile heights: 256-row tiles (the wide
+  // kernel), and one 32-row tile for an expert whose last tile would hold at most 32 rows (the
+  // long Zipf tail of experts with a handful of rows each), whose cost is mostly the decoding
+  // of its expert's weights.
   const bool split = rt.tile_m == e4b::kTileM && flags != E4B_PATH_GEMV;
   e4b_routing rbig = rt, rsmall = rt;
   if (split) {
-    rbig.tile_m = e4b::kTileM;
+    rbig.tile_m = e4b::kTileMBig;
     rbig.max_tiles = static_cast<int32_t>(max_big_tiles(M, E));
     rbig.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rbig.max_tiles));
     rbig.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
@@ -976,13 +948,23 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
 
   rc = e4b_route(top_k_index, tokens, top_k, E, &rt, stream);
   if (rc) return rc;
-  if (f16c) {  // token row exponents and scaled fp16 rows; the h row exponents zeroed
+  if (f16c) {  // token row exponents and scaled fp16 rows
     const int64_t blocks = cdiv(tokens, e4b::kScaleThreads / e4b::kWave);
     hipLaunchKernelGGL(e4b::row_exp_kernel, dim3(static_cast<unsigned>(blocks)), dim3(e4b::kScaleThreads), 0, stream,
-                       static_cast<const uint16_t*>(hidden), tokens, w1->k, xexp, x16, hexp, M);
+                       static_cast<const uint16_t*>(hidden), tokens, w1->k, xexp, x16, nullptr, int64_t(0));
     rc = check_launch("row_exp_kernel");
     if (rc) return rc;
   }
+  // fp16 mode: h row exponents, and h rewritten in place as scaled fp16 rows for the down GEMM
+  auto h_to_f16 = [&]() {
+    if (!f16c) return 0;
+    const int64_t blocks = cdiv(M, e4b::kScaleThreads / e4b::kWave);
+    hipLaunchKernelGGL(e4b::row_exp_kernel, dim3(static_cast<unsigned>(blocks)), dim3(e4b::kScaleThreads), 0, stream,
+                       static_cast<const uint16_t*>(h), M, h_cols, hexp, static_cast<uint16_t*>(h), nullptr,
+                       int64_t(0));
+    return check_launch("row_exp_kernel");
+  };
+  const int down_f16 = f16c ? 1 : 0;
   if (split) {
     hipLaunchKernelGGL(e4b::split_tiles_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, rt.offsets, rt.meta, E,
                        rbig, rsmall);
@@ -990,20 +972,24 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
     if (rc) return rc;
     for (const e4b_routing* r : {&rbig, &rsmall}) {
       rc = grouped_gemm_impl(up_a, act_dtype, top_k, w1, r, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
-                             up_exp, 1, h_exp, stream);
+                             up_exp, 1, nullptr, stream);
       if (rc) return rc;
     }
+    rc = h_to_f16();
+    if (rc) return rc;
     for (const e4b_routing* r : {&rbig, &rsmall}) {
       rc = grouped_gemm_impl(h, act_dtype, 0, w2, r, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
-                             h_exp, 0, nullptr, stream);
+                             h_exp, down_f16, nullptr, stream);
       if (rc) return rc;
     }
   } else {
     rc = grouped_gemm_impl(up_a, act_dtype, top_k, w1, &rt, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
-                           up_exp, 1, h_exp, stream);
+                           up_exp, 1, nullptr, stream);
+    if (rc) return rc;
+    rc = h_to_f16();
     if (rc) return rc;
     rc = grouped_gemm_impl(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
-                           h_exp, 0, nullptr, stream);
+                           h_exp, down_f16, nullptr, stream);
     if (rc) return rc;
   }
   return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,

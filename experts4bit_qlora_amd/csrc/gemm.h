@@ -1,9 +1,9 @@
 // Prefill / large-batch grouped GEMM on the bf16 (fp16) matrix cores of gfx950.
 //
 // One workgroup computes a BM-row x BN-weight-row tile of one expert: 128 x 256 (8 waves) for
-// prefill-sized groups, 32 x 128 (4 waves) for mid-size batches where experts get few rows,
-// 256 x 128 (8 waves) for full 256-row runs. Every dequantized weight feeds BM rows, so the
-// decode work per MFMA falls as BM grows, and every activation tile feeds BN weight rows: its
+// prefill-sized groups, 32 x 128 (4 waves) for mid-size batches where experts get few rows (the
+// 256-row tiles of the fused prefill run gemm_wide_kernel). Every dequantized weight feeds BM
+// rows, so the decode work per MFMA falls as BM grows, and every activation tile feeds BN weight rows: its
 // global (L2) reads repeat once per N tile, so the prefill tile is wide. Tiles come from
 // the route kernel's (expert, first sorted row) list, so skewed expert sizes cost at most one
 // partial tile per expert and the grid never depends on host-side counts.
@@ -62,9 +62,27 @@ constexpr int kTileK = 64;
 E4B_DEV int lds_at(int row, int col) { return row * kTileK + ((((col >> 3) ^ row) & 7) << 3); }
 // K steps of global loads in flight ahead of the MFMAs (6 for the 32-row tiles was measured:
 // no change at bs=64, whose blocks are bound by their decode and LDS work, not by latency).
-// The 128- and 256-row tiles hold two: a third set spills at their 256-register budget.
+// The 128-row tiles hold two: a third set spills at their 256-register budget.
 constexpr int gemm_stages(int bm) { return bm >= kTileM ? 2 : 3; }
 constexpr int kXcds = 8;    // accelerator dies of an MI355X; blocks go round-robin over them
+
+// XCD-aware, balanced block -> (M tile, N tile) map. Workgroups go round-robin over the 8 XCDs
+// (block L runs on XCD L % 8). The num_tiles x n_tiles work items, in (M tile, N tile) order, are
+// cut into 8 runs of equal length, run x for XCD x: every XCD gets the same number of blocks
+// (to within one), and consecutive items -- the N sweep of one M tile (the same activation
+// rows), an expert's consecutive M tiles (the same weights) -- share that XCD's L2. false: the
+// block is past the work (the grid is sized for the routing's max_tiles).
+E4B_DEV bool tile_of_block(int num_tiles, int n_tiles, int& tile, int& n_tile) {
+  const int total = num_tiles * n_tiles;
+  const int per = (total + kXcds - 1) / kXcds;
+  const int xcd = static_cast<int>(blockIdx.x % kXcds);
+  const int q = static_cast<int>(blockIdx.x / kXcds);
+  const int w = xcd * per + q;
+  if (q >= per || w >= total) return false;
+  tile = w / n_tiles;
+  n_tile = w % n_tiles;
+  return true;
+}
 
 template <int DT>
 E4B_DEV f32x4_t mfma_16x16x32(const uint4& a, const uint4& b, const f32x4_t& c) {
@@ -128,63 +146,93 @@ E4B_DEV uint32_t fp4_scaled_pair(uint32_t w, float scale) {
   }
 }
 
+// The 16 entries dt(fp32(code[c] * scale)) of one weight row and step as byte planes: lo[k] /
+// hi[k] hold the low / high bytes of entries 4k .. 4k+3 (16 products, 8 conversions, 8 v_perm).
+struct NibPlanes {
+  uint32_t lo[4], hi[4];
+};
+template <int DT, bool REF = true>
+E4B_DEV NibPlanes nib_planes(const float (&code)[16], float scale) {
+  uint32_t q[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    q[i] = cvt_pair<DT>(code_times_scale<DT, REF>(code[2 * i], scale), code_times_scale<DT, REF>(code[2 * i + 1], scale));
+  NibPlanes t;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    t.lo[k] = __builtin_amdgcn_perm(q[2 * k + 1], q[2 * k], 0x06040200u);
+    t.hi[k] = __builtin_amdgcn_perm(q[2 * k + 1], q[2 * k], 0x07050301u);
+  }
+  return t;
+}
+
+// One packed word (four bytes; byte i = elements 2i and 2i + 1, the first in the high nibble for
+// NF4, in the low one for e2m1) -> four words of DT pairs, looked up in the planes.
+template <int FMT>
+E4B_DEV void nib_word(const NibPlanes& t, uint32_t w, uint32_t (&wv)[4]) {
+  // four nibbles: sel = their low three bits (one per byte), m = 0xff in each byte whose
+  // nibble is 8..15 -> the low and the high bytes of their four entries
+  auto look = [&](uint32_t sel, uint32_t m, uint32_t& l, uint32_t& h) {
+    l = bfi(m, __builtin_amdgcn_perm(t.lo[3], t.lo[2], sel), __builtin_amdgcn_perm(t.lo[1], t.lo[0], sel));
+    h = bfi(m, __builtin_amdgcn_perm(t.hi[3], t.hi[2], sel), __builtin_amdgcn_perm(t.hi[1], t.hi[0], sel));
+  };
+  // v_perm selectors 8..11 replicate bit 15 / 31 of either source into a whole byte; the
+  // nibbles' bit 3 are shifted there: low nibbles (w bits 3, 11, 19, 27) and high nibbles
+  // (w bits 7, 15, 23, 31)
+  const uint32_t sel_l = w & 0x07070707u, sel_h = (w >> 4) & 0x07070707u;
+  const uint32_t m_l = __builtin_amdgcn_perm(w << 4, w << 12, 0x0B090A08u);
+  const uint32_t m_h = __builtin_amdgcn_perm(w, w << 8, 0x0B090A08u);
+  uint32_t lf, hf, ls, hs;
+  if constexpr (FMT == E4B_FMT_MXFP4) {
+    look(sel_l, m_l, lf, hf);  // first elements: low nibbles
+    look(sel_h, m_h, ls, hs);
+  } else {
+    look(sel_h, m_h, lf, hf);  // first elements: high nibbles
+    look(sel_l, m_l, ls, hs);
+  }
+  const uint32_t f01 = __builtin_amdgcn_perm(hf, lf, 0x05010400u), f23 = __builtin_amdgcn_perm(hf, lf, 0x07030602u);
+  const uint32_t s01 = __builtin_amdgcn_perm(hs, ls, 0x05010400u), s23 = __builtin_amdgcn_perm(hs, ls, 0x07030602u);
+  wv[0] = __builtin_amdgcn_perm(s01, f01, 0x05040100u);
+  wv[1] = __builtin_amdgcn_perm(s01, f01, 0x07060302u);
+  wv[2] = __builtin_amdgcn_perm(s23, f23, 0x05040100u);
+  wv[3] = __builtin_amdgcn_perm(s23, f23, 0x07060302u);
+}
+
+// e2m1: one v_cvt_scalef32_pk_{bf16,f16}_fp4 per byte forms its two values dt(code * scale).
+template <int DT>
+E4B_DEV void fp4_word(uint32_t w, float scale, uint32_t (&wv)[4]) {
+  wv[0] = fp4_scaled_pair<DT, 0>(w, scale);
+  wv[1] = fp4_scaled_pair<DT, 1>(w, scale);
+  wv[2] = fp4_scaled_pair<DT, 2>(w, scale);
+  wv[3] = fp4_scaled_pair<DT, 3>(w, scale);
+}
+
 template <int DT, int FMT, int NB, bool REF = true>
 E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float (&code)[16], float scale, uint32_t (&wv)[NB]) {
   if constexpr (FMT == E4B_FMT_MXFP4) {
 #pragma unroll
     for (int wi = 0; wi < NB / 4; ++wi) {
-      wv[4 * wi + 0] = fp4_scaled_pair<DT, 0>(words[wi], scale);
-      wv[4 * wi + 1] = fp4_scaled_pair<DT, 1>(words[wi], scale);
-      wv[4 * wi + 2] = fp4_scaled_pair<DT, 2>(words[wi], scale);
-      wv[4 * wi + 3] = fp4_scaled_pair<DT, 3>(words[wi], scale);
+      uint32_t o[4];
+      fp4_word<DT>(words[wi], scale, o);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) wv[4 * wi + j] = o[j];
     }
     return;
   }
-  uint32_t q[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i)
-    q[i] = cvt_pair<DT>(code_times_scale<DT, REF>(code[2 * i], scale), code_times_scale<DT, REF>(code[2 * i + 1], scale));
-  uint32_t lo[4], hi[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    lo[k] = __builtin_amdgcn_perm(q[2 * k + 1], q[2 * k], 0x06040200u);
-    hi[k] = __builtin_amdgcn_perm(q[2 * k + 1], q[2 * k], 0x07050301u);
-  }
-  // four nibbles: sel = their low three bits (one per byte), m = 0xff in each byte whose
-  // nibble is 8..15 -> the low and the high bytes of their four entries
-  auto look = [&](uint32_t sel, uint32_t m, uint32_t& l, uint32_t& h) {
-    l = bfi(m, __builtin_amdgcn_perm(lo[3], lo[2], sel), __builtin_amdgcn_perm(lo[1], lo[0], sel));
-    h = bfi(m, __builtin_amdgcn_perm(hi[3], hi[2], sel), __builtin_amdgcn_perm(hi[1], hi[0], sel));
-  };
+  const NibPlanes t = nib_planes<DT, REF>(code, scale);
 #pragma unroll
   for (int wi = 0; wi < NB / 4; ++wi) {
-    const uint32_t w = words[wi];
-    // v_perm selectors 8..11 replicate bit 15 / 31 of either source into a whole byte; the
-    // nibbles' bit 3 are shifted there: low nibbles (w bits 3, 11, 19, 27) and high nibbles
-    // (w bits 7, 15, 23, 31)
-    const uint32_t sel_l = w & 0x07070707u, sel_h = (w >> 4) & 0x07070707u;
-    const uint32_t m_l = __builtin_amdgcn_perm(w << 4, w << 12, 0x0B090A08u);
-    const uint32_t m_h = __builtin_amdgcn_perm(w, w << 8, 0x0B090A08u);
-    uint32_t lf, hf, ls, hs;
-    if constexpr (FMT == E4B_FMT_MXFP4) {
-      look(sel_l, m_l, lf, hf);  // first elements: low nibbles
-      look(sel_h, m_h, ls, hs);
-    } else {
-      look(sel_h, m_h, lf, hf);  // first elements: high nibbles
-      look(sel_l, m_l, ls, hs);
-    }
-    const uint32_t f01 = __builtin_amdgcn_perm(hf, lf, 0x05010400u), f23 = __builtin_amdgcn_perm(hf, lf, 0x07030602u);
-    const uint32_t s01 = __builtin_amdgcn_perm(hs, ls, 0x05010400u), s23 = __builtin_amdgcn_perm(hs, ls, 0x07030602u);
-    wv[4 * wi + 0] = __builtin_amdgcn_perm(s01, f01, 0x05040100u);
-    wv[4 * wi + 1] = __builtin_amdgcn_perm(s01, f01, 0x07060302u);
-    wv[4 * wi + 2] = __builtin_amdgcn_perm(s23, f23, 0x05040100u);
-    wv[4 * wi + 3] = __builtin_amdgcn_perm(s23, f23, 0x07060302u);
+    uint32_t o[4];
+    nib_word<FMT>(t, words[wi], o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wv[4 * wi + j] = o[j];
   }
 }
 
 // Tile shapes: weight rows per tile and threads (8 waves for the 128- and 256-row tiles, else 4).
-constexpr int gemm_tile_nw(int bm) { return bm == kTileM ? kTileNWWide : kTileNW; }
-constexpr int gemm_threads(int bm) { return bm >= kTileM ? 512 : 256; }
+// (The 256-row tiles run gemm_wide_kernel: 256 weight rows, four waves.)
+constexpr int gemm_tile_nw(int bm) { return bm >= kTileM ? kTileNWWide : kTileNW; }
+constexpr int gemm_threads(int bm) { return bm == kTileM ? 512 : 256; }
 
 // F16: 0 = operands in the activation dtype; fp16 mode with A rows converted while staged (1)
 // or already stored as scaled fp16 by row_exp_kernel (2).
@@ -196,7 +244,7 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   constexpr int NT = gemm_threads(BM);
   constexpr int BN = gemm_tile_nw(BM);
   constexpr int WAVES = NT / kWave;
-  constexpr int WAVES_M = BM >= 256 ? 4 : BM >= 128 ? 2 : 1;
+  constexpr int WAVES_M = BM >= 128 ? 2 : 1;
   constexpr int WAVES_N = WAVES / WAVES_M;
   constexpr int WM = BM / WAVES_M;       // rows per wave
   constexpr int WN = BN / WAVES_N;       // weight rows per wave
@@ -205,6 +253,7 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   constexpr int AV = kTileK / TPR / 8;    // uint4 of A per thread per step
   constexpr int TPW = NT / BN;            // threads per weight row
   constexpr int WB = kTileK / 2 / TPW;    // packed weight bytes per thread per step
+  static_assert(BM == kTileM || BM == kTileMSmall, "tile rows: 128 or 32 (256: gemm_wide_kernel)");
   static_assert(AV >= 1 && NS % 2 == 0 && (WB == 16 || WB == 8), "tile shape");
   constexpr int ST = gemm_stages(BM);
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kTileK];
@@ -213,21 +262,11 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   __shared__ int row_shift_s[F16C ? BM : 1];  // fp16 mode: each tile row's activation shift
   __shared__ int hexp_s[F16C ? BM : 1];       // fp16 mode, gate_up: each tile row's h exponent
 
-  // XCD-aware tile order: workgroups are dispatched round-robin over the 8 XCDs, so linear
-  // block L runs on XCD L % 8. XCD x takes the contiguous run of M tiles
-  // [x * chunk, (x + 1) * chunk) and sweeps all N tiles of one M tile before the next: the
-  // activation tile stays in that XCD's L2 across the N sweep, and an expert's consecutive M
-  // tiles (same weights) stay on one XCD as well.
   const int num_tiles = p.rt.meta[0];
   const int n_tiles = static_cast<int>((p.n_out + (is_gated(p.epi) ? BN / 2 : BN) - 1) /
                                        (is_gated(p.epi) ? BN / 2 : BN));
-  const int xcd = static_cast<int>(blockIdx.x % kXcds);
-  const int q = static_cast<int>(blockIdx.x / kXcds);
-  const int chunk = (num_tiles + kXcds - 1) / kXcds;
-  const int m_local = q / n_tiles;
-  const int tile = xcd * chunk + m_local;
-  if (m_local >= chunk || tile >= num_tiles) return;
-  const int n_tile = q % n_tiles;
+  int tile, n_tile;
+  if (!tile_of_block(num_tiles, n_tiles, tile, n_tile)) return;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wid = tid / kWave;

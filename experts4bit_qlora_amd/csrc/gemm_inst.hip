@@ -1,0 +1,63 @@
+// Grouped MFMA GEMM instantiations for one (activation dtype, weight format) pair, selected by
+// -DE4B_INST_DT=<e4b_dtype> -DE4B_INST_FMT=<e4b_format> (the build compiles this file once per
+// pair, in parallel).
+#include "gemm.h"
+#include "gemm_launch.h"
+#include "gemm_wide.h"
+
+#ifndef E4B_INST_DT
+#error "E4B_INST_DT must be defined"
+#endif
+#ifndef E4B_INST_FMT
+#error "E4B_INST_FMT must be defined"
+#endif
+
+namespace e4b {
+
+namespace {
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// 256-row tiles run the wide kernel (four waves of 128 x 128), the others gemm_mfma_kernel.
+template <int DT, int FMT, int BM, int F16>
+void launch_mfma_kernel(const GemmArgs& a, dim3 grid, hipStream_t s) {
+  if constexpr (BM == kTileMBig) {
+    hipLaunchKernelGGL((gemm_wide_kernel<DT, FMT, F16>), grid, dim3(kWideThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((gemm_mfma_kernel<DT, FMT, BM, F16>), grid, dim3(gemm_threads(BM)), 0, s, a);
+  }
+}
+
+// One tile height; the fp16 mode (a.a_exp set) exists for bf16 activations with NF4 weights.
+template <int DT, int FMT, int BM>
+void launch_mfma_bm(const GemmArgs& a, dim3 grid, hipStream_t s) {
+  if constexpr (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4) {
+    if (a.a_exp && a.a_f16) {
+      launch_mfma_kernel<DT, FMT, BM, 2>(a, grid, s);
+      return;
+    }
+    if (a.a_exp) {
+      launch_mfma_kernel<DT, FMT, BM, 1>(a, grid, s);
+      return;
+    }
+  }
+  launch_mfma_kernel<DT, FMT, BM, 0>(a, grid, s);
+}
+
+}  // namespace
+
+template <int DT, int FMT>
+void launch_mfma_gemm(const GemmArgs& a, hipStream_t s) {
+  const int64_t nw = gemm_tile_nw(a.rt.tile_m);
+  const int64_t cols = is_gated(a.epi) ? nw / 2 : nw;
+  // 8 XCDs x ceil(max_tiles / 8) M tiles x n_tiles blocks, mapped to tiles in the kernel
+  const int64_t n_tiles = cdiv(a.n_out, cols);
+  dim3 grid(static_cast<unsigned>(kXcds * cdiv(a.rt.max_tiles, kXcds) * n_tiles));
+  if (a.rt.tile_m == kTileMSmall) launch_mfma_bm<DT, FMT, kTileMSmall>(a, grid, s);
+  else if (a.rt.tile_m == kTileMBig) launch_mfma_bm<DT, FMT, kTileMBig>(a, grid, s);
+  else launch_mfma_bm<DT, FMT, kTileM>(a, grid, s);
+}
+
+template void launch_mfma_gemm<E4B_INST_DT, E4B_INST_FMT>(const GemmArgs&, hipStream_t);
+
+}  // namespace e4b

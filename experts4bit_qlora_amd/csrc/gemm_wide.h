@@ -1,0 +1,457 @@
+// Prefill grouped GEMM, wide tiles: 256 sorted rows x 256 weight rows per workgroup, four waves
+// (one per SIMD) of 128 x 128 each, on v_mfma_f32_32x32x16_{bf16,f16}.
+//
+// The 128 x 256 tile of gemm_mfma_kernel gives each of its eight waves a 64 x 64 block: per
+// 64-deep step a CU then moves 48 KB of staged operands and 128 KB of MFMA fragments through
+// LDS for 2M multiply-adds, and decodes every weight for 128 rows. Here a 128 x 128 wave block
+// halves the fragment bytes per multiply-add (128 KB for 4M), and every decoded weight feeds 256
+// rows, half the decode work. One wave per SIMD holds 256 accumulator registers (AGPRs); the
+// fragments are double-buffered per 16-deep sub-step (2 x 32 registers); global loads run two
+// steps ahead in two register sets.
+//
+// With one wave per SIMD nothing else hides a stall, so the main loop is laid out by hand: each
+// 64-deep step is four 16-deep sub-steps of sixteen MFMAs, cut into chunks of four MFMAs (one
+// accumulator row) by scheduling barriers, with the staging of a later step (a weight word's
+// decode, an activation store) and the global loads placed between them; an MFMA then hides
+// about six VALU instructions of its own wave (measured: 32 cycles per MFMA alone, ~35 with
+// four VALU, ~40 with six, ~49 with eight). Step s + 2 is staged from sub-step 3 of step s into
+// the buffer step s has just released, through sub-steps 0-2 of step s + 1; the activation
+// loads take 128 contiguous bytes per eight lanes (a load with one 16-byte row piece per lane
+// costs the load pipeline about twice the issue time). The decode is that of gemm_mfma_kernel
+// (dequant_bytes' byte-plane lookups, the fp16 matrix-core mode's row and expert shifts), so the
+// two kernels form the same per-element products; only the fp32 summation order differs.
+//
+// The output layout of a 32 x 32 MFMA: lane l holds column l % 32 of rows
+// 8 * (i / 4) + 4 * (l / 32) + i % 4, i = 0..15, of its tile.
+#pragma once
+
+#include <utility>
+
+#include "gemm.h"
+
+namespace e4b {
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): indices known at compile
+// time whatever the unroller decides, so the accumulator array never needs an address (a loop
+// left rolled would put all 256 accumulators in scratch memory).
+template <class F, int... I>
+E4B_DEV void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+E4B_DEV void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+constexpr int kWideThreads = 256;
+constexpr int kWideTileM = kTileMBig;  // sorted rows per tile
+constexpr int kWideTileN = 256;  // weight rows per tile
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// LDS tile layout of this kernel: 128-byte rows of 64 elements, the row's eight 16-byte groups in
+// the order group ^ ((row ^ (row >> 3)) & 7). Measured with SQ_LDS_BANK_CONFLICT on the two
+// access patterns: a 32 x 32 fragment read (32 consecutive rows at one group) and the staging
+// stores (thread t: row t, one group per store) are both conflict-free. (group ^ (row & 7), the
+// layout of gemm_mfma_kernel, costs the fragment reads a 2-way conflict, and group ^ ((row >> 1)
+// & 7) the stores.)
+E4B_DEV int lds_at_w(int row, int col) { return row * kTileK + ((((col >> 3) ^ row ^ (row >> 3)) & 7) << 3); }
+
+template <int DT>
+E4B_DEV f32x16_t mfma_32x32x16(const uint4& a, const uint4& b, const f32x16_t& c) {
+  if constexpr (DT == E4B_BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                  c, 0, 0, 0);
+  }
+}
+
+template <int DT, int FMT, int F16 = 0>
+__global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
+  constexpr bool F16C = F16 != 0;
+  static_assert(!F16C || (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4), "fp16 mode: bf16 activations, NF4 weights");
+  constexpr int CT = F16C ? E4B_FP16 : DT;
+  constexpr int BM = kWideTileM, BN = kWideTileN, NT = kWideThreads;
+  constexpr int MS = 4, NS = 4;  // 32 x 32 MFMA tiles per wave: 128 x 128
+  constexpr int ST = 2;          // register sets of global loads in flight
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kTileK];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kTileK];
+  __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
+  __shared__ int row_shift_s[F16C ? BM : 1];
+  __shared__ int hexp_s[F16C ? BM : 1];
+
+  const int num_tiles = p.rt.meta[0];
+  const bool pair = is_gated(p.epi);
+  const int cols = pair ? BN / 2 : BN;
+  const int n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
+  int tile, n_tile;
+  if (!tile_of_block(num_tiles, n_tiles, tile, n_tile)) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wid = tid / kWave;
+  const int wave_m = wid & 1;
+  const int wave_n = wid >> 1;
+  const int e = p.rt.tiles[2 * tile];
+  const int row0 = p.rt.tiles[2 * tile + 1];
+  const int row_end = min(row0 + BM, p.rt.offsets[e + 1]);
+  const int64_t n = p.w.n;
+  const int64_t k = p.w.k;
+  const int64_t col0 = int64_t(n_tile) * cols;
+  if (col0 >= p.n_out) return;
+
+  float code[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) code[i] = (FMT == E4B_FMT_MXFP4) ? kFp4E2M1[i] : p.w.code[i];
+  if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[tid] = p.w.code2[tid];
+
+  // A: a step's 256 x 64 tile is 2048 16-byte pieces; load i (0..7) of thread t takes tile row
+  // 32 i + t / 8, columns 8 (t % 8) .. + 7, so eight lanes read one row's 128 contiguous bytes
+  // (one lane per row, 16 bytes from each of 64 rows per load, costs the load pipeline about
+  // twice the issue time). aoff[i]: that piece of step 0, in 16-byte units of p.a.
+  const int apart = tid & 7;
+  uint32_t aoff[8];
+  int ash[8];
+  int wsh = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = row0 + 32 * i + (tid >> 3);
+    const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
+    aoff[i] = static_cast<uint32_t>((src * k) / 8 + apart);
+    ash[i] = 0;
+    if constexpr (F16C) ash[i] = exp_shift(p.a_exp[src]);
+  }
+  if constexpr (F16C) {
+    wsh = p.w.shift[e];
+    // row_shift_s: the shift of tile row tid, for the epilogue
+    const int r = row0 + tid;
+    const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
+    row_shift_s[tid] = exp_shift(p.a_exp[src]);
+    hexp_s[tid] = 0;
+  }
+  // W: thread tid stages LDS weight row tid (for a gated epilogue rows 0..127 are the gate rows
+  // of the tile's 128 output columns and rows 128..255 their up rows); rows past n_out read
+  // weight row 0 and feed only columns that are never stored
+  int64_t grow;
+  if (pair) {
+    const int64_t jj = col0 + (tid & (BN / 2 - 1));
+    grow = jj < p.n_out ? ((tid < BN / 2) ? jj : n / 2 + jj) : 0;
+  } else {
+    grow = col0 + tid < p.n_out ? col0 + tid : 0;
+  }
+  const uint8_t* wptr = p.w.packed + (int64_t(e) * n + grow) * (k / 2);
+  const int64_t nb = n * (k / 64);
+  const float offset = (FMT == E4B_FMT_NF4_DQ) ? p.w.offset[e] : 0.0f;
+
+  f32x16_t acc[MS][NS];
+  static_for<MS>([&](auto ms) { static_for<NS>([&](auto ns) { acc[ms][ns] = f32x16_t{}; }); });
+
+  u32x4_t areg[ST][8];
+  uint32_t wq[ST][8];
+  float sa[ST];
+  uint32_t sq[ST];
+  auto load_step = [&](int set, int64_t kb) {
+    const u32x4_t* ap = reinterpret_cast<const u32x4_t*>(p.a) + kb * (kTileK / 8);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) areg[set][i] = ap[aoff[i]];
+    const uint4 v0 = *reinterpret_cast<const uint4*>(wptr + kb * 32);
+    const uint4 v1 = *reinterpret_cast<const uint4*>(wptr + kb * 32 + 16);
+    wq[set][0] = v0.x; wq[set][1] = v0.y; wq[set][2] = v0.z; wq[set][3] = v0.w;
+    wq[set][4] = v1.x; wq[set][5] = v1.y; wq[set][6] = v1.z; wq[set][7] = v1.w;
+    if constexpr (FMT == E4B_FMT_MXFP4) {  // both e8m0 scales of the step (k % 64 == 0: aligned)
+      sq[set] = reinterpret_cast<const uint16_t*>(p.w.absmax)[((int64_t(e) * n + grow) * (k / 32) + kb * 2) / 2];
+    } else if constexpr (FMT == E4B_FMT_NF4) {
+      sa[set] = static_cast<const float*>(p.w.absmax)[e * nb + grow * (k / 64) + kb];
+    } else {
+      const int64_t blk = grow * (k / 64) + kb;
+      sq[set] = static_cast<const uint8_t*>(p.w.absmax)[e * nb + blk];
+      sa[set] = p.w.absmax2[e * ((nb + 255) / 256) + blk / 256];
+    }
+  };
+  // The NF4 block scale of a staged step, formed one sub-step ahead of its staging: the
+  // double-quant scale reads code2 from LDS, and a wait for that read in the staging would also
+  // wait for every fragment read issued before it, holding the decode back behind the MFMAs.
+  auto block_scale = [&](int set) {
+    float scale = 0.0f;
+    if constexpr (FMT == E4B_FMT_NF4) {
+      scale = sa[set];
+    } else if constexpr (FMT == E4B_FMT_NF4_DQ) {
+      const float prod = code2_s[sq[set]] * sa[set];
+      scale = prod + offset;
+    }
+    if constexpr (F16C) scale = __builtin_amdgcn_ldexpf(scale, wsh);
+    return scale;
+  };
+  // Staging of one step, in pieces the main loop spreads over the MFMAs: the activation row
+  // (eight 16-byte stores; converted to scaled fp16 in fp16 mode 1) and the weight row, one
+  // packed word (eight values, one 16-byte store) at a time.
+  auto store_a = [&](int set, int buf, int i) {
+    u32x4_t* as = reinterpret_cast<u32x4_t*>(&As[buf][lds_at_w(32 * i + (tid >> 3), 8 * apart)]);
+    if constexpr (F16 == 1) {
+      const u32x4_t v = areg[set][i];
+      *as = u32x4_t{bf16x2_to_f16x2(v[0], ash[i]), bf16x2_to_f16x2(v[1], ash[i]), bf16x2_to_f16x2(v[2], ash[i]),
+                    bf16x2_to_f16x2(v[3], ash[i])};
+    } else {
+      *as = areg[set][i];
+    }
+  };
+  auto store_w = [&](int set, int buf, int wi, const NibPlanes& t) {
+    uint32_t o[4];
+    if constexpr (FMT == E4B_FMT_MXFP4) {  // words 0-3: the first 32-value block, 4-7: the second
+      fp4_word<CT>(wq[set][wi], e8m0_to_f32(wi < 4 ? (sq[set] & 0xffu) : (sq[set] >> 8)), o);
+    } else {
+      nib_word<FMT>(t, wq[set][wi], o);
+    }
+    *reinterpret_cast<uint4*>(&Ws[buf][lds_at_w(tid, 8 * wi)]) = make_uint4(o[0], o[1], o[2], o[3]);
+  };
+  auto planes = [&](float scale) {
+    if constexpr (FMT == E4B_FMT_MXFP4) return NibPlanes{};
+    else return nib_planes<CT, !F16C>(code, scale);
+  };
+  auto stage = [&](int set, int buf, float scale) {
+    const NibPlanes t = planes(scale);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) store_a(set, buf, i);
+#pragma unroll
+    for (int wi = 0; wi < 8; ++wi) store_w(set, buf, wi, t);
+  };
+  // Fragments of sub-step ks (k = 16 ks .. 16 ks + 15): lane l reads row (base + l % 32), the
+  // eight values at k = 16 ks + 8 (l / 32). Every base is a multiple of 32, so the row's swizzle
+  // term is (l & 7) ^ ((l >> 3) & 3) ^ 4 (base / 32 & 1), and base / 32 & 1 is the parity of the
+  // tile index (ms, or ns: the gate and up halves start at multiples of 64).
+  int nbase[NS];
+#pragma unroll
+  for (int ns = 0; ns < NS; ++ns)
+    nbase[ns] = pair ? ((ns < NS / 2) ? wave_n * 64 + ns * 32 : BN / 2 + wave_n * 64 + (ns - NS / 2) * 32)
+                     : wave_n * 128 + ns * 32;
+  const int a_frag = (wave_m * 128 + (lane & 31)) * kTileK;
+  const int w_frag = (lane & 31) * kTileK;
+  auto read_frags = [&](int buf, int ks, uint4 (&av)[MS], uint4 (&bv)[NS]) {
+    const int fcol = (((2 * ks + (lane >> 5)) ^ lane ^ ((lane >> 3) & 3)) & 7) << 3;
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+      av[ms] = *reinterpret_cast<const uint4*>(&As[buf][a_frag + ms * 32 * kTileK + (fcol ^ ((ms & 1) << 5))]);
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns)
+      bv[ns] = *reinterpret_cast<const uint4*>(&Ws[buf][w_frag + nbase[ns] * kTileK + (fcol ^ ((ns & 1) << 5))]);
+  };
+  auto mfma_row = [&](int ms, const uint4 (&av)[MS], const uint4 (&bv)[NS]) {
+    static_for<NS>([&](auto ns) { acc[ms][ns] = mfma_32x32x16<CT>(av[ms], bv[ns], acc[ms][ns]); });
+  };
+  auto mfmas = [&](const uint4 (&av)[MS], const uint4 (&bv)[NS]) {
+    static_for<MS>([&](auto ms) {
+      static_for<NS>([&](auto ns) { acc[ms][ns] = mfma_32x32x16<CT>(av[ms], bv[ns], acc[ms][ns]); });
+    });
+  };
+
+  const int64_t ksteps = k / kTileK;
+  const int64_t klast = ksteps - 1;
+  // Prologue: step 0 staged whole into buffer 0; of step 1, the part an iteration's sub-step 3
+  // stages (the weight row's code planes, its first two words, the activation row).
+  static_assert(ST == 2, "step s lives in register set s % 2");
+  load_step(0, 0);
+  load_step(1, min<int64_t>(1, klast));
+  __syncthreads();  // code2 table
+  stage(0, 0, block_scale(0));
+  load_step(0, min<int64_t>(2, klast));
+  NibPlanes tp = planes(block_scale(1));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) store_a(1, 1, i);
+  store_w(1, 1, 0, tp);
+  store_w(1, 1, 1, tp);
+  __syncthreads();
+  uint4 fa0[MS], fb0[NS], fa1[MS], fb1[NS];
+  read_frags(0, 0, fa0, fb0);
+  // Step kb in sixteen chunks of four MFMAs (one accumulator row), each closed by a scheduling
+  // barrier so the staging pieces stay between them: a weight word's decode (about 26 VALU
+  // instructions) next to four 32-cycle MFMAs. The staging of a step is spread over four
+  // sub-steps: step kb + 2 starts in sub-step 3 of step kb, into buffer kb % 2 (free once the
+  // barrier has passed: its last fragments were read before it), and ends in sub-steps 0-2 of
+  // step kb + 1, whose sub-step 2 then reloads its register set with step kb + 3. Each sub-step
+  // reads the next one's fragments at its start. (The compiler left to itself puts the MFMAs
+  // ahead of the decode, and with one wave per SIMD the matrix core then idles through it.)
+  auto iteration = [&](auto uc, int64_t kb) __attribute__((always_inline)) {
+    constexpr int u = decltype(uc)::value;
+    constexpr int sS = (u + 1) % ST;  // register set of step kb + 1, whose staging ends here
+    constexpr int sT = u;             // register set of step kb + 2, whose staging starts here
+    const int cur = static_cast<int>(kb & 1);
+    // sub-step 0
+    read_frags(cur, 1, fa1, fb1);
+    mfma_row(0, fa0, fb0);
+    store_w(sS, cur ^ 1, 2, tp);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(1, fa0, fb0);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(2, fa0, fb0);
+    store_w(sS, cur ^ 1, 3, tp);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(3, fa0, fb0);
+    __builtin_amdgcn_sched_barrier(0);
+    // sub-step 1
+    read_frags(cur, 2, fa0, fb0);
+    mfma_row(0, fa1, fb1);
+    store_w(sS, cur ^ 1, 4, tp);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(1, fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(2, fa1, fb1);
+    store_w(sS, cur ^ 1, 5, tp);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(3, fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+    // sub-step 2
+    read_frags(cur, 3, fa1, fb1);
+    mfma_row(0, fa0, fb0);
+    store_w(sS, cur ^ 1, 6, tp);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(1, fa0, fb0);
+    store_w(sS, cur ^ 1, 7, tp);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(2, fa0, fb0);
+    load_step(sS, min<int64_t>(kb + 1 + ST, klast));
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(3, fa0, fb0);
+    __syncthreads();
+    // sub-step 3: the block scale first (its code2 read then waits for no fragment read)
+    const float sc = block_scale(sT);
+    read_frags(cur ^ 1, 0, fa0, fb0);
+    mfma_row(0, fa1, fb1);
+    tp = planes(sc);
+    store_a(sT, cur, 0);
+    store_a(sT, cur, 1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(1, fa1, fb1);
+    store_w(sT, cur, 0, tp);
+    store_a(sT, cur, 2);
+    store_a(sT, cur, 3);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(2, fa1, fb1);
+    store_w(sT, cur, 1, tp);
+    store_a(sT, cur, 4);
+    store_a(sT, cur, 5);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(3, fa1, fb1);
+    store_a(sT, cur, 6);
+    store_a(sT, cur, 7);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  const int64_t kmain = ksteps - ksteps % ST;
+  for (int64_t kb0 = 0; kb0 < kmain; kb0 += ST) {
+    iteration(std::integral_constant<int, 0>{}, kb0);
+    iteration(std::integral_constant<int, 1>{}, kb0 + 1);
+  }
+  if (kmain < ksteps) iteration(std::integral_constant<int, 0>{}, kmain);
+
+  // Epilogue. Tile row of accumulator register i of MFMA tile ms; the lane's column is
+  // nbase[ns] + (lane & 31).
+  auto row_of = [&](int ms, int i) { return wave_m * 128 + ms * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); };
+  if constexpr (F16C) {
+    static_for<MS>([&](auto ms) {
+      static_for<16>([&](auto i) {
+        const int d = -(row_shift_s[row_of(ms, i)] + wsh);
+        static_for<NS>([&](auto ns) { acc[ms][ns][int(i)] = __builtin_amdgcn_ldexpf(acc[ms][ns][int(i)], d); });
+      });
+    });
+  }
+  // fp16 mode, gate_up: the largest h exponent of each tile row over the 32 lanes that hold it
+  // (a DPP max within each 16-lane row, then across the pair of rows), folded into the block's
+  // row maxima and then into out_exp (atomicMax: independent of order)
+  const bool collect = F16C && p.out_exp != nullptr;
+  auto note_row_exp = [&](int lr, uint32_t hm) {
+    auto dpp_max = [](uint32_t v, auto ctrl) {
+      return max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), decltype(ctrl)::value,
+                                                                       0xf, 0xf, false)));
+    };
+    hm = dpp_max(hm, std::integral_constant<int, 0xb1>{});   // quad_perm [1,0,3,2]
+    hm = dpp_max(hm, std::integral_constant<int, 0x4e>{});   // quad_perm [2,3,0,1]
+    hm = dpp_max(hm, std::integral_constant<int, 0x141>{});  // row_half_mirror
+    hm = dpp_max(hm, std::integral_constant<int, 0x140>{});  // row_mirror
+    hm = max(hm, static_cast<uint32_t>(__shfl_xor(static_cast<int>(hm), 16)));
+    if ((lane & 31) == 0 && hm != 0) atomicMax(&hexp_s[lr], static_cast<int>(hm));
+  };
+  auto flush_row_exps = [&]() {
+    __syncthreads();
+    if (row0 + tid < row_end && hexp_s[tid] != 0) atomicMax(&p.out_exp[row0 + tid], hexp_s[tid]);
+  };
+  const bool has_bias = p.w.bias != nullptr;
+  const uint16_t* bias = static_cast<const uint16_t*>(p.w.bias);
+  if (pair && p.epi == E4B_EPI_SWIGLU && !has_bias && !p.out_f32) {  // gate_up: silu(g) * u -> dt
+    uint16_t* const out = static_cast<uint16_t*>(p.out);
+    const int64_t cbase = col0 + wave_n * 64 + (lane & 31);
+    static_for<MS>([&](auto ms) {
+      static_for<16>([&](auto i) {
+        const int lr = row_of(ms, i);
+        const int rr = row0 + lr;
+        uint16_t* const orow = out + int64_t(rr) * p.n_out + cbase;
+        uint32_t hm = 0;
+        static_for<NS / 2>([&](auto ns) {
+          const float v = silu_f32(acc[ms][ns][int(i)]) * acc[ms][ns + NS / 2][int(i)];
+          const uint16_t hb = from_f<DT>(v);
+          const bool st = rr < row_end && cbase + ns * 32 < p.n_out;
+          if (st) orow[ns * 32] = hb;
+          if (collect && st) hm = max(hm, (static_cast<uint32_t>(hb) >> 7) & 0xffu);
+        });
+        if (collect) note_row_exp(lr, hm);
+      });
+    });
+    if (collect) flush_row_exps();
+    return;
+  }
+  if (!pair && p.epi == E4B_EPI_NONE && !has_bias && p.out_f32) {  // down: fp32 rows
+    float* const out = static_cast<float*>(p.out);
+    const int64_t cbase = col0 + wave_n * 128 + (lane & 31);
+    static_for<MS>([&](auto ms) {
+      static_for<16>([&](auto i) {
+        const int rr = row0 + row_of(ms, i);
+        float* const orow = out + int64_t(rr) * p.n_out + cbase;
+        static_for<NS>([&](auto ns) {
+          if (rr < row_end && cbase + ns * 32 < p.n_out) orow[ns * 32] = acc[ms][ns][int(i)];
+        });
+      });
+    });
+    return;
+  }
+  // general path; in fp16 mode a gate_up output (never fp32 there) also notes its exponents
+  auto put = [&](int64_t idx, float v, uint32_t& hm) {
+    if (collect) {
+      const uint16_t hb = from_f<DT>(v);
+      static_cast<uint16_t*>(p.out)[idx] = hb;
+      hm = max(hm, (static_cast<uint32_t>(hb) >> 7) & 0xffu);
+    } else {
+      store_elem<DT>(p, idx, v);
+    }
+  };
+  static_for<MS>([&](auto ms) {
+    static_for<16>([&](auto i) {
+      const int lr = row_of(ms, i);
+      const int rr = row0 + lr;
+      uint32_t hm = 0;
+      if (rr < row_end) {  // the 32 lanes of a row agree, so the reduction below is not split
+        const int64_t orow = int64_t(rr) * p.n_out;
+        if (pair) {
+          static_for<NS / 2>([&](auto ns) {
+            const int64_t jj = col0 + wave_n * 64 + ns * 32 + (lane & 31);
+            if (jj < p.n_out) {
+              const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + jj]) : 0.0f;
+              const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + n / 2 + jj]) : 0.0f;
+              put(orow + jj, gated(p.epi, acc[ms][ns][int(i)], acc[ms][ns + NS / 2][int(i)], p.alpha, p.limit, bg, bu), hm);
+            }
+          });
+        } else {
+          static_for<NS>([&](auto ns) {
+            const int64_t nn = col0 + wave_n * 128 + ns * 32 + (lane & 31);
+            if (nn < p.n_out) {
+              const float b = has_bias ? to_f<DT>(bias[int64_t(e) * n + nn]) : 0.0f;
+              put(orow + nn, single(p.epi, acc[ms][ns][int(i)], b), hm);
+            }
+          });
+        }
+      }
+      if (collect) note_row_exp(lr, hm);
+    });
+  });
+  if (collect) flush_row_exps();
+}
+
+}  // namespace e4b

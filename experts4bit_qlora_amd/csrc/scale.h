@@ -5,7 +5,8 @@
 // reference) at the same matrix-core rate. fp16's range is narrower than bf16's, so operands
 // are scaled by powers of two, which is exact and removed from the fp32 sums afterwards:
 //   row_exp_kernel       the largest biased exponent of every activation row (one wave per
-//                        row), and the zeroing of the h-row exponents the gate_up GEMM collects;
+//                        row) and the row as scaled fp16: the tokens before the gate_up GEMM,
+//                        h (in place) before the down GEMM;
 //   weight_shift_kernel  per expert, the shift that brings its largest block scale (decoded, for
 //                        double quantization) into [2^14, 2^15): computed once per weight version.
 #pragma once
@@ -23,15 +24,16 @@ E4B_DEV uint32_t wave_max_u32(uint32_t v) {
 }
 
 // row_exp[r] = the largest biased exponent over row r of x [rows, k] (bf16, k % 8 == 0), and
-// x16[r] = fp16(x[r] * 2^exp_shift(row_exp[r])) (exact; see bf16x2_to_f16x2), the gate_up
-// GEMM's operand staged once instead of once per output tile; zero[0 .. nzero) = 0 (grid-stride:
-// the grid has rows / 4 blocks of 256 threads). One wave per row; a row's pieces stay in
-// registers between the two passes when k <= 64 * 8 * kRowPieces.
+// x16[r] = fp16(x[r] * 2^exp_shift(row_exp[r])) (exact; see bf16x2_to_f16x2), a GEMM operand
+// staged once instead of once per output tile; zero[0 .. nzero) = 0 (grid-stride: the grid has
+// rows / 4 blocks of 256 threads). One wave per row; a row's pieces stay in registers between
+// the two passes when k <= 64 * 8 * kRowPieces. x16 may be x (in place): a wave reads every piece
+// of its row for the maximum before it writes any, and writes each piece after reading it.
 constexpr int kRowPieces = 8;  // 16-byte pieces per lane held across the passes (k <= 4096)
 
-__global__ void __launch_bounds__(kScaleThreads) row_exp_kernel(const uint16_t* __restrict__ x, int64_t rows,
+__global__ void __launch_bounds__(kScaleThreads) row_exp_kernel(const uint16_t* x, int64_t rows,
                                                                 int64_t k, int32_t* __restrict__ row_exp,
-                                                                uint16_t* __restrict__ x16,
+                                                                uint16_t* x16,
                                                                 int32_t* __restrict__ zero, int64_t nzero) {
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nzero; i += int64_t(gridDim.x) * blockDim.x)
     zero[i] = 0;

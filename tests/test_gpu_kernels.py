@@ -260,6 +260,57 @@ def test_grouped_gemm_plain(path, fmt, T):
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("fmt", ["nf4", "nf4_dq", "mxfp4"])
+@pytest.mark.parametrize("k", [64, 192, 320, 512])
+def test_grouped_gemm_wide_tiles(fmt, k, dt):
+    """256-row tiles (gemm_wide_kernel, four waves of 128 x 128, 32 x 32 MFMAs, the staging of a
+    step spread over the previous step's MFMAs): 1, 3, 5 and 8 steps of 64 (the odd counts take
+    the loop's single-step tail), partial tiles (experts of 37 to 300 rows, two tiles for the
+    largest), bf16 rows and fp32 rows, against the fp64 oracle over the oracle's weights."""
+    _announce(f"grouped gemm wide tiles fmt={fmt} k={k} dt={dt}")
+    E, n, top = 5, 320, 2
+    sizes = [300, 37, 150, 0, 113]
+    if fmt == "mxfp4":
+        g = torch.Generator().manual_seed(70 + k)
+        w = torch.randn(E, n, k, generator=g) * 0.02
+        b, s = Q.quantize_mxfp4(w)
+        qw = ops.mxfp4_qweight(b.reshape(E, -1).to(DEV), s.reshape(E, -1).to(DEV), n, k, num_experts=E)
+    else:
+        qw, _, _ = _nf4_stack(E, n, k, seed=71 + k, dq=(fmt == "nf4_dq"))
+    W = _dense_from_oracle(qw)
+    # token t's two slots: experts chosen so that expert e gets sizes[e] rows in all
+    slots = np.concatenate([np.full(c, e) for e, c in enumerate(sizes)])
+    rng = np.random.default_rng(k)
+    rng.shuffle(slots)
+    idx = slots.reshape(-1, top).astype(np.int64)
+    T = idx.shape[0]
+    x = torch.randn(T, k, generator=torch.Generator().manual_seed(72 + k)).to(dt)
+    rb = ops.route(torch.from_numpy(idx).to(DEV), E, tile_m=256)
+    ref = orouting.route(idx, E)
+    Wm = numerics.round_bf16(W) if dt == torch.bfloat16 else numerics.round_fp16(W)
+    want = _gemm_oracle(x.float().numpy()[ref["token_rows"]], Wm, idx.reshape(-1)[ref["order"]])
+    # 16-bit rows: errors net of the row's own rounding (half an ulp of each element)
+    errs = _errs_rounded_bf16 if dt == torch.bfloat16 else _errs
+    out = ops.grouped_gemm(x.to(DEV), qw, rb, T, T * top, N.EPI_NONE, gather_k=top, path=N.PATH_MFMA)
+    fro, maxabs = errs(out.float().cpu().numpy(), want)
+    assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
+    out32 = ops.grouped_gemm(x.to(DEV), qw, rb, T, T * top, N.EPI_NONE, gather_k=top, path=N.PATH_MFMA,
+                             out_dtype=torch.float32)
+    fro32, _ = _errs(out32.cpu().numpy(), want)
+    assert fro32 < 1e-5, fro32
+    # the 128-row tiles of the same rows give the same fp32 rows up to summation order
+    out128 = ops.grouped_gemm(x.to(DEV), qw, ops.route(torch.from_numpy(idx).to(DEV), E, tile_m=128), T, T * top,
+                              N.EPI_NONE, gather_k=top, path=N.PATH_MFMA, out_dtype=torch.float32)
+    assert torch.allclose(out32, out128, rtol=1e-5, atol=1e-6)
+    # gated epilogue: silu(g) * u on the fp32 sums, one rounding
+    gated = ops.grouped_gemm(x.to(DEV), qw, rb, T, T * top, N.EPI_SWIGLU, gather_k=top, path=N.PATH_MFMA)
+    half = n // 2
+    h_want = moe._glu_exact(want, "swiglu", half)
+    fro_g, maxabs_g = errs(gated.float().cpu().numpy(), h_want)
+    assert fro_g <= 1e-2 and maxabs_g <= 2e-2, (fro_g, maxabs_g)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_mxfp4_mfma_weights_at_every_scale(dt):
     """One-hot activations turn the MFMA GEMM's output into the weights it multiplies: row i of
     the output is column i of W (one product by 1.0, the rest zeros, fp32 accumulation). The
