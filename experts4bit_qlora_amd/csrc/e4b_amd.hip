@@ -435,11 +435,12 @@ int64_t e4b_route_scratch_ints(int64_t M, int32_t num_experts) {
 }
 
 // e4b_grouped_gemm, plus the fp16 matrix-core mode of the fused forward: a_exp (the A rows'
-// largest exponents) selects it on the MFMA path, out_exp collects the h rows' exponents.
+// largest exponents, the rows stored as scaled fp16 by row_exp_kernel) selects it on the MFMA
+// path.
 static int grouped_gemm_impl(const void* a, int32_t act_dtype, int32_t gather_k, const e4b_qweight* w,
                              const e4b_routing* rt, int64_t tokens, int64_t M, int32_t epilogue, float alpha,
                              float limit, int32_t flags, void* out, int32_t out_dtype, const int32_t* a_exp,
-                             int a_f16, int32_t* out_exp, hipStream_t stream) {
+                             hipStream_t stream) {
   int rc = check_weight(w);
   if (rc) return rc;
   rc = check_routing(rt, M);
@@ -481,8 +482,6 @@ static int grouped_gemm_impl(const void* a, int32_t act_dtype, int32_t gather_k,
   if (f16c && (gemv || act_dtype != E4B_BF16 || w->format == E4B_FMT_MXFP4 || !w->shift))
     return fail(E4B_EINVAL, "the fp16 matrix-core mode needs the MFMA path, bf16 activations and NF4 weight shifts");
   args.a_exp = a_exp;
-  args.a_f16 = a_exp != nullptr && a_f16;
-  args.out_exp = out_exp;
   const int64_t max_active = std::min<int64_t>(w->num_experts, M);
   return act_dtype == E4B_BF16 ? launch_gemm_dt<E4B_BF16>(args, gemv, max_active, stream)
                                : launch_gemm_dt<E4B_FP16>(args, gemv, max_active, stream);
@@ -492,7 +491,7 @@ int e4b_grouped_gemm(const void* a, int32_t act_dtype, int32_t gather_k, const e
                      int64_t tokens, int64_t M, int32_t epilogue, float alpha, float limit, int32_t flags, void* out,
                      int32_t out_dtype, hipStream_t stream) {
   return grouped_gemm_impl(a, act_dtype, gather_k, w, rt, tokens, M, epilogue, alpha, limit, flags, out, out_dtype,
-                           nullptr, 0, nullptr, stream);
+                           nullptr, stream);
 }
 
 int e4b_weight_shift(const e4b_qweight* w, int32_t* shift, hipStream_t stream) {
@@ -964,7 +963,6 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
                        int64_t(0));
     return check_launch("row_exp_kernel");
   };
-  const int down_f16 = f16c ? 1 : 0;
   if (split) {
     hipLaunchKernelGGL(e4b::split_tiles_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, rt.offsets, rt.meta, E,
                        rbig, rsmall);
@@ -972,24 +970,24 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
     if (rc) return rc;
     for (const e4b_routing* r : {&rbig, &rsmall}) {
       rc = grouped_gemm_impl(up_a, act_dtype, top_k, w1, r, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
-                             up_exp, 1, nullptr, stream);
+                             up_exp, stream);
       if (rc) return rc;
     }
     rc = h_to_f16();
     if (rc) return rc;
     for (const e4b_routing* r : {&rbig, &rsmall}) {
       rc = grouped_gemm_impl(h, act_dtype, 0, w2, r, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
-                             h_exp, down_f16, nullptr, stream);
+                             h_exp, stream);
       if (rc) return rc;
     }
   } else {
     rc = grouped_gemm_impl(up_a, act_dtype, top_k, w1, &rt, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
-                           up_exp, 1, nullptr, stream);
+                           up_exp, stream);
     if (rc) return rc;
     rc = h_to_f16();
     if (rc) return rc;
     rc = grouped_gemm_impl(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
-                           h_exp, down_f16, nullptr, stream);
+                           h_exp, stream);
     if (rc) return rc;
   }
   return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
@@ -1137,13 +1135,13 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
   rc = e4b_route(top_k_index, tokens, top_k, E, &rt, stream);
   if (rc) return rc;
   rc = grouped_gemm_impl(hidden, act_dtype, top_k, w1, &rt, tokens, M, E4B_EPI_NONE, 1.0f, limit, flags, up, E4B_FP32,
-                         nullptr, 0, nullptr, stream);
+                         nullptr, stream);
   if (rc) return rc;
   rc = e4b_lora_delta_epilogue(hidden, act_dtype, top_k, &rt, M, E, lora->a1, lora->b1, lora->dtype, r, w1->k, w1->n,
                                lora->scaling, E4B_FP32, t, up, epilogue, limit, h, act_dtype, stream);
   if (rc) return rc;
   rc = grouped_gemm_impl(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, 1.0f, limit, flags, down, E4B_FP32,
-                         nullptr, 0, nullptr, stream);
+                         nullptr, stream);
   if (rc) return rc;
   rc = e4b_lora_delta(h, act_dtype, 0, &rt, M, E, lora->a2, lora->b2, lora->dtype, r, w2->k, w2->n, lora->scaling,
                       E4B_FP32, t, down, stream);

@@ -27,11 +27,10 @@
 //
 // fp16 mode (F16C, bf16 activations with NF4 weights): the MFMAs multiply fp16 operands. The
 // weights are decoded as fp16(fl32(code * absmax) * 2^shift[e]) -- one rounding, 2^-11 relative
-// where the bf16 weight carries 2^-8 -- and each A row is staged as its bf16 values times
-// 2^exp_shift(row exponent), exact in fp16. The accumulators are scaled back by
-// 2^-(row shift + expert shift) before the epilogue, so the results are those of the exact
-// weights to within fp16's rounding of each weight. The gate_up GEMM also collects every h
-// row's largest exponent (an order-independent atomicMax) for the down GEMM's row scales.
+// where the bf16 weight carries 2^-8 -- and the A rows arrive as their bf16 values times
+// 2^exp_shift(row exponent), exact in fp16 (row_exp_kernel). The accumulators are scaled back
+// by 2^-(row shift + expert shift) before the epilogue, so the results are those of the exact
+// weights to within fp16's rounding of each weight.
 #pragma once
 
 #include "common.h"
@@ -229,16 +228,29 @@ E4B_DEV void dequant_bytes(const uint32_t (&words)[NB / 4], const float (&code)[
   }
 }
 
+// fp16 matrix-core mode of the wide tiles: packed bytes decoded through an LDS table of the 256
+// byte values' code pairs, entry b = (fp16(code[b >> 4]), fp16(code[b & 15])) (the first element,
+// the high nibble, in the low half), times the row's block scale as an fp16 pair (v_pk_mul_f16):
+// one lookup and one multiply per two weights, where the register decode above spends about six
+// VALU instructions per two. kPairCopies copies of the table, copy c in word c of each entry's
+// 64 bytes, lane l reading copy l % kPairCopies. Each weight is then
+// fp16(fp16(code) * fp16(absmax * 2^shift)), three fp16 roundings (relative error <= 3 * 2^-11,
+// against 2^-8 for the reference's bf16 weight).
+constexpr int kPairCopies = 16;
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+E4B_DEV uint32_t pk_mul_f16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, a) * __builtin_bit_cast(h2_t, b));
+}
+
 // Tile shapes: weight rows per tile and threads (8 waves for the 128- and 256-row tiles, else 4).
 // (The 256-row tiles run gemm_wide_kernel: 256 weight rows, four waves.)
 constexpr int gemm_tile_nw(int bm) { return bm >= kTileM ? kTileNWWide : kTileNW; }
 constexpr int gemm_threads(int bm) { return bm == kTileM ? 512 : 256; }
 
-// F16: 0 = operands in the activation dtype; fp16 mode with A rows converted while staged (1)
-// or already stored as scaled fp16 by row_exp_kernel (2).
-template <int DT, int FMT, int BM, int F16 = 0>
+// F16C: fp16 mode, the A rows already stored as scaled fp16 by row_exp_kernel; else the
+// operands are in the activation dtype.
+template <int DT, int FMT, int BM, bool F16C = false>
 __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p) {
-  constexpr bool F16C = F16 != 0;
   static_assert(!F16C || (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4), "fp16 mode: bf16 activations, NF4 weights");
   constexpr int CT = F16C ? E4B_FP16 : DT;  // MFMA operand type
   constexpr int NT = gemm_threads(BM);
@@ -260,7 +272,6 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kTileK];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
   __shared__ int row_shift_s[F16C ? BM : 1];  // fp16 mode: each tile row's activation shift
-  __shared__ int hexp_s[F16C ? BM : 1];       // fp16 mode, gate_up: each tile row's h exponent
 
   const int num_tiles = p.rt.meta[0];
   const int n_tiles = static_cast<int>((p.n_out + (is_gated(p.epi) ? BN / 2 : BN) - 1) /
@@ -295,15 +306,11 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   const int r = row0 + ar;
   const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
   const uint16_t* aptr = p.a + src * k + aseg;
-  // fp16 mode: this thread's A-row shift and the tile expert's weight shift
-  int ash = 0, wsh = 0;
+  // fp16 mode: the tile row's activation shift (for the epilogue) and the expert's weight shift
+  int wsh = 0;
   if constexpr (F16C) {
-    ash = exp_shift(p.a_exp[src]);
     wsh = p.w.shift[e];
-    if (tid % TPR == 0) {
-      row_shift_s[ar] = ash;
-      hexp_s[ar] = 0;
-    }
+    if (tid % TPR == 0) row_shift_s[ar] = exp_shift(p.a_exp[src]);
   }
 
   // W assignment: LDS row tid / TPW (0..BN-1), 2 * WB values of the 64-deep step at
@@ -396,14 +403,7 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
           make_uint4(wv[4 * i], wv[4 * i + 1], wv[4 * i + 2], wv[4 * i + 3]);
 #pragma unroll
     for (int i = 0; i < AV; ++i) {
-      u32x4_t* as = reinterpret_cast<u32x4_t*>(&As[buf][lds_at(arow, aseg + 8 * i)]);
-      if constexpr (F16 == 1) {
-        const u32x4_t v = areg[set][i];
-        *as = u32x4_t{bf16x2_to_f16x2(v[0], ash), bf16x2_to_f16x2(v[1], ash), bf16x2_to_f16x2(v[2], ash),
-                      bf16x2_to_f16x2(v[3], ash)};
-      } else {
-        *as = areg[set][i];
-      }
+      *reinterpret_cast<u32x4_t*>(&As[buf][lds_at(arow, aseg + 8 * i)]) = areg[set][i];
     }
   };
   // MFMA operands of one 32-deep half step (ks) of LDS buffer buf, and the MFMAs on them. Every
@@ -497,29 +497,6 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
         for (int ns = 0; ns < NS; ++ns) acc[ms][ns][i] = __builtin_amdgcn_ldexpf(acc[ms][ns][i], d);
       }
   }
-  // fp16 mode, gate_up: hm is the largest exponent of the h values this lane stored in tile row
-  // lr; the 16 lanes holding that row reduce it, one of them folds it into the block's row
-  // maximum, and after the epilogue the block folds those into out_exp (atomicMax: the result
-  // does not depend on the order)
-  const bool collect = F16C && p.out_exp != nullptr;
-  // (a DPP max over each 16-lane row of the wave: VALU moves, not LDS permutes, so the 16 rows'
-  // reductions of a lane do not queue behind LDS round trips)
-  auto note_row_exp = [&](int lr, uint32_t hm) {
-    auto dpp_max = [](uint32_t v, auto ctrl) {
-      return max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), decltype(ctrl)::value,
-                                                                       0xf, 0xf, false)));
-    };
-    hm = dpp_max(hm, std::integral_constant<int, 0xb1>{});   // quad_perm [1,0,3,2]
-    hm = dpp_max(hm, std::integral_constant<int, 0x4e>{});   // quad_perm [2,3,0,1]
-    hm = dpp_max(hm, std::integral_constant<int, 0x141>{});  // row_half_mirror
-    hm = dpp_max(hm, std::integral_constant<int, 0x140>{});  // row_mirror
-    if ((lane & 15) == 0 && hm != 0) atomicMax(&hexp_s[lr], static_cast<int>(hm));
-  };
-  auto flush_row_exps = [&]() {
-    __syncthreads();
-    for (int t = tid; t < BM; t += NT)
-      if (row0 + t < row_end && hexp_s[t] != 0) atomicMax(&p.out_exp[row0 + t], hexp_s[t]);
-  };
   const bool has_bias = p.w.bias != nullptr;
   const uint16_t* bias = static_cast<const uint16_t*>(p.w.bias);
   // The two prefill projections take a branch-free path: epilogue kind, bias and output type
@@ -531,22 +508,15 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
     for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int lr = wave_m * WM + ms * 16 + 4 * (lane >> 4) + i;
-        const int rr = row0 + lr;
+        const int rr = row0 + wave_m * WM + ms * 16 + 4 * (lane >> 4) + i;
         uint16_t* const orow = out + int64_t(rr) * p.n_out + cbase;
-        uint32_t hm = 0;
 #pragma unroll
         for (int ns = 0; ns < NS / 2; ++ns) {
           const float v = silu_f32(acc[ms][ns][i]) * acc[ms][ns + NS / 2][i];
-          const uint16_t hb = from_f<DT>(v);
-          const bool st = rr < row_end && cbase + ns * 16 < p.n_out;
-          if (st) orow[ns * 16] = hb;
-          if (collect && st) hm = max(hm, (static_cast<uint32_t>(hb) >> 7) & 0xffu);
+          if (rr < row_end && cbase + ns * 16 < p.n_out) orow[ns * 16] = from_f<DT>(v);
         }
-        if (collect) note_row_exp(lr, hm);
       }
     }
-    if (collect) flush_row_exps();
     return;
   }
   if (!pair && p.epi == E4B_EPI_NONE && !has_bias && p.out_f32) {  // down: fp32 rows
@@ -566,24 +536,13 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
     }
     return;
   }
-  // general path; in fp16 mode a gate_up output (never fp32 there) also notes its exponents
-  auto put = [&](int64_t i, float v, uint32_t& hm) {
-    if (collect) {
-      const uint16_t hb = from_f<DT>(v);
-      static_cast<uint16_t*>(p.out)[i] = hb;
-      hm = max(hm, (static_cast<uint32_t>(hb) >> 7) & 0xffu);
-    } else {
-      store_elem<DT>(p, i, v);
-    }
-  };
+  // general path
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int lr = wave_m * WM + ms * 16 + 4 * (lane >> 4) + i;
-      const int rr = row0 + lr;
-      uint32_t hm = 0;
-      if (rr < row_end) {  // the 16 lanes of a row agree, so the reduction below is not split
+      const int rr = row0 + wave_m * WM + ms * 16 + 4 * (lane >> 4) + i;
+      if (rr < row_end) {
         const int64_t orow = int64_t(rr) * p.n_out;
         if (pair) {
 #pragma unroll
@@ -592,7 +551,7 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
             if (jj >= p.n_out) continue;
             const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + jj]) : 0.0f;
             const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + n / 2 + jj]) : 0.0f;
-            put(orow + jj, gated(p.epi, acc[ms][ns][i], acc[ms][ns + NS / 2][i], p.alpha, p.limit, bg, bu), hm);
+            store_elem<DT>(p, orow + jj, gated(p.epi, acc[ms][ns][i], acc[ms][ns + NS / 2][i], p.alpha, p.limit, bg, bu));
           }
         } else {
 #pragma unroll
@@ -600,14 +559,12 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
             const int64_t nn = col0 + wave_n * WN + ns * 16 + (lane & 15);
             if (nn >= p.n_out) continue;
             const float b = has_bias ? to_f<DT>(bias[int64_t(e) * n + nn]) : 0.0f;
-            put(orow + nn, single(p.epi, acc[ms][ns][i], b), hm);
+            store_elem<DT>(p, orow + nn, single(p.epi, acc[ms][ns][i], b));
           }
         }
       }
-      if (collect) note_row_exp(lr, hm);
     }
   }
-  if (collect) flush_row_exps();
 }
 
 }  // namespace e4b

@@ -19,29 +19,26 @@ namespace {
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // 256-row tiles run the wide kernel (four waves of 128 x 128), the others gemm_mfma_kernel.
-template <int DT, int FMT, int BM, int F16>
+template <int DT, int FMT, int BM, bool F16C>
 void launch_mfma_kernel(const GemmArgs& a, dim3 grid, hipStream_t s) {
   if constexpr (BM == kTileMBig) {
-    hipLaunchKernelGGL((gemm_wide_kernel<DT, FMT, F16>), grid, dim3(kWideThreads), 0, s, a);
+    hipLaunchKernelGGL((gemm_wide_kernel<DT, FMT, F16C>), grid, dim3(kWideThreads), 0, s, a);
   } else {
-    hipLaunchKernelGGL((gemm_mfma_kernel<DT, FMT, BM, F16>), grid, dim3(gemm_threads(BM)), 0, s, a);
+    hipLaunchKernelGGL((gemm_mfma_kernel<DT, FMT, BM, F16C>), grid, dim3(gemm_threads(BM)), 0, s, a);
   }
 }
 
-// One tile height; the fp16 mode (a.a_exp set) exists for bf16 activations with NF4 weights.
+// One tile height; the fp16 mode (a.a_exp set: A rows stored as scaled fp16) exists for bf16
+// activations with NF4 weights.
 template <int DT, int FMT, int BM>
 void launch_mfma_bm(const GemmArgs& a, dim3 grid, hipStream_t s) {
   if constexpr (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4) {
-    if (a.a_exp && a.a_f16) {
-      launch_mfma_kernel<DT, FMT, BM, 2>(a, grid, s);
-      return;
-    }
     if (a.a_exp) {
-      launch_mfma_kernel<DT, FMT, BM, 1>(a, grid, s);
+      launch_mfma_kernel<DT, FMT, BM, true>(a, grid, s);
       return;
     }
   }
-  launch_mfma_kernel<DT, FMT, BM, 0>(a, grid, s);
+  launch_mfma_kernel<DT, FMT, BM, false>(a, grid, s);
 }
 
 }  // namespace

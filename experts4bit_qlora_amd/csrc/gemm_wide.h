@@ -68,31 +68,39 @@ E4B_DEV f32x16_t mfma_32x32x16(const uint4& a, const uint4& b, const f32x16_t& c
   }
 }
 
-template <int DT, int FMT, int F16 = 0>
-__global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
-  constexpr bool F16C = F16 != 0;
-  static_assert(!F16C || (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4), "fp16 mode: bf16 activations, NF4 weights");
-  constexpr int CT = F16C ? E4B_FP16 : DT;
-  constexpr int BM = kWideTileM, BN = kWideTileN, NT = kWideThreads;
-  constexpr int MS = 4, NS = 4;  // 32 x 32 MFMA tiles per wave: 128 x 128
-  constexpr int ST = 2;          // register sets of global loads in flight
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kTileK];
-  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kTileK];
-  __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
-  __shared__ int row_shift_s[F16C ? BM : 1];
-  __shared__ int hexp_s[F16C ? BM : 1];
+// Work items, tile by tile: tile t runs on XCD t % 8 (workgroups go round-robin over the 8
+// XCDs: block L runs on XCD L % 8), and each XCD sweeps all N tiles of one M tile before its
+// next M tile, in list order -- the activation rows of a tile stay in that XCD's L2 across its
+// N sweep, and a list that holds the long tiles first runs them first on every XCD. false: the
+// block is past the work (the grid is sized for the routing's max_tiles).
+E4B_DEV bool wide_tile_of_block(int num_tiles, int n_tiles, int& tile, int& n_tile) {
+  const int xcd = static_cast<int>(blockIdx.x % kXcds);
+  const int q = static_cast<int>(blockIdx.x / kXcds);
+  tile = (q / n_tiles) * kXcds + xcd;
+  n_tile = q % n_tiles;
+  return tile < num_tiles;
+}
 
-  const int num_tiles = p.rt.meta[0];
+// One tile. HALF: a tile of at most 128 rows (an expert's last, partial tile) as 128 rows x 256
+// weight rows, each wave 128 x 64 (two 32 x 32 MFMA columns), instead of padding it to 256 rows.
+template <int DT, int FMT, bool F16C, bool HALF>
+E4B_DEV void wide_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2][kWideTileM * kTileK],
+                       uint16_t (&Ws)[2][kWideTileN * kTileK], float* code2_s, int* row_shift_s,
+                       const uint32_t* ptab) {
+  constexpr bool PTAB = F16C;  // fp16 mode: weights decoded through the LDS table of code pairs
+  constexpr int CT = F16C ? E4B_FP16 : DT;
+  constexpr int BM = kWideTileM, BN = kWideTileN;
+  constexpr int MS = 4, NS = HALF ? 2 : 4;  // 32 x 32 MFMA tiles per wave: 128 x 32 NS
+  constexpr int WCOL = 32 * NS;             // weight rows per wave
+  constexpr int AP = HALF ? 4 : 8;          // activation pieces per thread and step
+  constexpr int ST = 2;                     // register sets of global loads in flight
   const bool pair = is_gated(p.epi);
   const int cols = pair ? BN / 2 : BN;
-  const int n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
-  int tile, n_tile;
-  if (!tile_of_block(num_tiles, n_tiles, tile, n_tile)) return;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
-  const int wid = tid / kWave;
-  const int wave_m = wid & 1;
-  const int wave_n = wid >> 1;
+  const int wid = __builtin_amdgcn_readfirstlane(tid) / kWave;  // wave-uniform: a scalar register
+  const int wave_m = HALF ? 0 : (wid & 1);
+  const int wave_n = HALF ? wid : (wid >> 1);
   const int e = p.rt.tiles[2 * tile];
   const int row0 = p.rt.tiles[2 * tile + 1];
   const int row_end = min(row0 + BM, p.rt.offsets[e + 1]);
@@ -111,24 +119,20 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
   // (one lane per row, 16 bytes from each of 64 rows per load, costs the load pipeline about
   // twice the issue time). aoff[i]: that piece of step 0, in 16-byte units of p.a.
   const int apart = tid & 7;
-  uint32_t aoff[8];
-  int ash[8];
-  int wsh = 0;
+  uint32_t aoff[AP];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < AP; ++i) {
     const int r = row0 + 32 * i + (tid >> 3);
     const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
     aoff[i] = static_cast<uint32_t>((src * k) / 8 + apart);
-    ash[i] = 0;
-    if constexpr (F16C) ash[i] = exp_shift(p.a_exp[src]);
   }
+  int wsh = 0;
   if constexpr (F16C) {
     wsh = p.w.shift[e];
     // row_shift_s: the shift of tile row tid, for the epilogue
     const int r = row0 + tid;
     const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
     row_shift_s[tid] = exp_shift(p.a_exp[src]);
-    hexp_s[tid] = 0;
   }
   // W: thread tid stages LDS weight row tid (for a gated epilogue rows 0..127 are the gate rows
   // of the tile's 128 output columns and rows 128..255 their up rows); rows past n_out read
@@ -147,14 +151,16 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
   f32x16_t acc[MS][NS];
   static_for<MS>([&](auto ms) { static_for<NS>([&](auto ns) { acc[ms][ns] = f32x16_t{}; }); });
 
-  u32x4_t areg[ST][8];
+  u32x4_t areg[AP];  // one set: a step's activations are loaded and staged within one step
   uint32_t wq[ST][8];
   float sa[ST];
   uint32_t sq[ST];
-  auto load_step = [&](int set, int64_t kb) {
-    const u32x4_t* ap = reinterpret_cast<const u32x4_t*>(p.a) + kb * (kTileK / 8);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) areg[set][i] = ap[aoff[i]];
+  // the global loads of a step: activation piece i, and the weight row's bytes and scales
+  auto load_a = [&](int64_t kb, int i) {
+    if (i >= AP) return;  // (i is a constant at every call)
+    areg[i] = (reinterpret_cast<const u32x4_t*>(p.a) + kb * (kTileK / 8))[aoff[i]];
+  };
+  auto load_w = [&](int set, int64_t kb) {
     const uint4 v0 = *reinterpret_cast<const uint4*>(wptr + kb * 32);
     const uint4 v1 = *reinterpret_cast<const uint4*>(wptr + kb * 32 + 16);
     wq[set][0] = v0.x; wq[set][1] = v0.y; wq[set][2] = v0.z; wq[set][3] = v0.w;
@@ -168,6 +174,10 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
       sq[set] = static_cast<const uint8_t*>(p.w.absmax)[e * nb + blk];
       sa[set] = p.w.absmax2[e * ((nb + 255) / 256) + blk / 256];
     }
+  };
+  auto load_a_all = [&](int64_t kb) {
+#pragma unroll
+    for (int i = 0; i < AP; ++i) load_a(kb, i);
   };
   // The NF4 block scale of a staged step, formed one sub-step ahead of its staging: the
   // double-quant scale reads code2 from LDS, and a wait for that read in the staging would also
@@ -186,45 +196,53 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
   // Staging of one step, in pieces the main loop spreads over the MFMAs: the activation row
   // (eight 16-byte stores; converted to scaled fp16 in fp16 mode 1) and the weight row, one
   // packed word (eight values, one 16-byte store) at a time.
-  auto store_a = [&](int set, int buf, int i) {
-    u32x4_t* as = reinterpret_cast<u32x4_t*>(&As[buf][lds_at_w(32 * i + (tid >> 3), 8 * apart)]);
-    if constexpr (F16 == 1) {
-      const u32x4_t v = areg[set][i];
-      *as = u32x4_t{bf16x2_to_f16x2(v[0], ash[i]), bf16x2_to_f16x2(v[1], ash[i]), bf16x2_to_f16x2(v[2], ash[i]),
-                    bf16x2_to_f16x2(v[3], ash[i])};
-    } else {
-      *as = areg[set][i];
-    }
+  auto store_a = [&](int buf, int i) {
+    if (i >= AP) return;  // (i is a constant at every call)
+    *reinterpret_cast<u32x4_t*>(&As[buf][lds_at_w(32 * i + (tid >> 3), 8 * apart)]) = areg[i];
   };
   auto store_w = [&](int set, int buf, int wi, const NibPlanes& t) {
     uint32_t o[4];
     if constexpr (FMT == E4B_FMT_MXFP4) {  // words 0-3: the first 32-value block, 4-7: the second
       fp4_word<CT>(wq[set][wi], e8m0_to_f32(wi < 4 ? (sq[set] & 0xffu) : (sq[set] >> 8)), o);
+    } else if constexpr (PTAB) {  // byte b's code pair from the lane's table copy, times the scale pair t.lo[0]
+      const uint32_t* tab = ptab + (lane & (kPairCopies - 1));
+      const uint32_t w = wq[set][wi];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) o[b] = pk_mul_f16(tab[((w >> (8 * b)) & 0xffu) * kPairCopies], t.lo[0]);
     } else {
       nib_word<FMT>(t, wq[set][wi], o);
     }
     *reinterpret_cast<uint4*>(&Ws[buf][lds_at_w(tid, 8 * wi)]) = make_uint4(o[0], o[1], o[2], o[3]);
   };
   auto planes = [&](float scale) {
-    if constexpr (FMT == E4B_FMT_MXFP4) return NibPlanes{};
-    else return nib_planes<CT, !F16C>(code, scale);
+    if constexpr (FMT == E4B_FMT_MXFP4) {
+      return NibPlanes{};
+    } else if constexpr (PTAB) {  // the table decode needs only the scale, as an fp16 pair
+      NibPlanes t{};
+      t.lo[0] = cvt_pair<E4B_FP16>(scale, scale);
+      return t;
+    } else {
+      return nib_planes<CT, !F16C>(code, scale);
+    }
   };
   auto stage = [&](int set, int buf, float scale) {
     const NibPlanes t = planes(scale);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) store_a(set, buf, i);
+    for (int i = 0; i < AP; ++i) store_a(buf, i);
 #pragma unroll
     for (int wi = 0; wi < 8; ++wi) store_w(set, buf, wi, t);
   };
   // Fragments of sub-step ks (k = 16 ks .. 16 ks + 15): lane l reads row (base + l % 32), the
   // eight values at k = 16 ks + 8 (l / 32). Every base is a multiple of 32, so the row's swizzle
-  // term is (l & 7) ^ ((l >> 3) & 3) ^ 4 (base / 32 & 1), and base / 32 & 1 is the parity of the
-  // tile index (ms, or ns: the gate and up halves start at multiples of 64).
-  int nbase[NS];
+  // term is (l & 7) ^ ((l >> 3) & 3) ^ 4 (base / 32 & 1): bpar[ns] for the weight fragments,
+  // ms & 1 for the activation ones (whose bases are ms * 32 past a multiple of 64).
+  int nbase[NS], bpar[NS];
 #pragma unroll
-  for (int ns = 0; ns < NS; ++ns)
-    nbase[ns] = pair ? ((ns < NS / 2) ? wave_n * 64 + ns * 32 : BN / 2 + wave_n * 64 + (ns - NS / 2) * 32)
-                     : wave_n * 128 + ns * 32;
+  for (int ns = 0; ns < NS; ++ns) {
+    nbase[ns] = pair ? ((ns < NS / 2) ? wave_n * (WCOL / 2) + ns * 32 : BN / 2 + wave_n * (WCOL / 2) + (ns - NS / 2) * 32)
+                     : wave_n * WCOL + ns * 32;
+    bpar[ns] = ((nbase[ns] >> 5) & 1) << 5;
+  }
   const int a_frag = (wave_m * 128 + (lane & 31)) * kTileK;
   const int w_frag = (lane & 31) * kTileK;
   auto read_frags = [&](int buf, int ks, uint4 (&av)[MS], uint4 (&bv)[NS]) {
@@ -234,7 +252,7 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
       av[ms] = *reinterpret_cast<const uint4*>(&As[buf][a_frag + ms * 32 * kTileK + (fcol ^ ((ms & 1) << 5))]);
 #pragma unroll
     for (int ns = 0; ns < NS; ++ns)
-      bv[ns] = *reinterpret_cast<const uint4*>(&Ws[buf][w_frag + nbase[ns] * kTileK + (fcol ^ ((ns & 1) << 5))]);
+      bv[ns] = *reinterpret_cast<const uint4*>(&Ws[buf][w_frag + nbase[ns] * kTileK + (fcol ^ bpar[ns])]);
   };
   auto mfma_row = [&](int ms, const uint4 (&av)[MS], const uint4 (&bv)[NS]) {
     static_for<NS>([&](auto ns) { acc[ms][ns] = mfma_32x32x16<CT>(av[ms], bv[ns], acc[ms][ns]); });
@@ -249,15 +267,17 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
   const int64_t klast = ksteps - 1;
   // Prologue: step 0 staged whole into buffer 0; of step 1, the part an iteration's sub-step 3
   // stages (the weight row's code planes, its first two words, the activation row).
-  static_assert(ST == 2, "step s lives in register set s % 2");
-  load_step(0, 0);
-  load_step(1, min<int64_t>(1, klast));
+  static_assert(ST == 2, "step s lives in weight register set s % 2");
+  load_a_all(0);
+  load_w(0, 0);
+  load_w(1, min<int64_t>(1, klast));
   __syncthreads();  // code2 table
   stage(0, 0, block_scale(0));
-  load_step(0, min<int64_t>(2, klast));
+  load_a_all(min<int64_t>(1, klast));
+  load_w(0, min<int64_t>(2, klast));
   NibPlanes tp = planes(block_scale(1));
 #pragma unroll
-  for (int i = 0; i < 8; ++i) store_a(1, 1, i);
+  for (int i = 0; i < AP; ++i) store_a(1, i);
   store_w(1, 1, 0, tp);
   store_w(1, 1, 1, tp);
   __syncthreads();
@@ -276,17 +296,28 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
     constexpr int sS = (u + 1) % ST;  // register set of step kb + 1, whose staging ends here
     constexpr int sT = u;             // register set of step kb + 2, whose staging starts here
     const int cur = static_cast<int>(kb & 1);
-    // sub-step 0
+    // sub-step 0 (the activation registers were staged in the previous sub-step 3: the loads of
+    // step kb + 2's activations go out here, two per chunk, and are staged in sub-step 3)
+    const int64_t knext = min<int64_t>(kb + 1 + ST, klast);
+    const int64_t ka = min<int64_t>(kb + 2, klast);
     read_frags(cur, 1, fa1, fb1);
     mfma_row(0, fa0, fb0);
     store_w(sS, cur ^ 1, 2, tp);
+    load_a(ka, 0);
+    load_a(ka, 1);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(1, fa0, fb0);
+    load_a(ka, 2);
+    load_a(ka, 3);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(2, fa0, fb0);
     store_w(sS, cur ^ 1, 3, tp);
+    load_a(ka, 4);
+    load_a(ka, 5);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(3, fa0, fb0);
+    load_a(ka, 6);
+    load_a(ka, 7);
     __builtin_amdgcn_sched_barrier(0);
     // sub-step 1
     read_frags(cur, 2, fa0, fb0);
@@ -309,7 +340,7 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
     store_w(sS, cur ^ 1, 7, tp);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(2, fa0, fb0);
-    load_step(sS, min<int64_t>(kb + 1 + ST, klast));
+    load_w(sS, knext);  // the weight registers of set sS are free after word 7
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(3, fa0, fb0);
     __syncthreads();
@@ -318,22 +349,22 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
     read_frags(cur ^ 1, 0, fa0, fb0);
     mfma_row(0, fa1, fb1);
     tp = planes(sc);
-    store_a(sT, cur, 0);
-    store_a(sT, cur, 1);
+    store_a(cur, 0);
+    store_a(cur, 1);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(1, fa1, fb1);
     store_w(sT, cur, 0, tp);
-    store_a(sT, cur, 2);
-    store_a(sT, cur, 3);
+    store_a(cur, 2);
+    store_a(cur, 3);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(2, fa1, fb1);
     store_w(sT, cur, 1, tp);
-    store_a(sT, cur, 4);
-    store_a(sT, cur, 5);
+    store_a(cur, 4);
+    store_a(cur, 5);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(3, fa1, fb1);
-    store_a(sT, cur, 6);
-    store_a(sT, cur, 7);
+    store_a(cur, 6);
+    store_a(cur, 7);
     __builtin_amdgcn_sched_barrier(0);
   };
   const int64_t kmain = ksteps - ksteps % ST;
@@ -344,8 +375,11 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
   if (kmain < ksteps) iteration(std::integral_constant<int, 0>{}, kmain);
 
   // Epilogue. Tile row of accumulator register i of MFMA tile ms; the lane's column is
-  // nbase[ns] + (lane & 31).
-  auto row_of = [&](int ms, int i) { return wave_m * 128 + ms * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); };
+  // nbase[ns] + (lane & 31). The lane index is formed again here (v_mbcnt): values kept from
+  // before the loop would be spilled across it, and a scratch reload in the epilogue waits for
+  // every store issued before it.
+  const int lane_e = static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+  auto row_of = [&](int ms, int i) { return wave_m * 128 + ms * 32 + 8 * (i >> 2) + 4 * (lane_e >> 5) + (i & 3); };
   if constexpr (F16C) {
     static_for<MS>([&](auto ms) {
       static_for<16>([&](auto i) {
@@ -354,53 +388,26 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
       });
     });
   }
-  // fp16 mode, gate_up: the largest h exponent of each tile row over the 32 lanes that hold it
-  // (a DPP max within each 16-lane row, then across the pair of rows), folded into the block's
-  // row maxima and then into out_exp (atomicMax: independent of order)
-  const bool collect = F16C && p.out_exp != nullptr;
-  auto note_row_exp = [&](int lr, uint32_t hm) {
-    auto dpp_max = [](uint32_t v, auto ctrl) {
-      return max(v, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), decltype(ctrl)::value,
-                                                                       0xf, 0xf, false)));
-    };
-    hm = dpp_max(hm, std::integral_constant<int, 0xb1>{});   // quad_perm [1,0,3,2]
-    hm = dpp_max(hm, std::integral_constant<int, 0x4e>{});   // quad_perm [2,3,0,1]
-    hm = dpp_max(hm, std::integral_constant<int, 0x141>{});  // row_half_mirror
-    hm = dpp_max(hm, std::integral_constant<int, 0x140>{});  // row_mirror
-    hm = max(hm, static_cast<uint32_t>(__shfl_xor(static_cast<int>(hm), 16)));
-    if ((lane & 31) == 0 && hm != 0) atomicMax(&hexp_s[lr], static_cast<int>(hm));
-  };
-  auto flush_row_exps = [&]() {
-    __syncthreads();
-    if (row0 + tid < row_end && hexp_s[tid] != 0) atomicMax(&p.out_exp[row0 + tid], hexp_s[tid]);
-  };
   const bool has_bias = p.w.bias != nullptr;
   const uint16_t* bias = static_cast<const uint16_t*>(p.w.bias);
   if (pair && p.epi == E4B_EPI_SWIGLU && !has_bias && !p.out_f32) {  // gate_up: silu(g) * u -> dt
     uint16_t* const out = static_cast<uint16_t*>(p.out);
-    const int64_t cbase = col0 + wave_n * 64 + (lane & 31);
+    const int64_t cbase = col0 + wave_n * (WCOL / 2) + (lane_e & 31);
     static_for<MS>([&](auto ms) {
       static_for<16>([&](auto i) {
-        const int lr = row_of(ms, i);
-        const int rr = row0 + lr;
+        const int rr = row0 + row_of(ms, i);
         uint16_t* const orow = out + int64_t(rr) * p.n_out + cbase;
-        uint32_t hm = 0;
         static_for<NS / 2>([&](auto ns) {
           const float v = silu_f32(acc[ms][ns][int(i)]) * acc[ms][ns + NS / 2][int(i)];
-          const uint16_t hb = from_f<DT>(v);
-          const bool st = rr < row_end && cbase + ns * 32 < p.n_out;
-          if (st) orow[ns * 32] = hb;
-          if (collect && st) hm = max(hm, (static_cast<uint32_t>(hb) >> 7) & 0xffu);
+          if (rr < row_end && cbase + ns * 32 < p.n_out) orow[ns * 32] = from_f<DT>(v);
         });
-        if (collect) note_row_exp(lr, hm);
       });
     });
-    if (collect) flush_row_exps();
     return;
   }
   if (!pair && p.epi == E4B_EPI_NONE && !has_bias && p.out_f32) {  // down: fp32 rows
     float* const out = static_cast<float*>(p.out);
-    const int64_t cbase = col0 + wave_n * 128 + (lane & 31);
+    const int64_t cbase = col0 + wave_n * WCOL + (lane_e & 31);
     static_for<MS>([&](auto ms) {
       static_for<16>([&](auto i) {
         const int rr = row0 + row_of(ms, i);
@@ -412,46 +419,61 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
     });
     return;
   }
-  // general path; in fp16 mode a gate_up output (never fp32 there) also notes its exponents
-  auto put = [&](int64_t idx, float v, uint32_t& hm) {
-    if (collect) {
-      const uint16_t hb = from_f<DT>(v);
-      static_cast<uint16_t*>(p.out)[idx] = hb;
-      hm = max(hm, (static_cast<uint32_t>(hb) >> 7) & 0xffu);
-    } else {
-      store_elem<DT>(p, idx, v);
-    }
-  };
+  // general path
   static_for<MS>([&](auto ms) {
     static_for<16>([&](auto i) {
-      const int lr = row_of(ms, i);
-      const int rr = row0 + lr;
-      uint32_t hm = 0;
-      if (rr < row_end) {  // the 32 lanes of a row agree, so the reduction below is not split
+      const int rr = row0 + row_of(ms, i);
+      if (rr < row_end) {
         const int64_t orow = int64_t(rr) * p.n_out;
         if (pair) {
           static_for<NS / 2>([&](auto ns) {
-            const int64_t jj = col0 + wave_n * 64 + ns * 32 + (lane & 31);
+            const int64_t jj = col0 + wave_n * (WCOL / 2) + ns * 32 + (lane_e & 31);
             if (jj < p.n_out) {
               const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + jj]) : 0.0f;
               const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + n / 2 + jj]) : 0.0f;
-              put(orow + jj, gated(p.epi, acc[ms][ns][int(i)], acc[ms][ns + NS / 2][int(i)], p.alpha, p.limit, bg, bu), hm);
+              store_elem<DT>(p, orow + jj,
+                             gated(p.epi, acc[ms][ns][int(i)], acc[ms][ns + NS / 2][int(i)], p.alpha, p.limit, bg, bu));
             }
           });
         } else {
           static_for<NS>([&](auto ns) {
-            const int64_t nn = col0 + wave_n * 128 + ns * 32 + (lane & 31);
+            const int64_t nn = col0 + wave_n * WCOL + ns * 32 + (lane_e & 31);
             if (nn < p.n_out) {
               const float b = has_bias ? to_f<DT>(bias[int64_t(e) * n + nn]) : 0.0f;
-              put(orow + nn, single(p.epi, acc[ms][ns][int(i)], b), hm);
+              store_elem<DT>(p, orow + nn, single(p.epi, acc[ms][ns][int(i)], b));
             }
           });
         }
       }
-      if (collect) note_row_exp(lr, hm);
     });
   });
-  if (collect) flush_row_exps();
+}
+
+template <int DT, int FMT, bool F16C = false>
+__global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
+  static_assert(!F16C || (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4), "fp16 mode: bf16 activations, NF4 weights");
+  constexpr int BM = kWideTileM, BN = kWideTileN;
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kTileK];
+  __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kTileK];
+  __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
+  __shared__ int row_shift_s[F16C ? BM : 1];
+  __shared__ uint32_t ptab[F16C ? 256 * kPairCopies : 1];
+  const int cols = is_gated(p.epi) ? BN / 2 : BN;
+  const int n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
+  int tile, n_tile;
+  if (!wide_tile_of_block(p.rt.meta[0], n_tiles, tile, n_tile)) return;
+  if constexpr (F16C) {
+    // the table of code pairs: pass j fills entries 16 j .. 16 j + 15, all copies; entry
+    // 16 j + t / 16 of copy t % 16 (high nibble j, low nibble t / 16)
+    static_assert(kWideThreads == 16 * kPairCopies, "table fill");
+    const float lo = p.w.code[threadIdx.x / kPairCopies];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) ptab[j * kWideThreads + threadIdx.x] = cvt_pair<E4B_FP16>(p.w.code[j], lo);
+  }
+  const int e = p.rt.tiles[2 * tile];
+  const int rows = p.rt.offsets[e + 1] - p.rt.tiles[2 * tile + 1];  // the tile's rows, capped at BM below
+  if (rows <= BM / 2) wide_tile<DT, FMT, F16C, true>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
+  else wide_tile<DT, FMT, F16C, false>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
 }
 
 }  // namespace e4b

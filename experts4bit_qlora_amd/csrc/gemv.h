@@ -29,14 +29,11 @@ struct GemmArgs {
   void* out;          // [M, n_out] in the activation dtype, or fp32 when out_f32
   int64_t n_out;
   int out_f32;
-  // fp16 matrix-core mode (MFMA kernel, bf16 activations, NF4 weights with w.shift): the
-  // largest biased exponent of every A row, indexed like the A rows themselves (token when
-  // gather_k > 0, else sorted row); NULL selects the bf16 mode.
+  // fp16 matrix-core mode (MFMA kernels, bf16 activations, NF4 weights with w.shift): the A
+  // rows are stored as fp16, each scaled by 2^exp_shift(a_exp[row]) (row_exp_kernel), a_exp
+  // indexed like the A rows themselves (token when gather_k > 0, else sorted row); NULL selects
+  // the bf16 mode.
   const int32_t* a_exp;
-  int a_f16;  // fp16 mode: the A rows are already fp16 scaled by their row shift (row_exp_kernel)
-  // gate_up in fp16 mode: per sorted row, atomicMax of the biased exponents of the h values
-  // stored (the down GEMM's a_exp); zeroed beforehand. NULL: not collected.
-  int32_t* out_exp;
 };
 
 // Store one output element: fp32, or rounded once into the activation dtype.

@@ -473,9 +473,11 @@ __global__ void __launch_bounds__(kRouteThreads) route_groups_kernel(GroupOffset
 // costs about the same whatever its height until its MFMA work catches up with its weight
 // decoding (the whole expert matrix per tile), so every expert keeps big tiles
 // (`big.tile_m` rows, the last one partial) unless its last big tile would hold at most
-// `small.tile_m` rows: those rows go to one small tile instead. One 512-thread block; thread t
-// owns experts 2t and 2t + 1. meta[1] / meta[2] (active, dropped) are copied from the routing
-// the offsets came from.
+// `small.tile_m` rows: those rows go to one small tile instead. The big list holds every
+// expert's full tiles first, then the partial ones, so a grid that takes the list in order runs
+// the long tiles first and the short ones last. One 512-thread block; thread t owns experts 2t
+// and 2t + 1. meta[1] / meta[2] (active, dropped) are copied from the routing the offsets came
+// from.
 __global__ void __launch_bounds__(kRouteThreads) split_tiles_kernel(const int32_t* __restrict__ offsets,
                                                                    const int32_t* __restrict__ meta, int E,
                                                                    e4b_routing big, e4b_routing small) {
@@ -485,31 +487,39 @@ __global__ void __launch_bounds__(kRouteThreads) split_tiles_kernel(const int32_
   const int oa = ea < E ? offsets[ea] : 0, ob = eb < E ? offsets[eb] : 0;
   const int ca = ea < E ? offsets[ea + 1] - oa : 0, cb = eb < E ? offsets[eb + 1] - ob : 0;
   const int bt = big.tile_m, st = small.tile_m;
-  // remainder past the full big tiles: one more big tile, or one small tile when it fits
+  // remainder past the full big tiles: one partial big tile, or one small tile when it fits
   const int ra = ca % bt, rb = cb % bt;
   const int nsa = (ra > 0 && ra <= st) ? 1 : 0, nsb = (rb > 0 && rb <= st) ? 1 : 0;
-  const int nba = ca / bt + (ra > st ? 1 : 0), nbb = cb / bt + (rb > st ? 1 : 0);
-  int nbig, nsmall;
-  const int b0 = block_exclusive_scan(nba + nbb, &nbig, wsum);
+  const int nfa = ca / bt, nfb = cb / bt;                        // full big tiles
+  const int npa = ra > st ? 1 : 0, npb = rb > st ? 1 : 0;        // partial big tiles
+  int nfull, npart, nsmall;
+  const int f0 = block_exclusive_scan(nfa + nfb, &nfull, wsum);
+  const int p0 = block_exclusive_scan(npa + npb, &npart, wsum);
   const int s0 = block_exclusive_scan(nsa + nsb, &nsmall, wsum);
-  for (int j = 0; j < nba + nbb; ++j) {
-    const int t = b0 + j;
-    const bool in_a = j < nba;
+  auto put_big = [&](int t, int e, int row) {
     if (t < big.max_tiles) {
-      big.tiles[2 * t] = in_a ? ea : eb;
-      big.tiles[2 * t + 1] = in_a ? oa + j * bt : ob + (j - nba) * bt;
+      big.tiles[2 * t] = e;
+      big.tiles[2 * t + 1] = row;
     }
+  };
+  for (int j = 0; j < nfa + nfb; ++j) {
+    const bool in_a = j < nfa;
+    put_big(f0 + j, in_a ? ea : eb, in_a ? oa + j * bt : ob + (j - nfa) * bt);
+  }
+  for (int j = 0; j < npa + npb; ++j) {
+    const bool in_a = j < npa;
+    put_big(nfull + p0 + j, in_a ? ea : eb, in_a ? oa + nfa * bt : ob + nfb * bt);
   }
   for (int j = 0; j < nsa + nsb; ++j) {
     const int t = s0 + j;
     const bool in_a = j < nsa;
     if (t < small.max_tiles) {
       small.tiles[2 * t] = in_a ? ea : eb;
-      small.tiles[2 * t + 1] = in_a ? oa + nba * bt : ob + nbb * bt;  // at most one small tile per expert
+      small.tiles[2 * t + 1] = in_a ? oa + nfa * bt : ob + nfb * bt;  // at most one small tile per expert
     }
   }
   if (tid == 0) {
-    big.meta[0] = min(nbig, big.max_tiles);
+    big.meta[0] = min(nfull + npart, big.max_tiles);
     small.meta[0] = min(nsmall, small.max_tiles);
     big.meta[1] = small.meta[1] = meta[1];
     big.meta[2] = small.meta[2] = meta[2];
