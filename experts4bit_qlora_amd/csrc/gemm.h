@@ -26,11 +26,12 @@
 // only store.
 //
 // fp16 mode (F16C, bf16 activations with NF4 weights): the MFMAs multiply fp16 operands. The
-// weights are decoded as fp16(fl32(code * absmax) * 2^shift[e]) -- one rounding, 2^-11 relative
-// where the bf16 weight carries 2^-8 -- and the A rows arrive as their bf16 values times
-// 2^exp_shift(row exponent), exact in fp16 (row_exp_kernel). The accumulators are scaled back
-// by 2^-(row shift + expert shift) before the epilogue, so the results are those of the exact
-// weights to within fp16's rounding of each weight.
+// weights are decoded through the LDS table of code pairs as
+// fp16(fp16(code) * fp16(absmax * 2^shift[e])) -- three fp16 roundings, at most 3 * 2^-11
+// relative where the bf16 weight carries 2^-8 -- and the A rows arrive as their bf16 values
+// times 2^exp_shift(row exponent), exact in fp16 (row_exp_kernel). The accumulators are scaled
+// back by 2^-(row shift + expert shift) before the epilogue, so the results are those of the
+// exact weights to within those roundings.
 #pragma once
 
 #include "common.h"
@@ -272,6 +273,9 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kTileK];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
   __shared__ int row_shift_s[F16C ? BM : 1];  // fp16 mode: each tile row's activation shift
+  // fp16 mode: the LDS table of code pairs (see kPairCopies), PC copies
+  constexpr int PC = BM == kTileMSmall ? 8 : kPairCopies;
+  __shared__ uint32_t ptab[F16C ? 256 * PC : 1];
 
   const int num_tiles = p.rt.meta[0];
   const int n_tiles = static_cast<int>((p.n_out + (is_gated(p.epi) ? BN / 2 : BN) - 1) /
@@ -298,6 +302,17 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   for (int i = 0; i < 16; ++i) code[i] = (FMT == E4B_FMT_MXFP4) ? kFp4E2M1[i] : p.w.code[i];
   if constexpr (FMT == E4B_FMT_NF4_DQ) {
     if (tid < 256) code2_s[tid] = p.w.code2[tid];
+  }
+  if constexpr (F16C) {
+    // pass j fills entries 32 j .. 32 j + 31 (all copies): this thread's entry is
+    // 32 j + tid / PC, high nibble 2 j + (tid / PC) / 16, low nibble (tid / PC) % 16
+    static_assert(NT / PC == 32, "table fill");
+    const int t = tid / PC;
+    const float lo = p.w.code[t & 15];
+    const bool odd = t >= 16;
+#pragma unroll
+    for (int j = 0; j < 256 * PC / NT; ++j)
+      ptab[j * NT + tid] = cvt_pair<E4B_FP16>(odd ? code[2 * j + 1] : code[2 * j], lo);
   }
 
   // A assignment: row tid / TPR, AV * 8 activations at column (tid % TPR) * AV * 8.
@@ -392,7 +407,19 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
     }
     if constexpr (F16C) scale = __builtin_amdgcn_ldexpf(scale, wsh);  // exact: a power of two
     uint32_t wv[WB];
-    dequant_bytes<CT, FMT, WB, !F16C>(wq[set], code, scale, wv);
+    if constexpr (F16C) {
+      // table decode: every lookup first, then the multiplies by the scale pair
+      const uint32_t s2 = cvt_pair<E4B_FP16>(scale, scale);
+      const uint32_t* tab = ptab + (lane & (PC - 1));
+#pragma unroll
+      for (int wi = 0; wi < WB / 4; ++wi)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) wv[4 * wi + b] = tab[((wq[set][wi] >> (8 * b)) & 0xffu) * PC];
+#pragma unroll
+      for (int i = 0; i < WB; ++i) wv[i] = pk_mul_f16(wv[i], s2);
+    } else {
+      dequant_bytes<CT, FMT, WB, !F16C>(wq[set], code, scale, wv);
+    }
     // the swizzled store addresses are recomputed every step (a few integer ops): held across
     // the loop they would take registers the pipeline needs
     int wr = lrow, arow = ar;
@@ -457,7 +484,7 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
     read_frags(cur, 1, fa1, fb1);
     mfmas(fa0, fb0);
     stage((u + 1) % ST, cur ^ 1);
-    constexpr int kValu = (WB == 16 ? 200 : 136) / (MS * NS);
+    constexpr int kValu = (F16C ? 48 : WB == 16 ? 200 : 136) / (MS * NS);
 #pragma unroll
     for (int i = 0; i < MS * NS; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      // one MFMA

@@ -200,19 +200,32 @@ E4B_DEV void wide_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2
     if (i >= AP) return;  // (i is a constant at every call)
     *reinterpret_cast<u32x4_t*>(&As[buf][lds_at_w(32 * i + (tid >> 3), 8 * apart)]) = areg[i];
   };
-  auto store_w = [&](int set, int buf, int wi, const NibPlanes& t) {
-    uint32_t o[4];
+  // A weight word in two halves, so the table lookups of the fp16 mode can be issued a chunk
+  // before the multiplies that wait for them: fetch_w leaves in r the looked-up code pairs
+  // (fp16 mode) or the decoded values, put_w applies the scale pair t.lo[0] (fp16 mode) and
+  // stores the word's eight values.
+  auto fetch_w = [&](int set, int wi, const NibPlanes& t, uint32_t (&r)[4]) {
     if constexpr (FMT == E4B_FMT_MXFP4) {  // words 0-3: the first 32-value block, 4-7: the second
-      fp4_word<CT>(wq[set][wi], e8m0_to_f32(wi < 4 ? (sq[set] & 0xffu) : (sq[set] >> 8)), o);
-    } else if constexpr (PTAB) {  // byte b's code pair from the lane's table copy, times the scale pair t.lo[0]
+      fp4_word<CT>(wq[set][wi], e8m0_to_f32(wi < 4 ? (sq[set] & 0xffu) : (sq[set] >> 8)), r);
+    } else if constexpr (PTAB) {  // byte b's code pair from the lane's table copy
       const uint32_t* tab = ptab + (lane & (kPairCopies - 1));
       const uint32_t w = wq[set][wi];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) o[b] = pk_mul_f16(tab[((w >> (8 * b)) & 0xffu) * kPairCopies], t.lo[0]);
+      for (int b = 0; b < 4; ++b) r[b] = tab[((w >> (8 * b)) & 0xffu) * kPairCopies];
     } else {
-      nib_word<FMT>(t, wq[set][wi], o);
+      nib_word<FMT>(t, wq[set][wi], r);
     }
+  };
+  auto put_w = [&](int buf, int wi, const NibPlanes& t, const uint32_t (&r)[4]) {
+    uint32_t o[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) o[b] = PTAB ? pk_mul_f16(r[b], t.lo[0]) : r[b];
     *reinterpret_cast<uint4*>(&Ws[buf][lds_at_w(tid, 8 * wi)]) = make_uint4(o[0], o[1], o[2], o[3]);
+  };
+  auto store_w = [&](int set, int buf, int wi, const NibPlanes& t) {
+    uint32_t r[4];
+    fetch_w(set, wi, t, r);
+    put_w(buf, wi, t, r);
   };
   auto planes = [&](float scale) {
     if constexpr (FMT == E4B_FMT_MXFP4) {
@@ -280,6 +293,8 @@ E4B_DEV void wide_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2
   for (int i = 0; i < AP; ++i) store_a(1, i);
   store_w(1, 1, 0, tp);
   store_w(1, 1, 1, tp);
+  uint32_t lk[4];  // a word's fetched half, carried to the next chunk
+  fetch_w(1, 2, tp, lk);
   __syncthreads();
   uint4 fa0[MS], fb0[NS], fa1[MS], fb1[NS];
   read_frags(0, 0, fa0, fb0);
@@ -302,7 +317,8 @@ E4B_DEV void wide_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2
     const int64_t ka = min<int64_t>(kb + 2, klast);
     read_frags(cur, 1, fa1, fb1);
     mfma_row(0, fa0, fb0);
-    store_w(sS, cur ^ 1, 2, tp);
+    put_w(cur ^ 1, 2, tp, lk);
+    fetch_w(sS, 3, tp, lk);
     load_a(ka, 0);
     load_a(ka, 1);
     __builtin_amdgcn_sched_barrier(0);
@@ -311,54 +327,63 @@ E4B_DEV void wide_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2
     load_a(ka, 3);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(2, fa0, fb0);
-    store_w(sS, cur ^ 1, 3, tp);
+    put_w(cur ^ 1, 3, tp, lk);
+    fetch_w(sS, 4, tp, lk);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_row(3, fa0, fb0);
     load_a(ka, 4);
     load_a(ka, 5);
     __builtin_amdgcn_sched_barrier(0);
-    mfma_row(3, fa0, fb0);
-    load_a(ka, 6);
-    load_a(ka, 7);
-    __builtin_amdgcn_sched_barrier(0);
-    // sub-step 1
+    // sub-step 1 (with the block scale of step kb + 2, whose set sT was loaded a step ago: its
+    // code2 read is then long done when sub-step 3 stages the step)
     read_frags(cur, 2, fa0, fb0);
     mfma_row(0, fa1, fb1);
-    store_w(sS, cur ^ 1, 4, tp);
+    put_w(cur ^ 1, 4, tp, lk);
+    fetch_w(sS, 5, tp, lk);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(1, fa1, fb1);
+    load_a(ka, 6);
+    load_a(ka, 7);
+    const float sc = block_scale(sT);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(2, fa1, fb1);
-    store_w(sS, cur ^ 1, 5, tp);
+    put_w(cur ^ 1, 5, tp, lk);
+    fetch_w(sS, 6, tp, lk);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(3, fa1, fb1);
     __builtin_amdgcn_sched_barrier(0);
     // sub-step 2
     read_frags(cur, 3, fa1, fb1);
     mfma_row(0, fa0, fb0);
-    store_w(sS, cur ^ 1, 6, tp);
+    put_w(cur ^ 1, 6, tp, lk);
+    fetch_w(sS, 7, tp, lk);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(1, fa0, fb0);
-    store_w(sS, cur ^ 1, 7, tp);
+    put_w(cur ^ 1, 7, tp, lk);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(2, fa0, fb0);
     load_w(sS, knext);  // the weight registers of set sS are free after word 7
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(3, fa0, fb0);
+    const NibPlanes tn = planes(sc);  // step kb + 2's planes, while this step's are still in use
     __syncthreads();
-    // sub-step 3: the block scale first (its code2 read then waits for no fragment read)
-    const float sc = block_scale(sT);
+    // sub-step 3
     read_frags(cur ^ 1, 0, fa0, fb0);
     mfma_row(0, fa1, fb1);
-    tp = planes(sc);
+    tp = tn;
     store_a(cur, 0);
     store_a(cur, 1);
+    fetch_w(sT, 0, tp, lk);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(1, fa1, fb1);
-    store_w(sT, cur, 0, tp);
+    put_w(cur, 0, tp, lk);
+    fetch_w(sT, 1, tp, lk);
     store_a(cur, 2);
     store_a(cur, 3);
     __builtin_amdgcn_sched_barrier(0);
     mfma_row(2, fa1, fb1);
-    store_w(sT, cur, 1, tp);
+    put_w(cur, 1, tp, lk);
+    fetch_w(sT, 2, tp, lk);
     store_a(cur, 4);
     store_a(cur, 5);
     __builtin_amdgcn_sched_barrier(0);
