@@ -3,6 +3,7 @@
 // pair, in parallel).
 #include "gemm.h"
 #include "gemm_launch.h"
+#include "gemm_narrow.h"
 #include "gemm_wide.h"
 
 #ifndef E4B_INST_DT
@@ -41,15 +42,25 @@ void launch_mfma_bm(const GemmArgs& a, dim3 grid, hipStream_t s) {
   launch_mfma_kernel<DT, FMT, BM, false>(a, grid, s);
 }
 
+// 8 XCDs x ceil(max_tiles / 8) M tiles x n_tiles blocks (tiles of nw weight rows), mapped to
+// tiles in the kernel
+dim3 gemm_grid(const GemmArgs& a, int64_t nw) {
+  const int64_t cols = is_gated(a.epi) ? nw / 2 : nw;
+  return dim3(static_cast<unsigned>(kXcds * cdiv(a.rt.max_tiles, kXcds) * cdiv(a.n_out, cols)));
+}
+
 }  // namespace
 
 template <int DT, int FMT>
 void launch_mfma_gemm(const GemmArgs& a, hipStream_t s) {
-  const int64_t nw = gemm_tile_nw(a.rt.tile_m);
-  const int64_t cols = is_gated(a.epi) ? nw / 2 : nw;
-  // 8 XCDs x ceil(max_tiles / 8) M tiles x n_tiles blocks, mapped to tiles in the kernel
-  const int64_t n_tiles = cdiv(a.n_out, cols);
-  dim3 grid(static_cast<unsigned>(kXcds * cdiv(a.rt.max_tiles, kXcds) * n_tiles));
+  if constexpr (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4) {
+    // 32-row tiles in the fp16 mode: the narrow kernel, when K is a whole number of its steps
+    if (a.rt.tile_m == kTileMSmall && a.a_exp && narrow_fits(a.w.k)) {
+      hipLaunchKernelGGL((gemm_narrow_kernel<FMT>), gemm_grid(a, kNarrowN), dim3(kNarrowThreads), 0, s, a);
+      return;
+    }
+  }
+  const dim3 grid = gemm_grid(a, gemm_tile_nw(a.rt.tile_m));
   if (a.rt.tile_m == kTileMSmall) launch_mfma_bm<DT, FMT, kTileMSmall>(a, grid, s);
   else if (a.rt.tile_m == kTileMBig) launch_mfma_bm<DT, FMT, kTileMBig>(a, grid, s);
   else launch_mfma_bm<DT, FMT, kTileM>(a, grid, s);

@@ -771,6 +771,39 @@ def test_fp16_matrix_core_mode_keeps_the_bf16_range(xscale, wscale, dq):
     _assert_fidelity(got, ref, _oracle(mod, x, idx, w), f"fp16 mode x*{xscale} w*{wscale} dq={dq}")
 
 
+@pytest.mark.parametrize("H,I,dq", [(1024, 192, False), (384, 256, True), (1280, 512, False), (1792, 640, True)])
+def test_narrow_tiles_in_fp16_mode(H, I, dq):
+    """32-row tiles in the fp16 mode with K a multiple of 256 (the narrow kernel: pairs of 128-deep
+    steps, the weight bytes decoded in the MFMA operand layout): 2 to 14 steps (the loop's six-step
+    passes and its two- and four-step tails), partial column tiles (n_out 192 and 384 against 128
+    gated / 256 plain columns per tile), experts with more than one 32-row tile, NF4 and double
+    quantization; the GEMMs whose K is not a multiple of 256 (192, 384, 640) take the 32-row MFMA
+    kernel in the same forward."""
+    _announce(f"narrow tiles H={H} I={I} dq={dq}")
+    E, k, T = 16, 4, 48
+    g = torch.Generator().manual_seed(H + I + dq)
+    gu = torch.randn(E, 2 * I, H, generator=g) * 0.05
+    dn = torch.randn(E, H, I, generator=g) * 0.05
+    mod = e4b.Experts4bit.from_float(gu.to(DEV), dn.to(DEV), compute_dtype=torch.bfloat16,
+                                     compress_statistics=dq).eval()
+    del gu, dn
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(DEV)
+    # a skewed routing: expert 0 in every token (48 rows: two tiles), the rest spread
+    scores = torch.randn(T, E, generator=g)
+    scores[:, 0] += 100.0
+    val, idx = torch.topk(scores, k, dim=-1)
+    w = torch.softmax(val - val[:, :1], -1).to(torch.bfloat16).to(DEV)
+    idx = idx.to(DEV)
+    with torch.no_grad():
+        ref = mod(x, idx, w)
+        assert e4b.enable_fast(mod) == 1
+        w1, w2 = F._qweights(mod)
+        assert w1.shift is not None and w2.shift is not None  # the fp16 mode is on
+        got = mod(x, idx, w)
+    assert torch.isfinite(got).all()
+    _assert_fidelity(got, ref, _oracle(mod, x, idx, w), f"narrow tiles H={H} I={I} dq={dq}")
+
+
 def test_weight_shift_matches_the_oracle_exponents():
     """e4b_weight_shift: 141 - max(E, 20), E the largest biased exponent of each expert's block
     scales (decoded ones for double quantization), from the oracle's decode of the same bytes."""
