@@ -267,8 +267,10 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg):
     eager forwards: algorithmic FLOP of each launch (the rows its tiles hold, both gate_up halves)
     / its average duration, against the dense bf16/fp16 peak. The 256-row tiles
     (gemm_wide_kernel) carry every expert's rows except a last tile of at most 32 rows, which the
-    32-row launch (gemm_mfma_kernel) takes; each forward runs gate_up then down with each kernel,
-    so a kernel's calls alternate between the two projections in time order."""
+    32-row launch (gemm_narrow_kernel) takes; each forward runs gate_up then down with each kernel,
+    so a kernel's calls alternate between the two projections in time order. The 32-row launches
+    stream a whole expert's weights per tile for a few rows: their entries also carry the weight
+    bytes of those tiles and the HBM rate."""
     import collections
 
     import torch
@@ -280,6 +282,13 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg):
     rows = {256: sum(counts) - sum(tail), 32: sum(tail)}
     flop = {(bm, "gate_up"): 2 * r * 2 * I * H for bm, r in rows.items()}
     flop.update({(bm, "down"): 2 * r * H * I for bm, r in rows.items()})
+    # weight bytes per expert and projection (the prefill layer is double-quantized NF4)
+    n_tail = sum(1 for t in tail if t)
+
+    def proj_bytes(n, k):
+        nb = n * k // 64
+        return n * k // 2 + nb + math.ceil(nb / 256) * 4 + 4
+    tail_bytes = {"gate_up": n_tail * proj_bytes(2 * I, H), "down": n_tail * proj_bytes(H, I)}
     with torch.no_grad():
         mod(x, idx, w)
         torch.cuda.synchronize()
@@ -290,12 +299,18 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg):
     calls = collections.defaultdict(list)
     for ev in prof.events():
         if ev.device_type == torch.autograd.DeviceType.CUDA and ("gemm_wide_kernel" in ev.name or
+                                                                 "gemm_narrow_kernel" in ev.name or
                                                                  "gemm_mfma_kernel" in ev.name):
             t = getattr(ev, "device_time", None)
             calls[ev.name.split("(")[0]].append((ev.time_range.start, t if t is not None else ev.cuda_time))
     durs = collections.defaultdict(list)
     for name, cs in calls.items():
-        bm = 256 if "gemm_wide_kernel" in name else int(name[name.index("<") + 1:name.index(">")].split(",")[2])
+        if "gemm_wide_kernel" in name:
+            bm = 256
+        elif "gemm_narrow_kernel" in name:
+            bm = 32
+        else:
+            bm = int(name[name.index("<") + 1:name.index(">")].split(",")[2])
         for i, (_, d) in enumerate(sorted(cs)):
             durs[(name, bm, "gate_up" if i % 2 == 0 else "down")].append(d)
     out = {}
@@ -305,6 +320,10 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg):
         out[f"{proj}_{bm}row"] = {"kernel": name, "avg_launch_us": round(us, 2), "calls": len(d),
                                   "flop_per_launch": flop[(bm, proj)], "achieved": round(tf, 1),
                                   "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+        if bm == 32:  # whole experts' weights for a few rows each: the HBM view
+            gbs = tail_bytes[proj] / (us * 1e-6) / 1e9
+            out[f"{proj}_{bm}row"].update({"tiles": n_tail, "weight_bytes": tail_bytes[proj],
+                                           "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
     if not out:
         return None
     dom_key = max(out, key=lambda key: out[key]["avg_launch_us"])
@@ -377,6 +396,33 @@ def prefill_bench(steps, warmup):
     }
 
 
+def qwen3_decode_benches(steps, warmup, layers=8, batches=(1, 32, 256)):
+    """configs[2], Qwen3 decode with double-quant weights: a stack of layers per graph replay;
+    batch 1 runs the decode kernels, 32 and 256 the 32-row MFMA tiles (gemm_narrow_kernel)."""
+    import torch
+
+    import experts4bit_qlora_amd as e4b
+
+    out = {}
+    cfg = QWEN3
+    mods = [make_layer(cfg, seed=1000 + 200 + l, dq=True) for l in range(layers)]
+    for m in mods:
+        e4b.enable_fast(m)
+    per_expert = dq_expert_bytes(cfg["H"], cfg["I"])
+    for T in batches:
+        inputs = [make_inputs(cfg, T, seed=1000 + 210 + T + 7 * l) for l in range(layers)]
+
+        def step():
+            with torch.no_grad():
+                return [m(x, idx, w) for m, (x, idx, w) in zip(mods, inputs)]
+
+        g, _ = graph_of(step)
+        ms = time_graph(g, steps * 2, warmup) / layers
+        nbytes = sum(int(torch.unique(idx).numel()) for _, idx, _ in inputs) / layers * per_expert
+        out[f"qwen3_dq_bs{T}"] = {"us": ms * 1e3, "hbm_gbs": nbytes / (ms / 1e3) / 1e9, "layers": layers}
+    return out
+
+
 def extra_benches(steps, warmup, qwen_layers=8, gptoss_layers=4):
     """configs[2] (Qwen3 decode, double-quant) and configs[4] (gpt-oss MXFP4 + biases): a stack of
     layers (independent weights and inputs) per graph replay, as for the OLMoE decode step, so the
@@ -385,24 +431,7 @@ def extra_benches(steps, warmup, qwen_layers=8, gptoss_layers=4):
 
     import experts4bit_qlora_amd as e4b
 
-    out = {}
-    cfg = QWEN3
-    mods = [make_layer(cfg, seed=1000 + 200 + l, dq=True) for l in range(qwen_layers)]
-    for m in mods:
-        e4b.enable_fast(m)
-    per_expert = dq_expert_bytes(cfg["H"], cfg["I"])
-    for T in (1, 32, 256):
-        inputs = [make_inputs(cfg, T, seed=1000 + 210 + T + 7 * l) for l in range(qwen_layers)]
-
-        def step():
-            with torch.no_grad():
-                return [m(x, idx, w) for m, (x, idx, w) in zip(mods, inputs)]
-
-        g, _ = graph_of(step)
-        ms = time_graph(g, steps * 2, warmup) / qwen_layers
-        nbytes = sum(int(torch.unique(idx).numel()) for _, idx, _ in inputs) / qwen_layers * per_expert
-        out[f"qwen3_dq_bs{T}"] = {"us": ms * 1e3, "hbm_gbs": nbytes / (ms / 1e3) / 1e9, "layers": qwen_layers}
-    del mods
+    out = qwen3_decode_benches(steps, warmup, qwen_layers)
     torch.cuda.empty_cache()
     cfg = GPTOSS
     E, H, I = cfg["E"], cfg["H"], cfg["I"]
@@ -579,6 +608,8 @@ def main():
     ap.add_argument("--kernel-only", action="store_true", help="only the dominant-kernel loop (for profiling)")
     ap.add_argument("--prefill-only", action="store_true", help="only the configs[3] prefill (for profiling)")
     ap.add_argument("--train-only", action="store_true", help="only the training-lane leg (for profiling)")
+    ap.add_argument("--qwen-decode-only", action="store_true",
+                    help="only the configs[2] Qwen3 double-quant decode legs, batches 1, 32, 256 (for profiling)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for counter runs: the dominant kernel eagerly once per layer, then a 256 MiB "
                          "device copy whose counter reading calibrates bytes per counted KiB")
@@ -602,6 +633,9 @@ def main():
         return
     if args.train_only:
         print(json.dumps({"train": train_bench(args.steps, args.warmup)}), flush=True)
+        return
+    if args.qwen_decode_only:
+        print(json.dumps({"qwen3_decode": qwen3_decode_benches(args.steps, args.warmup)}), flush=True)
         return
     cfg = OLMOE
     log("building 16 OLMoE-geometry NF4 layers")

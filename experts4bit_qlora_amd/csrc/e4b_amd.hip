@@ -274,9 +274,10 @@ int mfma_tile_for(int64_t M, int E) {
   return M >= 64 * groups ? e4b::kTileM : e4b::kTileMSmall;
 }
 
-// Prefill re-tiling (split_tiles_kernel): 256-row tiles, except that an expert whose last
-// tile would hold at most 32 rows runs those rows in one 32-row tile.
-int64_t max_big_tiles(int64_t M, int E) { return max_tiles_for(M, E, e4b::kTileMBig); }
+// Prefill re-tiling (split_tiles_kernel): 256-row tiles in the fp16 matrix-core mode (the wide
+// kernel), 128-row tiles otherwise, except that an expert whose last tile would hold at most 32
+// rows runs those rows in one 32-row tile. The workspace holds the longer (128-row) tile list.
+int64_t max_big_tiles(int64_t M, int E) { return max_tiles_for(M, E, e4b::kTileM); }
 int64_t max_small_tiles(int64_t M, int E) { return std::max<int64_t>(1, std::min<int64_t>(E, M)); }
 
 bool is_gated_epi(int epi) {
@@ -916,15 +917,20 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   rt.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rt.max_tiles));
   rt.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
   rt.scratch = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * e4b_route_scratch_ints(M, E)));
-  // Prefill-sized groups on the MFMA path run at two tile heights: 256-row tiles (the wide
-  // kernel), and one 32-row tile for an expert whose last tile would hold at most 32 rows (the
-  // long Zipf tail of experts with a handful of rows each), whose cost is mostly the decoding
-  // of its expert's weights.
+  // fp16 matrix-core mode: both GEMMs on the MFMA path, bf16 activations, NF4 weight shifts
+  const bool gemv_path = flags == E4B_PATH_GEMV || (flags == E4B_PATH_AUTO && tokens <= 4);
+  const bool f16c = !gemv_path && act_dtype == E4B_BF16 && w1->format != E4B_FMT_MXFP4 && w1->shift && w2->shift;
+  // Prefill-sized groups on the MFMA path run at two tile heights: big tiles -- 256 rows (the
+  // wide kernel) in the fp16 mode; 128 rows otherwise, where the wide kernel's bf16 / fp16
+  // operands measured slower (gpt-oss 2,048 tokens: 687 us with 128-row tiles, 812 with 256) --
+  // and one 32-row tile for an expert whose last tile would hold at most 32 rows (the long Zipf
+  // tail of experts with a handful of rows each), whose cost is mostly the streaming and
+  // decoding of its expert's weights.
   const bool split = rt.tile_m == e4b::kTileM && flags != E4B_PATH_GEMV;
   e4b_routing rbig = rt, rsmall = rt;
   if (split) {
-    rbig.tile_m = e4b::kTileMBig;
-    rbig.max_tiles = static_cast<int32_t>(max_big_tiles(M, E));
+    rbig.tile_m = f16c ? e4b::kTileMBig : e4b::kTileM;
+    rbig.max_tiles = static_cast<int32_t>(max_tiles_for(M, E, rbig.tile_m));
     rbig.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rbig.max_tiles));
     rbig.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
     rsmall.tile_m = e4b::kTileMSmall;
@@ -937,9 +943,6 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   int32_t* xexp = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * tokens));
   int32_t* hexp = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));
   uint16_t* x16 = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * tokens * w1->k));
-  // fp16 matrix-core mode: both GEMMs on the MFMA path, bf16 activations, NF4 weight shifts
-  const bool gemv_path = flags == E4B_PATH_GEMV || (flags == E4B_PATH_AUTO && tokens <= 4);
-  const bool f16c = !gemv_path && act_dtype == E4B_BF16 && w1->format != E4B_FMT_MXFP4 && w1->shift && w2->shift;
   const int32_t* up_exp = f16c ? xexp : nullptr;
   int32_t* h_exp = f16c ? hexp : nullptr;
   // the gate_up GEMM reads the tokens as scaled fp16 rows in fp16 mode
