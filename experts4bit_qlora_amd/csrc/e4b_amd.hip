@@ -95,6 +95,38 @@ DecodeSync* decode_sync_device() {
   return s.ok ? &s : nullptr;
 }
 
+// The second stream of a prefill forward on the current device, with its fork / join events
+// (created on first use outside graph capture, default priority, kept for the process). The
+// 32-row tile launches run on it beside the big-tile launches: the wide kernel holds one
+// workgroup per CU and its last round leaves CUs idle, which the 32-row tiles fill.
+struct SideStream {
+  bool init = false, ok = false;
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+std::mutex g_side_mu;
+SideStream g_side[kMaxDevices];
+
+const SideStream* side_stream(hipStream_t stream) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_side_mu);
+  SideStream& ss = g_side[dev];
+  if (!ss.init) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+      (void)hipGetLastError();
+      return nullptr;  // no stream or event creation under capture: this call stays on one stream
+    }
+    ss.init = true;
+    ss.ok = hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) == hipSuccess &&
+            hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) == hipSuccess &&
+            hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) == hipSuccess;
+    if (!ss.ok) (void)hipGetLastError();  // one stream on this device
+  }
+  return ss.ok ? &ss : nullptr;
+}
+
 // The counters and exchange buffers of `stream`'s slot (a stream keeps its slot for the life of
 // the process); false when every slot is taken or the state is unavailable.
 bool decode_sync_slot(hipStream_t stream, unsigned** ctr, uint16_t** hx, unsigned** errors) {
@@ -849,10 +881,13 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
   return b;
 }
 
-int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
-                    const void* top_k_weights, int32_t weight_dtype, int32_t top_k, const e4b_qweight* w1,
-                    const e4b_qweight* w2, int32_t epilogue, float alpha, float limit, int32_t flags, void* workspace,
-                    size_t workspace_bytes, void* out, int32_t out_dtype, hipStream_t stream) {
+// side_ok: the prefill's 32-row tiles may run on the device's second stream (not for the
+// allocation-free entry point).
+static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                            const void* top_k_weights, int32_t weight_dtype, int32_t top_k, const e4b_qweight* w1,
+                            const e4b_qweight* w2, int32_t epilogue, float alpha, float limit, int32_t flags,
+                            void* workspace, size_t workspace_bytes, void* out, int32_t out_dtype, hipStream_t stream,
+                            bool side_ok) {
   int rc = check_weight(w1);
   if (rc) return rc;
   rc = check_weight(w2);
@@ -971,18 +1006,36 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
                        rbig, rsmall);
     rc = check_launch("split_tiles_kernel");
     if (rc) return rc;
-    for (const e4b_routing* r : {&rbig, &rsmall}) {
-      rc = grouped_gemm_impl(up_a, act_dtype, top_k, w1, r, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
-                             up_exp, stream);
-      if (rc) return rc;
-    }
+    // the two tile heights write disjoint rows: the 32-row tiles go to the side stream (forked
+    // after everything they read, joined before anything reads what they write)
+    const SideStream* side = side_ok ? side_stream(stream) : nullptr;
+    auto both = [&](auto&& launch) -> int {
+      if (side) {
+        if (hipEventRecord(side->fork, stream) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)
+          return check_launch("side stream fork");
+        int r = launch(&rbig, stream);
+        if (!r) r = launch(&rsmall, side->s);
+        // joined whatever happened, so the caller's stream never runs ahead of the side stream
+        const bool joined = hipEventRecord(side->join, side->s) == hipSuccess &&
+                            hipStreamWaitEvent(stream, side->join, 0) == hipSuccess;
+        if (r) return r;
+        return joined ? 0 : check_launch("side stream join");
+      }
+      int r = launch(&rbig, stream);
+      return r ? r : launch(&rsmall, stream);
+    };
+    rc = both([&](const e4b_routing* r, hipStream_t s) {
+      return grouped_gemm_impl(up_a, act_dtype, top_k, w1, r, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
+                               up_exp, s);
+    });
+    if (rc) return rc;
     rc = h_to_f16();
     if (rc) return rc;
-    for (const e4b_routing* r : {&rbig, &rsmall}) {
-      rc = grouped_gemm_impl(h, act_dtype, 0, w2, r, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
-                             h_exp, stream);
-      if (rc) return rc;
-    }
+    rc = both([&](const e4b_routing* r, hipStream_t s) {
+      return grouped_gemm_impl(h, act_dtype, 0, w2, r, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
+                               h_exp, s);
+    });
+    if (rc) return rc;
   } else {
     rc = grouped_gemm_impl(up_a, act_dtype, top_k, w1, &rt, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
                            up_exp, stream);
@@ -995,6 +1048,14 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
   }
   return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
                      stream);
+}
+
+int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
+                    const void* top_k_weights, int32_t weight_dtype, int32_t top_k, const e4b_qweight* w1,
+                    const e4b_qweight* w2, int32_t epilogue, float alpha, float limit, int32_t flags, void* workspace,
+                    size_t workspace_bytes, void* out, int32_t out_dtype, hipStream_t stream) {
+  return moe_forward_impl(hidden, act_dtype, tokens, top_k_index, top_k_weights, weight_dtype, top_k, w1, w2,
+                          epilogue, alpha, limit, flags, workspace, workspace_bytes, out, out_dtype, stream, true);
 }
 
 static_assert(e4b::kDecLoraMaxRank == e4b::kLoraMaxRank, "one rank limit for both LoRA paths");
@@ -1219,8 +1280,8 @@ int e4b_moe_forward_noalloc(const void* hidden, int32_t act_dtype, int64_t token
   void* ws = nullptr;
   const int rc = scratch_address(&ws);
   if (rc) return rc;
-  return e4b_moe_forward(hidden, act_dtype, tokens, top_k_index, top_k_weights, weight_dtype, top_k, w1, w2, epilogue,
-                         alpha, limit, flags, ws, size_t(E4B_NOALLOC_WORKSPACE_BYTES), out, out_dtype, stream);
+  return moe_forward_impl(hidden, act_dtype, tokens, top_k_index, top_k_weights, weight_dtype, top_k, w1, w2, epilogue,
+                          alpha, limit, flags, ws, size_t(E4B_NOALLOC_WORKSPACE_BYTES), out, out_dtype, stream, false);
 }
 
 }  // extern "C"
