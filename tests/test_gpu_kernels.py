@@ -407,8 +407,10 @@ def test_gemm_4bit_grouped_api_shape():
 
 
 @pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("H", [256, 2880, 100])
+@pytest.mark.parametrize("H", [256, 512, 2048, 2880, 100])
 def test_combine_bit_exact(wdt, H):
+    """k-slot combine, bit for bit against fp32 slot-order sums: multiples of 8 (256, 512, 2048,
+    2880) take the eight-value vector path, 100 the scalar path."""
     _announce(f"combine H={H} w={wdt}")
     T, k, E = 33, 4, 16
     rng = np.random.default_rng(H)
