@@ -130,7 +130,11 @@ gemm_narrow_kernel(GemmArgs p) {
   const int ac = tid & 7;
   const int ag = ac * 2;
   const int r = row0 + ar;
-  const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
+  // the row's source is loaded at a clamped index before row_end is known (one round trip
+  // fewer ahead of the activation loads), then dropped for rows past the expert's end
+  const int rcl = min(r, static_cast<int>(p.M) - 1);
+  const int64_t src_any = p.gather_k > 0 ? p.rt.sorted_flat[rcl] / p.gather_k : rcl;
+  const int64_t src = (r < row_end) ? src_any : 0;
   const uint16_t* aptr = p.a + src * k + 64 * (ac >> 1) + 16 * (ac & 1);
 
   constexpr int PS = 3;  // scale sets: pairs in use or in flight
