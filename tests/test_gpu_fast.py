@@ -878,3 +878,44 @@ def test_prefill_side_stream_is_deterministic_and_graph_safe():
             assert torch.equal(mod(x, idx, w), first)
             torch.cuda.synchronize()
     _assert_fidelity(first, ref_loop, _oracle(mod, x, idx, w), "prefill side stream")
+
+
+def test_narrow_tiles_general_epilogues():
+    """The narrow kernel's general epilogue paths (32-row tiles in fp16 mode, K = 512 and 256):
+    a plain up projection (has_gate=False, the activation epilogue, bf16 rows) against the oracle,
+    and DeepSeek-V4's clamped SwiGLU against the module's own forward with the clamp visibly
+    active."""
+    _announce("narrow tiles: act and clamp epilogues")
+    mod, hs, top_i, top_w = _make(E=8, H=512, inter=256, k=4, tokens=48, seed=41, has_gate=False, scale=0.05)
+    with torch.no_grad():
+        ref = mod(hs, top_i, top_w)
+        assert e4b.enable_fast(mod) == 1
+        w1, w2 = F._qweights(mod)
+        assert w1.shift is not None  # the fp16 mode, so the narrow kernel
+        fast = mod(hs, top_i, top_w)
+    _assert_fidelity(fast, ref, _oracle(mod, hs, top_i, top_w), "narrow act epilogue")
+
+    from experts4bit_qlora_amd.arch.deepseek_v4 import _DeepseekV4ForwardMixin
+
+    TOL = 1.5e-2
+    E, H, INTER, K, T = 8, 512, 256, 3, 48
+
+    def v4(limit):
+        g = torch.Generator().manual_seed(42)
+        m = _DeepseekV4ForwardMixin.from_deepseek_v4(torch.randn(E, 2 * INTER, H, generator=g) * 0.2,
+                                                     torch.randn(E, H, INTER, generator=g) * 0.2, limit=limit,
+                                                     compute_dtype=torch.bfloat16).to(DEV).eval()
+        x = (torch.randn(T, H, generator=g) * 1.5).to(torch.bfloat16).to(DEV)
+        val, idx = torch.topk(torch.randn(T, E, generator=g), K, dim=-1)
+        return m, x, idx.to(DEV), torch.softmax(val, dim=-1).to(torch.bfloat16).to(DEV)
+
+    mod, x, idx, w = v4(2.0)
+    unclamped, *_ = v4(0.0)
+    with torch.no_grad():
+        ref = mod(x, idx, w)
+        ref_noclamp = unclamped(x, idx, w)
+        assert _b_rel(ref, ref_noclamp) > 10 * TOL
+        assert e4b.enable_fast(mod) == 1
+        got = mod(x, idx, w)
+    assert _b_rel(got, ref) < TOL, _b_rel(got, ref)
+    assert _b_rel(got, ref_noclamp) > 10 * TOL
