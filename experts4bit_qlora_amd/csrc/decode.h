@@ -25,8 +25,8 @@
 // (scale 1) turns a byte into its two codes as an activation-dtype pair, exact in either type.
 // NF4 goes through a 64 KB LDS table that holds, for every byte value b, the two codes the byte
 // encodes, one 256-byte row per byte value, in one of two forms:
-//   single  one 4-byte entry (two 16-bit codes), 64 copies, lane l reads copy l: NF4 codes in
-//           fp16 (up kernels).
+//   single  one 4-byte entry (two 16-bit codes), 32 copies in the first half of the row, lane
+//           l reads copy l % 32: NF4 codes in fp16 (up kernels).
 //   split   NF4 codes as activation-dtype pairs hi = dt(code), lo = dt(code - hi), so hi + lo
 //           carries the fp32 code to ~16 significant bits (8-byte entries, 32 copies, lane l
 //           reads copy l % 32): the down kernel, whose activations are read straight from
@@ -67,11 +67,16 @@ constexpr int kDecMaxExperts = 256;
 constexpr int kDecExpWords = kDecMaxExperts / 64;
 constexpr int kLutRowBytes = 256;  // one table row per byte value: 256 rows, 64 KB
 
-// Table geometry: split entries carry (hi, lo) pairs, single entries the codes alone.
+// Table geometry: split entries carry (hi, lo) pairs, single entries the codes alone. 32 copies
+// either way (LDS serves a wave's reads in half-waves, so lane l reading copy l % 32 is
+// conflict-free); single entries fill the first half of each 256-byte row, so a byte's address
+// stays one v_perm_b32 (byte -> bits 8..15) and the table build stores half as much.
 template <bool SPLIT>
 struct LutGeom {
   static constexpr int kEntryBytes = SPLIT ? 8 : 4;
-  static constexpr int kCopies = kLutRowBytes / kEntryBytes;
+  static constexpr int kCopies = 32;
+  static constexpr int kFillBytes = kCopies * kEntryBytes;
+  static_assert(kFillBytes <= kLutRowBytes, "copies fit a row");
   // byte offset of lane's copy within a row
   static E4B_DEV uint32_t lane_off(int lane) { return static_cast<uint32_t>(lane % kCopies) * kEntryBytes; }
 };
@@ -265,8 +270,8 @@ template <bool SPLIT>
 E4B_DEV void store_pair_entry(uint4* lut, uint2 e) {
   const uint32_t b = threadIdx.x;
   const uint4 v = SPLIT ? make_uint4(e.x, e.y, e.x, e.y) : make_uint4(e.x, e.x, e.x, e.x);
-  constexpr uint32_t kStores = kLutRowBytes / 16;
-  uint4* row = lut + b * kStores;
+  constexpr uint32_t kStores = LutGeom<SPLIT>::kFillBytes / 16;
+  uint4* row = lut + b * (kLutRowBytes / 16);
 #pragma unroll
   for (uint32_t c = 0; c < kStores; ++c) row[(c + b) & (kStores - 1)] = v;
 }
@@ -291,6 +296,44 @@ E4B_DEV RawScale load_scale(const e4b_qweight& w, int e, int64_t row, int c) {
     s.q = static_cast<const uint8_t*>(w.absmax)[e * nb + blk];
     s.a = w.absmax2[e * ((nb + 255) / 256) + blk / 256];
   }
+  return s;
+}
+
+// Double quant, per weight row: the absmax2 entries of the row's first and last blocks. A row
+// holds at most kDecMaxK / 64 = 64 blocks and an absmax2 entry covers 256, so these are the
+// only two the row uses; its chunks pick theirs with pick_absmax2 instead of one load each.
+struct RowAbsmax2 {
+  float a0, a1;
+  int64_t g0;  // absmax2 group of the row's first block
+};
+
+template <int FMT>
+E4B_DEV RowAbsmax2 load_row_absmax2(const e4b_qweight& w, int e, int64_t row) {
+  if constexpr (FMT != E4B_FMT_NF4_DQ) {
+    return RowAbsmax2{0.0f, 0.0f, 0};
+  } else {
+    const int64_t bpr = w.k / 64, nb = w.n * bpr, base = int64_t(e) * ((nb + 255) / 256);
+    const int64_t g0 = (row * bpr) >> 8, g1 = (row * bpr + bpr - 1) >> 8;
+    return RowAbsmax2{w.absmax2[base + g0], w.absmax2[base + g1], g0};
+  }
+}
+
+// Scale data of chunk c of weight row `row` without the absmax2 entry (taken from the row's
+// RowAbsmax2 after the loads have landed).
+template <int FMT>
+E4B_DEV RawScale load_scale_block(const e4b_qweight& w, int e, int64_t row, int c) {
+  if constexpr (FMT != E4B_FMT_NF4_DQ) {
+    return load_scale<FMT>(w, e, row, c);
+  } else {
+    RawScale s{0.0f, 0u};
+    s.q = static_cast<const uint8_t*>(w.absmax)[int64_t(e) * w.n * (w.k / 64) + row * (w.k / 64) + c / 2];
+    return s;
+  }
+}
+
+template <int FMT>
+E4B_DEV RawScale pick_absmax2(RawScale s, const RowAbsmax2& ra2, const e4b_qweight& w, int64_t row, int c) {
+  if constexpr (FMT == E4B_FMT_NF4_DQ) s.a = ((row * (w.k / 64) + c / 2) >> 8) == ra2.g0 ? ra2.a0 : ra2.a1;
   return s;
 }
 
@@ -601,9 +644,11 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
     cidx[i] = c;
     qa[i] = load_chunk_w(w, e, row_a, c);
     if constexpr (pair) qb[i] = load_chunk_w(w, e, row_b, c);
-    ra[i] = load_scale<FMT>(w, e, row_a, c);
-    if constexpr (pair) rb[i] = load_scale<FMT>(w, e, row_b, c);
+    ra[i] = load_scale_block<FMT>(w, e, row_a, c);
+    if constexpr (pair) rb[i] = load_scale_block<FMT>(w, e, row_b, c);
   }
+  const RowAbsmax2 r2a = load_row_absmax2<FMT>(w, e, row_a);
+  const RowAbsmax2 r2b = pair ? load_row_absmax2<FMT>(w, e, row_b) : r2a;
   // biases as raw bits, loaded without a branch (a spare load of x[0] when there is none) and
   // converted after the loop, so nothing here waits on the loads in flight
   const bool has_bias = w.bias != nullptr;
@@ -631,8 +676,9 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
   float sa[CPL], sb[CPL];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
-    sa[i] = valid[i] ? resolve_scale<FMT>(ra[i], code2_s, off) : 0.0f;
-    sb[i] = (pair && valid[i]) ? resolve_scale<FMT>(rb[i], code2_s, off) : 0.0f;
+    sa[i] = valid[i] ? resolve_scale<FMT>(pick_absmax2<FMT>(ra[i], r2a, w, row_a, cidx[i]), code2_s, off) : 0.0f;
+    sb[i] = (pair && valid[i]) ? resolve_scale<FMT>(pick_absmax2<FMT>(rb[i], r2b, w, row_b, cidx[i]), code2_s, off)
+                               : 0.0f;
   }
   for (;;) {
     // the table addresses depend only on the weights, which do not change from row to row;
