@@ -172,6 +172,47 @@ def decode_bench(mods, cfg, T, steps, warmup, seed0):
     }
 
 
+def rotating_decode_bench(mods, cfg, steps, warmup, seed0):
+    """The bs=1 decode step with the routed experts rotated between replays, to show the graph
+    replays are not served from the 256 MB Infinity Cache: each layer's experts are split into
+    E / k disjoint sets of k, and replay r routes every layer's token to set r mod (E / k), so an
+    expert's weights are read again only after E / k - 1 replays of other experts (3.2 GB at
+    OLMoE geometry). One device copy before each replay installs the set; the same copies are
+    timed alone and subtracted."""
+    import torch
+
+    L, E, k = len(mods), cfg["E"], cfg["k"]
+    R = E // k
+    g = torch.Generator().manual_seed(seed0)
+    bank = torch.stack([torch.randperm(E, generator=g)[: R * k].view(R, 1, k) for _ in range(L)], 1).cuda()
+    ids = bank[0].clone()  # [L, 1, k]: the graph reads layer l's ids from ids[l]
+    inputs = [make_inputs(cfg, 1, seed0 + 10 * l) for l in range(L)]
+
+    def step():
+        with torch.no_grad():
+            return [m(x, ids[l], w) for l, (m, (x, _, w)) in enumerate(zip(mods, inputs))]
+
+    gr, _ = graph_of(step)
+
+    def run(n, replay):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for r in range(n):
+            ids.copy_(bank[r % R])
+            if replay:
+                gr.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / n
+
+    run(warmup * R, True)
+    n = max(steps, 4 * R)
+    ms = run(n, True)
+    copy_ms = run(n, False)
+    return {"us_per_layer": round((ms - copy_ms) * 1e3 / L, 3), "id_sets": R,
+            "copy_us_per_step": round(copy_ms * 1e3, 2)}
+
+
 def lora_bench(mods, cfg, steps, warmup, seed0, bare, rank=16):
     """The 16-layer decode step through ExpertsLoRA wrappers (the module load_moe_4bit_streaming
     builds) over the same bases: rank-16 fp32 adapters with nonzero B (a trained adapter, so the
@@ -659,6 +700,8 @@ def main():
         log(f"decode step, batch {T}")
         decode[T] = decode_bench(mods, cfg, T, args.steps, args.warmup, seed0=1000 + 100)
     main_line = decode[1]
+    log("decode step, batch 1, experts rotated between replays")
+    decode[1]["rotating_experts"] = rotating_decode_bench(mods, cfg, args.steps, args.warmup, seed0=1000 + 100)
     log("ExpertsLoRA decode step, batches 1 and 8")
     lora = lora_bench(mods, cfg, args.steps, args.warmup, 1000 + 100, decode)
 

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/e4b_amd.h"
 
 #define E4B_DEV __device__ __forceinline__

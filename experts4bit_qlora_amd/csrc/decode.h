@@ -81,6 +81,15 @@ struct LutGeom {
   static E4B_DEV uint32_t lane_off(int lane) { return static_cast<uint32_t>(lane % kCopies) * kEntryBytes; }
 };
 constexpr int kDownCols = 4;         // output columns per decode_down block
+// decode_up_kernel: chunks per lane issued before the table barrier, the rest at the chunk loop's
+// steps. Only NF4 defers, and at most two chunks: its steps are long (table lookups), so a
+// deferred chunk is issued two steps before its use (OLMoE / Qwen3 double-quant bs=1 per layer,
+// four chunks per lane: 15.33 / 14.85 us with all four up front, 15.04 / 13.84 with two). e2m1
+// steps are short, and deferring four of six chunks there took gpt-oss bs=1 from 20.3 to 28.2 us.
+template <int FMT, int CPL>
+constexpr int up_issue_chunks() {
+  return FMT == E4B_FMT_MXFP4 || CPL <= 2 ? CPL : CPL <= 4 ? 2 : CPL - 2;
+}
 constexpr int kDecMaxK = 4096;       // longest row the decode kernels take
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -466,12 +475,14 @@ E4B_DEV float lut_dot_split(const uint2 (&t)[16], const uint4 (&xq)[4]) {
 // chunk i, so the table round trip of one chunk overlaps the arithmetic of the previous
 // (OLMoE bs=1 gate_up: 8.03 -> 7.45 us per launch; it holds 32 more registers); e2m1 converts
 // in registers.
-template <int DT, int FMT, int CPL, bool PAIR, bool AHEAD, class XR, class FA, class FB>
+// pre(i) runs at the top of chunk i's step (the up kernel issues later chunks' loads there).
+template <int DT, int FMT, int CPL, bool PAIR, bool AHEAD, class XR, class FA, class FB, class PRE>
 E4B_DEV void pair_chunk_dots(const uint4 (&qa)[CPL], const uint4 (&qb)[CPL], const char* lut_bytes,
-                             uint32_t lane_off, XR&& xread, FA&& fin_a, FB&& fin_b) {
+                             uint32_t lane_off, XR&& xread, FA&& fin_a, FB&& fin_b, PRE&& pre) {
   if constexpr (FMT == E4B_FMT_MXFP4 || !AHEAD) {
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
+      pre(i);
       uint4 xv[4];
       const int sh = xread(i, xv);
       fin_a(i, weight_dot<DT, FMT, false>(qa[i], xv, lut_bytes, lane_off), sh);
@@ -489,6 +500,7 @@ E4B_DEV void pair_chunk_dots(const uint4 (&qa)[CPL], const uint4 (&qb)[CPL], con
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
       constexpr int kLast = CPL - 1;
+      pre(i);
       uint4 xv[4];
       const int sh = xread(i, xv);
       const float da = lut_dot<DT>(ta, xv);
@@ -632,21 +644,27 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
   // the decode table first: its stores then overlap the ids' wait, not the weight issue
   if constexpr (FMT != E4B_FMT_MXFP4) store_pair_entry<false>(lut, pair_entry<CDT, false>(cf, cs));
 
-  // round trip 2: the activation row, then weights and scales chunk by chunk, biases
+  // round trip 2: the activation row, then the weights and scales of the first kIssue chunks,
+  // biases; the remaining chunks are issued at the top of the chunk loop's steps, so a wave
+  // does not sit in the load issue while the data of its first chunks is already there
   load_x(f);
   uint4 qa[CPL], qb[CPL];
   RawScale ra[CPL], rb[CPL];
   bool valid[CPL];
   int cidx[CPL];
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
+  auto issue_chunk = [&](int i) {
     const int c = slot_chunk<G, FULL>(gl, i, nchunk, valid[i]);
     cidx[i] = c;
     qa[i] = load_chunk_w(w, e, row_a, c);
     if constexpr (pair) qb[i] = load_chunk_w(w, e, row_b, c);
     ra[i] = load_scale_block<FMT>(w, e, row_a, c);
     if constexpr (pair) rb[i] = load_scale_block<FMT>(w, e, row_b, c);
-  }
+  };
+  // chunk i + 1's table entries are read in step i: it must be issued by then
+  constexpr int kIssue = up_issue_chunks<FMT, CPL>();
+  static_assert(kIssue >= 2 || kIssue == CPL, "chunk 1 is issued before the loop");
+#pragma unroll
+  for (int i = 0; i < kIssue; ++i) issue_chunk(i);
   const RowAbsmax2 r2a = load_row_absmax2<FMT>(w, e, row_a);
   const RowAbsmax2 r2b = pair ? load_row_absmax2<FMT>(w, e, row_b) : r2a;
   // biases as raw bits, loaded without a branch (a spare load of x[0] when there is none) and
@@ -673,14 +691,12 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
 
   uint32_t lane_off = LutGeom<false>::lane_off(lane);
   const char* lut_bytes = reinterpret_cast<const char*>(lut);
+  // chunk scales, resolved at their first use (the first row's pass)
   float sa[CPL], sb[CPL];
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    sa[i] = valid[i] ? resolve_scale<FMT>(pick_absmax2<FMT>(ra[i], r2a, w, row_a, cidx[i]), code2_s, off) : 0.0f;
-    sb[i] = (pair && valid[i]) ? resolve_scale<FMT>(pick_absmax2<FMT>(rb[i], r2b, w, row_b, cidx[i]), code2_s, off)
-                               : 0.0f;
-  }
-  for (;;) {
+  // One routed row: the first row's pass (FIRST) issues the deferred chunks and resolves the
+  // scales; later rows of the same expert reuse both.
+  auto row_pass = [&](auto first_tag) {
+    constexpr bool kFirst = decltype(first_tag)::value;
     // the table addresses depend only on the weights, which do not change from row to row;
     // recomputing them per row keeps 128 addresses from being hoisted and held in registers
     asm volatile("" : "+v"(lane_off));
@@ -693,12 +709,24 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
           return kConv ? xsh[cidx[i]] : 0;
         },
         [&](int i, float d, int sh) {
+          if constexpr (kFirst)
+            sa[i] = valid[i] ? resolve_scale<FMT>(pick_absmax2<FMT>(ra[i], r2a, w, row_a, cidx[i]), code2_s, off)
+                             : 0.0f;
           if constexpr (kConv) d = __builtin_amdgcn_ldexpf(d, sh);
           acc_a += valid[i] ? d * sa[i] : 0.0f;
         },
         [&](int i, float d, int sh) {
+          if constexpr (kFirst)
+            sb[i] = (pair && valid[i])
+                        ? resolve_scale<FMT>(pick_absmax2<FMT>(rb[i], r2b, w, row_b, cidx[i]), code2_s, off)
+                        : 0.0f;
           if constexpr (kConv) d = __builtin_amdgcn_ldexpf(d, sh);
           acc_b += valid[i] ? d * sb[i] : 0.0f;
+        },
+        [&](int i) {
+          if constexpr (kFirst) {
+            if (i + kIssue < CPL) issue_chunk(i + kIssue < CPL ? i + kIssue : CPL - 1);
+          }
         });
     if constexpr (LORA) {
       acc_a += lora_partial<G, LR>(p, ltv, lba);
@@ -716,15 +744,36 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
       const float v = pair ? gated(p.epi, acc_a, acc_b, p.alpha, p.limit, bg, bu) : single(p.epi, acc_a, bg);
       static_cast<uint16_t*>(p.out)[int64_t(f) * p.n_out + j] = from_f<DT>(v);
     }
-    rows &= rows - 1;
-    if (!rows) break;
-    // next routed row of this expert (the same for the whole block): restage its activations
+  };
+  // next routed row of this expert (the same for the whole block): restage its activations
+  auto next_row = [&]() {
     f = __ffsll(static_cast<long long>(rows)) - 1;
     load_x(f);
     if constexpr (LORA) load_lora_t<G, LR>(p, f, gl, ltv);
     __syncthreads();  // every wave is done with the current row
     store_x();
     __syncthreads();
+  };
+  if constexpr (FMT != E4B_FMT_MXFP4) {
+    row_pass(std::true_type{});
+    for (rows &= rows - 1; rows; rows &= rows - 1) {
+      next_row();
+      row_pass(std::false_type{});
+    }
+  } else {
+    // e2m1 defers nothing: scales resolved up front and one loop body (a peeled first row
+    // measured 217 -> 255 VGPRs at six chunks per lane)
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      sa[i] = valid[i] ? resolve_scale<FMT>(ra[i], code2_s, off) : 0.0f;
+      sb[i] = (pair && valid[i]) ? resolve_scale<FMT>(rb[i], code2_s, off) : 0.0f;
+    }
+    for (;;) {
+      row_pass(std::false_type{});
+      rows &= rows - 1;
+      if (!rows) break;
+      next_row();
+    }
   }
 }
 
@@ -900,7 +949,8 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
           [&](int i, float d, int sh) {
             if constexpr (kConv) d = __builtin_amdgcn_ldexpf(d, sh);
             acc_b += valid[i] ? d * sb[i] : 0.0f;
-          });
+          },
+          [](int) {});
       if constexpr (LORA) {
         float ltv[lora_slots<G, LR>()];
 #pragma unroll
@@ -955,6 +1005,9 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
   constexpr int C = kDownCols;
   constexpr int kGroups = kDecThreads / G;
   constexpr bool kSplit = FMT != E4B_FMT_MXFP4;  // NF4: (hi, lo) entries in the activation dtype
+  // one chunk per lane and column (the split-table path): scales resolved column by column at
+  // their first use, so column 0's products wait for column 0's loads only
+  constexpr bool kLazy = kSplit && CPL == 1;
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
   const int M = p.tokens * p.k;
@@ -991,6 +1044,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
     // column's weight chunk and scale, chunk by chunk
     uint4 q[JOBS][CPL][C], xv[JOBS][CPL][4];
     RawScale rs[JOBS][CPL][C];
+    float joff[JOBS];      // double quant: the expert's absmax offset
     uint16_t bb[JOBS][C];  // raw bias bits, converted when the job runs
     uint32_t lbw[JOBS][C][lora_slots<G, LR>()];  // LoRA: B entries of the job's columns
     float ltv[JOBS][lora_slots<G, LR>()];        // LoRA: t entries of the job's current row
@@ -1017,6 +1071,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
           }
         }
       }
+      joff[t] = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
       // a spare load of x[0] when there is no bias: no branch on the loaded value
       const uint16_t* bp = has_bias ? bias + int64_t(e) * n : p.x;
 #pragma unroll
@@ -1039,19 +1094,26 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
 #pragma unroll
     for (int t = 0; t < JOBS; ++t) {
       if (je[t] < 0) continue;  // whole group skips together
-      const int e = je[t];
-      const float off = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
+      const float off = joff[t];
       float sc[CPL][C], b[C];
+      auto resolve = [&](int i, int cl) {
+        sc[i][cl] = valid[i] ? resolve_scale<FMT>(rs[t][i][cl], code2_s, off) : 0.0f;
+      };
+      if constexpr (!kLazy) {
 #pragma unroll
-      for (int i = 0; i < CPL; ++i) {
+        for (int i = 0; i < CPL; ++i) {
 #pragma unroll
-        for (int cl = 0; cl < C; ++cl) sc[i][cl] = valid[i] ? resolve_scale<FMT>(rs[t][i][cl], code2_s, off) : 0.0f;
+          for (int cl = 0; cl < C; ++cl) resolve(i, cl);
+        }
       }
 #pragma unroll
       for (int cl = 0; cl < C; ++cl) b[cl] = has_bias ? to_f<DT>(bb[t][cl]) : 0.0f;
       unsigned long long rows = jrows[t];
       int f = jf[t];
-      for (;;) {
+      // One routed row of the job. The first row's pass (FIRST) resolves the scales column by
+      // column; later rows reuse them.
+      auto row_pass = [&](auto first_tag) {
+        constexpr bool kFirst = decltype(first_tag)::value;
         asm volatile("" : "+v"(lane_off));  // no hoisting of the per-row table addresses
         float acc[C];
 #pragma unroll
@@ -1064,6 +1126,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int cl = 0; cl < C; ++cl) {
+            if constexpr (kFirst && kLazy) resolve(0, cl);
             const float d = lut_dot_split<DT>(te, xv[t][0]) * sc[0][cl];
             if (cl + 1 < C) lut_lookup_split(q[t][0][cl + 1 < C ? cl + 1 : cl], lut_bytes, lane_off, te);
             __builtin_amdgcn_sched_barrier(0);
@@ -1089,14 +1152,31 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
           const float v = group_reduce<G>(acc[cl]);
           if (gl == 0) res[f * C + cl] = v + b[cl];
         }
-        rows &= rows - 1;
-        if (!rows) break;
+      };
+      // the next routed row of the job: its activations (and LoRA t entries)
+      auto next_row = [&]() {
         f = __ffsll(static_cast<long long>(rows)) - 1;
         if constexpr (LORA) load_lora_t<G, LR>(p, f, gl, ltv[t]);
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
           bool v;
           load_chunk_x(p.x + int64_t(f) * k, slot_chunk<G, FULL>(gl, i, nchunk, v), xv[t][i]);
+        }
+      };
+      if constexpr (kLazy) {
+        row_pass(std::true_type{});
+        for (rows &= rows - 1; rows; rows &= rows - 1) {
+          next_row();
+          row_pass(std::false_type{});
+        }
+      } else {
+        // one loop body: a peeled first row measured 168 -> 256 VGPRs (one wave per SIMD) at
+        // three chunks per lane
+        for (;;) {
+          row_pass(std::false_type{});
+          rows &= rows - 1;
+          if (!rows) break;
+          next_row();
         }
       }
     }

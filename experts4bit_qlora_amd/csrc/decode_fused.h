@@ -275,7 +275,8 @@ __global__ void __launch_bounds__(kDecThreads) decode_fused_kernel(FusedArgs p) 
         [&](int i, float dd, int sh) {
           if constexpr (kConv) dd = __builtin_amdgcn_ldexpf(dd, sh);
           acc_b += valid[i] ? dd * sb[i] : 0.0f;
-        });
+        },
+        [](int) {});
     acc_a = group_reduce<G>(acc_a);
     acc_b = group_reduce<G>(acc_b);
     if (live && gl == 0) {
