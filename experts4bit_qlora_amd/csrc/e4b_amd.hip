@@ -986,19 +986,15 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
   rc = e4b_route(top_k_index, tokens, top_k, E, &rt, stream);
   if (rc) return rc;
   if (f16c) {  // token row exponents and scaled fp16 rows
-    const int64_t blocks = cdiv(tokens, e4b::kScaleThreads / e4b::kWave);
-    hipLaunchKernelGGL(e4b::row_exp_kernel, dim3(static_cast<unsigned>(blocks)), dim3(e4b::kScaleThreads), 0, stream,
-                       static_cast<const uint16_t*>(hidden), tokens, w1->k, xexp, x16, nullptr, int64_t(0));
+    e4b::launch_row_exp(static_cast<const uint16_t*>(hidden), tokens, w1->k, xexp, x16, nullptr, 0, stream);
     rc = check_launch("row_exp_kernel");
     if (rc) return rc;
   }
   // fp16 mode: h row exponents, and h rewritten in place as scaled fp16 rows for the down GEMM
   auto h_to_f16 = [&]() {
     if (!f16c) return 0;
-    const int64_t blocks = cdiv(M, e4b::kScaleThreads / e4b::kWave);
-    hipLaunchKernelGGL(e4b::row_exp_kernel, dim3(static_cast<unsigned>(blocks)), dim3(e4b::kScaleThreads), 0, stream,
-                       static_cast<const uint16_t*>(h), M, h_cols, hexp, static_cast<uint16_t*>(h), nullptr,
-                       int64_t(0));
+    e4b::launch_row_exp(static_cast<const uint16_t*>(h), M, h_cols, hexp, static_cast<uint16_t*>(h), nullptr, 0,
+                        stream);
     return check_launch("row_exp_kernel");
   };
   if (split) {

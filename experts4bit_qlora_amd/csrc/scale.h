@@ -27,10 +27,11 @@ E4B_DEV uint32_t wave_max_u32(uint32_t v) {
 // x16[r] = fp16(x[r] * 2^exp_shift(row_exp[r])) (exact; see bf16x2_to_f16x2), a GEMM operand
 // staged once instead of once per output tile; zero[0 .. nzero) = 0 (grid-stride: the grid has
 // rows / 4 blocks of 256 threads). One wave per row; a row's pieces stay in registers between
-// the two passes when k <= 64 * 8 * kRowPieces. x16 may be x (in place): a wave reads every piece
-// of its row for the maximum before it writes any, and writes each piece after reading it.
-constexpr int kRowPieces = 8;  // 16-byte pieces per lane held across the passes (k <= 4096)
-
+// the two passes when k <= 64 * 8 * RP. x16 may be x (in place): a wave reads every piece of its
+// row for the maximum before it writes any, and writes each piece after reading it. RP (16-byte
+// pieces per lane held across the passes) follows the row length (row_exp_pieces): a fixed 8 made
+// a 768-value h row issue 8 loads per lane for its 96 pieces, 5 in 6 of them clamped re-reads.
+template <int RP>
 __global__ void __launch_bounds__(kScaleThreads) row_exp_kernel(const uint16_t* x, int64_t rows,
                                                                 int64_t k, int32_t* __restrict__ row_exp,
                                                                 uint16_t* x16,
@@ -44,14 +45,14 @@ __global__ void __launch_bounds__(kScaleThreads) row_exp_kernel(const uint16_t* 
   uint4* yr = reinterpret_cast<uint4*>(x16 + row * k);
   const int64_t pieces = k / 8;
   uint32_t m = 0;
-  uint4 v[kRowPieces];
+  uint4 v[RP];
 #pragma unroll
-  for (int j = 0; j < kRowPieces; ++j) {
+  for (int j = 0; j < RP; ++j) {
     const int64_t i = lane + int64_t(j) * kWave;
     v[j] = xr[i < pieces ? i : 0];
     m = max(m, bf16_exp_max(v[j]));
   }
-  for (int64_t i = lane + int64_t(kRowPieces) * kWave; i < pieces; i += kWave) m = max(m, bf16_exp_max(xr[i]));
+  for (int64_t i = lane + int64_t(RP) * kWave; i < pieces; i += kWave) m = max(m, bf16_exp_max(xr[i]));
   m = wave_max_u32(m);
   if (lane == 0) row_exp[row] = static_cast<int32_t>(m >> 7);
   const int d = exp_shift(static_cast<int>(m >> 7));
@@ -60,11 +61,29 @@ __global__ void __launch_bounds__(kScaleThreads) row_exp_kernel(const uint16_t* 
                       bf16x2_to_f16x2(a.w, d));
   };
 #pragma unroll
-  for (int j = 0; j < kRowPieces; ++j) {
+  for (int j = 0; j < RP; ++j) {
     const int64_t i = lane + int64_t(j) * kWave;
     if (i < pieces) yr[i] = conv(v[j]);
   }
-  for (int64_t i = lane + int64_t(kRowPieces) * kWave; i < pieces; i += kWave) yr[i] = conv(xr[i]);
+  for (int64_t i = lane + int64_t(RP) * kWave; i < pieces; i += kWave) yr[i] = conv(xr[i]);
+}
+
+// Pieces per lane for a row of k values: enough to hold the row (k <= 4096), rounded up to 1, 2,
+// 4 or 8.
+inline int row_exp_pieces(int64_t k) {
+  const int64_t per = (k / 8 + kWave - 1) / kWave;
+  return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
+}
+
+inline void launch_row_exp(const uint16_t* x, int64_t rows, int64_t k, int32_t* row_exp, uint16_t* x16,
+                           int32_t* zero, int64_t nzero, hipStream_t s) {
+  const unsigned blocks = static_cast<unsigned>((rows + kScaleThreads / kWave - 1) / (kScaleThreads / kWave));
+  switch (row_exp_pieces(k)) {
+    case 1: hipLaunchKernelGGL(row_exp_kernel<1>, dim3(blocks), dim3(kScaleThreads), 0, s, x, rows, k, row_exp, x16, zero, nzero); break;
+    case 2: hipLaunchKernelGGL(row_exp_kernel<2>, dim3(blocks), dim3(kScaleThreads), 0, s, x, rows, k, row_exp, x16, zero, nzero); break;
+    case 4: hipLaunchKernelGGL(row_exp_kernel<4>, dim3(blocks), dim3(kScaleThreads), 0, s, x, rows, k, row_exp, x16, zero, nzero); break;
+    default: hipLaunchKernelGGL(row_exp_kernel<8>, dim3(blocks), dim3(kScaleThreads), 0, s, x, rows, k, row_exp, x16, zero, nzero); break;
+  }
 }
 
 // shift[e] = exp_shift(largest biased fp32 exponent of expert e's block scales), one block per
