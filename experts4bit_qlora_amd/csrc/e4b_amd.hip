@@ -407,16 +407,12 @@ int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t
   const int64_t nchunks = cdiv(M, e4b::kRouteChunk);
   hipLaunchKernelGGL(e4b::route_count_kernel, dim3(static_cast<unsigned>(nchunks)), dim3(e4b::kRouteChunk), 0, stream,
                      top_k_index, M, num_experts, rt->scratch);
-  if (nchunks * (int64_t(num_experts) + 1) <= e4b::kScanLdsInts) {
-    hipLaunchKernelGGL(e4b::route_scan_kernel<true>, dim3(1), dim3(e4b::kRouteThreads), 0, stream, nchunks,
-                       num_experts, rt->scratch, *rt);
-  } else {
-    hipLaunchKernelGGL(e4b::route_scan_kernel<false>, dim3(1), dim3(e4b::kRouteThreads), 0, stream, nchunks,
-                       num_experts, rt->scratch, *rt);
-  }
+  hipLaunchKernelGGL(e4b::route_colscan_kernel, dim3(static_cast<unsigned>(num_experts + 1)),
+                     dim3(e4b::kRouteThreads), 0, stream, nchunks, num_experts, rt->scratch, rt->offsets);
+  hipLaunchKernelGGL(e4b::route_tables_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, num_experts, *rt);
   hipLaunchKernelGGL(e4b::route_place_kernel, dim3(static_cast<unsigned>(nchunks)), dim3(e4b::kRouteChunk), 0, stream,
                      top_k_index, M, num_experts, rt->scratch, *rt);
-  return check_launch("route_count/scan/place kernels");
+  return check_launch("route_count/colscan/tables/place kernels");
 }
 
 int e4b_route_groups(const int64_t* sizes, int32_t groups, const int64_t* expert_ids, int32_t num_experts,

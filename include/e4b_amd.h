@@ -112,7 +112,7 @@ int e4b_dequant(const e4b_qweight* w, int32_t expert_begin, int32_t expert_count
 int e4b_weight_shift(const e4b_qweight* w, int32_t* shift, hipStream_t stream);
 
 /* int32 scratch the route needs for M = tokens * top_k routed rows over E experts: 0 up to
- * 4096 rows (one workgroup routes them), else ceil(M / 256) * (E + 1) (three launches over
+ * 4096 rows (one workgroup routes them), else ceil(M / 256) * (E + 1) (four launches over
  * 256-row chunks). */
 int64_t e4b_route_scratch_ints(int64_t M, int32_t num_experts);
 
