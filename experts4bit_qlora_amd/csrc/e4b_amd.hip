@@ -13,6 +13,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <utility>
 
 #include "common.h"
 #include "decode.h"
@@ -95,37 +96,98 @@ DecodeSync* decode_sync_device() {
   return s.ok ? &s : nullptr;
 }
 
-// The second stream of a prefill forward on the current device, with its fork / join events
+// Second streams of prefill forwards on each device, each with its own fork / join events
 // (created on first use outside graph capture, default priority, kept for the process). The
-// 32-row tile launches run on it beside the big-tile launches: the wide kernel holds one
+// 32-row tile launches run on one beside the big-tile launches: the wide kernel holds one
 // workgroup per CU and its last round leaves CUs idle, which the 32-row tiles fill.
+//
+// A call checks a stream out of its device's pool for the whole of its enqueue (fork record,
+// wait, launches, join record, wait) and returns it afterwards, so the events a call waits on
+// are its own records whatever other host threads do. A stream that another thread's graph
+// capture has joined stays part of that capture until the capture ends, so it is only taken by
+// calls of the same capture (same capture id) or once the capture is over. With every stream of
+// the pool busy or captured (and no new one allowed: the pool is full, or this call is being
+// captured) the call runs both tile heights on its own stream.
 struct SideStream {
-  bool init = false, ok = false;
   hipStream_t s = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
+  bool busy = false;
+};
+constexpr int kSidePool = 8;
+struct SidePool {
+  SideStream slot[kSidePool];
+  int used = 0;
+  bool failed = false;  // creation failed once: one stream on this device from then on
 };
 std::mutex g_side_mu;
-SideStream g_side[kMaxDevices];
+SidePool g_side[kMaxDevices];
 
-const SideStream* side_stream(hipStream_t stream) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  std::lock_guard<std::mutex> lk(g_side_mu);
-  SideStream& ss = g_side[dev];
-  if (!ss.init) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
-      (void)hipGetLastError();
-      return nullptr;  // no stream or event creation under capture: this call stays on one stream
-    }
-    ss.init = true;
-    ss.ok = hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) == hipSuccess &&
-            hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) == hipSuccess &&
-            hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) == hipSuccess;
-    if (!ss.ok) (void)hipGetLastError();  // one stream on this device
+// capture status and id of `s` (status None with id 0 when the query fails)
+std::pair<hipStreamCaptureStatus, unsigned long long> capture_of(hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  if (hipStreamGetCaptureInfo(s, &cs, &id) != hipSuccess) {
+    (void)hipGetLastError();
+    return {hipStreamCaptureStatusInvalidated, 0};
   }
-  return ss.ok ? &ss : nullptr;
+  return {cs, id};
 }
+
+class SideLease {
+ public:
+  // enabled = false: no stream is leased (the call runs on its own stream)
+  SideLease(hipStream_t stream, bool enabled) {
+    if (!enabled) return;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+      (void)hipGetLastError();
+      return;
+    }
+    const auto mine = capture_of(stream);
+    if (mine.first == hipStreamCaptureStatusInvalidated) return;
+    std::lock_guard<std::mutex> lk(g_side_mu);
+    SidePool& p = g_side[dev];
+    if (p.failed) return;
+    for (int i = 0; i < p.used; ++i) {
+      SideStream& ss = p.slot[i];
+      if (ss.busy) continue;
+      const auto c = capture_of(ss.s);
+      const bool free_eager = c.first == hipStreamCaptureStatusNone;
+      const bool same_capture = mine.first == hipStreamCaptureStatusActive &&
+                                c.first == hipStreamCaptureStatusActive && c.second == mine.second;
+      if (free_eager || same_capture) {
+        ss.busy = true;
+        ss_ = &ss;
+        return;
+      }
+    }
+    // a new stream: never under capture (no stream or event creation there)
+    if (p.used == kSidePool || mine.first != hipStreamCaptureStatusNone) return;
+    SideStream& ss = p.slot[p.used];
+    const bool ok = hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking) == hipSuccess &&
+                    hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) == hipSuccess &&
+                    hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+      (void)hipGetLastError();
+      p.failed = true;
+      return;
+    }
+    ++p.used;
+    ss.busy = true;
+    ss_ = &ss;
+  }
+  ~SideLease() {
+    if (!ss_) return;
+    std::lock_guard<std::mutex> lk(g_side_mu);
+    ss_->busy = false;
+  }
+  SideLease(const SideLease&) = delete;
+  SideLease& operator=(const SideLease&) = delete;
+  const SideStream* get() const { return ss_; }
+
+ private:
+  SideStream* ss_ = nullptr;
+};
 
 // The counters and exchange buffers of `stream`'s slot (a stream keeps its slot for the life of
 // the process); false when every slot is taken or the state is unavailable.
@@ -528,12 +590,19 @@ int e4b_weight_shift(const e4b_qweight* w, int32_t* shift, hipStream_t stream) {
   if (rc) return rc;
   if (w->format == E4B_FMT_MXFP4) return fail(E4B_EUNSUPPORTED, "MXFP4 weights need no shift (exact in bf16)");
   if (!shift) return fail(E4B_EINVAL, "shift is NULL");
+  const int E = w->num_experts;
+  if (E > 65535) return fail(E4B_EUNSUPPORTED, "num_experts=%d above 65535 (one grid row per expert)", E);
+  hipLaunchKernelGGL(e4b::weight_shift_init_kernel, dim3((E + e4b::kScaleThreads - 1) / e4b::kScaleThreads),
+                     dim3(e4b::kScaleThreads), 0, stream, shift, E);
+  rc = check_launch("weight_shift_init_kernel");
+  if (rc) return rc;
+  const int64_t nb = w->n * (w->k / 64);
+  const dim3 grid(static_cast<unsigned>((nb + e4b::kShiftSpan - 1) / e4b::kShiftSpan), static_cast<unsigned>(E));
   if (w->format == E4B_FMT_NF4)
-    hipLaunchKernelGGL((e4b::weight_shift_kernel<E4B_FMT_NF4>), dim3(w->num_experts), dim3(e4b::kScaleThreads), 0,
-                       stream, *w, shift);
+    hipLaunchKernelGGL((e4b::weight_shift_kernel<E4B_FMT_NF4>), grid, dim3(e4b::kScaleThreads), 0, stream, *w, shift);
   else
-    hipLaunchKernelGGL((e4b::weight_shift_kernel<E4B_FMT_NF4_DQ>), dim3(w->num_experts), dim3(e4b::kScaleThreads),
-                       0, stream, *w, shift);
+    hipLaunchKernelGGL((e4b::weight_shift_kernel<E4B_FMT_NF4_DQ>), grid, dim3(e4b::kScaleThreads), 0, stream, *w,
+                       shift);
   return check_launch("weight_shift_kernel");
 }
 
@@ -1000,7 +1069,8 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
     if (rc) return rc;
     // the two tile heights write disjoint rows: the 32-row tiles go to the side stream (forked
     // after everything they read, joined before anything reads what they write)
-    const SideStream* side = side_ok ? side_stream(stream) : nullptr;
+    SideLease lease(stream, side_ok);
+    const SideStream* side = lease.get();
     auto both = [&](auto&& launch) -> int {
       if (side) {
         if (hipEventRecord(side->fork, stream) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)

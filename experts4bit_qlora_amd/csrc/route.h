@@ -33,7 +33,7 @@ namespace e4b {
 constexpr int kRouteThreads = 512;
 constexpr int kRouteWaves = kRouteThreads / kWave;
 constexpr int kRouteMaxExperts = 1024;
-constexpr int kRouteSingleMaxRows = 4096;  // above: the three-launch chunked route
+constexpr int kRouteSingleMaxRows = 4096;  // above: the four-launch chunked route
 constexpr int kRouteChunk = 4 * kWave;     // ids per chunk (one workgroup) in the chunked route
 
 // Exclusive scan of one int per thread across the 512-thread block (order = thread order).

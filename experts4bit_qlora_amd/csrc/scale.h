@@ -86,25 +86,35 @@ inline void launch_row_exp(const uint16_t* x, int64_t rows, int64_t k, int32_t* 
   }
 }
 
-// shift[e] = exp_shift(largest biased fp32 exponent of expert e's block scales), one block per
-// expert (blockIdx.x), NF4 (fp32 absmax) or NF4_DQ (decoded absmax).
+// shift[e] = exp_shift(largest biased fp32 exponent of expert e's block scales), NF4 (fp32
+// absmax) or NF4_DQ (decoded absmax). Grid (ceil(nb / kShiftSpan), E): each block reduces the
+// exponents of kShiftSpan consecutive block scales of expert blockIdx.y (kShiftPer independent
+// loads per thread in flight) and folds exp_shift of its maximum into shift[e] with an atomic
+// minimum; exp_shift is non-increasing, so the minimum over blocks is exp_shift of the expert's
+// maximum, whatever the order. shift must hold kShiftInit first (weight_shift_init_kernel).
+// A block past an expert's scales contributes exp_shift(0) = the largest possible value.
+constexpr int kShiftPer = 16;
+constexpr int64_t kShiftSpan = int64_t(kScaleThreads) * kShiftPer;
+constexpr int32_t kShiftInit = 0x7fffffff;
+
+__global__ void __launch_bounds__(kScaleThreads) weight_shift_init_kernel(int32_t* __restrict__ shift, int E) {
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < E; e += gridDim.x * blockDim.x) shift[e] = kShiftInit;
+}
+
 template <int FMT>
 __global__ void __launch_bounds__(kScaleThreads) weight_shift_kernel(e4b_qweight w, int32_t* __restrict__ shift) {
-  __shared__ uint32_t wm[kScaleThreads / kWave];
-  const int e = blockIdx.x;
+  const int e = blockIdx.y;
   const int64_t nb = w.n * (w.k / 64);
+  const int64_t base = int64_t(blockIdx.x) * kShiftSpan + threadIdx.x;
   uint32_t m = 0;
-  for (int64_t b = threadIdx.x; b < nb; b += blockDim.x)
-    m = max(m, (__float_as_uint(nf4_block_scale<FMT>(w, e, b)) >> 23) & 0xffu);
-  m = wave_max_u32(m);
-  if ((threadIdx.x & (kWave - 1)) == 0) wm[threadIdx.x / kWave] = m;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint32_t t = 0;
 #pragma unroll
-    for (int i = 0; i < kScaleThreads / kWave; ++i) t = max(t, wm[i]);
-    shift[e] = exp_shift(static_cast<int>(t));
+  for (int j = 0; j < kShiftPer; ++j) {
+    const int64_t b = base + int64_t(j) * kScaleThreads;
+    const uint32_t x = (__float_as_uint(nf4_block_scale<FMT>(w, e, b < nb ? b : nb - 1)) >> 23) & 0xffu;
+    m = max(m, b < nb ? x : 0u);
   }
+  m = wave_max_u32(m);
+  if ((threadIdx.x & (kWave - 1)) == 0) atomicMin(&shift[e], exp_shift(static_cast<int>(m)));
 }
 
 }  // namespace e4b

@@ -132,8 +132,25 @@ def _build_qweights(mod):
     else:
         w1 = ops.nf4_qweight(mod.gate_up_proj, mod.gate_up_absmax, mod.code, n1, k1, num_experts=E)
         w2 = ops.nf4_qweight(mod.down_proj, mod.down_absmax, mod.code, n2, k2, num_experts=E)
-    # per-expert exponents: the fused forward's matrix-core GEMMs then run on fp16 operands
-    return ops.with_weight_shift(w1), ops.with_weight_shift(w2)
+    return w1, w2
+
+
+# Up to this many tokens the fused forward runs the decode / GEMV kernels, which never read the
+# per-expert weight exponents (the C side's fp16 matrix-core mode starts above it).
+_SHIFT_FREE_TOKENS = 4
+
+
+def _for_tokens(descs, tokens):
+    """The (gate_up, down) descriptors a call of ``tokens`` tokens needs: above
+    ``_SHIFT_FREE_TOKENS`` with the per-expert exponents that let the matrix-core GEMMs run on
+    fp16 operands, computed on the first such call and kept with the cached descriptors (once per
+    weight version); below it as they are, so decode calls never launch the exponent kernels."""
+    if tokens <= _SHIFT_FREE_TOKENS:
+        return descs
+    for qw in descs:
+        if qw.shift is None:
+            ops.with_weight_shift(qw)
+    return descs
 
 
 def _mxfp4_qweights(mod, cd):
@@ -195,7 +212,7 @@ def _bare_forward(mod, hidden_states, top_k_index, top_k_weights, compute_dtype)
     hidden = mod._down_shape[0]
     if tokens == 0:
         return torch.zeros(0, hidden, dtype=input_dtype, device=x.device)
-    w1, w2 = _qweights(mod)
+    w1, w2 = _for_tokens(_qweights(mod), tokens)
     epi = _fused_epilogue(mod)
     if epi is not None:
         code, limit = epi

@@ -244,3 +244,65 @@ def test_descriptor_structs_follow_field_changes():
     qw.bias = bias
     s2 = qw.struct()
     assert s2 is not s1 and s2.bias == bias.data_ptr()
+
+
+def _header_fields(struct):
+    src = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    body = re.search(rf"typedef struct {struct} \{{(.*?)\}} {struct};", src, flags=re.S).group(1)
+    return re.findall(r"(\w+)\s*;", body)
+
+
+def _integration_binding():
+    """Execute the reference-side ctypes binding documented in INTEGRATION.md (its library path
+    pointed at the built library) and return its namespace."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
+    snippet = next(b for b in blocks if "class QWeight" in b)
+    path = re.search(r'ctypes\.CDLL\("([^"]+)"\)', snippet).group(1)
+    ns = {}
+    exec(compile(snippet.replace(path, N.LIB_PATH), "INTEGRATION.md", "exec"), ns)
+    return ns
+
+
+def test_integration_binding_matches_header_and_native():
+    """The binding a maintainer copies from INTEGRATION.md must lay out e4b_qweight exactly as the
+    header and _native do: a short struct would make the library read past its end."""
+    ns = _integration_binding()
+    doc = ns["QWeight"]
+    names = [f[0] for f in doc._fields_]
+    assert names == [f[0] for f in N.QWeight._fields_] == _header_fields("e4b_qweight")
+    assert [f[1] for f in doc._fields_] == [f[1] for f in N.QWeight._fields_]
+    assert ctypes.sizeof(doc) == ctypes.sizeof(N.QWeight)
+    for name, _ in doc._fields_:
+        assert getattr(doc, name).offset == getattr(N.QWeight, name).offset, name
+
+    def norm(types):  # POINTER(<doc QWeight>) and POINTER(N.QWeight) compare by their layout
+        out = []
+        for t in types:
+            base = getattr(t, "_type_", None)
+            out.append(("ptr", tuple(base._fields_)) if isinstance(base, type) and
+                       issubclass(base, ctypes.Structure) else t)
+        return out
+
+    L, D = N.lib(), ns["_lib"]
+    for fn in ("e4b_moe_forward", "e4b_moe_workspace_bytes"):
+        assert norm(getattr(D, fn).argtypes) == norm(getattr(L, fn).argtypes), fn
+        assert getattr(D, fn).restype == getattr(L, fn).restype, fn
+
+    # the documented descriptor helper fills every field (shift left NULL: no fp16 mode)
+    import torch
+
+    class _Mod:
+        num_experts = 4
+        code = torch.zeros(16)
+
+    pk, am = torch.zeros(64, dtype=torch.uint8), torch.zeros(8)
+    q = ns["_qw"](_Mod(), pk, am, 32, 64)
+    assert (q.format, q.num_experts, q.n, q.k) == (ns["NF4"], 4, 32, 64)
+    assert q.packed == pk.data_ptr() and q.absmax == am.data_ptr() and q.code == _Mod.code.data_ptr()
+    assert not q.shift and not q.bias and not q.absmax2
+
+
+def test_routing_and_lora_structs_match_header():
+    assert [f[0] for f in N.Routing._fields_] == _header_fields("e4b_routing")
+    assert [f[0] for f in N.Lora._fields_] == _header_fields("e4b_lora")

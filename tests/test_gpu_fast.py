@@ -336,6 +336,42 @@ def test_lora_fused_matches_the_lora_oracle_at_olmoe_geometry(T, r, adt):
     _assert_fidelity(got, ref, want, f"lora T={T} r={r} {adt}")
 
 
+@pytest.mark.parametrize("T,r,adt", [(512, 16, torch.bfloat16), (512, 64, torch.float32), (4096, 16, torch.float32)])
+def test_lora_fused_matches_the_lora_oracle_at_prefill_sizes(T, r, adt):
+    """The grouped (prefill) form of the fused LoRA forward -- 128-row tiles at 4,096 tokens, the
+    deltas added in the grouped GEMMs' epilogues -- against the fp64 restatement of
+    ExpertsLoRA.forward on the first and the last token routed to every expert (every expert's
+    first tile and its last), at the layer bars and no worse than the reference loop's own error
+    rule (the reference runs this grouped path for every batch, fast.py:209-257)."""
+    _announce(f"lora vs oracle OLMoE prefill T={T} r={r} adapters={adt}")
+    mod = _olmoe_lora(r, adt, seed=7500 + T + r)
+    x, idx, w = _cfg_inputs(T, 64, 2048, 8, seed=7600 + T, renorm=False)
+    assert e4b.enable_fast(mod) == 1
+    with torch.no_grad():
+        got = mod(x, idx, w)
+    assert torch.isfinite(got).all()
+    flat = idx.reshape(-1).cpu().numpy()
+    rows = set()
+    for e in np.unique(flat):
+        hits = np.nonzero(flat == e)[0] // 8
+        rows.update([int(hits[0]), int(hits[-1])])
+    rows = sorted(rows)
+    w1, w2 = oracle_weights(mod.base)
+    lo1 = tuple(t.detach().float().cpu().numpy() for t in (mod.gate_up_lora_A, mod.gate_up_lora_B))
+    lo2 = tuple(t.detach().float().cpu().numpy() for t in (mod.down_lora_A, mod.down_lora_B))
+    xs, ids, ws = x[rows].float().cpu().numpy(), idx[rows].cpu().numpy(), w[rows].float().cpu().numpy()
+    want = moe.forward_lora_fp32(xs, ids, ws, w1, w2, lo1, lo2, mod.scaling)
+    delta = np.linalg.norm(want - moe.forward_fp32(xs, ids, ws, w1, w2)) / np.linalg.norm(want)
+    assert delta > 0.05, delta
+    lt1 = tuple(t.detach().cpu() for t in (mod.gate_up_lora_A, mod.gate_up_lora_B))
+    lt2 = tuple(t.detach().cpu() for t in (mod.down_lora_A, mod.down_lora_B))
+    ref = moe.reference_lora_loop(x[rows].cpu(), idx[rows].cpu(), w[rows].cpu(),
+                                  lambda e, dt: torch.from_numpy(w1[e]).to(dt),
+                                  lambda e, dt: torch.from_numpy(w2[e]).to(dt), lt1, lt2, mod.scaling,
+                                  num_experts=64, compute_dtype=torch.bfloat16)
+    _assert_fidelity(got[rows], ref, want, f"lora prefill T={T} r={r} {adt} on {len(rows)} tokens")
+
+
 def test_lora_fused_forward_never_syncs():
     """The LoRA deltas of every expert group are added on the device (e4b_lora_delta), so the
     fused LoRA forward needs no group sizes on the host: no device synchronisation at all
@@ -450,6 +486,37 @@ def test_v4_fused_keeps_the_clamps(lora):
         got = mod(x, idx, w)
     assert _b_rel(got, ref) < TOL, _b_rel(got, ref)
     assert _b_rel(got, ref_noclamp) > 10 * TOL
+    e4b.disable_fast(mod)
+
+
+@pytest.mark.parametrize("T", [24, 96])
+def test_v4_clamped_layer_matches_the_oracle(T):
+    """DeepSeek-V4's clamped SwiGLU through the fused path against the fp32 oracle with the same
+    clamp (``forward_fp32(..., ("clamp_swiglu", L))``, ref tests/test_fast_v4.py:73-104), on
+    weights and activations large enough that the clamp changes most gate and up values; T=24
+    runs the decode / GEMV kernels, T=96 the matrix-core ones. A negative control: the unclamped
+    oracle is far from the result."""
+    _announce(f"v4 clamped layer vs oracle T={T}")
+    from experts4bit_qlora_amd.arch.deepseek_v4 import _DeepseekV4ForwardMixin
+
+    E, H, INTER, K, L = 16, 256, 128, 4, 2.0
+    g = torch.Generator().manual_seed(60 + T)
+    mod = _DeepseekV4ForwardMixin.from_deepseek_v4(torch.randn(E, 2 * INTER, H, generator=g) * 0.35,
+                                                   torch.randn(E, H, INTER, generator=g) * 0.35, limit=L,
+                                                   compute_dtype=torch.bfloat16).to(DEV).eval()
+    x = (torch.randn(T, H, generator=g) * 1.5).to(torch.bfloat16).to(DEV)
+    val, idx = torch.topk(torch.randn(T, E, generator=g), K, dim=-1)
+    idx, w = idx.to(DEV), torch.softmax(val, dim=-1).to(torch.bfloat16).to(DEV)
+    with torch.no_grad():
+        ref = mod(x, idx, w)
+        assert e4b.enable_fast(mod) == 1
+        got = mod(x, idx, w)
+    ow1, ow2 = oracle_weights(mod)
+    args = (x.float().cpu().numpy(), idx.cpu().numpy(), w.float().cpu().numpy(), ow1, ow2)
+    oracle = moe.forward_fp32(*args, ("clamp_swiglu", L))
+    _assert_fidelity(got, ref, oracle, f"v4 clamp T={T}")
+    fro_nc, _, _ = moe.rel_errors(got.float().cpu().numpy(), moe.forward_fp32(*args, ("clamp_swiglu", 0.0)))
+    assert fro_nc > 0.1, fro_nc  # the clamp is active and the result follows it
     e4b.disable_fast(mod)
 
 
@@ -710,16 +777,26 @@ def test_gptoss_config_shapes(T):
     val, idx = torch.topk(torch.randn(T, E, generator=g, device=DEV), k, dim=-1)
     w = torch.softmax(val, -1).to(torch.bfloat16)
     e4b.enable_fast(mod)
+    # tokens 0-3, plus at T=2048 the first and the last token routed to every expert: every
+    # expert's first 128-row tile and its last tile (partial 128-row tiles and the 32-row tail
+    # tiles included) is compared with the oracle (ref tests/test_mxfp4_arena_train.py:663-722)
+    rows = set(range(min(T, 4)))
+    if T > 4:
+        flat = idx.reshape(-1).cpu().numpy()
+        for e in np.unique(flat):
+            hits = np.nonzero(flat == e)[0] // k
+            rows.update([int(hits[0]), int(hits[-1])])
+    rows = sorted(rows)
+    _announce(f"gpt-oss T={T}: oracle on {len(rows)} tokens")
     with torch.no_grad():
         got = mod(x, idx, w)
-        ref = mod._e4b_fast_ref(x[:4], idx[:4], w[:4])
-    rows = list(range(min(T, 4)))
+        ref = mod._e4b_fast_ref(x[rows], idx[rows], w[rows])
     sub = idx[rows].cpu().numpy()
     w1, w2 = oracle_weights(mod)
     oracle = moe.forward_fp32(x[rows].float().cpu().numpy(), sub, w[rows].float().cpu().numpy(), w1, w2,
                               ("gptoss", 1.702, 7.0), b1=mod.gate_up_bias.float().cpu().numpy(),
                               b2=mod.down_bias.float().cpu().numpy())
-    _assert_fidelity(got[rows], ref[rows], oracle, f"gptoss T={T}")
+    _assert_fidelity(got[rows], ref, oracle, f"gptoss T={T}")
 
 
 @pytest.mark.parametrize("T", [2, 8, 64])
@@ -764,9 +841,9 @@ def test_fp16_matrix_core_mode_keeps_the_bf16_range(xscale, wscale, dq):
     with torch.no_grad():
         ref = mod(x, idx, w)
         assert e4b.enable_fast(mod) == 1
-        w1, w2 = F._qweights(mod)
-        assert w1.shift is not None and w2.shift is not None  # the fp16 mode is on
         got = mod(x, idx, w)
+        w1, w2 = F._qweights(mod)
+        assert w1.shift is not None and w2.shift is not None  # the fp16 mode ran
     assert torch.isfinite(got).all()
     _assert_fidelity(got, ref, _oracle(mod, x, idx, w), f"fp16 mode x*{xscale} w*{wscale} dq={dq}")
 
@@ -797,30 +874,42 @@ def test_narrow_tiles_in_fp16_mode(H, I, dq):
     with torch.no_grad():
         ref = mod(x, idx, w)
         assert e4b.enable_fast(mod) == 1
-        w1, w2 = F._qweights(mod)
-        assert w1.shift is not None and w2.shift is not None  # the fp16 mode is on
         got = mod(x, idx, w)
+        w1, w2 = F._qweights(mod)
+        assert w1.shift is not None and w2.shift is not None  # the fp16 mode ran
     assert torch.isfinite(got).all()
     _assert_fidelity(got, ref, _oracle(mod, x, idx, w), f"narrow tiles H={H} I={I} dq={dq}")
 
 
-def test_weight_shift_matches_the_oracle_exponents():
+@pytest.mark.parametrize("H,inter", [(128, 64), (1024, 320)])
+def test_weight_shift_matches_the_oracle_exponents(H, inter):
     """e4b_weight_shift: 141 - max(E, 20), E the largest biased exponent of each expert's block
-    scales (decoded ones for double quantization), from the oracle's decode of the same bytes."""
-    _announce("weight shift")
+    scales (decoded ones for double quantization), from the oracle's decode of the same bytes.
+    At H=1024 the gate_up projection has 10,240 block scales per expert, three blocks of the
+    kernel's grid, and each expert's largest scale is planted in a different one (its first,
+    middle or last row). Decode-sized calls never compute the exponents."""
+    _announce(f"weight shift H={H} inter={inter}")
+    E = 6
     for dq in (False, True):
-        mod, *_ = _make(E=6, seed=20 + dq, dq=dq, scale=0.05)
-        w1, _ = F._qweights(mod)
-        got = w1.shift.cpu().numpy()
-        ow, _ = oracle_weights(mod)
-        for e in range(6):
-            am = ow.absmax[e]
-            if dq:
-                from oracle import c_oracle
+        torch.manual_seed(20 + dq)
+        gu = torch.randn(E, 2 * inter, H) * 0.05
+        for e in range(E):
+            gu[e, (0, inter, 2 * inter - 1)[e % 3]] *= 2.0 ** (1 + e)
+        dn = torch.randn(E, H, inter) * 0.05
+        mod = e4b.Experts4bit.from_float(gu.to(DEV), dn.to(DEV), compute_dtype=torch.bfloat16,
+                                         compress_statistics=dq).eval()
+        assert F._for_tokens(F._qweights(mod), F._SHIFT_FREE_TOKENS)[0].shift is None
+        for i, qw in enumerate(F._for_tokens(F._qweights(mod), F._SHIFT_FREE_TOKENS + 1)):
+            got = qw.shift.cpu().numpy()
+            ow = oracle_weights(mod)[i]
+            for e in range(E):
+                am = ow.absmax[e]
+                if dq:
+                    from oracle import c_oracle
 
-                am = c_oracle.dequant_absmax_dq(am, ow.absmax2[e], ow.offset[e], ow.code2)
-            E_ = int(((np.abs(am).astype(np.float32).view(np.uint32) >> 23) & 0xFF).max())
-            assert got[e] == 141 - max(E_, 20), (dq, e, got[e], E_)
+                    am = c_oracle.dequant_absmax_dq(am, ow.absmax2[e], ow.offset[e], ow.code2)
+                E_ = int(((np.abs(am).astype(np.float32).view(np.uint32) >> 23) & 0xFF).max())
+                assert got[e] == 141 - max(E_, 20), (dq, i, e, got[e], E_)
 
 
 def test_out_of_range_ids_contribute_nothing():
@@ -890,9 +979,9 @@ def test_narrow_tiles_general_epilogues():
     with torch.no_grad():
         ref = mod(hs, top_i, top_w)
         assert e4b.enable_fast(mod) == 1
-        w1, w2 = F._qweights(mod)
-        assert w1.shift is not None  # the fp16 mode, so the narrow kernel
         fast = mod(hs, top_i, top_w)
+        w1, w2 = F._qweights(mod)
+        assert w1.shift is not None  # the fp16 mode ran, so the narrow kernel
     _assert_fidelity(fast, ref, _oracle(mod, hs, top_i, top_w), "narrow act epilogue")
 
     from experts4bit_qlora_amd.arch.deepseek_v4 import _DeepseekV4ForwardMixin

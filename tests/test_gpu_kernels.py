@@ -146,10 +146,13 @@ def test_route_drops_out_of_range_ids():
     assert ref["counts"].sum() == 4
 
 
-@pytest.mark.parametrize("M,E", [(4096, 64), (4097, 64), (4353, 1024), (40000, 256)])
+@pytest.mark.parametrize("M,E", [(4096, 64), (4097, 64), (4353, 1024), (40000, 256), (140000, 128),
+                                 (262144, 64)])
 def test_chunked_route_boundaries_and_dropped_ids(M, E):
     """Around the one-workgroup limit (4096 rows) and on the chunked route: ragged last chunk,
-    many experts, ~1% invalid ids spread through the chunks."""
+    many experts, ~1% invalid ids spread through the chunks. Above 512 chunks (131,072 ids) the
+    per-expert column scan carries its running sum from one pass of 512 chunks to the next
+    (140,000 and 262,144 ids); the tile list and its count are checked against the offsets."""
     _announce(f"chunked route M={M} E={E}")
     rng = np.random.default_rng(M + E)
     flat = rng.integers(0, E, M).astype(np.int64)
@@ -169,6 +172,9 @@ def test_chunked_route_boundaries_and_dropped_ids(M, E):
     counts = np.bincount(flat[valid], minlength=E)
     assert rb.offsets.cpu().numpy().tolist() == np.concatenate([[0], np.cumsum(counts)]).tolist()
     assert meta[1] == (counts > 0).sum()
+    tiles = orouting.m_tiles(counts, rb.tile_m)
+    assert meta[0] == len(tiles)
+    assert rb.tiles[:2 * meta[0]].cpu().numpy().reshape(-1, 2).tolist() == [list(t) for t in tiles]
 
 
 # --------------------------------------------------------------------------------- GEMMs

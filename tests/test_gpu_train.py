@@ -234,3 +234,22 @@ def test_split_lora_passes_equal_the_fused_delta():
     t = ops.lora_t(x, rb, M, E_, A, gather_k=top)
     split = ops.lora_t_add(t, rb, M, E_, B, 2.0, base.clone())
     assert torch.equal(fused, split)
+
+
+@pytest.mark.parametrize("n_tok,E_,top", [(64, 8, 2), (1024, 8, 4)])
+def test_training_lane_is_bit_identical_across_runs(n_tok, E_, top):
+    """ref tests/test_deterministic_scatter.py:62-80: the training forward and every gradient are
+    bit-identical over repeated runs (no float atomics anywhere in the lane). 1,024 tokens x 4
+    slots over 8 experts runs the 128-row tiles; 64 x 2 the 32-row ones."""
+    _announce(f"train determinism n_tok={n_tok} E={E_} top={top}")
+    mod = _build(seed=3, E_=E_)
+    assert e4b.enable_fast_train(mod) == 1
+    args = _inputs(n_tok=n_tok, seed=4, E_=E_, top_k=top)
+    out0, dx0, g0 = _forward_backward(mod, *args)
+    assert set(g0) == {"gate_up_lora_A", "gate_up_lora_B", "down_lora_A", "down_lora_B"}, sorted(g0)
+    for run in range(1, 8):
+        out, dx, grads = _forward_backward(mod, *args)
+        assert torch.equal(out, out0), f"run {run}: forward differs"
+        assert torch.equal(dx, dx0), f"run {run}: dL/dx differs"
+        for n in g0:
+            assert torch.equal(grads[n], g0[n]), f"run {run}: dL/d{n} differs"
