@@ -15,95 +15,24 @@ import numpy as np
 import pytest
 import torch
 
+from decode_layers import Layer as _Layer, _check, _inputs
 from experts4bit_qlora_amd import _native as N
-from experts4bit_qlora_amd import ops, quant as Q
-from oracle import c_oracle, moe
+from experts4bit_qlora_amd import ops
+from oracle import moe
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _announce(msg):
-    print(f"[case] {msg}", flush=True)
-
-
-def _dense(qw) -> np.ndarray:
-    """``[E, n, k]`` fp32 weights of a descriptor decoded by the oracle's C restatement."""
-    E, n, k = qw.num_experts, qw.n, qw.k
-    packed = qw.packed.cpu().numpy().reshape(E, -1)
-    absmax = qw.absmax.cpu().numpy().reshape(E, -1)
-    out = np.empty((E, n, k), np.float32)
-    for e in range(E):
-        if qw.fmt == N.FMT_MXFP4:
-            out[e] = c_oracle.dequant_mxfp4(packed[e], absmax[e], n, k)
-            continue
-        am = absmax[e]
-        if qw.fmt == N.FMT_NF4_DQ:
-            am = c_oracle.dequant_absmax_dq(am, qw.absmax2.cpu().numpy().reshape(E, -1)[e],
-                                            float(qw.offset.cpu().numpy().reshape(E)[e]), qw.code2.cpu().numpy())
-        out[e] = c_oracle.dequant_4bit(packed[e], am, qw.code.cpu().numpy()).reshape(n, k)
-    return out
-
-
-def _stack(fmt, E, n, k, seed):
-    g = torch.Generator().manual_seed(seed)
-    if fmt == "mxfp4":
-        w = torch.randn(E, n, k, generator=g) * 0.05
-        b, s = Q.quantize_mxfp4(w)
-        return ops.mxfp4_qweight(b.reshape(E, -1).to(DEV), s.reshape(E, -1).to(DEV), n, k, num_experts=E)
-    w = torch.randn(E, n * k, generator=g) * 0.02
-    packed, absmax = Q.quantize_4bit(w)
-    code = Q.code_4bit("nf4")
-    if fmt == "nf4_dq":
-        q, a2, off = Q.double_quant(absmax)
-        return ops.nf4_dq_qweight(packed.to(DEV), q.to(DEV), a2.to(DEV), off.to(DEV), code.to(DEV),
-                                  Q.dynamic_map().to(DEV), n, k, num_experts=E)
-    return ops.nf4_qweight(packed.to(DEV), absmax.to(DEV), code.to(DEV), n, k, num_experts=E)
-
-
-class Layer:
-    """One MoE layer's quantized weights (and their oracle decode, made on first use)."""
-
-    def __init__(self, fmt, E, H, I, dt, seed=60):
-        self.fmt, self.E, self.H, self.I, self.dt = fmt, E, H, I, dt
-        self.w1 = _stack(fmt, E, 2 * I, H, seed)
-        self.w2 = _stack(fmt, E, H, I, seed + 1)
-        self.epi, self.spec = N.EPI_SWIGLU, "swiglu"
-        if fmt == "mxfp4":  # gpt-oss: biases in the activation type, clamped GLU
-            g = torch.Generator().manual_seed(seed + 2)
-            self.w1.bias = (torch.randn(E, 2 * I, generator=g) * 0.1).to(dt).to(DEV)
-            self.w2.bias = (torch.randn(E, H, generator=g) * 0.1).to(dt).to(DEV)
-            self.epi, self.spec = N.EPI_GPTOSS, ("gptoss", 1.702, 7.0)
-        self._dense = None
-
-    def dense(self):
-        if self._dense is None:
-            self._dense = (_dense(self.w1), _dense(self.w2))
-        return self._dense
+class Layer(_Layer):
+    """A layer whose run() defaults to the single-launch path."""
 
     def run(self, x, idx, wts, path=N.PATH_DECODE_FUSED, out_dtype=torch.float32):
-        return ops.moe_forward(x, idx, wts, self.w1, self.w2, self.epi, out_dtype, path=path)
-
-    def oracle(self, x, idx, wts):
-        W1, W2 = self.dense()
-        b1 = None if self.w1.bias is None else self.w1.bias.float().cpu().numpy()
-        b2 = None if self.w2.bias is None else self.w2.bias.float().cpu().numpy()
-        return moe.forward_fp32(x.float().cpu().numpy(), idx.cpu().numpy(), wts.float().cpu().numpy(), W1, W2,
-                                self.spec, b1, b2)
+        return super().run(x, idx, wts, path=path, out_dtype=out_dtype)
 
 
-def _inputs(E, H, top, seed, dt, ids=None):
-    rng = np.random.default_rng(seed)
-    idx = np.asarray(ids if ids is not None else rng.permutation(E)[:top][None, :], np.int64)
-    x = (torch.randn(1, H, generator=torch.Generator().manual_seed(seed)) * 2).to(dt)
-    wts = torch.rand(1, idx.shape[1], generator=torch.Generator().manual_seed(seed + 1)).to(torch.bfloat16)
-    return x.to(DEV), torch.from_numpy(idx).to(DEV), wts.to(DEV)
-
-
-def _check(got, want, what):
-    fro, maxabs, _ = moe.rel_errors(got.float().cpu().numpy(), want)
-    assert fro <= 1e-2 and maxabs <= 2e-2, (what, fro, maxabs)
-    return fro, maxabs
+def _announce(msg):
+    print(f"[case] {msg}", flush=True)
 
 
 _CASES = [  # fmt, E, H, I, top, dt
@@ -236,8 +165,8 @@ def test_wait_that_gives_up_raises_the_flag_and_later_calls_are_right():
 
 
 def test_single_launch_is_what_runs():
-    """With the fused flag one token's layer is one kernel launch (decode_fused_kernel), by
-    default two."""
+    """With the fused flag one token's layer is one kernel launch (decode_fused_kernel); the
+    two-launch decode path (forced with E4B_PATH_GEMV) runs the up and down kernels."""
     _announce("fused decode launch count")
     E, H, I, top = 8, 768, 320, 2
     L = Layer("nf4", E, H, I, torch.bfloat16)
@@ -252,7 +181,7 @@ def test_single_launch_is_what_runs():
             torch.cuda.synchronize()
         return [e.name for e in prof.events() if e.device_type == torch.autograd.DeviceType.CUDA]
 
-    fused, split = kernels(N.PATH_DECODE_FUSED), kernels(N.PATH_AUTO)
+    fused, split = kernels(N.PATH_DECODE_FUSED), kernels(N.PATH_GEMV)
     if not fused and not split:
         pytest.skip("the profiler recorded no device activity on this system")
     assert sum("decode_fused_kernel" in n for n in fused) == 1, fused
