@@ -165,6 +165,7 @@ def decode_bench(mods, cfg, T, steps, warmup, seed0):
         "us_per_layer": ms * 1e3 / L,
         "tok_per_s": T / (ms / 1e3),
         "routed_bytes_per_step": step_bytes,
+        "working_set_bytes": step_bytes,  # distinct weights one replay reads (each read once)
         "distinct_experts_per_layer": round(sum(distinct) / L, 2),
         "hbm_gbs": step_bytes / (ms / 1e3) / 1e9,
         "hbm_frac": step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
@@ -172,27 +173,24 @@ def decode_bench(mods, cfg, T, steps, warmup, seed0):
     }
 
 
-def rotating_decode_bench(mods, cfg, steps, warmup, seed0):
-    """The bs=1 decode step with the routed experts rotated between replays, to show the graph
-    replays are not served from the 256 MB Infinity Cache: each layer's experts are split into
-    E / k disjoint sets of k, and replay r routes every layer's token to set r mod (E / k), so an
-    expert's weights are read again only after E / k - 1 replays of other experts (3.2 GB at
-    OLMoE geometry). One device copy before each replay installs the set; the same copies are
-    timed alone and subtracted."""
+def rotating_ids(L, E, k, seed):
+    """Expert-id sets for cache-honest bs=1 legs: layer l's experts split into R = E // k disjoint
+    sets of k (bank [R, L, 1, k]) and the buffer a captured graph reads (ids [L, 1, k])."""
     import torch
 
-    L, E, k = len(mods), cfg["E"], cfg["k"]
     R = E // k
-    g = torch.Generator().manual_seed(seed0)
+    g = torch.Generator().manual_seed(seed)
     bank = torch.stack([torch.randperm(E, generator=g)[: R * k].view(R, 1, k) for _ in range(L)], 1).cuda()
-    ids = bank[0].clone()  # [L, 1, k]: the graph reads layer l's ids from ids[l]
-    inputs = [make_inputs(cfg, 1, seed0 + 10 * l) for l in range(L)]
+    return bank, bank[0].clone()
 
-    def step():
-        with torch.no_grad():
-            return [m(x, ids[l], w) for l, (m, (x, _, w)) in enumerate(zip(mods, inputs))]
 
-    gr, _ = graph_of(step)
+def time_rotating(gr, bank, ids, steps, warmup):
+    """ms per replay of a graph reading `ids`, with set r % R copied into it before replay r (so a
+    layer's experts come back only after R - 1 replays of other experts); the copies are timed
+    alone and subtracted. Returns (ms, copy_ms)."""
+    import torch
+
+    R = bank.shape[0]
 
     def run(n, replay):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -209,8 +207,32 @@ def rotating_decode_bench(mods, cfg, steps, warmup, seed0):
     n = max(steps, 4 * R)
     ms = run(n, True)
     copy_ms = run(n, False)
-    return {"us_per_layer": round((ms - copy_ms) * 1e3 / L, 3), "id_sets": R,
-            "copy_us_per_step": round(copy_ms * 1e3, 2)}
+    return ms - copy_ms, copy_ms
+
+
+def rotating_decode_bench(mods, cfg, steps, warmup, seed0):
+    """The bs=1 decode step with the routed experts rotated between replays, to show the graph
+    replays are not served from the 256 MB Infinity Cache: each layer's experts are split into
+    E / k disjoint sets of k, and replay r routes every layer's token to set r mod (E / k), so an
+    expert's weights are read again only after E / k - 1 replays of other experts (3.2 GB at
+    OLMoE geometry). One device copy before each replay installs the set; the same copies are
+    timed alone and subtracted."""
+    import torch
+
+    L, E, k = len(mods), cfg["E"], cfg["k"]
+    bank, ids = rotating_ids(L, E, k, seed0)  # the graph reads layer l's ids from ids[l]
+    inputs = [make_inputs(cfg, 1, seed0 + 10 * l) for l in range(L)]
+
+    def step():
+        with torch.no_grad():
+            return [m(x, ids[l], w) for l, (m, (x, _, w)) in enumerate(zip(mods, inputs))]
+
+    gr, _ = graph_of(step)
+    ms, copy_ms = time_rotating(gr, bank, ids, steps, warmup)
+    gu_b, dn_b = nf4_expert_bytes(cfg["H"], cfg["I"])
+    return {"us_per_layer": round(ms * 1e3 / L, 3), "id_sets": bank.shape[0],
+            "copy_us_per_step": round(copy_ms * 1e3, 2),
+            "working_set_bytes": L * E * (gu_b + dn_b)}
 
 
 def lora_bench(mods, cfg, steps, warmup, seed0, bare, rank=16):
@@ -244,6 +266,22 @@ def lora_bench(mods, cfg, steps, warmup, seed0, bare, rank=16):
         us = ms * 1e3 / len(mods)
         out[f"bs{T}"] = {"us_per_layer": round(us, 3), "vs_bare_layer": round(us / bare[T]["us_per_layer"], 3),
                          "rank": rank}
+    # prefill: one layer at 4,096 tokens (the grouped form: fp16 matrix-core GEMMs with the
+    # deltas in their epilogues), bare and with the adapter, each graph-replayed on its own
+    T = 4096
+    x, idx, w = make_inputs(cfg, T, seed0 + 7)
+
+    def layer_ms(mod):
+        def step():
+            with torch.no_grad():
+                return mod(x, idx, w)
+
+        g, _ = graph_of(step)
+        return time_graph(g, steps, warmup)
+
+    bare_ms, lora_ms = layer_ms(mods[0]), layer_ms(wrappers[0])
+    out["prefill4096"] = {"ms_lora": round(lora_ms, 4), "ms_bare": round(bare_ms, 4),
+                          "vs_bare_layer": round(lora_ms / bare_ms, 3), "rank": rank, "tokens": T}
     for w in wrappers:
         e4b.disable_fast(w)
     return out
@@ -253,34 +291,41 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
     """The decode gate_up kernel (routing + gate_up GEMV + SwiGLU) at bs=1 alone, 16 layers per
     graph replay, timed with HIP events on the launch stream: achieved = routed gate_up bytes
     per launch / average launch duration. The second decode kernel (down GEMV + k-slot combine)
-    is timed the same way, on the h the first one wrote; it is reported beside the roofline."""
+    is timed the same way, on the h the first one wrote; it is reported beside the roofline.
+    Both replay with rotating expert sets (time_rotating): one replay reads 302 MB (up) or 151 MB
+    (down) of weights, within the 256 MB Infinity Cache's reach, so each replay routes every layer
+    to the next of 8 disjoint expert sets and a set's weights return only after 7 other replays
+    (2.4 GB / 1.2 GB cycled)."""
     import torch
 
     from experts4bit_qlora_amd import _native as N
     from experts4bit_qlora_amd import fast as F
     from experts4bit_qlora_amd import ops
 
-    inputs = [make_inputs(cfg, 1, seed0 + 10 * l) for l in range(len(mods))]
+    L = len(mods)
+    inputs = [make_inputs(cfg, 1, seed0 + 10 * l) for l in range(L)]
     qws = [F._qweights(m) for m in mods]
+    bank, ids = rotating_ids(L, cfg["E"], cfg["k"], seed0 + 5)
     torch.cuda.synchronize()
 
     def launches():
-        return [ops.decode_gate_up(x, idx, qw[0], N.EPI_SWIGLU) for (x, idx, _), qw in zip(inputs, qws)]
+        return [ops.decode_gate_up(x, ids[l], qw[0], N.EPI_SWIGLU) for l, ((x, _, _), qw) in enumerate(zip(inputs, qws))]
 
     g, hs = graph_of(launches)
-    ms = time_graph(g, steps * 4, warmup)
-    per_launch_us = ms * 1e3 / len(mods)
+    ms, _ = time_rotating(g, bank, ids, steps * 4, warmup)
+    per_launch_us = ms * 1e3 / L
     gu_b, dn_b = nf4_expert_bytes(cfg["H"], cfg["I"])
     bytes_per_launch = cfg["k"] * gu_b  # 8 distinct routed experts at bs=1
     achieved = bytes_per_launch / (per_launch_us * 1e-6) / 1e9
     kernel = "decode_up_kernel<bf16, nf4, G=16, CPL=4, full, gated>"
 
     def down_launches():
-        return [ops.decode_down_combine(h, idx, w, qw[1], x.dtype) for h, (x, idx, w), qw in zip(hs, inputs, qws)]
+        return [ops.decode_down_combine(h, ids[l], w, qw[1], x.dtype)
+                for l, (h, (x, _, w), qw) in enumerate(zip(hs, inputs, qws))]
 
     g2, _ = graph_of(down_launches)
-    ms2 = time_graph(g2, steps * 4, warmup)
-    down_us = ms2 * 1e3 / len(mods)
+    ms2, _ = time_rotating(g2, bank, ids, steps * 4, warmup)
+    down_us = ms2 * 1e3 / L
     down_bytes = cfg["k"] * dn_b
     return {
         "bound": "hbm",
@@ -292,6 +337,8 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
         "traffic": MEASURED_TRAFFIC.get(kernel),
         "bytes_per_launch": bytes_per_launch,
         "avg_launch_us": round(per_launch_us, 3),
+        "timer": "HIP events on the launch stream, 16 launches per graph replay, expert sets rotated",
+        "working_set_bytes": L * cfg["E"] * gu_b,  # gate_up weights cycled by the rotation
         "second_kernel": {
             "kernel": "decode_down_kernel<bf16, nf4, G=32, CPL=1, JOBS=1, full> (down + k-slot combine, bs=1)",
             "avg_launch_us": round(down_us, 3),
@@ -299,6 +346,7 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
             "achieved": round(down_bytes / (down_us * 1e-6) / 1e9, 1),
             "frac": round(down_bytes / (down_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "traffic": MEASURED_TRAFFIC.get("decode_down_kernel<bf16, nf4, G=32, CPL=1, JOBS=1, full>"),
+            "working_set_bytes": L * cfg["E"] * dn_b,
         },
     }
 
@@ -452,15 +500,30 @@ def qwen3_decode_benches(steps, warmup, layers=8, batches=(1, 32, 256)):
     per_expert = dq_expert_bytes(cfg["H"], cfg["I"])
     for T in batches:
         inputs = [make_inputs(cfg, T, seed=1000 + 210 + T + 7 * l) for l in range(layers)]
+        if T == 1:
+            # 8 layers x 8 experts = 156 MB per replay, within the Infinity Cache's reach: rotate
+            # 16 disjoint expert sets per layer (a set returns after 15 other replays, 2.5 GB)
+            bank, ids = rotating_ids(layers, cfg["E"], cfg["k"], 1000 + 215)
 
-        def step():
-            with torch.no_grad():
-                return [m(x, idx, w) for m, (x, idx, w) in zip(mods, inputs)]
+            def step():
+                with torch.no_grad():
+                    return [m(x, ids[l], w) for l, (m, (x, _, w)) in enumerate(zip(mods, inputs))]
 
-        g, _ = graph_of(step)
-        ms = time_graph(g, steps * 2, warmup) / layers
-        nbytes = sum(int(torch.unique(idx).numel()) for _, idx, _ in inputs) / layers * per_expert
-        out[f"qwen3_dq_bs{T}"] = {"us": ms * 1e3, "hbm_gbs": nbytes / (ms / 1e3) / 1e9, "layers": layers}
+            g, _ = graph_of(step)
+            ms = time_rotating(g, bank, ids, steps * 2, warmup)[0] / layers
+            nbytes = cfg["k"] * per_expert
+            ws = layers * cfg["E"] * per_expert
+        else:
+            def step():
+                with torch.no_grad():
+                    return [m(x, idx, w) for m, (x, idx, w) in zip(mods, inputs)]
+
+            g, _ = graph_of(step)
+            ms = time_graph(g, steps * 2, warmup) / layers
+            nbytes = sum(int(torch.unique(idx).numel()) for _, idx, _ in inputs) / layers * per_expert
+            ws = nbytes * layers  # 8 layers of 112-128 distinct experts: 2.2-2.5 GB per replay
+        out[f"qwen3_dq_bs{T}"] = {"us": ms * 1e3, "hbm_gbs": nbytes / (ms / 1e3) / 1e9, "layers": layers,
+                                  "working_set_bytes": int(ws), "expert_sets_rotated": T == 1}
     return out
 
 
@@ -495,17 +558,32 @@ def extra_benches(steps, warmup, qwen_layers=8, gptoss_layers=4):
             x = torch.randn(T, H, generator=gi, device="cuda").to(torch.bfloat16)
             val, idx = torch.topk(torch.randn(T, E, generator=gi, device="cuda"), cfg["k"], dim=-1)
             inputs.append((x, idx, torch.softmax(val, -1).to(torch.bfloat16)))
+        if T == 1:
+            # 4 layers x 4 experts = 212 MB per replay, within the Infinity Cache's reach: rotate 8
+            # disjoint expert sets per layer (a set returns after 7 other replays, 1.7 GB)
+            bank, ids = rotating_ids(gptoss_layers, E, cfg["k"], 1415)
 
-        def step():
-            with torch.no_grad():
-                return [m(x, idx, w) for m, (x, idx, w) in zip(mods, inputs)]
+            def step():
+                with torch.no_grad():
+                    return [m(x, ids[l], w) for l, (m, (x, _, w)) in enumerate(zip(mods, inputs))]
 
-        g, _ = graph_of(step)
-        ms = time_graph(g, steps, warmup) / gptoss_layers
-        nbytes = sum(int(torch.unique(idx).numel()) for _, idx, _ in inputs) / gptoss_layers * per_expert
+            g, _ = graph_of(step)
+            ms = time_rotating(g, bank, ids, steps, warmup)[0] / gptoss_layers
+            nbytes = cfg["k"] * per_expert
+            ws = gptoss_layers * E * per_expert
+        else:
+            def step():
+                with torch.no_grad():
+                    return [m(x, idx, w) for m, (x, idx, w) in zip(mods, inputs)]
+
+            g, _ = graph_of(step)
+            ms = time_graph(g, steps, warmup) / gptoss_layers
+            nbytes = sum(int(torch.unique(idx).numel()) for _, idx, _ in inputs) / gptoss_layers * per_expert
+            ws = nbytes * gptoss_layers
         flops = 2 * cfg["k"] * T * (2 * I * H + H * I)
         out[f"gptoss_mxfp4_bs{T}"] = {"us": ms * 1e3, "hbm_gbs": nbytes / (ms / 1e3) / 1e9,
-                                      "tflops": flops / (ms / 1e3) / 1e12, "layers": gptoss_layers}
+                                      "tflops": flops / (ms / 1e3) / 1e12, "layers": gptoss_layers,
+                                      "working_set_bytes": int(ws), "expert_sets_rotated": T == 1}
     return out
 
 
@@ -702,7 +780,7 @@ def main():
     main_line = decode[1]
     log("decode step, batch 1, experts rotated between replays")
     decode[1]["rotating_experts"] = rotating_decode_bench(mods, cfg, args.steps, args.warmup, seed0=1000 + 100)
-    log("ExpertsLoRA decode step, batches 1 and 8")
+    log("ExpertsLoRA decode step, batches 1 and 8; one layer at 4096 tokens")
     lora = lora_bench(mods, cfg, args.steps, args.warmup, 1000 + 100, decode)
 
     prefill = None

@@ -25,6 +25,7 @@
 #include "gemm_launch.h"
 #include "gemv.h"
 #include "lora.h"
+#include "lora_mfma.h"
 #include "route.h"
 #include "scale.h"
 #include "train.h"
@@ -528,10 +529,19 @@ int64_t e4b_route_scratch_ints(int64_t M, int32_t num_experts) {
 // e4b_grouped_gemm, plus the fp16 matrix-core mode of the fused forward: a_exp (the A rows'
 // largest exponents, the rows stored as scaled fp16 by row_exp_kernel) selects it on the MFMA
 // path.
+// The LoRA delta a grouped GEMM adds in its epilogue: lscale * t[m, :] . B[e, row, :] (t fp32 [M, rank]
+// of the routed rows, B [E, n, rank] in dtype).
+struct LoraEpi {
+  const float* t;
+  const void* b;
+  int dtype, rank;
+  float scaling;
+};
+
 static int grouped_gemm_impl(const void* a, int32_t act_dtype, int32_t gather_k, const e4b_qweight* w,
                              const e4b_routing* rt, int64_t tokens, int64_t M, int32_t epilogue, float alpha,
                              float limit, int32_t flags, void* out, int32_t out_dtype, const int32_t* a_exp,
-                             hipStream_t stream) {
+                             hipStream_t stream, const LoraEpi* lora = nullptr) {
   int rc = check_weight(w);
   if (rc) return rc;
   rc = check_routing(rt, M);
@@ -573,6 +583,20 @@ static int grouped_gemm_impl(const void* a, int32_t act_dtype, int32_t gather_k,
   if (f16c && (gemv || act_dtype != E4B_BF16 || w->format == E4B_FMT_MXFP4 || !w->shift))
     return fail(E4B_EINVAL, "the fp16 matrix-core mode needs the MFMA path, bf16 activations and NF4 weight shifts");
   args.a_exp = a_exp;
+  args.lt = nullptr;
+  args.lb = nullptr;
+  args.lbdt = E4B_FP32;
+  args.lr = 0;
+  args.lscale = 0.0f;
+  if (lora) {
+    if (!f16c || !e4b::lora_gemm_fits(rt->tile_m, w->k))
+      return fail(E4B_EINVAL, "the LoRA epilogue needs the fp16 mode over 256-row tiles or 32-row tiles with k %% 256 == 0");
+    args.lt = lora->t;
+    args.lb = lora->b;
+    args.lbdt = lora->dtype;
+    args.lr = lora->rank;
+    args.lscale = lora->scaling;
+  }
   const int64_t max_active = std::min<int64_t>(w->num_experts, M);
   return act_dtype == E4B_BF16 ? launch_gemm_dt<E4B_BF16>(args, gemv, max_active, stream)
                                : launch_gemm_dt<E4B_FP16>(args, gemv, max_active, stream);
@@ -1122,6 +1146,100 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
 
 static_assert(e4b::kDecLoraMaxRank == e4b::kLoraMaxRank, "one rank limit for both LoRA paths");
 
+}  // extern "C"
+
+namespace {
+
+// Whether the grouped LoRA forward runs in the fp16 mode with the deltas in the GEMM epilogues.
+bool lora_fused_ok(int32_t act_dtype, const e4b_qweight* w1, const e4b_qweight* w2) {
+  return act_dtype == E4B_BF16 && w1->format != E4B_FMT_MXFP4 && w1->shift && w2->shift &&
+         e4b::lora_gemm_fits(e4b::kTileMSmall, w1->k) && e4b::lora_gemm_fits(e4b::kTileMSmall, w2->k);
+}
+
+// t = x . A^T for the sorted rows of rt's tiles on the matrix cores (bf16 x, in a multiple of 64,
+// which the narrow kernel's k limit of that path implies): 64-row parts of 128-row tiles, whole
+// 32-row tiles, the ranks in 16-rank blocks.
+int lora_t_mfma(const void* x, int32_t gather_k, const e4b_routing& rt, const void* A, int32_t adt, int rank,
+                int64_t in, float* t, hipStream_t stream) {
+  if (in <= 0 || in % e4b::kLoraTK != 0)
+    return fail(E4B_EINVAL, "in_features=%lld not a multiple of %d", (long long)in, e4b::kLoraTK);
+  const int bm = rt.tile_m % 64 == 0 ? 64 : 32;
+  if (rt.tile_m <= 0 || rt.tile_m % bm != 0) return fail(E4B_EINVAL, "tile_m=%d", rt.tile_m);
+  const int64_t blocks = int64_t(rt.max_tiles) * (rt.tile_m / bm);
+  if (blocks > 0x7fffffffLL) return fail(E4B_EUNSUPPORTED, "LoRA t grid too large");
+  const dim3 grid(static_cast<unsigned>(blocks));
+  const int nsm = rank <= 16 ? 1 : (rank <= 32 ? 2 : 4);
+#define E4B_TM(AD, BM, NS)                                                                                    \
+  if (adt == AD && bm == BM && nsm == NS)                                                                    \
+    hipLaunchKernelGGL((e4b::lora_t_mfma_kernel<AD, BM, NS>), grid, dim3(BM / 16 * e4b::kWave), 0, stream,     \
+                       static_cast<const uint16_t*>(x), gather_k, rt, A, rank, in, t);
+#define E4B_TM_AD(AD) E4B_TM(AD, 64, 1) E4B_TM(AD, 64, 2) E4B_TM(AD, 64, 4) E4B_TM(AD, 32, 1) E4B_TM(AD, 32, 2) \
+  E4B_TM(AD, 32, 4)
+  E4B_TM_AD(E4B_BF16) E4B_TM_AD(E4B_FP16) E4B_TM_AD(E4B_FP32)
+#undef E4B_TM_AD
+#undef E4B_TM
+  return check_launch("lora_t_mfma_kernel");
+}
+
+// The workspace of that path, carved from p when p is not NULL; returns its size. Routing (and for
+// prefill-sized batches the 256- / 32-row re-tiling), token and h row exponents, the scaled tokens,
+// h, the fp32 down rows and one fp32 t [M, rank] (gate_up's, then down's).
+size_t carve_lora_fused(char* p, int64_t tokens, int64_t M, int E, int64_t h_cols, int64_t k1, int64_t n2, int rank,
+                        e4b_routing* rt, e4b_routing* rbig, e4b_routing* rsmall, bool* split, int32_t** xexp,
+                        int32_t** hexp, uint16_t** x16, void** h, void** down, float** t) {
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    char* q = p ? p + off : nullptr;
+    off += align256(bytes);
+    return q;
+  };
+  e4b_routing a{}, b{}, c{};
+  a.sorted_flat = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));
+  a.inv = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));
+  a.offsets = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (E + 1)));
+  a.active = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * E));
+  a.tile_m = mfma_tile_for(M, E);
+  a.max_tiles = static_cast<int32_t>(max_tiles_for(M, E, a.tile_m));
+  a.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * a.max_tiles));
+  a.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
+  a.scratch = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * e4b_route_scratch_ints(M, E)));
+  const bool sp = a.tile_m == e4b::kTileM;  // prefill-sized: 256-row tiles plus 32-row tails
+  b = c = a;
+  if (sp) {
+    b.tile_m = e4b::kTileMBig;
+    b.max_tiles = static_cast<int32_t>(max_tiles_for(M, E, b.tile_m));
+    b.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * b.max_tiles));
+    b.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
+    c.tile_m = e4b::kTileMSmall;
+    c.max_tiles = static_cast<int32_t>(max_small_tiles(M, E));
+    c.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * c.max_tiles));
+    c.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));
+  }
+  int32_t* xe = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * tokens));
+  int32_t* he = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));
+  uint16_t* xs = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * tokens * k1));
+  void* hh = take(sizeof(uint16_t) * M * h_cols);
+  void* dn = take(sizeof(float) * M * n2);
+  float* tt = reinterpret_cast<float*>(take(sizeof(float) * M * rank));
+  if (p) {
+    *rt = a;
+    *rbig = b;
+    *rsmall = c;
+    *split = sp;
+    *xexp = xe;
+    *hexp = he;
+    *x16 = xs;
+    *h = hh;
+    *down = dn;
+    *t = tt;
+  }
+  return off;
+}
+
+}  // namespace
+
+extern "C" {
+
 size_t e4b_moe_lora_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_experts, int64_t n1, int64_t n2,
                                     int32_t epilogue, int32_t act_dtype, int32_t rank) {
   (void)act_dtype;
@@ -1136,7 +1254,10 @@ size_t e4b_moe_lora_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_e
   g += align256(sizeof(int32_t) * 2 * max_tiles_for(M, num_experts, mfma_tile_for(M, num_experts)));
   g += align256(sizeof(int32_t) * 4) + align256(sizeof(int32_t) * e4b_route_scratch_ints(M, num_experts));
   g += align256(sizeof(float) * M * n1) + h + align256(sizeof(float) * M * n2) + t;  // up, h, down, t
-  return std::max(dec, g);
+  // the fp16-mode path (k1 = n2, the hidden size)
+  const size_t f = carve_lora_fused(nullptr, tokens, M, num_experts, h_cols, n2, n2, std::max(rank, 1), nullptr,
+                                    nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr);
+  return std::max(dec, std::max(g, f));
 }
 
 int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
@@ -1241,9 +1362,63 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
     return check_launch("decode_down_kernel (LoRA)");
   }
 
-  // Grouped path: route once; gate_up GEMM to fp32 rows, its delta fused with the activation,
-  // down GEMM to fp32 rows plus its delta, combine. The deltas stay fp32 until h / out are
-  // rounded.
+  // Grouped path in the fp16 matrix-core mode with each delta inside its GEMM's epilogue (bf16
+  // activations, NF4 weights carrying shifts, both projections' k taken by the 32-row narrow
+  // kernel): t1 = x . A1^T; gate_up GEMM + lscale t1 . B1^T + epilogue -> h; t2 = h . A2^T; h as
+  // scaled fp16 rows; down GEMM + lscale t2 . B2^T -> fp32 rows; combine. No fp32 gate_up rows
+  // and no pass over the down rows: the deltas ride the GEMM tiles' accumulators.
+  const bool gemv_path = flags == E4B_PATH_GEMV || (flags == E4B_PATH_AUTO && tokens <= 4);
+  if (!gemv_path && lora_fused_ok(act_dtype, w1, w2)) {
+    e4b_routing rt, rbig, rsmall;
+    bool split = false;
+    int32_t *xexp, *hexp;
+    uint16_t* x16;
+    void *h, *down;
+    float* t;
+    carve_lora_fused(p, tokens, M, E, h_cols, w1->k, w2->n, r, &rt, &rbig, &rsmall, &split, &xexp, &hexp, &x16, &h,
+                     &down, &t);
+    rc = e4b_route(top_k_index, tokens, top_k, E, &rt, stream);
+    if (rc) return rc;
+    e4b::launch_row_exp(static_cast<const uint16_t*>(hidden), tokens, w1->k, xexp, x16, nullptr, 0, stream);
+    rc = check_launch("row_exp_kernel");
+    if (rc) return rc;
+    if (split) {
+      hipLaunchKernelGGL(e4b::split_tiles_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, rt.offsets, rt.meta,
+                         E, rbig, rsmall);
+      rc = check_launch("split_tiles_kernel");
+      if (rc) return rc;
+    }
+    const e4b_routing* parts[2] = {split ? &rbig : &rt, split ? &rsmall : nullptr};
+    rc = lora_t_mfma(hidden, top_k, rt, lora->a1, lora->dtype, r, w1->k, t, stream);
+    if (rc) return rc;
+    const LoraEpi l1{t, lora->b1, lora->dtype, r, lora->scaling};
+    for (const e4b_routing* rp : parts) {
+      if (!rp) continue;
+      rc = grouped_gemm_impl(x16, act_dtype, top_k, w1, rp, tokens, M, epilogue, 1.0f, limit, E4B_PATH_MFMA, h,
+                             act_dtype, xexp, stream, &l1);
+      if (rc) return rc;
+    }
+    // t2 from the bf16 h, before h is rewritten as scaled fp16 rows for the down GEMM
+    rc = lora_t_mfma(h, 0, rt, lora->a2, lora->dtype, r, w2->k, t, stream);
+    if (rc) return rc;
+    e4b::launch_row_exp(static_cast<const uint16_t*>(h), M, h_cols, hexp, static_cast<uint16_t*>(h), nullptr, 0,
+                        stream);
+    rc = check_launch("row_exp_kernel");
+    if (rc) return rc;
+    const LoraEpi l2{t, lora->b2, lora->dtype, r, lora->scaling};
+    for (const e4b_routing* rp : parts) {
+      if (!rp) continue;
+      rc = grouped_gemm_impl(h, act_dtype, 0, w2, rp, tokens, M, E4B_EPI_NONE, 1.0f, limit, E4B_PATH_MFMA, down,
+                             E4B_FP32, hexp, stream, &l2);
+      if (rc) return rc;
+    }
+    return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
+                       stream);
+  }
+
+  // Grouped path otherwise: route once; gate_up GEMM to fp32 rows, its delta fused with the
+  // activation, down GEMM to fp32 rows plus its delta, combine. The deltas stay fp32 until h / out
+  // are rounded.
   e4b_routing rt;
   rt.sorted_flat = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));
   rt.inv = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * M));

@@ -34,6 +34,8 @@
 // exact weights to within those roundings.
 #pragma once
 
+#include <utility>
+
 #include "common.h"
 #include "dequant.h"
 #include "gemv.h"
@@ -82,6 +84,31 @@ E4B_DEV bool tile_of_block(int num_tiles, int n_tiles, int& tile, int& n_tile) {
   tile = w / n_tiles;
   n_tile = w % n_tiles;
   return true;
+}
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): indices known at compile
+// time whatever the unroller decides, so the accumulator array never needs an address (a loop
+// left rolled would put all 256 accumulators in scratch memory).
+template <class F, int... I>
+E4B_DEV void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+E4B_DEV void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+template <int DT>
+E4B_DEV f32x16_t mfma_32x32x16(const uint4& a, const uint4& b, const f32x16_t& c) {
+  if constexpr (DT == E4B_BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                   c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                                  c, 0, 0, 0);
+  }
 }
 
 template <int DT>

@@ -54,6 +54,16 @@ dim3 gemm_grid(const GemmArgs& a, int64_t nw) {
 template <int DT, int FMT>
 void launch_mfma_gemm(const GemmArgs& a, hipStream_t s) {
   if constexpr (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4) {
+    // the LoRA epilogue: fp16 mode, 256-row tiles (wide) or 32-row tiles the narrow kernel takes
+    // (the host checks lora_gemm_fits before asking)
+    if (a.lt) {
+      if (a.rt.tile_m == kTileMBig)
+        hipLaunchKernelGGL((gemm_wide_kernel<DT, FMT, true, true>), gemm_grid(a, kWideTileN), dim3(kWideThreads), 0,
+                           s, a);
+      else
+        hipLaunchKernelGGL((gemm_narrow_kernel<FMT, true>), gemm_grid(a, kNarrowN), dim3(kNarrowThreads), 0, s, a);
+      return;
+    }
     // 32-row tiles in the fp16 mode: the narrow kernel, when K is a whole number of its steps
     if (a.rt.tile_m == kTileMSmall && a.a_exp && narrow_fits(a.w.k)) {
       hipLaunchKernelGGL((gemm_narrow_kernel<FMT>), gemm_grid(a, kNarrowN), dim3(kNarrowThreads), 0, s, a);

@@ -16,6 +16,12 @@ struct GemmArgs;
 template <int DT, int FMT>
 void launch_mfma_gemm(const GemmArgs& a, hipStream_t s);
 
+// Whether a grouped GEMM with a LoRA epilogue (GemmArgs::lt) can run: fp16 mode over 256-row
+// tiles, or over 32-row tiles with K a whole number of the narrow kernel's step pairs.
+inline bool lora_gemm_fits(int tile_m, int64_t k) {
+  return tile_m == 256 || (tile_m == 32 && k > 0 && k % 256 == 0 && k <= 256 * 64);
+}
+
 #define E4B_GEMM_EXTERN(DT, FMT) extern template void launch_mfma_gemm<DT, FMT>(const GemmArgs&, hipStream_t);
 E4B_GEMM_EXTERN(E4B_BF16, E4B_FMT_NF4)
 E4B_GEMM_EXTERN(E4B_BF16, E4B_FMT_NF4_DQ)

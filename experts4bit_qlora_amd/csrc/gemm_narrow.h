@@ -53,7 +53,9 @@ constexpr int kNarrowUnroll = 6;  // steps per loop pass: whole weight sets (3) 
 // a weight row's absmax blocks within two absmax2 groups.
 constexpr bool narrow_fits(int64_t k) { return k > 0 && k % (2 * kNarrowK) == 0 && k <= 256 * 64; }
 
-template <int FMT>
+// LORA: the accumulators start as the tile's LoRA delta (p.lt, p.lb), scaled like the products
+// (lora_mfma.h).
+template <int FMT, bool LORA = false>
 __global__ void __launch_bounds__(kNarrowThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_narrow_kernel(GemmArgs p) {
   static_assert(FMT == E4B_FMT_NF4 || FMT == E4B_FMT_NF4_DQ, "narrow tiles: NF4 weights in fp16 mode");
@@ -199,6 +201,25 @@ gemm_narrow_kernel(GemmArgs p) {
   for (int i = 0; i < MS; ++i)
 #pragma unroll
     for (int j = 0; j < NS; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (LORA) {
+    // the accumulators start as the tile's LoRA delta, scaled like the products (lora_mfma.h):
+    // t rows of the lane's fragment rows (clamped to the expert's rows) times their activation
+    // shifts, B rows of its columns as the weight loads took them (row 0 past n_out) times the
+    // expert's weight shift
+    int64_t brow[NS];
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) {
+      if (pair) {
+        const int64_t jj = col0 + wid * 32 + (ns & 1) * 16 + l16;
+        brow[ns] = jj < p.n_out ? (ns < 2 ? jj : n / 2 + jj) : 0;
+      } else {
+        const int64_t rr = col0 + wid * 64 + ns * 16 + l16;
+        brow[ns] = rr < p.n_out ? rr : 0;
+      }
+    }
+    lora_delta_16x16<MS, NS>(p, acc, e, row0 + l16, row_end - 1,
+                             [&](int ms) { return row_shift_s[ms * 16 + l16]; }, wsh, brow, lane);
+  }
 
   // fragment group slots of the lane for MFMA j: (4 g + j) ^ (row % 16), row % 16 = lane % 16
   const int fslot = (4 * g) ^ l16;

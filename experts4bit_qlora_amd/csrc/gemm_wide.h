@@ -25,29 +25,14 @@
 // 8 * (i / 4) + 4 * (l / 32) + i % 4, i = 0..15, of its tile.
 #pragma once
 
-#include <utility>
-
 #include "gemm.h"
+#include "lora_mfma.h"
 
 namespace e4b {
-
-// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): indices known at compile
-// time whatever the unroller decides, so the accumulator array never needs an address (a loop
-// left rolled would put all 256 accumulators in scratch memory).
-template <class F, int... I>
-E4B_DEV void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, class F>
-E4B_DEV void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
 
 constexpr int kWideThreads = 256;
 constexpr int kWideTileM = kTileMBig;  // sorted rows per tile
 constexpr int kWideTileN = 256;  // weight rows per tile
-
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 // LDS tile layout of this kernel: 128-byte rows of 64 elements, the row's eight 16-byte groups in
 // the order group ^ ((row ^ (row >> 3)) & 7). Measured with SQ_LDS_BANK_CONFLICT on the two
@@ -56,17 +41,6 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 // layout of gemm_mfma_kernel, costs the fragment reads a 2-way conflict, and group ^ ((row >> 1)
 // & 7) the stores.)
 E4B_DEV int lds_at_w(int row, int col) { return row * kTileK + ((((col >> 3) ^ row ^ (row >> 3)) & 7) << 3); }
-
-template <int DT>
-E4B_DEV f32x16_t mfma_32x32x16(const uint4& a, const uint4& b, const f32x16_t& c) {
-  if constexpr (DT == E4B_BF16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
-                                                   c, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
-                                                  c, 0, 0, 0);
-  }
-}
 
 // Work items, tile by tile: tile t runs on XCD t % 8 (workgroups go round-robin over the 8
 // XCDs: block L runs on XCD L % 8), and each XCD sweeps all N tiles of one M tile before its
@@ -83,7 +57,9 @@ E4B_DEV bool wide_tile_of_block(int num_tiles, int n_tiles, int& tile, int& n_ti
 
 // One tile. HALF: a tile of at most 128 rows (an expert's last, partial tile) as 128 rows x 256
 // weight rows, each wave 128 x 64 (two 32 x 32 MFMA columns), instead of padding it to 256 rows.
-template <int DT, int FMT, bool F16C, bool HALF>
+// LORA: the accumulators start as the tile's LoRA delta (p.lt, p.lb), scaled like the products
+// (lora_mfma.h).
+template <int DT, int FMT, bool F16C, bool HALF, bool LORA>
 E4B_DEV void wide_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2][kWideTileM * kTileK],
                        uint16_t (&Ws)[2][kWideTileN * kTileK], float* code2_s, int* row_shift_s,
                        const uint32_t* ptab) {
@@ -284,7 +260,28 @@ E4B_DEV void wide_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2
   load_a_all(0);
   load_w(0, 0);
   load_w(1, min<int64_t>(1, klast));
-  __syncthreads();  // code2 table
+  __syncthreads();  // code2 table, row shifts
+  if constexpr (LORA) {
+    // the accumulators start as the tile's LoRA delta, scaled like the products (lora_mfma.h):
+    // the lane's t rows (clamped to the expert's rows: the rest is never stored) times their
+    // activation shifts, the B rows of its columns (weight row 0 past n_out) times the expert's
+    // weight shift
+    const int la = lane;
+    int64_t brow[NS];
+#pragma unroll
+    for (int ns = 0; ns < NS; ++ns) {
+      const int tr = nbase[ns] + (la & 31);
+      if (pair) {
+        const int64_t jj = col0 + (tr & (BN / 2 - 1));
+        brow[ns] = jj < p.n_out ? (tr < BN / 2 ? jj : n / 2 + jj) : 0;
+      } else {
+        brow[ns] = col0 + tr < p.n_out ? col0 + tr : 0;
+      }
+    }
+    const int arow = wave_m * 128 + (la & 31);
+    lora_delta_32x32<MS, NS>(p, acc, e, row0 + arow, row_end - 1,
+                             [&](int ms) { return row_shift_s[arow + 32 * ms]; }, wsh, brow, la);
+  }
   stage(0, 0, block_scale(0));
   load_a_all(min<int64_t>(1, klast));
   load_w(0, min<int64_t>(2, klast));
@@ -474,9 +471,10 @@ E4B_DEV void wide_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2
   });
 }
 
-template <int DT, int FMT, bool F16C = false>
+template <int DT, int FMT, bool F16C = false, bool LORA = false>
 __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
   static_assert(!F16C || (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4), "fp16 mode: bf16 activations, NF4 weights");
+  static_assert(!LORA || F16C, "the LoRA epilogue runs in the fp16 mode");
   constexpr int BM = kWideTileM, BN = kWideTileN;
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kTileK];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kTileK];
@@ -497,8 +495,8 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
   }
   const int e = p.rt.tiles[2 * tile];
   const int rows = p.rt.offsets[e + 1] - p.rt.tiles[2 * tile + 1];  // the tile's rows, capped at BM below
-  if (rows <= BM / 2) wide_tile<DT, FMT, F16C, true>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
-  else wide_tile<DT, FMT, F16C, false>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
+  if (rows <= BM / 2) wide_tile<DT, FMT, F16C, true, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
+  else wide_tile<DT, FMT, F16C, false, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
 }
 
 }  // namespace e4b

@@ -34,6 +34,13 @@ struct GemmArgs {
   // indexed like the A rows themselves (token when gather_k > 0, else sorted row); NULL selects
   // the bf16 mode.
   const int32_t* a_exp;
+  // LoRA delta in the epilogue (the LORA instances of the fp16-mode wide and narrow kernels):
+  // output column j of sorted row m gains lscale * sum_q lt[m, q] * lb[e, w_row(j), q] before the
+  // epilogue, lt the fp32 t = x . A^T rows [M, lr] of the routed rows, lb B [E, w.n, lr] in lbdt.
+  const float* lt;
+  const void* lb;
+  int lbdt, lr;
+  float lscale;
 };
 
 // Store one output element: fp32, or rounded once into the activation dtype.

@@ -264,7 +264,7 @@ def fused_experts_lora_forward(mod, hidden_states, top_k_index, top_k_weights):
         return torch.zeros(0, hidden, dtype=input_dtype, device=x.device)
     E = base.num_experts
     M = tokens * k
-    w1, w2 = _qweights(base)
+    w1, w2 = _for_tokens(_qweights(base), tokens)
     r = mod.gate_up_lora_A.shape[1]
     if r > 64 or x.shape[1] % 8 or base._down_shape[1] % 8:  # beyond the delta kernel's limits
         return mod._e4b_fast_ref(hidden_states, top_k_index, top_k_weights)

@@ -336,7 +336,8 @@ def test_lora_fused_matches_the_lora_oracle_at_olmoe_geometry(T, r, adt):
     _assert_fidelity(got, ref, want, f"lora T={T} r={r} {adt}")
 
 
-@pytest.mark.parametrize("T,r,adt", [(512, 16, torch.bfloat16), (512, 64, torch.float32), (4096, 16, torch.float32)])
+@pytest.mark.parametrize("T,r,adt", [(512, 16, torch.bfloat16), (512, 64, torch.float32), (4096, 16, torch.float32),
+                                     (4096, 64, torch.bfloat16)])
 def test_lora_fused_matches_the_lora_oracle_at_prefill_sizes(T, r, adt):
     """The grouped (prefill) form of the fused LoRA forward -- 128-row tiles at 4,096 tokens, the
     deltas added in the grouped GEMMs' epilogues -- against the fp64 restatement of
