@@ -44,10 +44,11 @@ GPTOSS = dict(E=32, H=2880, I=2880, k=4)
 # WRITE_SIZE, scaled by what a 256 MiB device copy reads for each in the same runs). Keyed by
 # the kernel it was measured on, so a changed kernel reports null until it is measured again.
 MEASURED_TRAFFIC = {
-    "decode_up_kernel<bf16, nf4, G=16, CPL=4, full, gated>": 18_881_000,
-    "decode_down_kernel<bf16, nf4, G=32, CPL=1, JOBS=1, full>": 9_707_000,
+    "decode_up_kernel<bf16, nf4, G=16, CPL=4, full, gated>": 19_060_700,
+    "decode_down_kernel<bf16, nf4, G=32, CPL=1, JOBS=1, full>": 9_724_300,
     # prefill: keyed by the kernel and the projection ("<kernel> gate_up_256row"); measured
     # again for each kernel change (profiles/prefill_qwen3_4096_zipf.txt)
+    "void e4b::gemm_wide_kernel<0, 1, true, false> gate_up_256row": 428_035_000,
 }
 
 
@@ -266,8 +267,30 @@ def lora_bench(mods, cfg, steps, warmup, seed0, bare, rank=16):
         us = ms * 1e3 / len(mods)
         out[f"bs{T}"] = {"us_per_layer": round(us, 3), "vs_bare_layer": round(us / bare[T]["us_per_layer"], 3),
                          "rank": rank}
-    # prefill: one layer at 4,096 tokens (the grouped form: fp16 matrix-core GEMMs with the
-    # deltas in their epilogues), bare and with the adapter, each graph-replayed on its own
+    out["prefill4096"] = lora_prefill_bench(mods[0], cfg, steps, warmup, seed0, rank, torch.float32, wrappers[0])
+    out["prefill4096_r64_bf16"] = lora_prefill_bench(mods[0], cfg, steps, warmup, seed0, 64, torch.bfloat16)
+    for w, m in zip(wrappers, mods):
+        e4b.disable_fast(w)  # restores the wrapped bases too: patch them again
+        assert e4b.enable_fast(m) == 1
+    return out
+
+
+def lora_prefill_bench(base, cfg, steps, warmup, seed0, rank, dtype, wrapper=None):
+    """One layer at 4,096 tokens, bare and through an ExpertsLoRA wrapper (rank, adapter dtype,
+    nonzero B), each graph-replayed on its own: the grouped LoRA form (t = x . A^T on the matrix
+    cores, fp16-mode GEMMs whose accumulators start as the tile's delta)."""
+    import torch
+
+    import experts4bit_qlora_amd as e4b
+
+    made = wrapper is None
+    if made:
+        wrapper = e4b.ExpertsLoRA(base, r=rank, alpha=2 * rank, dtype=dtype).to("cuda").eval()
+        g = torch.Generator(device="cuda").manual_seed(seed0 + 90 + rank)
+        with torch.no_grad():
+            for p in (wrapper.gate_up_lora_B, wrapper.down_lora_B):
+                p.copy_((torch.randn(p.shape, generator=g, device="cuda") * 0.02).to(p.dtype))
+        assert e4b.enable_fast(wrapper) == 1
     T = 4096
     x, idx, w = make_inputs(cfg, T, seed0 + 7)
 
@@ -279,12 +302,10 @@ def lora_bench(mods, cfg, steps, warmup, seed0, bare, rank=16):
         g, _ = graph_of(step)
         return time_graph(g, steps, warmup)
 
-    bare_ms, lora_ms = layer_ms(mods[0]), layer_ms(wrappers[0])
-    out["prefill4096"] = {"ms_lora": round(lora_ms, 4), "ms_bare": round(bare_ms, 4),
-                          "vs_bare_layer": round(lora_ms / bare_ms, 3), "rank": rank, "tokens": T}
-    for w in wrappers:
-        e4b.disable_fast(w)
-    return out
+    bare_ms, lora_ms = layer_ms(base), layer_ms(wrapper)
+    # (no disable_fast on the wrapper: it would also restore the wrapped base's own forward)
+    return {"ms_lora": round(lora_ms, 4), "ms_bare": round(bare_ms, 4), "vs_bare_layer": round(lora_ms / bare_ms, 3),
+            "rank": rank, "adapter_dtype": str(dtype).replace("torch.", ""), "tokens": T}
 
 
 def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
@@ -351,9 +372,11 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
     }
 
 
-def prefill_gemm_roofline(mod, x, idx, w, cfg):
-    """The prefill's GEMM launches (fp16 matrix-core mode) timed by the device tracer over five
-    eager forwards: algorithmic FLOP of each launch (the rows its tiles hold, both gate_up halves)
+def prefill_gemm_roofline(mod, x, idx, w, cfg, graph=None):
+    """The prefill's GEMM launches (fp16 matrix-core mode) timed by the device tracer over twenty
+    back-to-back replays of the forward's graph (five eager forwards when no graph is given or the
+    tracer sees no kernels of graph replays), the launches the timed region runs and that a
+    rocprofv3 kernel trace of `bench.py --prefill-only` averages: algorithmic FLOP of each launch (the rows its tiles hold, both gate_up halves)
     / its average duration, against the dense bf16/fp16 peak. The 256-row tiles
     (gemm_wide_kernel) carry every expert's rows except a last tile of at most 32 rows, which the
     32-row launch (gemm_narrow_kernel) takes; each forward runs gate_up then down with each kernel,
@@ -378,20 +401,28 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg):
         nb = n * k // 64
         return n * k // 2 + nb + math.ceil(nb / 256) * 4 + 4
     tail_bytes = {"gate_up": n_tail * proj_bytes(2 * I, H), "down": n_tail * proj_bytes(H, I)}
-    with torch.no_grad():
-        mod(x, idx, w)
-        torch.cuda.synchronize()
-        with profile(activities=[ProfilerActivity.CUDA]) as prof:
-            for _ in range(5):
-                mod(x, idx, w)
+    def traced(run, reps):
+        with torch.no_grad():
+            run()
             torch.cuda.synchronize()
-    calls = collections.defaultdict(list)
-    for ev in prof.events():
-        if ev.device_type == torch.autograd.DeviceType.CUDA and ("gemm_wide_kernel" in ev.name or
-                                                                 "gemm_narrow_kernel" in ev.name or
-                                                                 "gemm_mfma_kernel" in ev.name):
-            t = getattr(ev, "device_time", None)
-            calls[ev.name.split("(")[0]].append((ev.time_range.start, t if t is not None else ev.cuda_time))
+            with profile(activities=[ProfilerActivity.CUDA]) as prof:
+                for _ in range(reps):
+                    run()
+                torch.cuda.synchronize()
+        calls = collections.defaultdict(list)
+        for ev in prof.events():
+            if ev.device_type == torch.autograd.DeviceType.CUDA and ("gemm_wide_kernel" in ev.name or
+                                                                     "gemm_narrow_kernel" in ev.name or
+                                                                     "gemm_mfma_kernel" in ev.name):
+                t = getattr(ev, "device_time", None)
+                calls[ev.name.split("(")[0]].append((ev.time_range.start, t if t is not None else ev.cuda_time))
+        return calls
+
+    timer = "device tracer (torch.profiler), 20 back-to-back graph replays of the forward"
+    calls = traced(graph.replay, 20) if graph is not None else {}
+    if not calls:
+        timer = "device tracer (torch.profiler), 5 eager forwards"
+        calls = traced(lambda: mod(x, idx, w), 5)
     durs = collections.defaultdict(list)
     for name, cs in calls.items():
         if "gemm_wide_kernel" in name:
@@ -421,7 +452,7 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg):
             "achieved": dom["achieved"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"],
             "traffic": MEASURED_TRAFFIC.get(f"{dom['kernel']} {dom_key}"),
             "flop_per_launch": dom["flop_per_launch"], "avg_launch_us": dom["avg_launch_us"],
-            "timer": "device tracer (torch.profiler), 5 eager forwards", "launches": out}
+            "timer": timer, "launches": out}
 
 
 def pmc_pass(mods, cfg, seed0):
@@ -472,7 +503,7 @@ def prefill_bench(steps, warmup):
     ms = time_graph(g, max(steps, 10), warmup)
     flops = 2 * cfg["k"] * 4096 * (2 * cfg["I"] * cfg["H"] + cfg["H"] * cfg["I"])
     tflops = flops / (ms / 1e3) / 1e12
-    roof = prefill_gemm_roofline(mod, x, idx, w, cfg)
+    roof = prefill_gemm_roofline(mod, x, idx, w, cfg, graph=g)
     return {
         "roofline": roof,
         "workload": "Qwen3-30B-A3B geometry, 1 layer, 4096-token prefill, Zipf(1.1), NF4 double-quant",
@@ -727,6 +758,8 @@ def main():
     ap.add_argument("--kernel-only", action="store_true", help="only the dominant-kernel loop (for profiling)")
     ap.add_argument("--prefill-only", action="store_true", help="only the configs[3] prefill (for profiling)")
     ap.add_argument("--train-only", action="store_true", help="only the training-lane leg (for profiling)")
+    ap.add_argument("--lora-prefill-only", action="store_true",
+                    help="only the 4096-token ExpertsLoRA layer legs, rank 16 fp32 and rank 64 bf16 (for profiling)")
     ap.add_argument("--qwen-decode-only", action="store_true",
                     help="only the configs[2] Qwen3 double-quant decode legs, batches 1, 32, 256 (for profiling)")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -749,6 +782,15 @@ def main():
     N.lib()  # fail loudly if the kernel library is missing
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_bench(args.steps, args.warmup)}), flush=True)
+        return
+    if args.lora_prefill_only:
+        cfg = OLMOE
+        base = make_layer(cfg, seed=1000 + 100)
+        assert e4b.enable_fast(base) == 1
+        res = {f"r{r}_{str(dt).replace('torch.', '')}": lora_prefill_bench(base, cfg, args.steps, args.warmup, 1000 + 100,
+                                                                          r, dt)
+               for r, dt in ((16, torch.float32), (64, torch.bfloat16))}
+        print(json.dumps({"lora_prefill": res}), flush=True)
         return
     if args.train_only:
         print(json.dumps({"train": train_bench(args.steps, args.warmup)}), flush=True)
