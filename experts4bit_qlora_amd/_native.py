@@ -20,7 +20,7 @@ E4B_OK = 0
 FMT_NF4, FMT_NF4_DQ, FMT_MXFP4 = 0, 1, 2
 BF16, FP16, FP32 = 0, 1, 2
 EPI_NONE, EPI_SWIGLU, EPI_ACT, EPI_CLAMP_SWIGLU, EPI_GPTOSS = 0, 1, 2, 3, 4
-PATH_AUTO, PATH_GEMV, PATH_MFMA, PATH_DECODE_FUSED = 0, 1, 2, 3
+PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
 NOALLOC_WORKSPACE_BYTES = 64 << 20  # E4B_NOALLOC_WORKSPACE_BYTES
 
 # every symbol include/e4b_amd.h declares (tests check the library exports all of them)
@@ -49,8 +49,6 @@ EXPORTS = (
     "e4b_moe_forward_noalloc",
     "e4b_moe_lora_workspace_bytes",
     "e4b_moe_lora_forward",
-    "e4b_decode_sync_errors",
-    "e4b_decode_wait_limit",
 )
 
 
@@ -169,10 +167,6 @@ def _bind(L):
     L.e4b_moe_lora_forward.restype = ctypes.c_int
     L.e4b_moe_lora_forward.argtypes = [P, I32, I64, P, P, I32, I32, QW, QW, ctypes.POINTER(Lora), I32, F32, I32, P,
                                        ctypes.c_size_t, P, I32, P]
-    L.e4b_decode_sync_errors.restype = ctypes.c_int
-    L.e4b_decode_sync_errors.argtypes = [ctypes.POINTER(ctypes.c_uint32), I32]
-    L.e4b_decode_wait_limit.restype = ctypes.c_int
-    L.e4b_decode_wait_limit.argtypes = [ctypes.c_uint64]
     return L
 
 

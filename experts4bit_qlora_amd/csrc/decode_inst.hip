@@ -2,7 +2,6 @@
 // -DE4B_INST_DT=<e4b_dtype> -DE4B_INST_FMT=<e4b_format> (the build compiles this file once per
 // pair, in parallel).
 #include "decode.h"
-#include "decode_fused.h"
 #include "decode_launch.h"
 
 #include <algorithm>
@@ -63,32 +62,6 @@ void down_gc(const DecodeArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((decode_down_kernel<DT, FMT, G, CPL, JOBS, FULL, LR>), grid, dim3(kDecThreads), 0, s, a);
 }
 
-// The fused kernel's grid: the largest power of two <= min(kFusedMaxGrid, blocks resident at
-// once), read once per device (its blocks wait on one another, so all must be resident).
-template <int DT, int FMT, int G, int CPL, int CPLD>
-bool fused_gc(FusedArgs& a, hipStream_t s) {
-  static std::atomic<int> grids[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  int P = grids[dev].load(std::memory_order_relaxed);
-  if (P == 0) {
-    int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_fused_kernel<DT, FMT, G, CPL, CPLD>, kDecThreads,
-                                                     0) != hipSuccess ||
-        per_cu < 1)
-      per_cu = 1;
-    const int resident = std::min(kFusedMaxGrid, per_cu * device_cus());
-    P = 1;
-    while (2 * P <= resident) P *= 2;
-    grids[dev].store(P, std::memory_order_relaxed);
-  }
-  if (P < kSyncCounters) return false;  // every counter needs a block
-  a.add = kSyncPerLaunch * kSyncCounters / static_cast<unsigned>(P);
-  hipLaunchKernelGGL((decode_fused_kernel<DT, FMT, G, CPL, CPLD>), dim3(static_cast<unsigned>(P)), dim3(kDecThreads),
-                     0, s, a);
-  return true;
-}
-
 }  // namespace
 
 template <int DT, int FMT, int LR>
@@ -137,23 +110,7 @@ void launch_decode_down(const DecodeArgs& a, DecShape d, hipStream_t s) {
   launch_decode_down_l<DT, FMT, 0>(a, d, s);
 }
 
-template <int DT, int FMT>
-bool launch_decode_fused(FusedArgs& a, hipStream_t s) {
-  const DecShape d = decode_up_shape(a.w1.k);
-  const int cpld = decode_fused_cpld(a.w2.k);
-#define E4B_FUSED(g, c)                                                       \
-  if (d.G == g && d.CPL == c) {                                               \
-    if (cpld == 1) return fused_gc<DT, FMT, g, c, 1>(a, s);                   \
-    if (cpld == 2) return fused_gc<DT, FMT, g, c, 2>(a, s);                   \
-    return fused_gc<DT, FMT, g, c, 3>(a, s);                                  \
-  }
-  E4B_FUSED(4, 2) E4B_FUSED(4, 4) E4B_FUSED(8, 4) E4B_FUSED(16, 4) E4B_FUSED(16, 6) E4B_FUSED(32, 4)
-#undef E4B_FUSED
-  return false;
-}
-
 template void launch_decode_up<E4B_INST_DT, E4B_INST_FMT>(const DecodeArgs&, DecShape, int64_t, hipStream_t);
 template void launch_decode_down<E4B_INST_DT, E4B_INST_FMT>(const DecodeArgs&, DecShape, hipStream_t);
-template bool launch_decode_fused<E4B_INST_DT, E4B_INST_FMT>(FusedArgs&, hipStream_t);
 
 }  // namespace e4b

@@ -12,7 +12,6 @@
 namespace e4b {
 
 struct DecodeArgs;
-struct FusedArgs;
 
 // G lanes per weight row, CPL 16-byte chunks per lane, JOBS routed experts per group in flight
 // (down kernel), and whether the row's chunk count is exactly G * CPL. G == 0: unsupported.
@@ -55,29 +54,15 @@ inline DecShape decode_down_shape(int64_t k, int64_t M) {
   return dec_finish(c, 32, cpl, 1);
 }
 
-// Single-token decode in one launch (decode_fused_kernel): down chunks per 32-lane job, 0 when
-// the down rows are too long (k2 > 3072: the job's weights held across the wait would spill).
-inline int decode_fused_cpld(int64_t k2) {
-  const int64_t c = k2 / 32;
-  return c <= 32 ? 1 : c <= 64 ? 2 : c <= 96 ? 3 : 0;
-}
-
 template <int DT, int FMT>
 void launch_decode_up(const DecodeArgs& a, DecShape d, int64_t max_active, hipStream_t s);
 
 template <int DT, int FMT>
 void launch_decode_down(const DecodeArgs& a, DecShape d, hipStream_t s);
 
-// Launches decode_fused_kernel on as many blocks as fit on the device at once (a power of two,
-// at most kFusedMaxGrid) and fills a.add for that grid; false (nothing launched) when fewer than
-// kSyncCounters blocks fit. a.ctr / a.hx / a.errors: the caller's.
-template <int DT, int FMT>
-bool launch_decode_fused(FusedArgs& a, hipStream_t s);
-
 #define E4B_DECODE_EXTERN(DT, FMT)                                                                   \
   extern template void launch_decode_up<DT, FMT>(const DecodeArgs&, DecShape, int64_t, hipStream_t); \
-  extern template void launch_decode_down<DT, FMT>(const DecodeArgs&, DecShape, hipStream_t); \
-  extern template bool launch_decode_fused<DT, FMT>(FusedArgs&, hipStream_t);
+  extern template void launch_decode_down<DT, FMT>(const DecodeArgs&, DecShape, hipStream_t);
 E4B_DECODE_EXTERN(E4B_BF16, E4B_FMT_NF4)
 E4B_DECODE_EXTERN(E4B_BF16, E4B_FMT_NF4_DQ)
 E4B_DECODE_EXTERN(E4B_BF16, E4B_FMT_MXFP4)

@@ -1,8 +1,7 @@
 // C-ABI entry points of libe4b_amd.so (declared in include/e4b_amd.h).
 //
 // Host code only validates, picks a kernel instantiation and launches on the caller's stream.
-// No device memory is allocated here and no call but the e4b_decode_sync_errors diagnostic
-// synchronises the device.
+// No device memory is allocated here and no call synchronises the device.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -11,13 +10,11 @@
 #include <cstring>
 #include <string>
 
-#include <atomic>
 #include <mutex>
 #include <utility>
 
 #include "common.h"
 #include "decode.h"
-#include "decode_fused.h"
 #include "decode_launch.h"
 #include "dequant.h"
 #include "gather.h"
@@ -53,50 +50,7 @@ int check_launch(const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// State of the single-launch decode (decode_fused.h) per stream slot: kSyncCounters launch
-// counters (zero when the library loads, never reset) and two h exchange buffers of
-// kFusedMaxH values (zero when the library loads; each launch zeroes the one the next launch
-// uses), 4 MB for all slots; and the sticky flag a wait that ran out of time raises. Each device
-// holds its own copy; host code reaches it through the addresses hipGetSymbolAddress gives on
-// that device.
-__device__ unsigned g_decode_sync[e4b::kSyncSlots * e4b::kSyncCounters * e4b::kSyncStride];
-__device__ __align__(256) uint16_t g_decode_h[e4b::kSyncSlots * 2 * e4b::kFusedMaxH];
-__device__ unsigned g_decode_sync_errors;
-
 constexpr int kMaxDevices = 64;
-struct DecodeSync {
-  bool init = false, ok = false;
-  unsigned* ctr = nullptr;     // device address of g_decode_sync
-  uint16_t* hx = nullptr;      // device address of g_decode_h
-  unsigned* errors = nullptr;  // device address of g_decode_sync_errors
-  hipStream_t streams[e4b::kSyncSlots] = {};
-  int used = 0;
-};
-std::mutex g_sync_mu;
-DecodeSync g_sync[kMaxDevices];
-std::atomic<unsigned long long> g_wait_ticks{10000000ull};  // 100 ms at the 100 MHz real-time clock
-
-// The device addresses of the current device's counters, set up on first use.
-DecodeSync* decode_sync_device() {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  DecodeSync& s = g_sync[dev];
-  if (!s.init) {
-    s.init = true;
-    void* c = nullptr;
-    void* h = nullptr;
-    void* e = nullptr;
-    s.ok = hipGetSymbolAddress(&c, HIP_SYMBOL(g_decode_sync)) == hipSuccess &&
-           hipGetSymbolAddress(&h, HIP_SYMBOL(g_decode_h)) == hipSuccess &&
-           hipGetSymbolAddress(&e, HIP_SYMBOL(g_decode_sync_errors)) == hipSuccess && c && h && e;
-    if (!s.ok) (void)hipGetLastError();  // no single-launch decode on this device; nothing left pending
-    s.ctr = static_cast<unsigned*>(c);
-    s.hx = static_cast<uint16_t*>(h);
-    s.errors = static_cast<unsigned*>(e);
-  }
-  return s.ok ? &s : nullptr;
-}
-
 // Second streams of prefill forwards on each device, each with its own fork / join events
 // (created on first use outside graph capture, default priority, kept for the process). The
 // 32-row tile launches run on one beside the big-tile launches: the wide kernel holds one
@@ -190,24 +144,25 @@ class SideLease {
   SideStream* ss_ = nullptr;
 };
 
-// The counters and exchange buffers of `stream`'s slot (a stream keeps its slot for the life of
-// the process); false when every slot is taken or the state is unavailable.
-bool decode_sync_slot(hipStream_t stream, unsigned** ctr, uint16_t** hx, unsigned** errors) {
-  std::lock_guard<std::mutex> lk(g_sync_mu);
-  DecodeSync* s = decode_sync_device();
-  if (!s) return false;
-  int slot = -1;
-  for (int i = 0; i < s->used; ++i)
-    if (s->streams[i] == stream) slot = i;
-  if (slot < 0) {
-    if (s->used == e4b::kSyncSlots) return false;
-    slot = s->used++;
-    s->streams[slot] = stream;
+// launch(rbig, stream) and launch(rsmall, the side stream), the side stream forked from `stream`
+// after everything enqueued so far and joined back into it (both on `stream` without a side
+// stream): the two tile heights write disjoint rows.
+template <class F>
+int run_tile_heights(const SideStream* side, hipStream_t stream, const e4b_routing* rbig, const e4b_routing* rsmall,
+                     F&& launch) {
+  if (side) {
+    if (hipEventRecord(side->fork, stream) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)
+      return check_launch("side stream fork");
+    int r = launch(rbig, stream);
+    if (!r) r = launch(rsmall, side->s);
+    // joined whatever happened, so the caller's stream never runs ahead of the side stream
+    const bool joined = hipEventRecord(side->join, side->s) == hipSuccess &&
+                        hipStreamWaitEvent(stream, side->join, 0) == hipSuccess;
+    if (r) return r;
+    return joined ? 0 : check_launch("side stream join");
   }
-  *ctr = s->ctr + size_t(slot) * e4b::kSyncCounters * e4b::kSyncStride;
-  *hx = s->hx + size_t(slot) * 2 * e4b::kFusedMaxH;
-  *errors = s->errors;
-  return true;
+  int r = launch(rbig, stream);
+  return r ? r : launch(rsmall, stream);
 }
 
 bool act_dtype_ok(int dt) { return dt == E4B_BF16 || dt == E4B_FP16; }
@@ -377,46 +332,6 @@ int64_t max_small_tiles(int64_t M, int E) { return std::max<int64_t>(1, std::min
 
 bool is_gated_epi(int epi) {
   return epi == E4B_EPI_SWIGLU || epi == E4B_EPI_CLAMP_SWIGLU || epi == E4B_EPI_GPTOSS;
-}
-
-// Shapes the single-launch decode takes: one token, a gated epilogue, the decode limits, down
-// rows of at most 3072 values, the routed experts' h within one exchange buffer.
-bool fused_supported(int64_t tokens, int64_t M, int E, const e4b_qweight* w1, const e4b_qweight* w2, int epi) {
-  return tokens == 1 && is_gated_epi(epi) && decode_supported(M, E, w1, true) && decode_supported(M, E, w2, false) &&
-         e4b::decode_fused_cpld(w2->k) > 0 && std::min<int64_t>(M, E) * w2->k <= e4b::kFusedMaxH;
-}
-
-// The single-launch decode on `stream`'s slot; E4B_EUNSUPPORTED when no slot is free or the
-// device holds too few blocks at once (the caller then takes the two-launch path).
-int launch_fused(const void* hidden, int act_dtype, const int64_t* top_k_index, const void* top_k_weights,
-                 int weight_dtype, int top_k, const e4b_qweight* w1, const e4b_qweight* w2, int epilogue, float alpha,
-                 float limit, void* out, int out_dtype, hipStream_t stream) {
-  e4b::FusedArgs a{};
-  if (!decode_sync_slot(stream, &a.ctr, &a.hx, &a.errors)) return E4B_EUNSUPPORTED;
-  a.x = static_cast<const uint16_t*>(hidden);
-  a.topk = top_k_index;
-  a.topk_w = top_k_weights;
-  a.wdt = weight_dtype;
-  a.k = top_k;
-  a.E = w1->num_experts;
-  a.w1 = *w1;
-  a.w2 = *w2;
-  a.epi = epilogue;
-  a.alpha = alpha;
-  a.limit = limit;
-  a.n_out = w2->k;
-  a.out = out;
-  a.odt = out_dtype;
-  a.timeout = g_wait_ticks.load(std::memory_order_relaxed);
-#define E4B_FUSED(DT, FMT)                                                    \
-  if (act_dtype == DT && w1->format == FMT) {                                 \
-    if (!e4b::launch_decode_fused<DT, FMT>(a, stream)) return E4B_EUNSUPPORTED; \
-    return check_launch("decode_fused_kernel");                               \
-  }
-  E4B_FUSED(E4B_BF16, E4B_FMT_NF4) E4B_FUSED(E4B_BF16, E4B_FMT_NF4_DQ) E4B_FUSED(E4B_BF16, E4B_FMT_MXFP4)
-  E4B_FUSED(E4B_FP16, E4B_FMT_NF4) E4B_FUSED(E4B_FP16, E4B_FMT_NF4_DQ) E4B_FUSED(E4B_FP16, E4B_FMT_MXFP4)
-#undef E4B_FUSED
-  return fail(E4B_EINVAL, "no single-launch decode for act_dtype %d / format %d", act_dtype, w1->format);
 }
 
 }  // namespace
@@ -1006,19 +921,13 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
   if (!top_k_index || !top_k_weights || !hidden || !out) return fail(E4B_EINVAL, "NULL pointer");
   if (!aligned16(hidden)) return fail(E4B_EINVAL, "hidden must be 16-byte aligned");
 
-  if (flags < E4B_PATH_AUTO || flags > E4B_PATH_DECODE_FUSED) return fail(E4B_EINVAL, "bad flags %d", flags);
+  if (flags < E4B_PATH_AUTO || flags > E4B_PATH_MFMA) return fail(E4B_EINVAL, "bad flags %d", flags);
   // Decode path: routing recomputed in LDS, combine fused into the down projection; two
-  // launches, or one for a single token when asked for.
+  // launches.
   const bool decode_ok = decode_supported(M, E, w1, true) && decode_supported(M, E, w2, false);
-  const bool use_decode =
-      decode_ok && (((flags == E4B_PATH_AUTO || flags == E4B_PATH_DECODE_FUSED) && tokens <= 8) || flags == E4B_PATH_GEMV);
+  const bool use_decode = decode_ok && ((flags == E4B_PATH_AUTO && tokens <= 8) || flags == E4B_PATH_GEMV);
   if (use_decode) {
     void* h = workspace;
-    if (flags == E4B_PATH_DECODE_FUSED && fused_supported(tokens, M, E, w1, w2, epilogue)) {
-      rc = launch_fused(hidden, act_dtype, top_k_index, top_k_weights, weight_dtype, top_k, w1, w2, epilogue, alpha,
-                        limit, out, out_dtype, stream);
-      if (rc != E4B_EUNSUPPORTED) return rc;  // no free slot or too small a device: two launches instead
-    }
     rc = e4b_decode_gate_up(hidden, act_dtype, tokens, top_k_index, top_k, w1, epilogue, alpha, limit, h, stream);
     if (rc) return rc;
     return e4b_decode_down_combine(h, act_dtype, tokens, top_k_index, top_k_weights, weight_dtype, top_k, w2, out,
@@ -1094,22 +1003,7 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
     // the two tile heights write disjoint rows: the 32-row tiles go to the side stream (forked
     // after everything they read, joined before anything reads what they write)
     SideLease lease(stream, side_ok);
-    const SideStream* side = lease.get();
-    auto both = [&](auto&& launch) -> int {
-      if (side) {
-        if (hipEventRecord(side->fork, stream) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)
-          return check_launch("side stream fork");
-        int r = launch(&rbig, stream);
-        if (!r) r = launch(&rsmall, side->s);
-        // joined whatever happened, so the caller's stream never runs ahead of the side stream
-        const bool joined = hipEventRecord(side->join, side->s) == hipSuccess &&
-                            hipStreamWaitEvent(stream, side->join, 0) == hipSuccess;
-        if (r) return r;
-        return joined ? 0 : check_launch("side stream join");
-      }
-      int r = launch(&rbig, stream);
-      return r ? r : launch(&rsmall, stream);
-    };
+    auto both = [&](auto&& launch) { return run_tile_heights(lease.get(), stream, &rbig, &rsmall, launch); };
     rc = both([&](const e4b_routing* r, hipStream_t s) {
       return grouped_gemm_impl(up_a, act_dtype, top_k, w1, r, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
                                up_exp, s);
@@ -1285,7 +1179,7 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
   if (!any_dtype_ok(lora->dtype)) return fail(E4B_EINVAL, "bad adapter dtype %d", lora->dtype);
   if (!act_dtype_ok(act_dtype)) return fail(E4B_EINVAL, "act_dtype must be bf16 or fp16 (got %d)", act_dtype);
   if (!any_dtype_ok(weight_dtype) || !any_dtype_ok(out_dtype)) return fail(E4B_EINVAL, "bad weight/out dtype");
-  if (flags < E4B_PATH_AUTO || flags > E4B_PATH_DECODE_FUSED) return fail(E4B_EINVAL, "bad flags %d", flags);
+  if (flags < E4B_PATH_AUTO || flags > E4B_PATH_MFMA) return fail(E4B_EINVAL, "bad flags %d", flags);
   if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "bad tokens/top_k");
   if (tokens == 0) return E4B_OK;
   const int E = w1->num_experts;
@@ -1297,7 +1191,6 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
     return fail(E4B_EINVAL, "NULL pointer");
   if (!aligned16(hidden) || !aligned16(workspace) || !aligned16(lora->a1) || !aligned16(lora->a2))
     return fail(E4B_EINVAL, "hidden, workspace and the A matrices must be 16-byte aligned");
-  if (flags == E4B_PATH_DECODE_FUSED) flags = E4B_PATH_AUTO;  // no single-launch form with adapters
 
   char* p = static_cast<char*>(workspace);
   auto take = [&](size_t bytes) {
@@ -1388,16 +1281,19 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
       rc = check_launch("split_tiles_kernel");
       if (rc) return rc;
     }
-    const e4b_routing* parts[2] = {split ? &rbig : &rt, split ? &rsmall : nullptr};
+    // the 32-row tiles of a split run on a side stream, as in e4b_moe_forward
+    SideLease lease(stream, split);
+    auto tiles = [&](auto&& launch) {
+      return split ? run_tile_heights(lease.get(), stream, &rbig, &rsmall, launch) : launch(&rt, stream);
+    };
     rc = lora_t_mfma(hidden, top_k, rt, lora->a1, lora->dtype, r, w1->k, t, stream);
     if (rc) return rc;
     const LoraEpi l1{t, lora->b1, lora->dtype, r, lora->scaling};
-    for (const e4b_routing* rp : parts) {
-      if (!rp) continue;
-      rc = grouped_gemm_impl(x16, act_dtype, top_k, w1, rp, tokens, M, epilogue, 1.0f, limit, E4B_PATH_MFMA, h,
-                             act_dtype, xexp, stream, &l1);
-      if (rc) return rc;
-    }
+    rc = tiles([&](const e4b_routing* rp, hipStream_t s) {
+      return grouped_gemm_impl(x16, act_dtype, top_k, w1, rp, tokens, M, epilogue, 1.0f, limit, E4B_PATH_MFMA, h,
+                               act_dtype, xexp, s, &l1);
+    });
+    if (rc) return rc;
     // t2 from the bf16 h, before h is rewritten as scaled fp16 rows for the down GEMM
     rc = lora_t_mfma(h, 0, rt, lora->a2, lora->dtype, r, w2->k, t, stream);
     if (rc) return rc;
@@ -1406,12 +1302,11 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
     rc = check_launch("row_exp_kernel");
     if (rc) return rc;
     const LoraEpi l2{t, lora->b2, lora->dtype, r, lora->scaling};
-    for (const e4b_routing* rp : parts) {
-      if (!rp) continue;
-      rc = grouped_gemm_impl(h, act_dtype, 0, w2, rp, tokens, M, E4B_EPI_NONE, 1.0f, limit, E4B_PATH_MFMA, down,
-                             E4B_FP32, hexp, stream, &l2);
-      if (rc) return rc;
-    }
+    rc = tiles([&](const e4b_routing* rp, hipStream_t s) {
+      return grouped_gemm_impl(h, act_dtype, 0, w2, rp, tokens, M, E4B_EPI_NONE, 1.0f, limit, E4B_PATH_MFMA, down,
+                               E4B_FP32, hexp, s, &l2);
+    });
+    if (rc) return rc;
     return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
                        stream);
   }
@@ -1449,24 +1344,6 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
   if (rc) return rc;
   return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
                      stream);
-}
-
-int e4b_decode_sync_errors(uint32_t* errors, int32_t reset) {
-  if (!errors) return fail(E4B_EINVAL, "NULL pointer");
-  std::lock_guard<std::mutex> lk(g_sync_mu);
-  DecodeSync* s = decode_sync_device();
-  if (!s) return fail(E4B_EUNSUPPORTED, "single-launch decode counters are not available on this device");
-  unsigned v = 0;
-  if (hipMemcpy(&v, s->errors, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess)
-    return check_launch("e4b_decode_sync_errors");
-  *errors = v;
-  if (reset && hipMemset(s->errors, 0, sizeof(unsigned)) != hipSuccess) return check_launch("e4b_decode_sync_errors");
-  return E4B_OK;
-}
-
-int e4b_decode_wait_limit(uint64_t ticks) {
-  g_wait_ticks.store(ticks ? ticks : 10000000ull, std::memory_order_relaxed);
-  return E4B_OK;
 }
 
 }  // extern "C"

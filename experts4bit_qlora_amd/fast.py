@@ -96,11 +96,12 @@ _DESC_CACHE: "weakref.WeakKeyDictionary[torch.nn.Module, dict]" = weakref.WeakKe
 
 def _cached_descriptors(mod, tag, sources, build):
     """``build()``'s result for ``mod``, rebuilt whenever a source tensor is replaced (storage
-    address) or updated in place (version counter, which ``load_state_dict`` copies bump).
-    Inference tensors carry no version counter: with any among the sources nothing is cached."""
-    if any(t.is_inference() for t in sources):
-        return build()
-    key = tuple((t.data_ptr(), t._version, t.dtype) for t in sources)
+    address, shape, dtype) or updated in place (version counter, which ``load_state_dict``
+    copies bump). Inference tensors carry no version counter and cannot be written in place
+    outside inference mode: they are keyed on storage, shape and dtype alone, so an in-place
+    write into one inside ``torch.inference_mode`` is not seen (``disable_fast`` /
+    ``enable_fast``, or a new tensor, drops the entry)."""
+    key = tuple((t.data_ptr(), -1 if t.is_inference() else t._version, t.dtype, tuple(t.shape)) for t in sources)
     per_mod = _DESC_CACHE.setdefault(mod, {})
     hit = per_mod.get(tag)
     if hit is not None and hit[0] == key:

@@ -458,21 +458,6 @@ def moe_lora_forward(hidden: torch.Tensor, top_k_index: torch.Tensor, top_k_weig
     return out
 
 
-def decode_sync_errors(device=None, reset: bool = False) -> int:
-    """The sticky give-up flag of the single-token decode launch on ``device`` (non-zero: a
-    launch stopped waiting for its other blocks and its output was undefined). Synchronises."""
-    L = N.lib()
-    v = ctypes.c_uint32(0)
-    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
-        N.check("e4b_decode_sync_errors", L.e4b_decode_sync_errors(ctypes.byref(v), int(bool(reset))))
-    return int(v.value)
-
-
-def decode_wait_limit(ticks: int = 0) -> None:
-    """Wait bound of later single-token decode launches, in 100 MHz clock ticks (0: 100 ms)."""
-    N.check("e4b_decode_wait_limit", N.lib().e4b_decode_wait_limit(int(ticks)))
-
-
 # ------------------------------------------------- the nf4_grouped / mxfp4_grouped API shape
 
 

@@ -50,10 +50,8 @@ enum e4b_epilogue {
                                after adding the per-expert gate_up bias */
 };
 
-/* Kernel-path selection flags for the grouped GEMMs (0 = automatic by token count).
- * E4B_PATH_DECODE_FUSED (e4b_moe_forward only): a single token runs the decode path in one
- * launch (see e4b_moe_forward); otherwise as E4B_PATH_AUTO. */
-enum e4b_flags { E4B_PATH_AUTO = 0, E4B_PATH_GEMV = 1, E4B_PATH_MFMA = 2, E4B_PATH_DECODE_FUSED = 3 };
+/* Kernel-path selection flags for the grouped GEMMs (0 = automatic by token count). */
+enum e4b_flags { E4B_PATH_AUTO = 0, E4B_PATH_GEMV = 1, E4B_PATH_MFMA = 2 };
 
 typedef struct e4b_qweight {
   int32_t format;        /* e4b_format */
@@ -261,16 +259,6 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
  * Small batches (tokens <= 8, or flags == E4B_PATH_GEMV within the decode limits) take the
  * decode path, two launches (gate_up, then down + combine); larger ones route once and run the
  * grouped GEMMs.
- * flags == E4B_PATH_DECODE_FUSED runs a single token (gated epilogue, w2->k <= 3072, routed
- * experts * w2->k <= 16384) in ONE launch: its blocks hand h to one another through exchange
- * buffers the library owns (4 MB per device), so the launch assumes that its blocks (up to 512,
- * those that fit on the device at once) all run concurrently -- true when nothing else occupies
- * the device's compute units. Each stream gets its own buffers (64 streams per device; further
- * streams take the two-launch form); two launches that overlap on one stream's buffers, e.g. the
- * same captured graph replayed on two streams at once, race. A wait that runs out (see
- * e4b_decode_wait_limit) raises the flag e4b_decode_sync_errors reads instead of hanging, and
- * leaves that call's output undefined. On MI355X it is slower than the two launches (the h
- * hand-off across the device costs more than a kernel boundary), hence not the default.
  * fp16 matrix-core mode (bf16 activations, NF4 / NF4_DQ weights whose descriptors both carry
  * `shift`): the GEMMs multiply fp16 operands -- every weight fp16(fl32(code * absmax) *
  * 2^shift[e]) (one rounding of the fp32 product, 2^-11 relative, where bf16 weights carry
@@ -324,27 +312,20 @@ size_t e4b_moe_lora_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_e
  * Decode path (tokens <= 8 within the decode limits, or flags == E4B_PATH_GEMV): four
  * launches -- t1 = x . A1^T per routed row; the gate_up GEMV with scaling * t1 . B1[e, n, :]
  * added to each column's fp32 sum before the epilogue; t2 = h . A2^T; the down GEMV with its
- * delta added the same way, then the combine. Otherwise: route, grouped GEMMs to fp32 rows,
- * the deltas of every expert group added on the device (as e4b_lora_delta_epilogue and
- * e4b_lora_delta), combine. No device->host synchronisation on either path. flags ==
- * E4B_PATH_DECODE_FUSED is taken as E4B_PATH_AUTO.
+ * delta added the same way, then the combine. Otherwise, with bf16 activations and both
+ * weights carrying `shift` (and both k multiples of 256 up to 16384): route; t1 = x . A1^T on
+ * the matrix cores; the gate_up grouped GEMM in the fp16 matrix-core mode whose tile
+ * accumulators start as the tile's scaling * t1 . B1^T (t and B split into bf16 hi / lo
+ * pairs: ~16 significant bits of the delta); the epilogue into h; t2 = h . A2^T; the down GEMM
+ * the same way into fp32 rows; combine. Other larger batches: grouped GEMMs to fp32 rows, the
+ * deltas of every expert group added on the device (as e4b_lora_delta_epilogue and
+ * e4b_lora_delta), combine. No device->host synchronisation on any path.
  * Replaces: engines/fast.py:163-257 fused_experts_lora_forward (the ExpertsLoRA forward that
  * enable_fast binds, fast.py:328-329), whose groups are sliced on the host after a .tolist(). */
 int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,
                          const void* top_k_weights, int32_t weight_dtype, int32_t top_k, const e4b_qweight* w1,
                          const e4b_qweight* w2, const e4b_lora* lora, int32_t epilogue, float limit, int32_t flags,
                          void* workspace, size_t workspace_bytes, void* out, int32_t out_dtype, hipStream_t stream);
-
-/* Sticky flag of the single-token decode launch on the current device: non-zero once a launch
- * gave up waiting for its other blocks (its output is then undefined). reset != 0 clears it.
- * Synchronises the device (a diagnostic, not for the decode loop).
- * No counterpart in the reference (its decode runs as separate launches). */
-int e4b_decode_sync_errors(uint32_t* errors, int32_t reset);
-
-/* Wait bound of the single-token decode launch, in ticks of the device's 100 MHz real-time
- * clock, for launches made after this call (0: the default, 10^7 = 100 ms).
- * No counterpart in the reference. */
-int e4b_decode_wait_limit(uint64_t ticks);
 
 #ifdef __cplusplus
 }

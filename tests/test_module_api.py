@@ -266,13 +266,16 @@ def _nf4_module(E=4, H=128, inter=64, dq=False):
 
 
 def test_descriptor_cache_works_for_inference_tensors():
-    """Weights built under inference_mode carry no version counter: the descriptors are then
-    rebuilt per call instead of raising."""
+    """Weights built under inference_mode carry no version counter: their descriptors are keyed on
+    storage, shape and dtype (cached, no raise), and a replaced tensor rebuilds them."""
     with torch.inference_mode():
         mod = _nf4_module()
     w1, w2 = F._qweights(mod)
     assert w1.struct().n == mod._gate_up_shape[0] and w2.struct().k == mod._down_shape[1]
-    assert F._build_qweights(mod)[0].n == w1.n
+    assert F._qweights(mod)[0] is w1  # cached: the per-call weight-exponent launches happen once
+    with torch.inference_mode():
+        mod.gate_up_absmax = mod.gate_up_absmax.clone()
+    assert F._qweights(mod)[0] is not w1
 
 
 def test_descriptor_cache_keeps_the_module_copyable_and_picklable():
