@@ -151,13 +151,14 @@ def decode_bench(mods, cfg, T, steps, warmup, seed0):
     torch.cuda.synchronize()
     for a, b in zip(eager, outs):  # the graph replays the exact eager computation
         assert torch.equal(a, b), "graph replay differs from the eager forward"
-    # eager wall time (Python + launches), for reference
+    # eager wall time (Python + launches, back-to-back steps), for reference
+    n_eager = max(10, steps)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(max(3, steps // 4)):
+    for _ in range(n_eager):
         step()
     torch.cuda.synchronize()
-    eager_ms = (time.perf_counter() - t0) * 1e3 / max(3, steps // 4)
+    eager_ms = (time.perf_counter() - t0) * 1e3 / n_eager
     ms = time_graph(g, steps, warmup)
     L = len(mods)
     return {
@@ -171,6 +172,7 @@ def decode_bench(mods, cfg, T, steps, warmup, seed0):
         "hbm_gbs": step_bytes / (ms / 1e3) / 1e9,
         "hbm_frac": step_bytes / (ms / 1e3) / 1e9 / HBM_PEAK_GBS,
         "eager_ms_per_step": eager_ms,
+        "eager_vs_graph": round(eager_ms / ms, 3),
     }
 
 
