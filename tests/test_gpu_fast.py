@@ -337,13 +337,17 @@ def test_lora_fused_matches_the_lora_oracle_at_olmoe_geometry(T, r, adt):
 
 
 @pytest.mark.parametrize("T,r,adt", [(512, 16, torch.bfloat16), (512, 64, torch.float32), (4096, 16, torch.float32),
-                                     (4096, 64, torch.bfloat16)])
+                                     (4096, 64, torch.bfloat16), (96, 12, torch.float16), (96, 33, torch.float32),
+                                     (600, 24, torch.float16), (600, 40, torch.bfloat16)])
 def test_lora_fused_matches_the_lora_oracle_at_prefill_sizes(T, r, adt):
-    """The grouped (prefill) form of the fused LoRA forward -- 128-row tiles at 4,096 tokens, the
-    deltas added in the grouped GEMMs' epilogues -- against the fp64 restatement of
-    ExpertsLoRA.forward on the first and the last token routed to every expert (every expert's
-    first tile and its last), at the layer bars and no worse than the reference loop's own error
-    rule (the reference runs this grouped path for every batch, fast.py:209-257)."""
+    """The grouped form of the fused LoRA forward -- t = x . A^T on the matrix cores, the GEMM
+    tiles' accumulators starting as their deltas; 256-row tiles (half tiles for <= 128 rows) with
+    32-row tails from 512 tokens, only 32-row tiles at 96 tokens; ranks that are and are not
+    multiples of 8, one and four 16-rank blocks, every adapter dtype -- against the fp64
+    restatement of ExpertsLoRA.forward on the first and the last token routed to every expert
+    (every expert's first tile and its last), at the layer bars and no worse than the reference
+    loop's own error rule (the reference runs this grouped path for every batch,
+    fast.py:209-257)."""
     _announce(f"lora vs oracle OLMoE prefill T={T} r={r} adapters={adt}")
     mod = _olmoe_lora(r, adt, seed=7500 + T + r)
     x, idx, w = _cfg_inputs(T, 64, 2048, 8, seed=7600 + T, renorm=False)
@@ -937,37 +941,82 @@ def test_prefill_side_stream_is_deterministic_and_graph_safe():
     bit-identical, and a captured forward replays bit-identically to eager, with eager forwards
     and synchronizations between the replays; the result meets the oracle bars."""
     _announce("prefill side stream, graph replays")
+    mod, x, idx, w = _skewed_prefill_layer()
+    with torch.no_grad():
+        ref_loop = mod(x, idx, w)
+        assert e4b.enable_fast(mod) == 1
+        first = _eager_and_graph_agree(mod, x, idx, w)
+    _assert_fidelity(first, ref_loop, _oracle(mod, x, idx, w), "prefill side stream")
+
+
+def _skewed_prefill_layer(seed=77):
+    """A double-quant layer at 1,024 tokens whose routing leaves the last experts a handful of
+    rows each, so a forward runs 256-row tiles and 32-row tail tiles (on the second stream)."""
     E, H, I, k, T = 16, 512, 256, 4, 1024
-    g = torch.Generator().manual_seed(77)
+    g = torch.Generator().manual_seed(seed)
     gu = torch.randn(E, 2 * I, H, generator=g) * 0.05
     dn = torch.randn(E, H, I, generator=g) * 0.05
     mod = e4b.Experts4bit.from_float(gu.to(DEV), dn.to(DEV), compute_dtype=torch.bfloat16,
                                      compress_statistics=True).eval()
     x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(DEV)
-    # skewed routing: the last experts get a handful of rows each (32-row tail tiles)
     bias = -3.0 * torch.log1p(torch.arange(E, dtype=torch.float32))
     val, idx = torch.topk(torch.randn(T, E, generator=g) + bias, k, dim=-1)
     w = torch.softmax(val, -1).to(torch.bfloat16).to(DEV)
     idx = idx.to(DEV)
     counts = torch.bincount(idx.flatten().cpu(), minlength=E)
     assert int(((counts % 256 > 0) & (counts % 256 <= 32)).sum()) >= 2, counts  # tails exist
-    with torch.no_grad():
-        ref_loop = mod(x, idx, w)
-        assert e4b.enable_fast(mod) == 1
-        first = mod(x, idx, w)
-        for _ in range(3):
-            assert torch.equal(mod(x, idx, w), first)
+    return mod, x, idx, w
+
+
+def _eager_and_graph_agree(mod, x, idx, w):
+    """Repeated eager forwards are bit-identical, and a captured forward replays bit-identically
+    to them, with eager forwards and synchronizations between the replays; returns the result."""
+    first = mod(x, idx, w)
+    for _ in range(3):
+        assert torch.equal(mod(x, idx, w), first)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = mod(x, idx, w)
+    for _ in range(3):
+        graph.replay()
         torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            out = mod(x, idx, w)
-        for _ in range(3):
-            graph.replay()
-            torch.cuda.synchronize()
-            assert torch.equal(out, first)
-            assert torch.equal(mod(x, idx, w), first)
-            torch.cuda.synchronize()
-    _assert_fidelity(first, ref_loop, _oracle(mod, x, idx, w), "prefill side stream")
+        assert torch.equal(out, first)
+        assert torch.equal(mod(x, idx, w), first)
+        torch.cuda.synchronize()
+    return first
+
+
+def test_lora_prefill_side_stream_is_deterministic_and_graph_safe():
+    """The grouped LoRA forward at prefill size also runs its 32-row tail tiles on a second
+    stream (t = x . A^T before the fork, t2 after the join): eager repeats and graph replays are
+    bit-identical, and the result meets the LoRA oracle bars on every expert's first and last
+    token."""
+    _announce("LoRA prefill side stream, graph replays")
+    base, x, idx, w = _skewed_prefill_layer(seed=78)
+    mod = e4b.ExpertsLoRA(base, r=16, alpha=32, dtype=torch.float32).to(DEV).eval()
+    g = torch.Generator(device=DEV).manual_seed(79)
+    with torch.no_grad():
+        for p in (mod.gate_up_lora_B, mod.down_lora_B):
+            p.copy_(torch.randn(p.shape, generator=g, device=DEV) * 0.05)
+        assert e4b.enable_fast(mod) == 1
+        first = _eager_and_graph_agree(mod, x, idx, w)
+    assert torch.isfinite(first).all()
+    flat = idx.reshape(-1).cpu().numpy()
+    rows = sorted({int(t) for e in np.unique(flat) for t in (np.nonzero(flat == e)[0][[0, -1]] // idx.shape[1])})
+    w1, w2 = oracle_weights(base)
+    lo1 = tuple(t.detach().float().cpu().numpy() for t in (mod.gate_up_lora_A, mod.gate_up_lora_B))
+    lo2 = tuple(t.detach().float().cpu().numpy() for t in (mod.down_lora_A, mod.down_lora_B))
+    xs, ids, ws = x[rows].float().cpu().numpy(), idx[rows].cpu().numpy(), w[rows].float().cpu().numpy()
+    want = moe.forward_lora_fp32(xs, ids, ws, w1, w2, lo1, lo2, mod.scaling)
+    assert np.linalg.norm(want - moe.forward_fp32(xs, ids, ws, w1, w2)) / np.linalg.norm(want) > 0.05
+    lt1 = tuple(t.detach().cpu() for t in (mod.gate_up_lora_A, mod.gate_up_lora_B))
+    lt2 = tuple(t.detach().cpu() for t in (mod.down_lora_A, mod.down_lora_B))
+    ref = moe.reference_lora_loop(x[rows].cpu(), idx[rows].cpu(), w[rows].cpu(),
+                                  lambda e, dt: torch.from_numpy(w1[e]).to(dt),
+                                  lambda e, dt: torch.from_numpy(w2[e]).to(dt), lt1, lt2, mod.scaling,
+                                  num_experts=base.num_experts, compute_dtype=torch.bfloat16)
+    _assert_fidelity(first[rows], ref, want, f"lora prefill side stream on {len(rows)} tokens")
 
 
 def test_narrow_tiles_general_epilogues():
