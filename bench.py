@@ -413,7 +413,7 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg, graph=None):
                 torch.cuda.synchronize()
         calls = collections.defaultdict(list)
         for ev in prof.events():
-            if ev.device_type == torch.autograd.DeviceType.CUDA and ("gemm_wide_kernel" in ev.name or
+            if ev.device_type == torch.autograd.DeviceType.CUDA and ("gemm_wide" in ev.name or
                                                                      "gemm_narrow_kernel" in ev.name or
                                                                      "gemm_mfma_kernel" in ev.name):
                 t = getattr(ev, "device_time", None)
@@ -427,7 +427,7 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg, graph=None):
         calls = traced(lambda: mod(x, idx, w), 5)
     durs = collections.defaultdict(list)
     for name, cs in calls.items():
-        if "gemm_wide_kernel" in name:
+        if "gemm_wide" in name:
             bm = 256
         elif "gemm_narrow_kernel" in name:
             bm = 32

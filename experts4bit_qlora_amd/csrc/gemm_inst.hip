@@ -5,6 +5,7 @@
 #include "gemm_launch.h"
 #include "gemm_narrow.h"
 #include "gemm_wide.h"
+#include "gemm_wide8.h"
 
 #ifndef E4B_INST_DT
 #error "E4B_INST_DT must be defined"
@@ -19,10 +20,13 @@ namespace {
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// 256-row tiles run the wide kernel (four waves of 128 x 128), the others gemm_mfma_kernel.
+// 256-row tiles run a wide kernel (fp16 mode: eight waves of 128 x 64; otherwise four of
+// 128 x 128), the others gemm_mfma_kernel.
 template <int DT, int FMT, int BM, bool F16C>
 void launch_mfma_kernel(const GemmArgs& a, dim3 grid, hipStream_t s) {
-  if constexpr (BM == kTileMBig) {
+  if constexpr (BM == kTileMBig && F16C) {
+    hipLaunchKernelGGL((gemm_wide8_kernel<FMT>), grid, dim3(kWide8Threads), 0, s, a);
+  } else if constexpr (BM == kTileMBig) {
     hipLaunchKernelGGL((gemm_wide_kernel<DT, FMT, F16C>), grid, dim3(kWideThreads), 0, s, a);
   } else {
     hipLaunchKernelGGL((gemm_mfma_kernel<DT, FMT, BM, F16C>), grid, dim3(gemm_threads(BM)), 0, s, a);
@@ -58,8 +62,7 @@ void launch_mfma_gemm(const GemmArgs& a, hipStream_t s) {
     // (the host checks lora_gemm_fits before asking)
     if (a.lt) {
       if (a.rt.tile_m == kTileMBig)
-        hipLaunchKernelGGL((gemm_wide_kernel<DT, FMT, true, true>), gemm_grid(a, kWideTileN), dim3(kWideThreads), 0,
-                           s, a);
+        hipLaunchKernelGGL((gemm_wide8_kernel<FMT, true>), gemm_grid(a, kWideTileN), dim3(kWide8Threads), 0, s, a);
       else
         hipLaunchKernelGGL((gemm_narrow_kernel<FMT, true>), gemm_grid(a, kNarrowN), dim3(kNarrowThreads), 0, s, a);
       return;
