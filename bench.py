@@ -48,7 +48,7 @@ MEASURED_TRAFFIC = {
     "decode_down_kernel<bf16, nf4, G=32, CPL=1, JOBS=1, full>": 9_724_300,
     # prefill: keyed by the kernel and the projection ("<kernel> gate_up_256row"); measured
     # again for each kernel change (profiles/prefill_qwen3_4096_zipf.txt)
-    "void e4b::gemm_wide_kernel<0, 1, true, false> gate_up_256row": 428_035_000,
+    "void e4b::gemm_wide8_kernel<1, false> gate_up_256row": 421_142_000,
 }
 
 
@@ -380,7 +380,7 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg, graph=None):
     tracer sees no kernels of graph replays), the launches the timed region runs and that a
     rocprofv3 kernel trace of `bench.py --prefill-only` averages: algorithmic FLOP of each launch (the rows its tiles hold, both gate_up halves)
     / its average duration, against the dense bf16/fp16 peak. The 256-row tiles
-    (gemm_wide_kernel) carry every expert's rows except a last tile of at most 32 rows, which the
+    (gemm_wide8_kernel) carry every expert's rows except a last tile of at most 32 rows, which the
     32-row launch (gemm_narrow_kernel) takes; each forward runs gate_up then down with each kernel,
     so a kernel's calls alternate between the two projections in time order. The 32-row launches
     stream a whole expert's weights per tile for a few rows: their entries also carry the weight
