@@ -86,6 +86,30 @@ E4B_DEV bool tile_of_block(int num_tiles, int n_tiles, int& tile, int& n_tile) {
   return true;
 }
 
+// A block's work item from its index alone: tile t runs on XCD t % 8 (workgroups go round-robin
+// over the 8 XCDs: block L runs on XCD L % 8), and each XCD sweeps all N tiles of one M tile
+// before its next M tile, in list order -- a tile's activation rows stay in that XCD's L2 across
+// its N sweep. The grid is sized for the routing's max_tiles, so the tile may lie past the list:
+// its (expert, first row) is read at an index clamped into the list's capacity, in the same round
+// trip as the tile count, and the block has work iff ok. (Computing the item from the count
+// instead would put one more dependent round trip ahead of every load of the block.)
+struct TileItem {
+  int tile, n_tile, e, row0;
+  bool ok;
+};
+E4B_DEV TileItem tile_item(const e4b_routing& rt, int n_tiles) {
+  TileItem t;
+  const int xcd = static_cast<int>(blockIdx.x % kXcds);
+  const int q = static_cast<int>(blockIdx.x / kXcds);
+  t.tile = (q / n_tiles) * kXcds + xcd;
+  t.n_tile = q % n_tiles;
+  const int tc = min(t.tile, rt.max_tiles - 1);
+  t.e = rt.tiles[2 * tc];
+  t.row0 = rt.tiles[2 * tc + 1];
+  t.ok = t.tile < rt.meta[0];
+  return t;
+}
+
 // f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): indices known at compile
 // time whatever the unroller decides, so the accumulator array never needs an address (a loop
 // left rolled would put all 256 accumulators in scratch memory).

@@ -70,16 +70,16 @@ gemm_narrow_kernel(GemmArgs p) {
 
   const bool pair = is_gated(p.epi);
   const int cols = pair ? BN / 2 : BN;  // output columns per tile
-  const int num_tiles = p.rt.meta[0];
   const int n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
-  int tile, n_tile;
-  if (!tile_of_block(num_tiles, n_tiles, tile, n_tile)) return;
+  const TileItem item = tile_item(p.rt, n_tiles);
+  if (!item.ok) return;
+  const int n_tile = item.n_tile;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wid = tid / kWave;
   const int l16 = lane & 15, g = lane >> 4;
-  const int e = p.rt.tiles[2 * tile];
-  const int row0 = p.rt.tiles[2 * tile + 1];
+  const int e = item.e;
+  const int row0 = item.row0;
   const int row_end = min(row0 + BM, p.rt.offsets[e + 1]);
   const int64_t n = p.w.n;
   const int64_t k = p.w.k;

@@ -42,19 +42,6 @@ constexpr int kWideTileN = 256;  // weight rows per tile
 // & 7) the stores.)
 E4B_DEV int lds_at_w(int row, int col) { return row * kTileK + ((((col >> 3) ^ row ^ (row >> 3)) & 7) << 3); }
 
-// Work items, tile by tile: tile t runs on XCD t % 8 (workgroups go round-robin over the 8
-// XCDs: block L runs on XCD L % 8), and each XCD sweeps all N tiles of one M tile before its
-// next M tile, in list order -- the activation rows of a tile stay in that XCD's L2 across its
-// N sweep, and a list that holds the long tiles first runs them first on every XCD. false: the
-// block is past the work (the grid is sized for the routing's max_tiles).
-E4B_DEV bool wide_tile_of_block(int num_tiles, int n_tiles, int& tile, int& n_tile) {
-  const int xcd = static_cast<int>(blockIdx.x % kXcds);
-  const int q = static_cast<int>(blockIdx.x / kXcds);
-  tile = (q / n_tiles) * kXcds + xcd;
-  n_tile = q % n_tiles;
-  return tile < num_tiles;
-}
-
 // One tile. HALF: a tile of at most 128 rows (an expert's last, partial tile) as 128 rows x 256
 // weight rows, each wave 128 x 64 (two 32 x 32 MFMA columns), instead of padding it to 256 rows.
 // LORA: the accumulators start as the tile's LoRA delta (p.lt, p.lb), scaled like the products
@@ -483,8 +470,9 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
   __shared__ uint32_t ptab[F16C ? 256 * kPairCopies : 1];
   const int cols = is_gated(p.epi) ? BN / 2 : BN;
   const int n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
-  int tile, n_tile;
-  if (!wide_tile_of_block(p.rt.meta[0], n_tiles, tile, n_tile)) return;
+  const TileItem item = tile_item(p.rt, n_tiles);
+  if (!item.ok) return;
+  const int tile = item.tile, n_tile = item.n_tile;
   if constexpr (F16C) {
     // the table of code pairs: pass j fills entries 16 j .. 16 j + 15, all copies; entry
     // 16 j + t / 16 of copy t % 16 (high nibble j, low nibble t / 16)
@@ -493,8 +481,7 @@ __global__ void __launch_bounds__(kWideThreads) gemm_wide_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) ptab[j * kWideThreads + threadIdx.x] = cvt_pair<E4B_FP16>(p.w.code[j], lo);
   }
-  const int e = p.rt.tiles[2 * tile];
-  const int rows = p.rt.offsets[e + 1] - p.rt.tiles[2 * tile + 1];  // the tile's rows, capped at BM below
+  const int rows = p.rt.offsets[item.e + 1] - item.row0;  // the tile's rows, capped at BM below
   if (rows <= BM / 2) wide_tile<DT, FMT, F16C, true, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
   else wide_tile<DT, FMT, F16C, false, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
 }

@@ -304,8 +304,9 @@ __global__ void __launch_bounds__(kWide8Threads) gemm_wide8_kernel(GemmArgs p) {
   __shared__ uint32_t ptab[256 * kPairCopies];
   const int cols = is_gated(p.epi) ? BN / 2 : BN;
   const int n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
-  int tile, n_tile;
-  if (!wide_tile_of_block(p.rt.meta[0], n_tiles, tile, n_tile)) return;
+  const TileItem item = tile_item(p.rt, n_tiles);
+  if (!item.ok) return;
+  const int tile = item.tile, n_tile = item.n_tile;
   if (threadIdx.x < 256) {
     // the table of code pairs: pass j fills entries 16 j .. 16 j + 15, all copies; entry
     // 16 j + t / 16 of copy t % 16 (high nibble j, low nibble t / 16)
@@ -315,8 +316,7 @@ __global__ void __launch_bounds__(kWide8Threads) gemm_wide8_kernel(GemmArgs p) {
     for (int j = 0; j < 16; ++j) ptab[j * 256 + threadIdx.x] = cvt_pair<E4B_FP16>(p.w.code[j], lo);
     if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = p.w.code2[threadIdx.x];
   }
-  const int e = p.rt.tiles[2 * tile];
-  const int rows = p.rt.offsets[e + 1] - p.rt.tiles[2 * tile + 1];  // the tile's rows, capped at BM below
+  const int rows = p.rt.offsets[item.e + 1] - item.row0;  // the tile's rows, capped at BM below
   if (rows <= BM / 2) wide8_tile<FMT, true, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
   else wide8_tile<FMT, false, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
 }
