@@ -570,6 +570,18 @@ def extra_benches(steps, warmup, qwen_layers=8, gptoss_layers=4):
 
     out = qwen3_decode_benches(steps, warmup, qwen_layers)
     torch.cuda.empty_cache()
+    out.update(gptoss_benches(steps, warmup, gptoss_layers))
+    return out
+
+
+def gptoss_benches(steps, warmup, gptoss_layers=4):
+    """gpt-oss MXFP4 layers with biases, batch 1 (decode kernels, expert sets rotated)
+    and 2,048 tokens (256-row tiles on the eight-wave wide kernel, 32-row tails)."""
+    import torch
+
+    import experts4bit_qlora_amd as e4b
+
+    out = {}
     cfg = GPTOSS
     E, H, I = cfg["E"], cfg["H"], cfg["I"]
     mods = []
@@ -762,6 +774,8 @@ def main():
     ap.add_argument("--train-only", action="store_true", help="only the training-lane leg (for profiling)")
     ap.add_argument("--lora-prefill-only", action="store_true",
                     help="only the 4096-token ExpertsLoRA layer legs, rank 16 fp32 and rank 64 bf16 (for profiling)")
+    ap.add_argument("--gptoss-only", action="store_true",
+                    help="only the configs[4] gpt-oss MXFP4 legs, batches 1 and 2048 (for profiling)")
     ap.add_argument("--qwen-decode-only", action="store_true",
                     help="only the configs[2] Qwen3 double-quant decode legs, batches 1, 32, 256 (for profiling)")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -796,6 +810,9 @@ def main():
         return
     if args.train_only:
         print(json.dumps({"train": train_bench(args.steps, args.warmup)}), flush=True)
+        return
+    if args.gptoss_only:
+        print(json.dumps({"gptoss": gptoss_benches(args.steps, args.warmup)}), flush=True)
         return
     if args.qwen_decode_only:
         print(json.dumps({"qwen3_decode": qwen3_decode_benches(args.steps, args.warmup)}), flush=True)

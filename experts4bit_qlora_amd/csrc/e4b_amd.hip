@@ -954,15 +954,15 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
   const bool gemv_path = flags == E4B_PATH_GEMV || (flags == E4B_PATH_AUTO && tokens <= 4);
   const bool f16c = !gemv_path && act_dtype == E4B_BF16 && w1->format != E4B_FMT_MXFP4 && w1->shift && w2->shift;
   // Prefill-sized groups on the MFMA path run at two tile heights: big tiles -- 256 rows (the
-  // wide kernel) in the fp16 mode; 128 rows otherwise, where the wide kernel's bf16 / fp16
-  // operands measured slower (gpt-oss 2,048 tokens: 687 us with 128-row tiles, 812 with 256) --
-  // and one 32-row tile for an expert whose last tile would hold at most 32 rows (the long Zipf
-  // tail of experts with a handful of rows each), whose cost is mostly the streaming and
-  // decoding of its expert's weights.
+  // eight-wave wide kernel) in the fp16 mode and for MXFP4 weights with bf16 activations; 128
+  // rows otherwise -- and one 32-row tile for an expert whose last tile would hold at most 32
+  // rows (the long Zipf tail of experts with a handful of rows each), whose cost is mostly the
+  // streaming and decoding of its expert's weights.
   const bool split = rt.tile_m == e4b::kTileM && flags != E4B_PATH_GEMV;
+  const bool wide = f16c || (act_dtype == E4B_BF16 && w1->format == E4B_FMT_MXFP4);
   e4b_routing rbig = rt, rsmall = rt;
   if (split) {
-    rbig.tile_m = f16c ? e4b::kTileMBig : e4b::kTileM;
+    rbig.tile_m = wide ? e4b::kTileMBig : e4b::kTileM;
     rbig.max_tiles = static_cast<int32_t>(max_tiles_for(M, E, rbig.tile_m));
     rbig.tiles = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 2 * rbig.max_tiles));
     rbig.meta = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * 4));

@@ -20,12 +20,12 @@ namespace {
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// 256-row tiles run a wide kernel (fp16 mode: eight waves of 128 x 64; otherwise four of
-// 128 x 128), the others gemm_mfma_kernel.
+// 256-row tiles run a wide kernel (fp16 mode, or MXFP4 with bf16 activations: eight waves of
+// 128 x 64; otherwise four of 128 x 128), the others gemm_mfma_kernel.
 template <int DT, int FMT, int BM, bool F16C>
 void launch_mfma_kernel(const GemmArgs& a, dim3 grid, hipStream_t s) {
-  if constexpr (BM == kTileMBig && F16C) {
-    hipLaunchKernelGGL((gemm_wide8_kernel<FMT>), grid, dim3(kWide8Threads), 0, s, a);
+  if constexpr (BM == kTileMBig && (F16C || (DT == E4B_BF16 && FMT == E4B_FMT_MXFP4))) {
+    hipLaunchKernelGGL((gemm_wide8_kernel<DT, FMT, F16C>), grid, dim3(kWide8Threads), 0, s, a);
   } else if constexpr (BM == kTileMBig) {
     hipLaunchKernelGGL((gemm_wide_kernel<DT, FMT, F16C>), grid, dim3(kWideThreads), 0, s, a);
   } else {
@@ -62,7 +62,8 @@ void launch_mfma_gemm(const GemmArgs& a, hipStream_t s) {
     // (the host checks lora_gemm_fits before asking)
     if (a.lt) {
       if (a.rt.tile_m == kTileMBig)
-        hipLaunchKernelGGL((gemm_wide8_kernel<FMT, true>), gemm_grid(a, kWideTileN), dim3(kWide8Threads), 0, s, a);
+        hipLaunchKernelGGL((gemm_wide8_kernel<DT, FMT, true, true>), gemm_grid(a, kWideTileN), dim3(kWide8Threads), 0,
+                           s, a);
       else
         hipLaunchKernelGGL((gemm_narrow_kernel<FMT, true>), gemm_grid(a, kNarrowN), dim3(kNarrowThreads), 0, s, a);
       return;

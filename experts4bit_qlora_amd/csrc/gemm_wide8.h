@@ -1,7 +1,9 @@
 // Prefill grouped GEMM, wide tiles with two waves per SIMD: 256 sorted rows x 256 weight rows
-// per workgroup in the fp16 matrix-core mode (bf16 activations stored as scaled fp16 rows,
-// NF4 / double-quant NF4 weights decoded through the LDS code-pair table), eight waves of
-// 128 x 64 each on v_mfma_f32_32x32x16_f16.
+// per workgroup, eight waves of 128 x 64 each on 32 x 32 x 16 MFMAs. Two weight formats: in the
+// fp16 matrix-core mode (F16C: bf16 activations stored as scaled fp16 rows, NF4 / double-quant
+// NF4 weights decoded through the LDS code-pair table, v_mfma_f32_32x32x16_f16), and MXFP4 with
+// bf16 activations (e2m1 bytes converted in registers by v_cvt_scalef32_pk_bf16_fp4, exact in
+// bf16, v_mfma_f32_32x32x16_bf16; a thread's 32 values of a step are one e8m0 scale block).
 //
 // gemm_wide_kernel runs the same tile with four waves of 128 x 128, one per SIMD: nothing covers
 // a stall of its wave, so its loop is laid out by hand, and still a 64-deep step takes ~3x its
@@ -31,11 +33,11 @@ namespace e4b {
 constexpr int kWide8Threads = 512;
 
 // One tile. HALF: a tile of at most 128 rows as 128 rows x 256 weight rows (waves of 64 x 64).
-template <int FMT, bool HALF, bool LORA>
+template <int DT, int FMT, bool F16C, bool HALF, bool LORA>
 E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2][kWideTileM * kTileK],
                         uint16_t (&Ws)[2][kWideTileN * kTileK], const float* code2_s, int* row_shift_s,
                         const uint32_t* ptab) {
-  constexpr int CT = E4B_FP16;
+  constexpr int CT = F16C ? E4B_FP16 : DT;
   constexpr int BM = HALF ? kWideTileM / 2 : kWideTileM, BN = kWideTileN;
   constexpr int MS = BM / 64;  // 32-row MFMA tiles per wave (each wave: BM / 2 rows)
   constexpr int NS = 2;        // 32-column MFMA tiles per wave
@@ -67,8 +69,8 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
     const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
     aoff[i] = static_cast<uint32_t>((src * k) / 8 + apart);
   }
-  const int wsh = p.w.shift[e];
-  if (tid < BM) {  // row_shift_s: the shift of tile row tid, for the epilogue
+  const int wsh = F16C ? p.w.shift[e] : 0;
+  if (F16C && tid < BM) {  // row_shift_s: the shift of tile row tid, for the epilogue
     const int r = row0 + tid;
     const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
     row_shift_s[tid] = exp_shift(p.a_exp[src]);
@@ -94,14 +96,16 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
   u32x4_t areg[RS][AP];
   uint4 wq[RS];
   float sa[RS];
-  uint32_t sq[RS];
+  uint32_t sq[RS];  // double quant: code index; MXFP4: the e8m0 scale of the thread's 32 values
   auto load_a = [&](int set, int64_t kb) {
 #pragma unroll
     for (int i = 0; i < AP; ++i) areg[set][i] = (reinterpret_cast<const u32x4_t*>(p.a) + kb * (kTileK / 8))[aoff[i]];
   };
   auto load_w = [&](int set, int64_t kb) {
     wq[set] = *reinterpret_cast<const uint4*>(wptr + kb * 32);
-    if constexpr (FMT == E4B_FMT_NF4) {
+    if constexpr (FMT == E4B_FMT_MXFP4) {
+      sq[set] = static_cast<const uint8_t*>(p.w.absmax)[(int64_t(e) * n + grow) * (k / 32) + 2 * kb + wh];
+    } else if constexpr (FMT == E4B_FMT_NF4) {
       sa[set] = static_cast<const float*>(p.w.absmax)[e * nb + grow * (k / 64) + kb];
     } else {
       const int64_t blk = grow * (k / 64) + kb;
@@ -109,8 +113,10 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
       sa[set] = p.w.absmax2[e * ((nb + 255) / 256) + blk / 256];
     }
   };
-  // the block scale of a staged step as an fp16 pair, 2^shift applied (exact)
-  auto scale_pair = [&](int set) {
+  // the block scale of a staged step: as an fp16 pair with 2^shift applied (exact) for the
+  // table decode, as the fp32 scale for the e2m1 conversion
+  auto scale_pair = [&](int set) -> uint32_t {
+    if constexpr (FMT == E4B_FMT_MXFP4) return sq[set];
     float scale;
     if constexpr (FMT == E4B_FMT_NF4) {
       scale = sa[set];
@@ -130,8 +136,12 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
   auto store_w = [&](int set, int buf, int wi, uint32_t sc) {
     const uint32_t w = wi == 0 ? wq[set].x : wi == 1 ? wq[set].y : wi == 2 ? wq[set].z : wq[set].w;
     uint32_t o[4];
+    if constexpr (FMT == E4B_FMT_MXFP4) {
+      fp4_word<CT>(w, e8m0_to_f32(sc), o);
+    } else {
 #pragma unroll
-    for (int b = 0; b < 4; ++b) o[b] = pk_mul_f16(tab[((w >> (8 * b)) & 0xffu) * kPairCopies], sc);
+      for (int b = 0; b < 4; ++b) o[b] = pk_mul_f16(tab[((w >> (8 * b)) & 0xffu) * kPairCopies], sc);
+    }
     *reinterpret_cast<uint4*>(&Ws[buf][lds_at_w(wr, 32 * wh + 8 * wi)]) = make_uint4(o[0], o[1], o[2], o[3]);
   };
 
@@ -230,12 +240,14 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
   auto row_of = [&](int ms, int i) {
     return wave_m * (BM / 2) + ms * 32 + 8 * (i >> 2) + 4 * (lane_e >> 5) + (i & 3);
   };
-  static_for<MS>([&](auto ms) {
-    static_for<16>([&](auto i) {
-      const int d = -(row_shift_s[row_of(ms, i)] + wsh);
-      static_for<NS>([&](auto ns) { acc[ms][ns][int(i)] = __builtin_amdgcn_ldexpf(acc[ms][ns][int(i)], d); });
+  if constexpr (F16C) {
+    static_for<MS>([&](auto ms) {
+      static_for<16>([&](auto i) {
+        const int d = -(row_shift_s[row_of(ms, i)] + wsh);
+        static_for<NS>([&](auto ns) { acc[ms][ns][int(i)] = __builtin_amdgcn_ldexpf(acc[ms][ns][int(i)], d); });
+      });
     });
-  });
+  }
   const bool has_bias = p.w.bias != nullptr;
   const uint16_t* bias = static_cast<const uint16_t*>(p.w.bias);
   if (pair && p.epi == E4B_EPI_SWIGLU && !has_bias && !p.out_f32) {  // gate_up: silu(g) * u -> bf16
@@ -246,7 +258,7 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
         static_for<16>([&](auto i) {
           const int rr = row0 + row_of(ms, i);
           const float v = silu_f32(acc[ms][0][int(i)]) * acc[ms][1][int(i)];
-          if (rr < row_end) out[int64_t(rr) * p.n_out + cc] = from_f<E4B_BF16>(v);
+          if (rr < row_end) out[int64_t(rr) * p.n_out + cc] = from_f<DT>(v);
         });
       });
     }
@@ -275,16 +287,16 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
         if (pair) {
           const int64_t jj = col0 + 32 * wave_n + (lane_e & 31);
           if (jj < p.n_out) {
-            const float bg = has_bias ? to_f<E4B_BF16>(bias[int64_t(e) * n + jj]) : 0.0f;
-            const float bu = has_bias ? to_f<E4B_BF16>(bias[int64_t(e) * n + n / 2 + jj]) : 0.0f;
-            store_elem<E4B_BF16>(p, orow + jj, gated(p.epi, acc[ms][0][int(i)], acc[ms][1][int(i)], p.alpha, p.limit, bg, bu));
+            const float bg = has_bias ? to_f<DT>(bias[int64_t(e) * n + jj]) : 0.0f;
+            const float bu = has_bias ? to_f<DT>(bias[int64_t(e) * n + n / 2 + jj]) : 0.0f;
+            store_elem<DT>(p, orow + jj, gated(p.epi, acc[ms][0][int(i)], acc[ms][1][int(i)], p.alpha, p.limit, bg, bu));
           }
         } else {
           static_for<NS>([&](auto ns) {
             const int64_t nn = col0 + 64 * wave_n + ns * 32 + (lane_e & 31);
             if (nn < p.n_out) {
-              const float b = has_bias ? to_f<E4B_BF16>(bias[int64_t(e) * n + nn]) : 0.0f;
-              store_elem<E4B_BF16>(p, orow + nn, single(p.epi, acc[ms][ns][int(i)], b));
+              const float b = has_bias ? to_f<DT>(bias[int64_t(e) * n + nn]) : 0.0f;
+              store_elem<DT>(p, orow + nn, single(p.epi, acc[ms][ns][int(i)], b));
             }
           });
         }
@@ -293,32 +305,36 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
   });
 }
 
-template <int FMT, bool LORA = false>
+template <int DT, int FMT, bool F16C, bool LORA = false>
 __global__ void __launch_bounds__(kWide8Threads) gemm_wide8_kernel(GemmArgs p) {
-  static_assert(FMT != E4B_FMT_MXFP4, "fp16 mode: NF4 weights");
+  static_assert(F16C ? (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4) : (DT == E4B_BF16 && FMT == E4B_FMT_MXFP4),
+                "fp16 mode with NF4 weights, or bf16 activations with MXFP4 weights");
+  static_assert(!LORA || F16C, "the LoRA epilogue runs in the fp16 mode");
   constexpr int BM = kWideTileM, BN = kWideTileN;
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kTileK];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kTileK];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
-  __shared__ int row_shift_s[BM];
-  __shared__ uint32_t ptab[256 * kPairCopies];
+  __shared__ int row_shift_s[F16C ? BM : 1];
+  __shared__ uint32_t ptab[F16C ? 256 * kPairCopies : 1];
   const int cols = is_gated(p.epi) ? BN / 2 : BN;
   const int n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
   const TileItem item = tile_item(p.rt, n_tiles);
   if (!item.ok) return;
   const int tile = item.tile, n_tile = item.n_tile;
-  if (threadIdx.x < 256) {
-    // the table of code pairs: pass j fills entries 16 j .. 16 j + 15, all copies; entry
-    // 16 j + t / 16 of copy t % 16 (high nibble j, low nibble t / 16)
-    static_assert(256 == 16 * kPairCopies, "table fill");
-    const float lo = p.w.code[threadIdx.x / kPairCopies];
+  if constexpr (F16C) {
+    if (threadIdx.x < 256) {
+      // the table of code pairs: pass j fills entries 16 j .. 16 j + 15, all copies; entry
+      // 16 j + t / 16 of copy t % 16 (high nibble j, low nibble t / 16)
+      static_assert(256 == 16 * kPairCopies, "table fill");
+      const float lo = p.w.code[threadIdx.x / kPairCopies];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) ptab[j * 256 + threadIdx.x] = cvt_pair<E4B_FP16>(p.w.code[j], lo);
-    if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = p.w.code2[threadIdx.x];
+      for (int j = 0; j < 16; ++j) ptab[j * 256 + threadIdx.x] = cvt_pair<E4B_FP16>(p.w.code[j], lo);
+      if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = p.w.code2[threadIdx.x];
+    }
   }
   const int rows = p.rt.offsets[item.e + 1] - item.row0;  // the tile's rows, capped at BM below
-  if (rows <= BM / 2) wide8_tile<FMT, true, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
-  else wide8_tile<FMT, false, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
+  if (rows <= BM / 2) wide8_tile<DT, FMT, F16C, true, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
+  else wide8_tile<DT, FMT, F16C, false, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
 }
 
 }  // namespace e4b
