@@ -48,7 +48,7 @@ MEASURED_TRAFFIC = {
     "decode_down_kernel<bf16, nf4, G=32, CPL=1, JOBS=1, full>": 9_724_300,
     # prefill: keyed by the kernel and the projection ("<kernel> gate_up_256row"); measured
     # again for each kernel change (profiles/prefill_qwen3_4096_zipf.txt)
-    "void e4b::gemm_wide8_kernel<1, false> gate_up_256row": 421_142_000,
+    "gemm_wide8_kernel<bf16, nf4_dq, fp16 mode> gate_up_256row": 421_320_000,
 }
 
 
@@ -374,22 +374,22 @@ def dominant_kernel_roofline(mods, cfg, steps, warmup, seed0):
     }
 
 
-def prefill_gemm_roofline(mod, x, idx, w, cfg, graph=None):
-    """The prefill's GEMM launches (fp16 matrix-core mode) timed by the device tracer over twenty
-    back-to-back replays of the forward's graph (five eager forwards when no graph is given or the
-    tracer sees no kernels of graph replays), the launches the timed region runs and that a
-    rocprofv3 kernel trace of `bench.py --prefill-only` averages: algorithmic FLOP of each launch (the rows its tiles hold, both gate_up halves)
-    / its average duration, against the dense bf16/fp16 peak. The 256-row tiles
+def prefill_gemm_roofline(mod, x, idx, w, cfg, reps=20):
+    """The prefill's four GEMM launches (fp16 matrix-core mode), each timed with HIP events that
+    the library records on the launch's own stream right before and after it (e4b_set_probe),
+    over `reps` forwards: algorithmic FLOP of each launch (the rows its tiles hold, both gate_up
+    halves) / its average duration, against the dense bf16/fp16 peak. The 256-row tiles
     (gemm_wide8_kernel) carry every expert's rows except a last tile of at most 32 rows, which the
-    32-row launch (gemm_narrow_kernel) takes; each forward runs gate_up then down with each kernel,
-    so a kernel's calls alternate between the two projections in time order. The 32-row launches
-    stream a whole expert's weights per tile for a few rows: their entries also carry the weight
-    bytes of those tiles and the HBM rate."""
-    import collections
-
+    32-row launch (gemm_narrow_kernel, on the library's second stream beside the 256-row launch)
+    takes. Each forward is queued behind a short device-side wait, so the host has issued the
+    whole forward before the device reaches the first recorded event. The 32-row launches stream a
+    whole expert's weights per tile for a few rows: their entries also carry the weight bytes of
+    those tiles and the HBM rate."""
     import torch
-    from torch.profiler import ProfilerActivity, profile
 
+    from experts4bit_qlora_amd import _native as N
+
+    L = N.lib()
     H, I = cfg["H"], cfg["I"]
     counts = torch.bincount(idx.reshape(-1), minlength=cfg["E"]).cpu().tolist()
     tail = [c % 256 if 0 < c % 256 <= 32 else 0 for c in counts]
@@ -403,58 +403,45 @@ def prefill_gemm_roofline(mod, x, idx, w, cfg, graph=None):
         nb = n * k // 64
         return n * k // 2 + nb + math.ceil(nb / 256) * 4 + 4
     tail_bytes = {"gate_up": n_tail * proj_bytes(2 * I, H), "down": n_tail * proj_bytes(H, I)}
-    def traced(run, reps):
-        with torch.no_grad():
-            run()
-            torch.cuda.synchronize()
-            with profile(activities=[ProfilerActivity.CUDA]) as prof:
-                for _ in range(reps):
-                    run()
-                torch.cuda.synchronize()
-        calls = collections.defaultdict(list)
-        for ev in prof.events():
-            if ev.device_type == torch.autograd.DeviceType.CUDA and ("gemm_wide" in ev.name or
-                                                                     "gemm_narrow_kernel" in ev.name or
-                                                                     "gemm_mfma_kernel" in ev.name):
-                t = getattr(ev, "device_time", None)
-                calls[ev.name.split("(")[0]].append((ev.time_range.start, t if t is not None else ev.cuda_time))
-        return calls
-
-    timer = "device tracer (torch.profiler), 20 back-to-back graph replays of the forward"
-    calls = traced(graph.replay, 20) if graph is not None else {}
-    if not calls:
-        timer = "device tracer (torch.profiler), 5 eager forwards"
-        calls = traced(lambda: mod(x, idx, w), 5)
-    durs = collections.defaultdict(list)
-    for name, cs in calls.items():
-        if "gemm_wide" in name:
-            bm = 256
-        elif "gemm_narrow_kernel" in name:
-            bm = 32
-        else:
-            bm = int(name[name.index("<") + 1:name.index(">")].split(",")[2])
-        for i, (_, d) in enumerate(sorted(cs)):
-            durs[(name, bm, "gate_up" if i % 2 == 0 else "down")].append(d)
+    kernels = {256: "gemm_wide8_kernel<bf16, nf4_dq, fp16 mode>", 32: "gemm_narrow_kernel<nf4_dq>"}
+    sites = {("gate_up", 256): N.PROBE_GATE_UP_BIG, ("gate_up", 32): N.PROBE_GATE_UP_TAIL,
+             ("down", 256): N.PROBE_DOWN_BIG, ("down", 32): N.PROBE_DOWN_TAIL}
+    before, after = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    before.record()
+    after.record()  # the events exist (torch creates them at their first record)
+    torch.cuda.synchronize()
     out = {}
-    for (name, bm, proj), d in durs.items():
-        us = sum(d) / len(d)
-        tf = flop[(bm, proj)] / (us * 1e-6) / 1e12
-        out[f"{proj}_{bm}row"] = {"kernel": name, "avg_launch_us": round(us, 2), "calls": len(d),
-                                  "flop_per_launch": flop[(bm, proj)], "achieved": round(tf, 1),
-                                  "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
-        if bm == 32:  # whole experts' weights for a few rows each: the HBM view
-            gbs = tail_bytes[proj] / (us * 1e-6) / 1e9
-            out[f"{proj}_{bm}row"].update({"tiles": n_tail, "weight_bytes": tail_bytes[proj],
-                                           "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
-    if not out:
-        return None
+    with torch.no_grad():
+        mod(x, idx, w)
+        for (proj, bm), site in sites.items():
+            durs = []
+            for _ in range(reps):
+                torch.cuda._sleep(100_000)
+                N.check("e4b_set_probe", L.e4b_set_probe(site, before.cuda_event, after.cuda_event))
+                try:
+                    mod(x, idx, w)
+                finally:
+                    N.check("e4b_set_probe", L.e4b_set_probe(N.PROBE_OFF, None, None))
+                torch.cuda.synchronize()
+                durs.append(before.elapsed_time(after) * 1e3)
+            us = sum(durs) / len(durs)
+            tf = flop[(bm, proj)] / (us * 1e-6) / 1e12
+            key = f"{proj}_{bm}row"
+            out[key] = {"kernel": kernels[bm], "avg_launch_us": round(us, 2), "median_launch_us":
+                        round(statistics.median(durs), 2), "calls": len(durs), "flop_per_launch": flop[(bm, proj)],
+                        "achieved": round(tf, 1), "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+            if bm == 32:  # whole experts' weights for a few rows each: the HBM view
+                gbs = tail_bytes[proj] / (us * 1e-6) / 1e9
+                out[key].update({"tiles": n_tail, "weight_bytes": tail_bytes[proj],
+                                 "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
     dom_key = max(out, key=lambda key: out[key]["avg_launch_us"])
     dom = out[dom_key]
     return {"bound": "mfma", "kernel": f"{dom['kernel']} ({dom_key.rsplit('_', 1)[0]}, dominant prefill GEMM)",
             "achieved": dom["achieved"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac"],
             "traffic": MEASURED_TRAFFIC.get(f"{dom['kernel']} {dom_key}"),
             "flop_per_launch": dom["flop_per_launch"], "avg_launch_us": dom["avg_launch_us"],
-            "timer": timer, "launches": out}
+            "timer": f"HIP events recorded by the library on the launch's stream (e4b_set_probe), {reps} forwards "
+                     "per launch", "launches": out}
 
 
 def pmc_pass(mods, cfg, seed0):
@@ -475,14 +462,23 @@ def pmc_pass(mods, cfg, seed0):
         h = ops.decode_gate_up(x, idx, w1, N.EPI_SWIGLU)
         ops.decode_down_combine(h, idx, w, w2, x.dtype)
     torch.cuda.synchronize()
+    copy_bytes = calibration_copy()
+    gu_b, _ = nf4_expert_bytes(cfg["H"], cfg["I"])
+    print(json.dumps({"pmc_pass": {"kernel_bytes_per_launch": cfg["k"] * gu_b, "launches": len(mods),
+                                   "copy_bytes": copy_bytes}}), flush=True)
+
+
+def calibration_copy():
+    """One 256 MiB device-to-device copy: a counter run reads its FETCH_SIZE / WRITE_SIZE against
+    the 268,435,456 bytes it must move, which gives the counters' bytes-per-KiB scale."""
+    import torch
+
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda").fill_(1)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
-    gu_b, _ = nf4_expert_bytes(cfg["H"], cfg["I"])
-    print(json.dumps({"pmc_pass": {"kernel_bytes_per_launch": cfg["k"] * gu_b, "launches": len(mods),
-                                   "copy_bytes": src.numel()}}), flush=True)
+    return src.numel()
 
 
 def prefill_bench(steps, warmup):
@@ -505,7 +501,7 @@ def prefill_bench(steps, warmup):
     ms = time_graph(g, max(steps, 10), warmup)
     flops = 2 * cfg["k"] * 4096 * (2 * cfg["I"] * cfg["H"] + cfg["H"] * cfg["I"])
     tflops = flops / (ms / 1e3) / 1e12
-    roof = prefill_gemm_roofline(mod, x, idx, w, cfg, graph=g)
+    roof = prefill_gemm_roofline(mod, x, idx, w, cfg)
     return {
         "roofline": roof,
         "workload": "Qwen3-30B-A3B geometry, 1 layer, 4096-token prefill, Zipf(1.1), NF4 double-quant",
@@ -781,6 +777,8 @@ def main():
     ap.add_argument("--pmc-pass", action="store_true",
                     help="for counter runs: the dominant kernel eagerly once per layer, then a 256 MiB "
                          "device copy whose counter reading calibrates bytes per counted KiB")
+    ap.add_argument("--pmc-copy", action="store_true",
+                    help="with --prefill-only: the 256 MiB calibration copy after the prefill (counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -798,6 +796,8 @@ def main():
     N.lib()  # fail loudly if the kernel library is missing
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_bench(args.steps, args.warmup)}), flush=True)
+        if args.pmc_copy:
+            calibration_copy()
         return
     if args.lora_prefill_only:
         cfg = OLMOE

@@ -20,6 +20,8 @@ E4B_OK = 0
 FMT_NF4, FMT_NF4_DQ, FMT_MXFP4 = 0, 1, 2
 BF16, FP16, FP32 = 0, 1, 2
 EPI_NONE, EPI_SWIGLU, EPI_ACT, EPI_CLAMP_SWIGLU, EPI_GPTOSS = 0, 1, 2, 3, 4
+# e4b_probe_site: launch sites of the prefill path that e4b_set_probe can watch
+PROBE_OFF, PROBE_GATE_UP_BIG, PROBE_GATE_UP_TAIL, PROBE_DOWN_BIG, PROBE_DOWN_TAIL = 0, 1, 2, 3, 4
 PATH_AUTO, PATH_GEMV, PATH_MFMA = 0, 1, 2
 NOALLOC_WORKSPACE_BYTES = 64 << 20  # E4B_NOALLOC_WORKSPACE_BYTES
 
@@ -49,6 +51,7 @@ EXPORTS = (
     "e4b_moe_forward_noalloc",
     "e4b_moe_lora_workspace_bytes",
     "e4b_moe_lora_forward",
+    "e4b_set_probe",
 )
 
 
@@ -167,6 +170,8 @@ def _bind(L):
     L.e4b_moe_lora_forward.restype = ctypes.c_int
     L.e4b_moe_lora_forward.argtypes = [P, I32, I64, P, P, I32, I32, QW, QW, ctypes.POINTER(Lora), I32, F32, I32, P,
                                        ctypes.c_size_t, P, I32, P]
+    L.e4b_set_probe.restype = ctypes.c_int
+    L.e4b_set_probe.argtypes = [I32, P, P]
     return L
 
 

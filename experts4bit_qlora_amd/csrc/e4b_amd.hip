@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -144,25 +145,52 @@ class SideLease {
   SideStream* ss_ = nullptr;
 };
 
+// Measurement hook (e4b_set_probe): the watched launch site and the caller's event pair, read
+// by every split forward (the atomic keeps the unwatched case to one load).
+std::atomic<int> g_probe_site{E4B_PROBE_OFF};
+std::mutex g_probe_mu;
+hipEvent_t g_probe_ev[2] = {nullptr, nullptr};
+
+struct ProbeEvents {
+  hipEvent_t before = nullptr, after = nullptr;
+};
+ProbeEvents probe_for(int site) {
+  if (g_probe_site.load(std::memory_order_relaxed) != site) return {};
+  std::lock_guard<std::mutex> lk(g_probe_mu);
+  if (g_probe_site.load(std::memory_order_relaxed) != site) return {};
+  return {g_probe_ev[0], g_probe_ev[1]};
+}
+
+// launch(r, s) between the probe's event records when `site` is watched
+template <class F>
+int probed(int site, const e4b_routing* r, hipStream_t s, F&& launch) {
+  const ProbeEvents pe = probe_for(site);
+  if (pe.before && hipEventRecord(pe.before, s) != hipSuccess) return check_launch("probe event");
+  const int rc = launch(r, s);
+  if (pe.after && hipEventRecord(pe.after, s) != hipSuccess) return check_launch("probe event");
+  return rc;
+}
+
 // launch(rbig, stream) and launch(rsmall, the side stream), the side stream forked from `stream`
 // after everything enqueued so far and joined back into it (both on `stream` without a side
-// stream): the two tile heights write disjoint rows.
+// stream): the two tile heights write disjoint rows. site_big / site_big + 1: the probe sites of
+// the two launches.
 template <class F>
 int run_tile_heights(const SideStream* side, hipStream_t stream, const e4b_routing* rbig, const e4b_routing* rsmall,
-                     F&& launch) {
+                     int site_big, F&& launch) {
   if (side) {
     if (hipEventRecord(side->fork, stream) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)
       return check_launch("side stream fork");
-    int r = launch(rbig, stream);
-    if (!r) r = launch(rsmall, side->s);
+    int r = probed(site_big, rbig, stream, launch);
+    if (!r) r = probed(site_big + 1, rsmall, side->s, launch);
     // joined whatever happened, so the caller's stream never runs ahead of the side stream
     const bool joined = hipEventRecord(side->join, side->s) == hipSuccess &&
                         hipStreamWaitEvent(stream, side->join, 0) == hipSuccess;
     if (r) return r;
     return joined ? 0 : check_launch("side stream join");
   }
-  int r = launch(rbig, stream);
-  return r ? r : launch(rsmall, stream);
+  int r = probed(site_big, rbig, stream, launch);
+  return r ? r : probed(site_big + 1, rsmall, stream, launch);
 }
 
 bool act_dtype_ok(int dt) { return dt == E4B_BF16 || dt == E4B_FP16; }
@@ -1003,15 +1031,17 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
     // the two tile heights write disjoint rows: the 32-row tiles go to the side stream (forked
     // after everything they read, joined before anything reads what they write)
     SideLease lease(stream, side_ok);
-    auto both = [&](auto&& launch) { return run_tile_heights(lease.get(), stream, &rbig, &rsmall, launch); };
-    rc = both([&](const e4b_routing* r, hipStream_t s) {
+    auto both = [&](int site, auto&& launch) {
+      return run_tile_heights(lease.get(), stream, &rbig, &rsmall, site, launch);
+    };
+    rc = both(E4B_PROBE_GATE_UP_BIG, [&](const e4b_routing* r, hipStream_t s) {
       return grouped_gemm_impl(up_a, act_dtype, top_k, w1, r, tokens, M, epilogue, alpha, limit, flags, h, act_dtype,
                                up_exp, s);
     });
     if (rc) return rc;
     rc = h_to_f16();
     if (rc) return rc;
-    rc = both([&](const e4b_routing* r, hipStream_t s) {
+    rc = both(E4B_PROBE_DOWN_BIG, [&](const e4b_routing* r, hipStream_t s) {
       return grouped_gemm_impl(h, act_dtype, 0, w2, r, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
                                h_exp, s);
     });
@@ -1036,6 +1066,16 @@ int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const
                     size_t workspace_bytes, void* out, int32_t out_dtype, hipStream_t stream) {
   return moe_forward_impl(hidden, act_dtype, tokens, top_k_index, top_k_weights, weight_dtype, top_k, w1, w2,
                           epilogue, alpha, limit, flags, workspace, workspace_bytes, out, out_dtype, stream, true);
+}
+
+int e4b_set_probe(int32_t site, hipEvent_t before, hipEvent_t after) {
+  if (site < E4B_PROBE_OFF || site > E4B_PROBE_DOWN_TAIL) return fail(E4B_EINVAL, "bad probe site %d", site);
+  if (site != E4B_PROBE_OFF && (!before || !after)) return fail(E4B_EINVAL, "NULL probe event");
+  std::lock_guard<std::mutex> lk(g_probe_mu);
+  g_probe_ev[0] = site == E4B_PROBE_OFF ? nullptr : before;
+  g_probe_ev[1] = site == E4B_PROBE_OFF ? nullptr : after;
+  g_probe_site.store(site, std::memory_order_relaxed);
+  return E4B_OK;
 }
 
 static_assert(e4b::kDecLoraMaxRank == e4b::kLoraMaxRank, "one rank limit for both LoRA paths");
@@ -1283,13 +1323,13 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
     }
     // the 32-row tiles of a split run on a side stream, as in e4b_moe_forward
     SideLease lease(stream, split);
-    auto tiles = [&](auto&& launch) {
-      return split ? run_tile_heights(lease.get(), stream, &rbig, &rsmall, launch) : launch(&rt, stream);
+    auto tiles = [&](int site, auto&& launch) {
+      return split ? run_tile_heights(lease.get(), stream, &rbig, &rsmall, site, launch) : launch(&rt, stream);
     };
     rc = lora_t_mfma(hidden, top_k, rt, lora->a1, lora->dtype, r, w1->k, t, stream);
     if (rc) return rc;
     const LoraEpi l1{t, lora->b1, lora->dtype, r, lora->scaling};
-    rc = tiles([&](const e4b_routing* rp, hipStream_t s) {
+    rc = tiles(E4B_PROBE_GATE_UP_BIG, [&](const e4b_routing* rp, hipStream_t s) {
       return grouped_gemm_impl(x16, act_dtype, top_k, w1, rp, tokens, M, epilogue, 1.0f, limit, E4B_PATH_MFMA, h,
                                act_dtype, xexp, s, &l1);
     });
@@ -1302,7 +1342,7 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
     rc = check_launch("row_exp_kernel");
     if (rc) return rc;
     const LoraEpi l2{t, lora->b2, lora->dtype, r, lora->scaling};
-    rc = tiles([&](const e4b_routing* rp, hipStream_t s) {
+    rc = tiles(E4B_PROBE_DOWN_BIG, [&](const e4b_routing* rp, hipStream_t s) {
       return grouped_gemm_impl(h, act_dtype, 0, w2, rp, tokens, M, E4B_EPI_NONE, 1.0f, limit, E4B_PATH_MFMA, down,
                                E4B_FP32, hexp, s, &l2);
     });

@@ -327,6 +327,28 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
                          const e4b_qweight* w2, const e4b_lora* lora, int32_t epilogue, float limit, int32_t flags,
                          void* workspace, size_t workspace_bytes, void* out, int32_t out_dtype, hipStream_t stream);
 
+/* Launch sites of the prefill path that e4b_set_probe can watch: the 256-row (big) tile launch
+ * of each projection and its 32-row tail launch (which runs on the library's second stream when
+ * one is free). */
+enum e4b_probe_site {
+  E4B_PROBE_OFF = 0,
+  E4B_PROBE_GATE_UP_BIG = 1,
+  E4B_PROBE_GATE_UP_TAIL = 2,
+  E4B_PROBE_DOWN_BIG = 3,
+  E4B_PROBE_DOWN_TAIL = 4
+};
+
+/* Measurement hook for benchmarks and profilers. While a site is set, every e4b_moe_forward /
+ * e4b_moe_lora_forward whose routed rows are re-tiled into 256- and 32-row tiles records `before`
+ * on the stream of that site's launch right before the launch and `after` right after it, so
+ * hipEventElapsedTime(before, after) is the launch's device time once `after` has completed.
+ * E4B_PROBE_OFF clears it. One setting per process; the caller keeps both events alive while it
+ * is set. Meant for eager calls (records made during a graph capture become graph nodes, whose
+ * elapsed time did not follow the replays when measured). Has no counterpart in the reference:
+ * it exists so that a benchmark can time one kernel of the fused forward with HIP events on the
+ * stream that kernel is launched on. */
+int e4b_set_probe(int32_t site, hipEvent_t before, hipEvent_t after);
+
 #ifdef __cplusplus
 }
 #endif

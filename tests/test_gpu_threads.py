@@ -132,3 +132,45 @@ def test_capture_in_one_thread_eager_in_another():
             again = mod(*b)
         torch.cuda.synchronize()
         assert torch.equal(again, ref_b)
+
+
+def test_probe_events_time_each_prefill_launch_without_changing_results():
+    """e4b_set_probe: the library records the caller's event pair around the watched launch on
+    that launch's stream. Each site yields a positive duration shorter than the whole forward,
+    the probed forward's output equals the unprobed one bit for bit, and clearing the probe
+    leaves later forwards unrecorded (the `after` event keeps its last timestamp)."""
+    from experts4bit_qlora_amd import _native as N
+
+    L = N.lib()
+    mod = _module()
+    x, idx, w = _inputs(2048, 16, 512, 4, seed=31)
+    with torch.no_grad():
+        ref = mod(x, idx, w)
+    before, after = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    before.record()
+    after.record()
+    torch.cuda.synchronize()
+    for site in (N.PROBE_GATE_UP_BIG, N.PROBE_GATE_UP_TAIL, N.PROBE_DOWN_BIG, N.PROBE_DOWN_TAIL):
+        _announce(f"probe site {site}")
+        torch.cuda._sleep(100_000)
+        N.check("e4b_set_probe", L.e4b_set_probe(site, before.cuda_event, after.cuda_event))
+        try:
+            start.record()
+            with torch.no_grad():
+                out = mod(x, idx, w)
+            end.record()
+        finally:
+            N.check("e4b_set_probe", L.e4b_set_probe(N.PROBE_OFF, None, None))
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"site {site}: the probed forward differs"
+        t_launch, t_all = before.elapsed_time(after), start.elapsed_time(end)
+        assert 0.0 < t_launch < t_all, (site, t_launch, t_all)
+    # cleared: a forward records nothing, so the pair still spans the last probed launch
+    last = before.elapsed_time(after)
+    with torch.no_grad():
+        mod(x, idx, w)
+    torch.cuda.synchronize()
+    assert before.elapsed_time(after) == last
+    with pytest.raises(N.NativeError):
+        N.check("e4b_set_probe", L.e4b_set_probe(7, None, None))
