@@ -178,7 +178,9 @@ int probed(int site, const e4b_routing* r, hipStream_t s, F&& launch) {
 template <class F>
 int run_tile_heights(const SideStream* side, hipStream_t stream, const e4b_routing* rbig, const e4b_routing* rsmall,
                      int site_big, F&& launch) {
-  if (side) {
+  // while a probe is set both heights run on the caller's stream: the probed launch then runs
+  // alone, so its time does not depend on whether the two streams share a hardware queue
+  if (side && g_probe_site.load(std::memory_order_relaxed) == E4B_PROBE_OFF) {
     if (hipEventRecord(side->fork, stream) != hipSuccess || hipStreamWaitEvent(side->s, side->fork, 0) != hipSuccess)
       return check_launch("side stream fork");
     int r = probed(site_big, rbig, stream, launch);

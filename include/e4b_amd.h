@@ -339,8 +339,9 @@ enum e4b_probe_site {
 };
 
 /* Measurement hook for benchmarks and profilers. While a site is set, every e4b_moe_forward /
- * e4b_moe_lora_forward whose routed rows are re-tiled into 256- and 32-row tiles records `before`
- * on the stream of that site's launch right before the launch and `after` right after it, so
+ * e4b_moe_lora_forward whose routed rows are re-tiled into 256- and 32-row tiles runs both tile
+ * heights on the caller's stream (no second stream, so each launch runs alone) and records
+ * `before` on that stream right before the watched launch and `after` right after it, so
  * hipEventElapsedTime(before, after) is the launch's device time once `after` has completed.
  * E4B_PROBE_OFF clears it. One setting per process; the caller keeps both events alive while it
  * is set. Meant for eager calls (records made during a graph capture become graph nodes, whose

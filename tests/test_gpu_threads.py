@@ -135,10 +135,11 @@ def test_capture_in_one_thread_eager_in_another():
 
 
 def test_probe_events_time_each_prefill_launch_without_changing_results():
-    """e4b_set_probe: the library records the caller's event pair around the watched launch on
-    that launch's stream. Each site yields a positive duration shorter than the whole forward,
-    the probed forward's output equals the unprobed one bit for bit, and clearing the probe
-    leaves later forwards unrecorded (the `after` event keeps its last timestamp)."""
+    """e4b_set_probe: while a site is set the forward runs both tile heights on the caller's
+    stream and records the caller's event pair around the watched launch. Each site yields a
+    positive duration shorter than the whole forward, the probed forward's output equals the
+    unprobed (two-stream) one bit for bit, and clearing the probe leaves later forwards
+    unrecorded (the pair keeps its last timestamps)."""
     from experts4bit_qlora_amd import _native as N
 
     L = N.lib()
