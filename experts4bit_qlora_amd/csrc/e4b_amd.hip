@@ -364,6 +364,17 @@ bool is_gated_epi(int epi) {
   return epi == E4B_EPI_SWIGLU || epi == E4B_EPI_CLAMP_SWIGLU || epi == E4B_EPI_GPTOSS;
 }
 
+// The fused forward's token rows in the fp16 matrix-core mode (row_exp_row over x), computed in
+// the routing's first launch by route_impl.
+struct RowExpArgs {
+  const uint16_t* x;  // [tokens, k] bf16
+  int64_t k;
+  int32_t* row_exp;   // [tokens]
+  uint16_t* x16;      // [tokens, k] scaled fp16
+};
+int route_impl(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t num_experts, const e4b_routing* rt,
+               const RowExpArgs* rx, hipStream_t stream);
+
 }  // namespace
 
 extern "C" {
@@ -395,6 +406,17 @@ int e4b_dequant(const e4b_qweight* w, int32_t expert_begin, int32_t expert_count
 
 int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t num_experts, const e4b_routing* rt,
               hipStream_t stream) {
+  return route_impl(top_k_index, tokens, top_k, num_experts, rt, nullptr, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// e4b_route, and with rx the fused forward's token rows (row_exp_row over x [tokens, k]) in the
+// routing's first launch.
+int route_impl(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t num_experts, const e4b_routing* rt,
+               const RowExpArgs* rx, hipStream_t stream) {
   if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "tokens must be >= 0 and top_k > 0");
   const int64_t M = tokens * top_k;
   if (M > 0x7fffffffLL) return fail(E4B_EUNSUPPORTED, "tokens*top_k=%lld exceeds int32", (long long)M);
@@ -406,15 +428,34 @@ int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t
   if (M > 0 && rt->max_tiles < max_tiles_for(M, num_experts, rt->tile_m))
     return fail(E4B_ESPACE, "max_tiles=%d < %lld needed", rt->max_tiles,
                 (long long)max_tiles_for(M, num_experts, rt->tile_m));
+  const int rp = rx ? e4b::row_exp_pieces(rx->k) : 0;
   if (M <= e4b::kRouteSingleMaxRows) {
-    hipLaunchKernelGGL(e4b::route_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, top_k_index, M, num_experts,
-                       *rt);
-    return check_launch("route_kernel");
+    if (!rx) {
+      hipLaunchKernelGGL(e4b::route_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, top_k_index, M, num_experts,
+                         *rt);
+      return check_launch("route_kernel");
+    }
+    const dim3 grid(static_cast<unsigned>(1 + cdiv(tokens, e4b::kRouteWaves)));
+#define E4B_RRX(RP)                                                                                                  \
+  hipLaunchKernelGGL(e4b::route_rowexp_kernel<RP>, grid, dim3(e4b::kRouteThreads), 0, stream, top_k_index, M,        \
+                     num_experts, *rt, rx->x, tokens, rx->k, rx->row_exp, rx->x16)
+    if (rp == 1) E4B_RRX(1); else if (rp == 2) E4B_RRX(2); else if (rp == 4) E4B_RRX(4); else E4B_RRX(8);
+#undef E4B_RRX
+    return check_launch("route_rowexp_kernel");
   }
   if (!rt->scratch) return fail(E4B_EINVAL, "routing scratch is NULL (needed above %d rows)", e4b::kRouteSingleMaxRows);
   const int64_t nchunks = cdiv(M, e4b::kRouteChunk);
-  hipLaunchKernelGGL(e4b::route_count_kernel, dim3(static_cast<unsigned>(nchunks)), dim3(e4b::kRouteChunk), 0, stream,
-                     top_k_index, M, num_experts, rt->scratch);
+  if (!rx) {
+    hipLaunchKernelGGL(e4b::route_count_kernel, dim3(static_cast<unsigned>(nchunks)), dim3(e4b::kRouteChunk), 0,
+                       stream, top_k_index, M, num_experts, rt->scratch);
+  } else {
+    const dim3 grid(static_cast<unsigned>(nchunks + cdiv(tokens, e4b::kChunkWaves)));
+#define E4B_RCX(RP)                                                                                                  \
+  hipLaunchKernelGGL(e4b::route_count_rowexp_kernel<RP>, grid, dim3(e4b::kRouteChunk), 0, stream, top_k_index, M,    \
+                     num_experts, rt->scratch, nchunks, rx->x, tokens, rx->k, rx->row_exp, rx->x16)
+    if (rp == 1) E4B_RCX(1); else if (rp == 2) E4B_RCX(2); else if (rp == 4) E4B_RCX(4); else E4B_RCX(8);
+#undef E4B_RCX
+  }
   hipLaunchKernelGGL(e4b::route_colscan_kernel, dim3(static_cast<unsigned>(num_experts + 1)),
                      dim3(e4b::kRouteThreads), 0, stream, nchunks, num_experts, rt->scratch, rt->offsets);
   hipLaunchKernelGGL(e4b::route_tables_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, num_experts, *rt);
@@ -422,6 +463,10 @@ int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t
                      top_k_index, M, num_experts, rt->scratch, *rt);
   return check_launch("route_count/colscan/tables/place kernels");
 }
+
+}  // namespace
+
+extern "C" {
 
 int e4b_route_groups(const int64_t* sizes, int32_t groups, const int64_t* expert_ids, int32_t num_experts,
                      const e4b_routing* rt, hipStream_t stream) {
@@ -1011,13 +1056,10 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
   // the gate_up GEMM reads the tokens as scaled fp16 rows in fp16 mode
   const void* up_a = f16c ? static_cast<const void*>(x16) : hidden;
 
-  rc = e4b_route(top_k_index, tokens, top_k, E, &rt, stream);
+  // fp16 mode: the token row exponents and scaled fp16 rows ride in the routing's first launch
+  const RowExpArgs rx{static_cast<const uint16_t*>(hidden), w1->k, xexp, x16};
+  rc = route_impl(top_k_index, tokens, top_k, E, &rt, f16c ? &rx : nullptr, stream);
   if (rc) return rc;
-  if (f16c) {  // token row exponents and scaled fp16 rows
-    e4b::launch_row_exp(static_cast<const uint16_t*>(hidden), tokens, w1->k, xexp, x16, nullptr, 0, stream);
-    rc = check_launch("row_exp_kernel");
-    if (rc) return rc;
-  }
   // fp16 mode: h row exponents, and h rewritten in place as scaled fp16 rows for the down GEMM
   auto h_to_f16 = [&]() {
     if (!f16c) return 0;
@@ -1312,10 +1354,8 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
     float* t;
     carve_lora_fused(p, tokens, M, E, h_cols, w1->k, w2->n, r, &rt, &rbig, &rsmall, &split, &xexp, &hexp, &x16, &h,
                      &down, &t);
-    rc = e4b_route(top_k_index, tokens, top_k, E, &rt, stream);
-    if (rc) return rc;
-    e4b::launch_row_exp(static_cast<const uint16_t*>(hidden), tokens, w1->k, xexp, x16, nullptr, 0, stream);
-    rc = check_launch("row_exp_kernel");
+    const RowExpArgs rx{static_cast<const uint16_t*>(hidden), w1->k, xexp, x16};
+    rc = route_impl(top_k_index, tokens, top_k, E, &rt, &rx, stream);
     if (rc) return rc;
     if (split) {
       hipLaunchKernelGGL(e4b::split_tiles_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, rt.offsets, rt.meta,

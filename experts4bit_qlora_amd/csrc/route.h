@@ -27,6 +27,7 @@
 #pragma once
 
 #include "common.h"
+#include "scale.h"
 
 namespace e4b {
 
@@ -132,8 +133,8 @@ E4B_DEV void emit_expert_tables(int ta, int tb, int E, int dropped, const e4b_ro
   }
 }
 
-__global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __restrict__ idx, int64_t M,
-                                                              int E, e4b_routing rt) {
+// The whole permutation in one kRouteThreads-thread workgroup (M <= kRouteSingleMaxRows).
+E4B_DEV void route_single(const int64_t* __restrict__ idx, int64_t M, int E, const e4b_routing& rt) {
   __shared__ int cnt[kRouteWaves * kRouteMaxExperts];
   __shared__ int wsum[kRouteWaves];
   __shared__ int dropped;
@@ -218,6 +219,27 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __r
   }
 }
 
+__global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __restrict__ idx, int64_t M,
+                                                              int E, e4b_routing rt) {
+  route_single(idx, M, E, rt);
+}
+
+// route_kernel and, in the same launch, row_exp_row over the T rows of x: block 0 routes, block
+// b > 0 takes rows kRouteWaves (b - 1) .. + kRouteWaves - 1, one wave each. The fused forward's
+// token rows (exponents and scaled fp16 copies) then cost no launch of their own.
+template <int RP>
+__global__ void __launch_bounds__(kRouteThreads) route_rowexp_kernel(const int64_t* __restrict__ idx, int64_t M,
+                                                                     int E, e4b_routing rt, const uint16_t* x,
+                                                                     int64_t T, int64_t k, int32_t* row_exp,
+                                                                     uint16_t* x16) {
+  if (blockIdx.x == 0) {
+    route_single(idx, M, E, rt);
+    return;
+  }
+  const int64_t row = int64_t(blockIdx.x - 1) * kRouteWaves + threadIdx.x / kWave;
+  if (row < T) row_exp_row<RP>(x, row, k, row_exp, x16);
+}
+
 // ---- chunked route (M > kRouteSingleMaxRows); counts is [nchunks, E + 1] int32, column E the
 // chunk's dropped ids. A chunk of kRouteChunk ids is one workgroup of 4 waves, 64 ids each.
 
@@ -243,18 +265,19 @@ E4B_DEV int wave_histogram(int e, bool drop, int* c, int E) {
   return __popcll(__ballot(drop));
 }
 
-__global__ void __launch_bounds__(kRouteChunk) route_count_kernel(const int64_t* __restrict__ idx, int64_t M, int E,
-                                                                  int32_t* __restrict__ counts) {
+// The counts of chunk `chunk` (one kRouteChunk-thread workgroup).
+E4B_DEV void route_count_chunk(const int64_t* __restrict__ idx, int64_t M, int E, int32_t* __restrict__ counts,
+                               int64_t chunk) {
   __shared__ int c[kChunkWaves][kRouteMaxExperts];
   __shared__ int nd[kChunkWaves];
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
   bool drop;
-  const int e = chunk_id(idx, int64_t(blockIdx.x) * kRouteChunk + threadIdx.x, M, E, drop);
+  const int e = chunk_id(idx, chunk * kRouteChunk + threadIdx.x, M, E, drop);
   const int d = wave_histogram(e, drop, c[wid], E);
   if (lane == 0) nd[wid] = d;
   __syncthreads();
-  int32_t* row = counts + int64_t(blockIdx.x) * (E + 1);
+  int32_t* row = counts + chunk * (E + 1);
   for (int x = threadIdx.x; x < E; x += kRouteChunk) {
     int t = 0;
 #pragma unroll
@@ -267,6 +290,26 @@ __global__ void __launch_bounds__(kRouteChunk) route_count_kernel(const int64_t*
     for (int w = 0; w < kChunkWaves; ++w) t += nd[w];
     row[E] = t;
   }
+}
+
+__global__ void __launch_bounds__(kRouteChunk) route_count_kernel(const int64_t* __restrict__ idx, int64_t M, int E,
+                                                                  int32_t* __restrict__ counts) {
+  route_count_chunk(idx, M, E, counts, blockIdx.x);
+}
+
+// route_count_kernel's nchunks blocks and, after them, row_exp_row over the T rows of x
+// (kChunkWaves rows per block, one wave each) in one launch.
+template <int RP>
+__global__ void __launch_bounds__(kRouteChunk) route_count_rowexp_kernel(const int64_t* __restrict__ idx, int64_t M,
+                                                                         int E, int32_t* __restrict__ counts,
+                                                                         int64_t nchunks, const uint16_t* x, int64_t T,
+                                                                         int64_t k, int32_t* row_exp, uint16_t* x16) {
+  if (blockIdx.x < nchunks) {
+    route_count_chunk(idx, M, E, counts, blockIdx.x);
+    return;
+  }
+  const int64_t row = (int64_t(blockIdx.x) - nchunks) * kChunkWaves + threadIdx.x / kWave;
+  if (row < T) row_exp_row<RP>(x, row, k, row_exp, x16);
 }
 
 // Column scan, one workgroup per column x of the [nchunks, E + 1] count matrix (x < E: expert x,

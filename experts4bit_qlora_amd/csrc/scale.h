@@ -23,24 +23,17 @@ E4B_DEV uint32_t wave_max_u32(uint32_t v) {
   return v;
 }
 
-// row_exp[r] = the largest biased exponent over row r of x [rows, k] (bf16, k % 8 == 0), and
-// x16[r] = fp16(x[r] * 2^exp_shift(row_exp[r])) (exact; see bf16x2_to_f16x2), a GEMM operand
-// staged once instead of once per output tile; zero[0 .. nzero) = 0 (grid-stride: the grid has
-// rows / 4 blocks of 256 threads). One wave per row; a row's pieces stay in registers between
-// the two passes when k <= 64 * 8 * RP. x16 may be x (in place): a wave reads every piece of its
-// row for the maximum before it writes any, and writes each piece after reading it. RP (16-byte
-// pieces per lane held across the passes) follows the row length (row_exp_pieces): a fixed 8 made
-// a 768-value h row issue 8 loads per lane for its 96 pieces, 5 in 6 of them clamped re-reads.
+// One wave, row `row` of x [rows, k] (bf16, k % 8 == 0): row_exp[row] = the row's largest biased
+// exponent, and x16[row] = fp16(x[row] * 2^exp_shift(row_exp[row])) (exact; see
+// bf16x2_to_f16x2), a GEMM operand staged once instead of once per output tile. The row's pieces
+// stay in registers between the two passes when k <= 64 * 8 * RP. x16 may be x (in place): the
+// wave reads every piece of its row for the maximum before it writes any, and writes each piece
+// after reading it. RP (16-byte pieces per lane held across the passes) follows the row length
+// (row_exp_pieces): a fixed 8 made a 768-value h row issue 8 loads per lane for its 96 pieces, 5
+// in 6 of them clamped re-reads. No barrier: a kernel may hand any wave any row.
 template <int RP>
-__global__ void __launch_bounds__(kScaleThreads) row_exp_kernel(const uint16_t* x, int64_t rows,
-                                                                int64_t k, int32_t* __restrict__ row_exp,
-                                                                uint16_t* x16,
-                                                                int32_t* __restrict__ zero, int64_t nzero) {
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nzero; i += int64_t(gridDim.x) * blockDim.x)
-    zero[i] = 0;
+E4B_DEV void row_exp_row(const uint16_t* x, int64_t row, int64_t k, int32_t* __restrict__ row_exp, uint16_t* x16) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = int64_t(blockIdx.x) * (kScaleThreads / kWave) + threadIdx.x / kWave;
-  if (row >= rows) return;  // whole waves; no barrier follows
   const uint4* xr = reinterpret_cast<const uint4*>(x + row * k);
   uint4* yr = reinterpret_cast<uint4*>(x16 + row * k);
   const int64_t pieces = k / 8;
@@ -66,6 +59,20 @@ __global__ void __launch_bounds__(kScaleThreads) row_exp_kernel(const uint16_t* 
     if (i < pieces) yr[i] = conv(v[j]);
   }
   for (int64_t i = lane + int64_t(RP) * kWave; i < pieces; i += kWave) yr[i] = conv(xr[i]);
+}
+
+// row_exp_row over every row, one wave per row (rows / 4 blocks of 256 threads), and zero[0 ..
+// nzero) = 0 (grid-stride).
+template <int RP>
+__global__ void __launch_bounds__(kScaleThreads) row_exp_kernel(const uint16_t* x, int64_t rows,
+                                                                int64_t k, int32_t* __restrict__ row_exp,
+                                                                uint16_t* x16,
+                                                                int32_t* __restrict__ zero, int64_t nzero) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nzero; i += int64_t(gridDim.x) * blockDim.x)
+    zero[i] = 0;
+  const int64_t row = int64_t(blockIdx.x) * (kScaleThreads / kWave) + threadIdx.x / kWave;
+  if (row >= rows) return;  // whole waves; no barrier follows
+  row_exp_row<RP>(x, row, k, row_exp, x16);
 }
 
 // Pieces per lane for a row of k values: enough to hold the row (k <= 4096), rounded up to 1, 2,
