@@ -153,14 +153,28 @@ E4B_DEV void route_single(const int64_t* __restrict__ idx, int64_t M, int E, con
   const int64_t seg1 = min(M, (wid + 1) * chunks_per_wave * kWave);
   int* mycnt = cnt + wid * E;
 
-  // 1. per-wave histogram
-  for (int64_t i = seg0 + lane; i < seg1; i += kWave) {
-    const int64_t v = idx[i];
-    if (v >= 0 && v < E) {
-      atomicAdd(&mycnt[v], 1);
-    } else {
-      atomicAdd(&dropped, 1);
+  // The wave's ids, loaded once with every load in flight (the histogram and the placement each
+  // walked them with one dependent load per 64-id chunk): chunk j of the wave holds ids seg0 +
+  // 64 j + lane, kept as experts (-1: past the segment, -2: dropped).
+  constexpr int kPer = kRouteSingleMaxRows / kRouteThreads;  // chunks per wave at most
+  static_assert(kPer * kRouteThreads == kRouteSingleMaxRows, "whole chunks per wave");
+  int ev[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) ev[j] = -1;
+  if (seg1 > seg0) {  // uniform; no load at all when the wave has no ids (M may be 0, idx NULL)
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int64_t i = seg0 + int64_t(j) * kWave + lane;
+      const int64_t v = idx[i < seg1 ? i : seg1 - 1];
+      ev[j] = i >= seg1 ? -1 : (v >= 0 && v < E) ? static_cast<int>(v) : -2;
     }
+  }
+
+  // 1. per-wave histogram
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    if (ev[j] >= 0) atomicAdd(&mycnt[ev[j]], 1);
+    else if (ev[j] == -2) atomicAdd(&dropped, 1);
   }
   __syncthreads();
 
@@ -196,17 +210,13 @@ E4B_DEV void route_single(const int64_t* __restrict__ idx, int64_t M, int E, con
   // is its expert's cursor plus its rank among the chunk's equal ids; then each id bumps its
   // expert's cursor (the wave's cursor reads precede its adds in LDS order).
   int* rs = rank_s[wid];
-  for (int64_t base = seg0; base < seg1; base += kWave) {
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int64_t base = seg0 + int64_t(j) * kWave;
+    if (base >= seg1) break;  // uniform over the wave
     const int64_t i = base + lane;
-    int e = -1;
-    if (i < seg1) {
-      const int64_t v = idx[i];
-      if (v >= 0 && v < E) {
-        e = static_cast<int>(v);
-      } else {
-        rt.inv[i] = -1;
-      }
-    }
+    const int e = ev[j] >= 0 ? ev[j] : -1;
+    if (ev[j] == -2) rt.inv[i] = -1;
     const int rank = wave_rank(e, rs);
     if (e >= 0) {
       const int pos = mycnt[e] + rank;
