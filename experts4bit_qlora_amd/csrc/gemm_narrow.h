@@ -60,7 +60,6 @@ __global__ void __launch_bounds__(kNarrowThreads) __attribute__((amdgpu_waves_pe
 gemm_narrow_kernel(GemmArgs p) {
   static_assert(FMT == E4B_FMT_NF4 || FMT == E4B_FMT_NF4_DQ, "narrow tiles: NF4 weights in fp16 mode");
   constexpr int BM = kTileMSmall, BN = kNarrowN, KS = kNarrowK, ST = kNarrowStages;
-  constexpr int MS = BM / 16;                   // 2 row sub-tiles
   constexpr int NS = BN / (kNarrowThreads / kWave) / 16;  // 4 weight sub-tiles per wave
   static_assert(kNarrowUnroll % ST == 0 && kNarrowUnroll % 6 == 0, "unroll: whole weight sets and scale sets");
   __shared__ __attribute__((aligned(16))) uint32_t ptab[256 * kNarrowCopies];
@@ -139,6 +138,16 @@ gemm_narrow_kernel(GemmArgs p) {
   const int64_t src = (r < row_end) ? src_any : 0;
   const uint16_t* aptr = p.a + src * k + 64 * (ac >> 1) + 16 * (ac & 1);
 
+  // The tile's rows as MS 16-row MFMA sub-tiles: one when the tile holds at most 16 rows (a
+  // mid-size batch's experts and most prefill tails hold a few rows each), halving the MFMAs and
+  // fragment reads per step. Everything from the first activation and weight loads on is
+  // instantiated for both (the branch comes before those loads, so no register of one
+  // instantiation is live in the other).
+  auto run_tile = [&](auto MSC) {
+  constexpr int MS = decltype(MSC)::value;
+  // a statement that differs between the instantiations, so the compiler does not hoist their
+  // identical first loads above the branch (which made their registers live in both)
+  asm volatile("; %0 row sub-tiles" ::"n"(MS));
   constexpr int PS = 3;  // scale sets: pairs in use or in flight
   u32x4_t areg[2][2];
   uint4 wq[ST][NS];
@@ -388,6 +397,10 @@ gemm_narrow_kernel(GemmArgs p) {
         store_elem<E4B_BF16>(p, int64_t(rr) * p.n_out + nn, single(p.epi, acc[ms][ns][i], b));
       }
     }
+  };
+  // (the row count is the same in every lane; readfirstlane makes the branch a scalar one)
+  if (__builtin_amdgcn_readfirstlane(row_end - row0) <= 16) run_tile(std::integral_constant<int, 1>{});
+  else run_tile(std::integral_constant<int, 2>{});
 }
 
 }  // namespace e4b
