@@ -295,31 +295,34 @@ int launch_gemm_dt(const e4b::GemmArgs& a, bool gemv, int64_t max_active, hipStr
   return check_launch(gemv ? "gemv_kernel" : "gemm_mfma_kernel");
 }
 
-template <int DDT, int WDT>
+template <int DDT, int WDT, bool SC>
 void launch_combine_w(const void* down, const int32_t* inv, const void* w, int64_t T, int k, int64_t H,
-                      void* out, int od, hipStream_t s) {
+                      void* out, int od, const e4b::CombineScale& cs, hipStream_t s) {
   const int64_t work = T * ((H % 8) == 0 ? H / 8 : H);
   const int grid = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(cdiv(work, 256), 16384)));
   switch (od) {
     case E4B_FP32:
-      hipLaunchKernelGGL((e4b::combine_kernel<DDT, WDT, E4B_FP32>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
+      hipLaunchKernelGGL((e4b::combine_kernel<DDT, WDT, E4B_FP32, SC>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k,
+                         H, out, cs);
       break;
     case E4B_BF16:
-      hipLaunchKernelGGL((e4b::combine_kernel<DDT, WDT, E4B_BF16>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
+      hipLaunchKernelGGL((e4b::combine_kernel<DDT, WDT, E4B_BF16, SC>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k,
+                         H, out, cs);
       break;
     default:
-      hipLaunchKernelGGL((e4b::combine_kernel<DDT, WDT, E4B_FP16>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k, H, out);
+      hipLaunchKernelGGL((e4b::combine_kernel<DDT, WDT, E4B_FP16, SC>), dim3(grid), dim3(256), 0, s, down, inv, w, T, k,
+                         H, out, cs);
       break;
   }
 }
 
-template <int DDT>
+template <int DDT, bool SC = false>
 void launch_combine_dt(const void* down, const int32_t* inv, const void* w, int wd, int64_t T, int k, int64_t H,
-                       void* out, int od, hipStream_t s) {
+                       void* out, int od, hipStream_t s, const e4b::CombineScale& cs = {}) {
   switch (wd) {
-    case E4B_FP32: launch_combine_w<DDT, E4B_FP32>(down, inv, w, T, k, H, out, od, s); break;
-    case E4B_BF16: launch_combine_w<DDT, E4B_BF16>(down, inv, w, T, k, H, out, od, s); break;
-    default: launch_combine_w<DDT, E4B_FP16>(down, inv, w, T, k, H, out, od, s); break;
+    case E4B_FP32: launch_combine_w<DDT, E4B_FP32, SC>(down, inv, w, T, k, H, out, od, cs, s); break;
+    case E4B_BF16: launch_combine_w<DDT, E4B_BF16, SC>(down, inv, w, T, k, H, out, od, cs, s); break;
+    default: launch_combine_w<DDT, E4B_FP16, SC>(down, inv, w, T, k, H, out, od, cs, s); break;
   }
 }
 
@@ -531,7 +534,7 @@ struct LoraEpi {
 static int grouped_gemm_impl(const void* a, int32_t act_dtype, int32_t gather_k, const e4b_qweight* w,
                              const e4b_routing* rt, int64_t tokens, int64_t M, int32_t epilogue, float alpha,
                              float limit, int32_t flags, void* out, int32_t out_dtype, const int32_t* a_exp,
-                             hipStream_t stream, const LoraEpi* lora = nullptr) {
+                             hipStream_t stream, const LoraEpi* lora = nullptr, int out_f16_shift = 0) {
   int rc = check_weight(w);
   if (rc) return rc;
   rc = check_routing(rt, M);
@@ -573,6 +576,11 @@ static int grouped_gemm_impl(const void* a, int32_t act_dtype, int32_t gather_k,
   if (f16c && (gemv || act_dtype != E4B_BF16 || w->format == E4B_FMT_MXFP4 || !w->shift))
     return fail(E4B_EINVAL, "the fp16 matrix-core mode needs the MFMA path, bf16 activations and NF4 weight shifts");
   args.a_exp = a_exp;
+  if (out_f16_shift && (!f16c || out_dtype != E4B_FP32 || epilogue != E4B_EPI_NONE || w->bias || lora ||
+                        !e4b::lora_gemm_fits(rt->tile_m, w->k)))
+    return fail(E4B_EINVAL, "fp16 down rows need the fp16 mode over 256-row tiles or 32-row tiles with k %% 256 == "
+                            "0, fp32 rows, and no epilogue, bias or LoRA");
+  args.out_f16_shift = out_f16_shift;
   args.lt = nullptr;
   args.lb = nullptr;
   args.lbdt = E4B_FP32;
@@ -1053,6 +1061,18 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
   uint16_t* x16 = reinterpret_cast<uint16_t*>(take(sizeof(uint16_t) * tokens * w1->k));
   const int32_t* up_exp = f16c ? xexp : nullptr;
   int32_t* h_exp = f16c ? hexp : nullptr;
+  // fp16 mode at prefill sizes (down k a multiple of 256: the wide and narrow kernels): the down
+  // rows leave the GEMM as fp16 with the operand scales left on, times 2^-c. Both operands stay
+  // within 2^15 in magnitude, so |sum| <= k 2^30 and c = 16 + ceil(log2 k) keeps every value
+  // within 2^14 (fp16's range), with fp16's 11 significant bits down to 2^-14: half the bytes of
+  // fp32 rows, written once and read once by the combine. (Mid-size batches keep fp32 rows: their
+  // rows are few, and the combine's scale lookups cost more than the bytes saved.)
+  int f16_shift = 0;
+  if (f16c && split && e4b::lora_gemm_fits(e4b::kTileMSmall, w2->k)) {
+    int lg = 0;
+    while ((int64_t(1) << lg) < w2->k) ++lg;
+    f16_shift = 16 + lg;
+  }
   // the gate_up GEMM reads the tokens as scaled fp16 rows in fp16 mode
   const void* up_a = f16c ? static_cast<const void*>(x16) : hidden;
 
@@ -1087,7 +1107,7 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
     if (rc) return rc;
     rc = both(E4B_PROBE_DOWN_BIG, [&](const e4b_routing* r, hipStream_t s) {
       return grouped_gemm_impl(h, act_dtype, 0, w2, r, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
-                               h_exp, s);
+                               h_exp, s, nullptr, f16_shift);
     });
     if (rc) return rc;
   } else {
@@ -1097,8 +1117,14 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
     rc = h_to_f16();
     if (rc) return rc;
     rc = grouped_gemm_impl(h, act_dtype, 0, w2, &rt, tokens, M, E4B_EPI_NONE, alpha, limit, flags, down, E4B_FP32,
-                           h_exp, stream);
+                           h_exp, stream, nullptr, f16_shift);
     if (rc) return rc;
+  }
+  if (f16_shift) {
+    const e4b::CombineScale cs{hexp, top_k_index, w2->shift, f16_shift};
+    launch_combine_dt<E4B_FP16, true>(down, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
+                                      stream, cs);
+    return check_launch("combine_kernel");
   }
   return e4b_combine(down, E4B_FP32, rt.inv, top_k_weights, weight_dtype, tokens, top_k, w2->n, out, out_dtype,
                      stream);

@@ -24,7 +24,12 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // 128 x 64; otherwise four of 128 x 128), the others gemm_mfma_kernel.
 template <int DT, int FMT, int BM, bool F16C>
 void launch_mfma_kernel(const GemmArgs& a, dim3 grid, hipStream_t s) {
-  if constexpr (BM == kTileMBig && (F16C || (DT == E4B_BF16 && FMT == E4B_FMT_MXFP4))) {
+  if constexpr (BM == kTileMBig && F16C) {
+    if (a.out_f16_shift)  // fp16 down rows (the host asks only for them here and in the narrow kernel)
+      hipLaunchKernelGGL((gemm_wide8_kernel<DT, FMT, true, false, true>), grid, dim3(kWide8Threads), 0, s, a);
+    else
+      hipLaunchKernelGGL((gemm_wide8_kernel<DT, FMT, true>), grid, dim3(kWide8Threads), 0, s, a);
+  } else if constexpr (BM == kTileMBig && DT == E4B_BF16 && FMT == E4B_FMT_MXFP4) {
     hipLaunchKernelGGL((gemm_wide8_kernel<DT, FMT, F16C>), grid, dim3(kWide8Threads), 0, s, a);
   } else if constexpr (BM == kTileMBig) {
     hipLaunchKernelGGL((gemm_wide_kernel<DT, FMT, F16C>), grid, dim3(kWideThreads), 0, s, a);
@@ -70,7 +75,11 @@ void launch_mfma_gemm(const GemmArgs& a, hipStream_t s) {
     }
     // 32-row tiles in the fp16 mode: the narrow kernel, when K is a whole number of its steps
     if (a.rt.tile_m == kTileMSmall && a.a_exp && narrow_fits(a.w.k)) {
-      hipLaunchKernelGGL((gemm_narrow_kernel<FMT>), gemm_grid(a, kNarrowN), dim3(kNarrowThreads), 0, s, a);
+      if (a.out_f16_shift)
+        hipLaunchKernelGGL((gemm_narrow_kernel<FMT, false, true>), gemm_grid(a, kNarrowN), dim3(kNarrowThreads), 0, s,
+                           a);
+      else
+        hipLaunchKernelGGL((gemm_narrow_kernel<FMT>), gemm_grid(a, kNarrowN), dim3(kNarrowThreads), 0, s, a);
       return;
     }
   }

@@ -16,8 +16,9 @@ struct GemmArgs;
 template <int DT, int FMT>
 void launch_mfma_gemm(const GemmArgs& a, hipStream_t s);
 
-// Whether a grouped GEMM with a LoRA epilogue (GemmArgs::lt) can run: fp16 mode over 256-row
-// tiles, or over 32-row tiles with K a whole number of the narrow kernel's step pairs.
+// Whether a grouped GEMM with a LoRA epilogue (GemmArgs::lt) or fp16 down rows
+// (GemmArgs::out_f16_shift) can run: fp16 mode over 256-row tiles (the eight-wave wide kernel), or
+// over 32-row tiles with K a whole number of the narrow kernel's step pairs.
 inline bool lora_gemm_fits(int tile_m, int64_t k) {
   return tile_m == 256 || (tile_m == 32 && k > 0 && k % 256 == 0 && k <= 256 * 64);
 }

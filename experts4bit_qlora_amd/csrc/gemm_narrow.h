@@ -55,10 +55,12 @@ constexpr bool narrow_fits(int64_t k) { return k > 0 && k % (2 * kNarrowK) == 0 
 
 // LORA: the accumulators start as the tile's LoRA delta (p.lt, p.lb), scaled like the products
 // (lora_mfma.h).
-template <int FMT, bool LORA = false>
+// H16: the down rows as fp16 with the operand scales left on (GemmArgs::out_f16_shift).
+template <int FMT, bool LORA = false, bool H16 = false>
 __global__ void __launch_bounds__(kNarrowThreads) __attribute__((amdgpu_waves_per_eu(2)))
 gemm_narrow_kernel(GemmArgs p) {
   static_assert(FMT == E4B_FMT_NF4 || FMT == E4B_FMT_NF4_DQ, "narrow tiles: NF4 weights in fp16 mode");
+  static_assert(!(H16 && LORA), "fp16 down rows without LoRA");
   constexpr int BM = kTileMSmall, BN = kNarrowN, KS = kNarrowK, ST = kNarrowStages;
   constexpr int NS = BN / (kNarrowThreads / kWave) / 16;  // 4 weight sub-tiles per wave
   static_assert(kNarrowUnroll % ST == 0 && kNarrowUnroll % 6 == 0, "unroll: whole weight sets and scale sets");
@@ -326,13 +328,13 @@ gemm_narrow_kernel(GemmArgs p) {
   for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int d = -(row_shift_s[ms * 16 + 4 * g + i] + wsh);
+      const int d = H16 ? -p.out_f16_shift : -(row_shift_s[ms * 16 + 4 * g + i] + wsh);
 #pragma unroll
       for (int ns = 0; ns < NS; ++ns) acc[ms][ns][i] = __builtin_amdgcn_ldexpf(acc[ms][ns][i], d);
     }
   const bool has_bias = p.w.bias != nullptr;
   const uint16_t* bias = static_cast<const uint16_t*>(p.w.bias);
-  if (pair) {
+  if (!H16 && pair) {
     const int64_t cbase = col0 + wid * 32 + l16;
     if (p.epi == E4B_EPI_SWIGLU && !has_bias && !p.out_f32) {  // gate_up: silu(g) * u -> bf16
       uint16_t* const out = static_cast<uint16_t*>(p.out);
@@ -369,6 +371,20 @@ gemm_narrow_kernel(GemmArgs p) {
     return;
   }
   const int64_t cbase = col0 + wid * 64 + l16;
+  if constexpr (H16) {  // down: fp16 rows, the operand scales left on (the host checks the form)
+    uint16_t* const out = static_cast<uint16_t*>(p.out);
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = row0 + ms * 16 + 4 * g + i;
+        uint16_t* const orow = out + int64_t(rr) * p.n_out + cbase;
+#pragma unroll
+        for (int ns = 0; ns < NS; ++ns)
+          if (rr < row_end && cbase + ns * 16 < p.n_out) orow[ns * 16] = from_f<E4B_FP16>(acc[ms][ns][i]);
+      }
+    return;
+  }
   if (p.epi == E4B_EPI_NONE && !has_bias && p.out_f32) {  // down: fp32 rows
     float* const out = static_cast<float*>(p.out);
 #pragma unroll

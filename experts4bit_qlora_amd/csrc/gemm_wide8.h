@@ -33,7 +33,7 @@ namespace e4b {
 constexpr int kWide8Threads = 512;
 
 // One tile. HALF: a tile of at most 128 rows as 128 rows x 256 weight rows (waves of 64 x 64).
-template <int DT, int FMT, bool F16C, bool HALF, bool LORA>
+template <int DT, int FMT, bool F16C, bool HALF, bool LORA, bool H16>
 E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2][kWideTileM * kTileK],
                         uint16_t (&Ws)[2][kWideTileN * kTileK], const float* code2_s, int* row_shift_s,
                         const uint32_t* ptab) {
@@ -243,7 +243,7 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
   if constexpr (F16C) {
     static_for<MS>([&](auto ms) {
       static_for<16>([&](auto i) {
-        const int d = -(row_shift_s[row_of(ms, i)] + wsh);
+        const int d = H16 ? -p.out_f16_shift : -(row_shift_s[row_of(ms, i)] + wsh);
         static_for<NS>([&](auto ns) { acc[ms][ns][int(i)] = __builtin_amdgcn_ldexpf(acc[ms][ns][int(i)], d); });
       });
     });
@@ -262,6 +262,20 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
         });
       });
     }
+    return;
+  }
+  if constexpr (H16) {  // down: fp16 rows, the operand scales left on (the host checks the form)
+    uint16_t* const out = static_cast<uint16_t*>(p.out);
+    const int64_t cbase = col0 + 64 * wave_n + (lane_e & 31);
+    static_for<MS>([&](auto ms) {
+      static_for<16>([&](auto i) {
+        const int rr = row0 + row_of(ms, i);
+        uint16_t* const orow = out + int64_t(rr) * p.n_out + cbase;
+        static_for<NS>([&](auto ns) {
+          if (rr < row_end && cbase + ns * 32 < p.n_out) orow[ns * 32] = from_f<E4B_FP16>(acc[ms][ns][int(i)]);
+        });
+      });
+    });
     return;
   }
   if (!pair && p.epi == E4B_EPI_NONE && !has_bias && p.out_f32) {  // down: fp32 rows
@@ -305,11 +319,13 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
   });
 }
 
-template <int DT, int FMT, bool F16C, bool LORA = false>
+// H16: the down rows as fp16 with the operand scales left on (GemmArgs::out_f16_shift).
+template <int DT, int FMT, bool F16C, bool LORA = false, bool H16 = false>
 __global__ void __launch_bounds__(kWide8Threads) gemm_wide8_kernel(GemmArgs p) {
   static_assert(F16C ? (DT == E4B_BF16 && FMT != E4B_FMT_MXFP4) : (DT == E4B_BF16 && FMT == E4B_FMT_MXFP4),
                 "fp16 mode with NF4 weights, or bf16 activations with MXFP4 weights");
   static_assert(!LORA || F16C, "the LoRA epilogue runs in the fp16 mode");
+  static_assert(!H16 || (F16C && !LORA), "fp16 down rows: the fp16 mode without LoRA");
   constexpr int BM = kWideTileM, BN = kWideTileN;
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * kTileK];
   __shared__ __attribute__((aligned(16))) uint16_t Ws[2][BN * kTileK];
@@ -333,8 +349,8 @@ __global__ void __launch_bounds__(kWide8Threads) gemm_wide8_kernel(GemmArgs p) {
     }
   }
   const int rows = p.rt.offsets[item.e + 1] - item.row0;  // the tile's rows, capped at BM below
-  if (rows <= BM / 2) wide8_tile<DT, FMT, F16C, true, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
-  else wide8_tile<DT, FMT, F16C, false, LORA>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
+  if (rows <= BM / 2) wide8_tile<DT, FMT, F16C, true, LORA, H16>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
+  else wide8_tile<DT, FMT, F16C, false, LORA, H16>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
 }
 
 }  // namespace e4b

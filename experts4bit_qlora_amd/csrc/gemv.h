@@ -34,6 +34,10 @@ struct GemmArgs {
   // indexed like the A rows themselves (token when gather_k > 0, else sorted row); NULL selects
   // the bf16 mode.
   const int32_t* a_exp;
+  // fp16 mode, down rows (epi NONE, no bias, out_f32 set): > 0 stores each row as fp16 of the
+  // scaled accumulator times 2^-out_f16_shift (the operand scales left on) instead of fp32 rows;
+  // the combine takes the scales off (combine_kernel's SC form)
+  int out_f16_shift;
   // LoRA delta in the epilogue (the LORA instances of the fp16-mode wide and narrow kernels):
   // output column j of sorted row m gains lscale * sum_q lt[m, q] * lb[e, w_row(j), q] before the
   // epilogue, lt the fp32 t = x . A^T rows [M, lr] of the routed rows, lb B [E, w.n, lr] in lbdt.

@@ -542,11 +542,23 @@ E4B_DEV float load_down(const void* d, int64_t i) {
   }
 }
 
-template <int DDT, int WDT, int ODT>
+// fp16 down rows with their operand scales left on (GemmArgs::out_f16_shift): the sorted row r
+// of slot (t, s) holds its values times 2^(exp_shift(rexp[r]) + wshift[e] - shift), e =
+// idx[t k + s]; the combine folds the inverse power of two into the slot's router weight (exact:
+// (v 2^d) w and v (w 2^d) round alike while w 2^d stays a normal fp32).
+struct CombineScale {
+  const int32_t* rexp;    // h row exponents by sorted row (row_exp_kernel)
+  const int64_t* idx;     // top_k_index [T, k]
+  const int32_t* wshift;  // the down weights' expert shifts
+  int shift;
+};
+
+template <int DDT, int WDT, int ODT, bool SC = false>
 __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ down,
                                                       const int32_t* __restrict__ inv,
                                                       const void* __restrict__ wts, int64_t T, int k,
-                                                      int64_t H, void* __restrict__ out) {
+                                                      int64_t H, void* __restrict__ out, CombineScale cs) {
+  static_assert(!SC || DDT == E4B_FP16, "scaled down rows are fp16");
   const bool vec = (H % 8) == 0;
   const int64_t per_tok = vec ? H / 8 : H;
   const int64_t total = T * per_tok;
@@ -565,16 +577,24 @@ __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ d
         int rr[kS];
         bool ok[kS];
         float w[kS], dv[kS][8];
+        int64_t ei[kS];        // SC: the slot's expert
+        int rx[kS], wx[kS];    // SC: its row exponent and expert shift
 #pragma unroll
         for (int u = 0; u < kS; ++u) {
           const int s = s0 + u < k ? s0 + u : k - 1;
           rr[u] = inv[t * k + s];
           w[u] = load_weight<WDT>(wts, t * k + s);
+          if constexpr (SC) ei[u] = cs.idx[t * k + s];
           ok[u] = s0 + u < k && rr[u] >= 0;
         }
+        // the scale loads go out beside the row loads; they are used only in the sum
 #pragma unroll
         for (int u = 0; u < kS; ++u) {
           const int64_t r = rr[u] >= 0 ? rr[u] : 0;
+          if constexpr (SC) {
+            rx[u] = cs.rexp[r];
+            wx[u] = cs.wshift[ok[u] ? ei[u] : 0];
+          }
           if constexpr (DDT == E4B_FP32) {
             const float4* dp = reinterpret_cast<const float4*>(static_cast<const float*>(down) + r * H + 8 * c);
             const float4 d0 = dp[0], d1 = dp[1];
@@ -592,6 +612,7 @@ __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ d
         }
 #pragma unroll
         for (int u = 0; u < kS; ++u) {
+          if constexpr (SC) w[u] = __builtin_amdgcn_ldexpf(w[u], cs.shift - exp_shift(rx[u]) - wx[u]);
 #pragma unroll
           for (int j = 0; j < 8; ++j) acc[j] = ok[u] ? __fadd_rn(acc[j], mul_f32(dv[u][j], w[u])) : acc[j];
         }
@@ -603,7 +624,8 @@ __global__ void __launch_bounds__(256) combine_kernel(const void* __restrict__ d
       for (int s = 0; s < k; ++s) {
         const int r = inv[t * k + s];
         if (r < 0) continue;
-        const float w = load_weight<WDT>(wts, t * k + s);
+        float w = load_weight<WDT>(wts, t * k + s);
+        if constexpr (SC) w = __builtin_amdgcn_ldexpf(w, cs.shift - exp_shift(cs.rexp[r]) - cs.wshift[cs.idx[t * k + s]]);
         acc = __fadd_rn(acc, mul_f32(load_down<DDT>(down, int64_t(r) * H + c), w));
       }
       store_out<ODT>(out, t * H + c, acc);

@@ -253,7 +253,7 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
                                int64_t n2, int32_t epilogue, int32_t act_dtype);
 
 /* The whole frozen-expert forward: route -> gate_up (+epilogue, h rounded once to act_dtype)
- * -> down (+bias, kept in fp32) -> combine (one rounding into out_dtype).
+ * -> down (+bias, fp32 sums) -> combine (one rounding into out_dtype).
  * hidden [tokens, w1->k] in act_dtype; top_k_index [tokens, top_k] int64; top_k_weights
  * [tokens, top_k] in weight_dtype; out [tokens, w2->n] in out_dtype.
  * Small batches (tokens <= 8, or flags == E4B_PATH_GEMV within the decode limits) take the
@@ -265,7 +265,11 @@ size_t e4b_moe_workspace_bytes(int64_t tokens, int32_t top_k, int32_t num_expert
  * 2^-8), every activation row scaled by a power of two that puts its largest value in
  * [2^14, 2^15) (exact for bf16 values), the scales removed from the fp32 sums before the
  * epilogue -- so the layer keeps the decode path's accuracy at any batch. h is still rounded
- * once to act_dtype. Without `shift` the GEMMs use the bf16 dequantized weights themselves.
+ * once to act_dtype. At prefill sizes with w2->k a multiple of 256 the down rows are kept as
+ * fp16 (11 significant bits) with the operand scales left on, times 2^-(16 + ceil(log2 k)) so
+ * that they stay within fp16's range, and the combine takes the scales off in the router
+ * weights; elsewhere they stay fp32. Without `shift` the GEMMs use the bf16 dequantized weights
+ * themselves.
  * Replaces: engines/fast.py:100-160 fused_experts_forward (the bare-module forward that
  * enable_fast binds, fast.py:371-372), with no device->host synchronisation. */
 int e4b_moe_forward(const void* hidden, int32_t act_dtype, int64_t tokens, const int64_t* top_k_index,

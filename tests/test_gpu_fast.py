@@ -853,6 +853,52 @@ def test_fp16_matrix_core_mode_keeps_the_bf16_range(xscale, wscale, dq):
     _assert_fidelity(got, ref, _oracle(mod, x, idx, w), f"fp16 mode x*{xscale} w*{wscale} dq={dq}")
 
 
+@pytest.mark.parametrize("xscale,wscale,dq,outlier", [(2.0 ** 20, 1.0, False, False), (2.0 ** -20, 1.0, True, False),
+                                                      (1.0, 2.0 ** -24, False, False), (1.0, 2.0 ** 12, True, False),
+                                                      (1.0, 1.0, False, True)])
+def test_prefill_fp16_down_rows_keep_the_range(xscale, wscale, dq, outlier):
+    """At prefill sizes (256-row and 32-row tiles) with the down K a multiple of 256, the fp16 mode
+    stores the down rows as fp16 with the operand scales left on, times 2^-(16 + ceil(log2 K)), and
+    the combine folds the scales into the router weights. With activations and weights far outside
+    fp16's own range, or a token column 2^12 above the others (h rows dominated by one value), the
+    layer still meets the bars against the oracle on the first and last token of every expert."""
+    _announce(f"prefill fp16 down rows x*{xscale} w*{wscale} dq={dq} outlier={outlier}")
+    E, H, I, k, T = 16, 512, 256, 4, 512
+    g = torch.Generator().manual_seed(int(abs(np.log2(xscale * wscale))) + 23 + outlier)
+    gu = torch.randn(E, 2 * I, H, generator=g) * 0.05 * wscale
+    dn = torch.randn(E, H, I, generator=g) * 0.05 * wscale
+    mod = e4b.Experts4bit.from_float(gu.to(DEV), dn.to(DEV), compute_dtype=torch.bfloat16,
+                                     compress_statistics=dq).eval()
+    del gu, dn
+    x = torch.randn(T, H, generator=g) * xscale
+    if outlier:
+        x[:, 7] *= 2.0 ** 12
+    x = x.to(torch.bfloat16).to(DEV)
+    # Zipf-skewed routing: head experts fill 256-row tiles, tail experts end in 32-row tiles
+    rank = torch.randperm(E, generator=g).float() + 1.0
+    val, idx = torch.topk(torch.randn(T, E, generator=g) - 1.1 * torch.log(rank), k, dim=-1)
+    w = torch.softmax(val, -1).to(torch.bfloat16).to(DEV)
+    idx = idx.to(DEV)
+    with torch.no_grad():
+        assert e4b.enable_fast(mod) == 1
+        got = mod(x, idx, w)
+        w1, w2 = F._qweights(mod)
+        assert w1.shift is not None and w2.shift is not None  # the fp16 mode ran
+    assert torch.isfinite(got).all()
+    flat = idx.reshape(-1).cpu().numpy()
+    assert np.bincount(flat, minlength=E).max() > 256  # a full 256-row tile
+    rows = set()
+    for e in np.unique(flat):
+        hits = np.nonzero(flat == e)[0] // k
+        rows.update([int(hits[0]), int(hits[-1])])
+    rows = sorted(rows)
+    oracle = _oracle_rows(mod, x, idx, w, rows)
+    fro, maxabs, brel = moe.rel_errors(got[rows].float().cpu().numpy(), oracle)
+    print(f"[fidelity] prefill fp16 down rows x*{xscale} w*{wscale} dq={dq} outlier={outlier}: rel-fro {fro:.2e} "
+          f"max-abs/row-rms {maxabs:.2e} max-abs/max {brel:.2e}", flush=True)
+    assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
+
+
 @pytest.mark.parametrize("H,I,dq", [(1024, 192, False), (384, 256, True), (1280, 512, False), (1792, 640, True)])
 def test_narrow_tiles_in_fp16_mode(H, I, dq):
     """32-row tiles in the fp16 mode with K a multiple of 256 (the narrow kernel: pairs of 128-deep
