@@ -126,6 +126,21 @@ struct DecodeArgs {
   float lscale;
 };
 
+// Every kernel argument a decode kernel reads, requested in one batch at its entry: left to
+// itself the compiler loads each just before its first use, so the pointers first read after
+// the routing (weights, scales, outputs) cost a scalar-cache round trip of their own. (Not in
+// the LoRA variants, whose scalar registers are already short.)
+template <bool LORA>
+E4B_DEV void preload_args(const DecodeArgs& p) {
+  if constexpr (LORA) return;
+  asm volatile("; decode args %0 %1 %2 %3 %4 %5" ::"s"(p.x), "s"(p.topk), "s"(p.topk_w), "s"(p.out), "s"(p.n_out),
+               "s"(p.w.packed));
+  asm volatile("; decode weights %0 %1 %2 %3 %4 %5" ::"s"(p.w.absmax), "s"(p.w.absmax2), "s"(p.w.offset),
+               "s"(p.w.code), "s"(p.w.code2), "s"(p.w.bias));
+  asm volatile("; decode sizes %0 %1 %2 %3 %4 %5 %6 %7" ::"s"(p.tokens), "s"(p.k), "s"(p.E), "s"(p.w.n), "s"(p.w.k),
+               "s"(p.epi), "s"(p.odt), "s"(p.wdt));
+}
+
 // LoRA inside the decode GEMVs: lane gl of a G-lane column group takes ranks q = gl + G * i
 // (i < lora_slots<G, LR>()), so its partial delta rides the group's existing reduction. B entries
 // are loaded as raw bits with the weights and converted when used. Every slot is loaded (a slot
@@ -586,6 +601,7 @@ __global__ void __launch_bounds__(kDecThreads) decode_up_kernel(DecodeArgs p) {
   __shared__ int xsh[kConv ? kDecMaxK / 32 + 1 : 1];     // per chunk: the inverse of its restaging shift
   __shared__ WaveRoute route[kDecWaves];
   __shared__ float code2_s[(FMT == E4B_FMT_NF4_DQ) ? 256 : 1];
+  preload_args<LORA>(p);
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
   const int M = p.tokens * p.k;
@@ -791,6 +807,7 @@ constexpr int kItemMaxX = 16384;  // tokens * k1 activation elements staged (32 
 template <int DT, int FMT, int G, int CPL, bool FULL, bool PAIR, int LR>
 __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArgs p) {
   constexpr bool LORA = LR > 0;
+  preload_args<LORA>(p);
   constexpr int CDT = FMT == E4B_FMT_MXFP4 ? DT : E4B_FP16;
   constexpr bool kConv = CDT != DT;
   constexpr int kXU = kItemMaxX / 8 / kItemThreads;  // 16-byte activation pieces per thread
@@ -997,6 +1014,7 @@ __global__ void __launch_bounds__(kItemThreads) decode_up_items_kernel(DecodeArg
 template <int DT, int FMT, int G, int CPL, int JOBS, bool FULL, int LR>
 __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) {
   constexpr bool LORA = LR > 0;
+  preload_args<LORA>(p);
   __shared__ __align__(16) uint4 lut[FMT == E4B_FMT_MXFP4 ? 1 : 256 * kLutRowBytes / 16];  // none for e2m1
   __shared__ WaveRoute route[kDecWaves];
   __shared__ float res[kDecMaxRows * kDownCols];

@@ -104,9 +104,13 @@ E4B_DEV TileItem tile_item(const e4b_routing& rt, int n_tiles) {
   t.tile = (q / n_tiles) * kXcds + xcd;
   t.n_tile = q % n_tiles;
   const int tc = min(t.tile, rt.max_tiles - 1);
+  const int num_tiles = rt.meta[0];
   t.e = rt.tiles[2 * tc];
   t.row0 = rt.tiles[2 * tc + 1];
-  t.ok = t.tile < rt.meta[0];
+  // one round trip for the three loads: without this use ahead of the caller's early exit the
+  // compiler sinks the tile's loads past it, behind the count's
+  asm volatile("; tile %0 %1 of %2" ::"s"(t.e), "s"(t.row0), "s"(num_tiles));
+  t.ok = t.tile < num_tiles;
   return t;
 }
 

@@ -69,6 +69,16 @@ gemm_narrow_kernel(GemmArgs p) {
   __shared__ float code2_s[FMT == E4B_FMT_NF4_DQ ? 256 : 1];
   __shared__ int row_shift_s[BM];
 
+  // every kernel argument the prologue reads, loaded in one batch: left to itself the compiler
+  // loads each just before its first use, behind the early exit and the tile's loads, one
+  // dependent round trip each
+  asm volatile("; narrow args %0 %1 %2 %3 %4 %5" ::"s"(p.rt.tiles), "s"(p.rt.meta), "s"(p.rt.offsets),
+               "s"(p.rt.sorted_flat), "s"(p.a), "s"(p.a_exp));
+  asm volatile("; narrow weights %0 %1 %2 %3 %4 %5" ::"s"(p.w.packed), "s"(p.w.absmax), "s"(p.w.absmax2),
+               "s"(p.w.shift), "s"(p.w.offset), "s"(p.w.code));
+  asm volatile("; narrow sizes %0 %1 %2 %3 %4" ::"s"(p.rt.max_tiles), "s"(p.M), "s"(p.gather_k), "s"(p.w.n),
+               "s"(p.w.k));
+
   const bool pair = is_gated(p.epi);
   const int cols = pair ? BN / 2 : BN;  // output columns per tile
   const int n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
