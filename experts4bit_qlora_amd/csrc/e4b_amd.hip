@@ -357,7 +357,7 @@ int mfma_tile_for(int64_t M, int E) {
   return M >= 64 * groups ? e4b::kTileM : e4b::kTileMSmall;
 }
 
-// Prefill re-tiling (split_tiles_kernel): 256-row tiles in the fp16 matrix-core mode (the wide
+// Prefill re-tiling (emit_split_tiles, in the routing's table step): 256-row tiles in the fp16 matrix-core mode (the wide
 // kernel), 128-row tiles otherwise, except that an expert whose last tile would hold at most 32
 // rows runs those rows in one 32-row tile. The workspace holds the longer (128-row) tile list.
 int64_t max_big_tiles(int64_t M, int E) { return max_tiles_for(M, E, e4b::kTileM); }
@@ -376,7 +376,7 @@ struct RowExpArgs {
   uint16_t* x16;      // [tokens, k] scaled fp16
 };
 int route_impl(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t num_experts, const e4b_routing* rt,
-               const RowExpArgs* rx, hipStream_t stream);
+               const RowExpArgs* rx, hipStream_t stream, const e4b::SplitTiles& sp = {});
 
 }  // namespace
 
@@ -417,9 +417,10 @@ int e4b_route(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t
 namespace {
 
 // e4b_route, and with rx the fused forward's token rows (row_exp_row over x [tokens, k]) in the
-// routing's first launch.
+// routing's first launch; with sp.on the prefill's two tile lists (sp.big, sp.small) from the
+// routing's table step.
 int route_impl(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_t num_experts, const e4b_routing* rt,
-               const RowExpArgs* rx, hipStream_t stream) {
+               const RowExpArgs* rx, hipStream_t stream, const e4b::SplitTiles& sp) {
   if (tokens < 0 || top_k <= 0) return fail(E4B_EINVAL, "tokens must be >= 0 and top_k > 0");
   const int64_t M = tokens * top_k;
   if (M > 0x7fffffffLL) return fail(E4B_EUNSUPPORTED, "tokens*top_k=%lld exceeds int32", (long long)M);
@@ -435,13 +436,13 @@ int route_impl(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_
   if (M <= e4b::kRouteSingleMaxRows) {
     if (!rx) {
       hipLaunchKernelGGL(e4b::route_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, top_k_index, M, num_experts,
-                         *rt);
+                         *rt, sp);
       return check_launch("route_kernel");
     }
     const dim3 grid(static_cast<unsigned>(1 + cdiv(tokens, e4b::kRouteWaves)));
 #define E4B_RRX(RP)                                                                                                  \
   hipLaunchKernelGGL(e4b::route_rowexp_kernel<RP>, grid, dim3(e4b::kRouteThreads), 0, stream, top_k_index, M,        \
-                     num_experts, *rt, rx->x, tokens, rx->k, rx->row_exp, rx->x16)
+                     num_experts, *rt, sp, rx->x, tokens, rx->k, rx->row_exp, rx->x16)
     if (rp == 1) E4B_RRX(1); else if (rp == 2) E4B_RRX(2); else if (rp == 4) E4B_RRX(4); else E4B_RRX(8);
 #undef E4B_RRX
     return check_launch("route_rowexp_kernel");
@@ -461,7 +462,7 @@ int route_impl(const int64_t* top_k_index, int64_t tokens, int32_t top_k, int32_
   }
   hipLaunchKernelGGL(e4b::route_colscan_kernel, dim3(static_cast<unsigned>(num_experts + 1)),
                      dim3(e4b::kRouteThreads), 0, stream, nchunks, num_experts, rt->scratch, rt->offsets);
-  hipLaunchKernelGGL(e4b::route_tables_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, num_experts, *rt);
+  hipLaunchKernelGGL(e4b::route_tables_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, num_experts, *rt, sp);
   hipLaunchKernelGGL(e4b::route_place_kernel, dim3(static_cast<unsigned>(nchunks)), dim3(e4b::kRouteChunk), 0, stream,
                      top_k_index, M, num_experts, rt->scratch, *rt);
   return check_launch("route_count/colscan/tables/place kernels");
@@ -1076,9 +1077,11 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
   // the gate_up GEMM reads the tokens as scaled fp16 rows in fp16 mode
   const void* up_a = f16c ? static_cast<const void*>(x16) : hidden;
 
-  // fp16 mode: the token row exponents and scaled fp16 rows ride in the routing's first launch
+  // fp16 mode: the token row exponents and scaled fp16 rows ride in the routing's first launch;
+  // a prefill's two tile lists come from the routing's table step
   const RowExpArgs rx{static_cast<const uint16_t*>(hidden), w1->k, xexp, x16};
-  rc = route_impl(top_k_index, tokens, top_k, E, &rt, f16c ? &rx : nullptr, stream);
+  rc = route_impl(top_k_index, tokens, top_k, E, &rt, f16c ? &rx : nullptr, stream,
+                  e4b::SplitTiles{rbig, rsmall, split ? 1 : 0});
   if (rc) return rc;
   // fp16 mode: h row exponents, and h rewritten in place as scaled fp16 rows for the down GEMM
   auto h_to_f16 = [&]() {
@@ -1088,10 +1091,6 @@ static int moe_forward_impl(const void* hidden, int32_t act_dtype, int64_t token
     return check_launch("row_exp_kernel");
   };
   if (split) {
-    hipLaunchKernelGGL(e4b::split_tiles_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, rt.offsets, rt.meta, E,
-                       rbig, rsmall);
-    rc = check_launch("split_tiles_kernel");
-    if (rc) return rc;
     // the two tile heights write disjoint rows: the 32-row tiles go to the side stream (forked
     // after everything they read, joined before anything reads what they write)
     SideLease lease(stream, side_ok);
@@ -1381,14 +1380,8 @@ int e4b_moe_lora_forward(const void* hidden, int32_t act_dtype, int64_t tokens, 
     carve_lora_fused(p, tokens, M, E, h_cols, w1->k, w2->n, r, &rt, &rbig, &rsmall, &split, &xexp, &hexp, &x16, &h,
                      &down, &t);
     const RowExpArgs rx{static_cast<const uint16_t*>(hidden), w1->k, xexp, x16};
-    rc = route_impl(top_k_index, tokens, top_k, E, &rt, &rx, stream);
+    rc = route_impl(top_k_index, tokens, top_k, E, &rt, &rx, stream, e4b::SplitTiles{rbig, rsmall, split ? 1 : 0});
     if (rc) return rc;
-    if (split) {
-      hipLaunchKernelGGL(e4b::split_tiles_kernel, dim3(1), dim3(e4b::kRouteThreads), 0, stream, rt.offsets, rt.meta,
-                         E, rbig, rsmall);
-      rc = check_launch("split_tiles_kernel");
-      if (rc) return rc;
-    }
     // the 32-row tiles of a split run on a side stream, as in e4b_moe_forward
     SideLease lease(stream, split);
     auto tiles = [&](int site, auto&& launch) {

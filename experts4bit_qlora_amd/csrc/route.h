@@ -22,8 +22,9 @@
 // (One workgroup doing the column sums and the rewrite took 18.5 us at 32,768 ids over 128
 // experts; the columns are independent.)
 //
-// split_tiles_kernel re-tiles the routed rows for prefill: big tiles, plus a small tile for an
-// expert whose last big tile would hold only a few rows.
+// For prefill the table step (route_kernel's, or route_tables_kernel's) also re-tiles the routed
+// rows into two lists (emit_split_tiles): big tiles, plus a small tile for an expert whose last
+// big tile would hold only a few rows.
 #pragma once
 
 #include "common.h"
@@ -89,11 +90,70 @@ E4B_DEV int wave_rank(int e, int* s) {
   return r;
 }
 
+// Two tile lists from the routed offsets, for grouped GEMMs run at two tile heights. A tile
+// costs about the same whatever its height until its MFMA work catches up with its weight
+// decoding (the whole expert matrix per tile), so every expert keeps big tiles
+// (`big.tile_m` rows, the last one partial) unless its last big tile would hold at most
+// `small.tile_m` rows: those rows go to one small tile instead. The big list holds every
+// expert's full tiles first, then the partial ones, so a grid that takes the list in order runs
+// the long tiles first and the short ones last. One 512-thread block; thread t owns experts 2t
+// and 2t + 1 (counts ca, cb from offsets oa, ob); active / dropped go to both lists' meta.
+struct SplitTiles {
+  e4b_routing big, small;
+  int on;  // 0: no split lists
+};
+
+E4B_DEV void emit_split_tiles(int ca, int cb, int oa, int ob, int active, int dropped, const e4b_routing& big,
+                              const e4b_routing& small, int* wsum) {
+  const int tid = threadIdx.x;
+  const int ea = 2 * tid, eb = 2 * tid + 1;
+  const int bt = big.tile_m, st = small.tile_m;
+  // remainder past the full big tiles: one partial big tile, or one small tile when it fits
+  const int ra = ca % bt, rb = cb % bt;
+  const int nsa = (ra > 0 && ra <= st) ? 1 : 0, nsb = (rb > 0 && rb <= st) ? 1 : 0;
+  const int nfa = ca / bt, nfb = cb / bt;                        // full big tiles
+  const int npa = ra > st ? 1 : 0, npb = rb > st ? 1 : 0;        // partial big tiles
+  int nfull, npart, nsmall;
+  const int f0 = block_exclusive_scan(nfa + nfb, &nfull, wsum);
+  const int p0 = block_exclusive_scan(npa + npb, &npart, wsum);
+  const int s0 = block_exclusive_scan(nsa + nsb, &nsmall, wsum);
+  auto put_big = [&](int t, int e, int row) {
+    if (t < big.max_tiles) {
+      big.tiles[2 * t] = e;
+      big.tiles[2 * t + 1] = row;
+    }
+  };
+  for (int j = 0; j < nfa + nfb; ++j) {
+    const bool in_a = j < nfa;
+    put_big(f0 + j, in_a ? ea : eb, in_a ? oa + j * bt : ob + (j - nfa) * bt);
+  }
+  for (int j = 0; j < npa + npb; ++j) {
+    const bool in_a = j < npa;
+    put_big(nfull + p0 + j, in_a ? ea : eb, in_a ? oa + nfa * bt : ob + nfb * bt);
+  }
+  for (int j = 0; j < nsa + nsb; ++j) {
+    const int t = s0 + j;
+    const bool in_a = j < nsa;
+    if (t < small.max_tiles) {
+      small.tiles[2 * t] = in_a ? ea : eb;
+      small.tiles[2 * t + 1] = in_a ? oa + nfa * bt : ob + nfb * bt;  // at most one small tile per expert
+    }
+  }
+  if (tid == 0) {
+    big.meta[0] = min(nfull + npart, big.max_tiles);
+    small.meta[0] = min(nsmall, small.max_tiles);
+    big.meta[1] = small.meta[1] = active;
+    big.meta[2] = small.meta[2] = dropped;
+    big.meta[3] = bt;
+    small.meta[3] = st;
+  }
+}
+
 // Offsets, tile list, active list and meta from per-expert totals. Thread t of the 512-thread
 // block owns experts 2t and 2t+1 with totals ta and tb; offa / offb receive their first sorted
 // rows. `dropped` must be the same value in every thread.
 E4B_DEV void emit_expert_tables(int ta, int tb, int E, int dropped, const e4b_routing& rt, int* wsum, int& offa,
-                                int& offb) {
+                                int& offb, const SplitTiles* sp = nullptr) {
   const int tid = threadIdx.x;
   const int ea = 2 * tid, eb = 2 * tid + 1;
   int total;
@@ -131,10 +191,13 @@ E4B_DEV void emit_expert_tables(int ta, int tb, int E, int dropped, const e4b_ro
     rt.meta[2] = dropped;
     rt.meta[3] = tm;
   }
+  // the prefill's two tile lists from the same counts and offsets: no launch of their own
+  if (sp && sp->on) emit_split_tiles(ta, tb, offa, offb, num_active, dropped, sp->big, sp->small, wsum);
 }
 
 // The whole permutation in one kRouteThreads-thread workgroup (M <= kRouteSingleMaxRows).
-E4B_DEV void route_single(const int64_t* __restrict__ idx, int64_t M, int E, const e4b_routing& rt) {
+E4B_DEV void route_single(const int64_t* __restrict__ idx, int64_t M, int E, const e4b_routing& rt,
+                          const SplitTiles* sp = nullptr) {
   __shared__ int cnt[kRouteWaves * kRouteMaxExperts];
   __shared__ int wsum[kRouteWaves];
   __shared__ int dropped;
@@ -187,7 +250,7 @@ E4B_DEV void route_single(const int64_t* __restrict__ idx, int64_t M, int E, con
     for (int w = 0; w < kRouteWaves; ++w) tb += cnt[w * E + eb];
   const int ndropped = dropped;
   int offa, offb;
-  emit_expert_tables(ta, tb, E, ndropped, rt, wsum, offa, offb);
+  emit_expert_tables(ta, tb, E, ndropped, rt, wsum, offa, offb, sp);
   if (ea < E) {
     int run = offa;
     for (int w = 0; w < kRouteWaves; ++w) {
@@ -230,8 +293,8 @@ E4B_DEV void route_single(const int64_t* __restrict__ idx, int64_t M, int E, con
 }
 
 __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __restrict__ idx, int64_t M,
-                                                              int E, e4b_routing rt) {
-  route_single(idx, M, E, rt);
+                                                              int E, e4b_routing rt, SplitTiles sp) {
+  route_single(idx, M, E, rt, &sp);
 }
 
 // route_kernel and, in the same launch, row_exp_row over the T rows of x: block 0 routes, block
@@ -239,11 +302,11 @@ __global__ void __launch_bounds__(kRouteThreads) route_kernel(const int64_t* __r
 // token rows (exponents and scaled fp16 copies) then cost no launch of their own.
 template <int RP>
 __global__ void __launch_bounds__(kRouteThreads) route_rowexp_kernel(const int64_t* __restrict__ idx, int64_t M,
-                                                                     int E, e4b_routing rt, const uint16_t* x,
-                                                                     int64_t T, int64_t k, int32_t* row_exp,
-                                                                     uint16_t* x16) {
+                                                                     int E, e4b_routing rt, SplitTiles sp,
+                                                                     const uint16_t* x, int64_t T, int64_t k,
+                                                                     int32_t* row_exp, uint16_t* x16) {
   if (blockIdx.x == 0) {
-    route_single(idx, M, E, rt);
+    route_single(idx, M, E, rt, &sp);
     return;
   }
   const int64_t row = int64_t(blockIdx.x - 1) * kRouteWaves + threadIdx.x / kWave;
@@ -346,7 +409,7 @@ __global__ void __launch_bounds__(kRouteThreads) route_colscan_kernel(int64_t nc
 
 // One workgroup: the expert totals route_colscan_kernel left in rt.offsets[0 .. E) (and the
 // dropped count in rt.offsets[E]) become the sorted offsets, tiles, active list and meta.
-__global__ void __launch_bounds__(kRouteThreads) route_tables_kernel(int E, e4b_routing rt) {
+__global__ void __launch_bounds__(kRouteThreads) route_tables_kernel(int E, e4b_routing rt, SplitTiles sp) {
   __shared__ int wsum[kRouteWaves];
   const int tid = threadIdx.x;
   const int ta = (2 * tid < E) ? rt.offsets[2 * tid] : 0;
@@ -354,7 +417,7 @@ __global__ void __launch_bounds__(kRouteThreads) route_tables_kernel(int E, e4b_
   const int dropped = rt.offsets[E];
   // every total is read before the first scan's barrier, so before any offset is written
   int offa, offb;
-  emit_expert_tables(ta, tb, E, dropped, rt, wsum, offa, offb);
+  emit_expert_tables(ta, tb, E, dropped, rt, wsum, offa, offb, &sp);
 }
 
 __global__ void __launch_bounds__(kRouteChunk) route_place_kernel(const int64_t* __restrict__ idx, int64_t M, int E,
@@ -462,65 +525,6 @@ __global__ void __launch_bounds__(kRouteThreads) route_groups_kernel(GroupOffset
         rt.inv[r0 + i] = -1;
       }
     }
-  }
-}
-
-// Two tile lists from the routed offsets, for grouped GEMMs run at two tile heights. A tile
-// costs about the same whatever its height until its MFMA work catches up with its weight
-// decoding (the whole expert matrix per tile), so every expert keeps big tiles
-// (`big.tile_m` rows, the last one partial) unless its last big tile would hold at most
-// `small.tile_m` rows: those rows go to one small tile instead. The big list holds every
-// expert's full tiles first, then the partial ones, so a grid that takes the list in order runs
-// the long tiles first and the short ones last. One 512-thread block; thread t owns experts 2t
-// and 2t + 1. meta[1] / meta[2] (active, dropped) are copied from the routing the offsets came
-// from.
-__global__ void __launch_bounds__(kRouteThreads) split_tiles_kernel(const int32_t* __restrict__ offsets,
-                                                                   const int32_t* __restrict__ meta, int E,
-                                                                   e4b_routing big, e4b_routing small) {
-  __shared__ int wsum[kRouteWaves];
-  const int tid = threadIdx.x;
-  const int ea = 2 * tid, eb = 2 * tid + 1;
-  const int oa = ea < E ? offsets[ea] : 0, ob = eb < E ? offsets[eb] : 0;
-  const int ca = ea < E ? offsets[ea + 1] - oa : 0, cb = eb < E ? offsets[eb + 1] - ob : 0;
-  const int bt = big.tile_m, st = small.tile_m;
-  // remainder past the full big tiles: one partial big tile, or one small tile when it fits
-  const int ra = ca % bt, rb = cb % bt;
-  const int nsa = (ra > 0 && ra <= st) ? 1 : 0, nsb = (rb > 0 && rb <= st) ? 1 : 0;
-  const int nfa = ca / bt, nfb = cb / bt;                        // full big tiles
-  const int npa = ra > st ? 1 : 0, npb = rb > st ? 1 : 0;        // partial big tiles
-  int nfull, npart, nsmall;
-  const int f0 = block_exclusive_scan(nfa + nfb, &nfull, wsum);
-  const int p0 = block_exclusive_scan(npa + npb, &npart, wsum);
-  const int s0 = block_exclusive_scan(nsa + nsb, &nsmall, wsum);
-  auto put_big = [&](int t, int e, int row) {
-    if (t < big.max_tiles) {
-      big.tiles[2 * t] = e;
-      big.tiles[2 * t + 1] = row;
-    }
-  };
-  for (int j = 0; j < nfa + nfb; ++j) {
-    const bool in_a = j < nfa;
-    put_big(f0 + j, in_a ? ea : eb, in_a ? oa + j * bt : ob + (j - nfa) * bt);
-  }
-  for (int j = 0; j < npa + npb; ++j) {
-    const bool in_a = j < npa;
-    put_big(nfull + p0 + j, in_a ? ea : eb, in_a ? oa + nfa * bt : ob + nfb * bt);
-  }
-  for (int j = 0; j < nsa + nsb; ++j) {
-    const int t = s0 + j;
-    const bool in_a = j < nsa;
-    if (t < small.max_tiles) {
-      small.tiles[2 * t] = in_a ? ea : eb;
-      small.tiles[2 * t + 1] = in_a ? oa + nfa * bt : ob + nfb * bt;  // at most one small tile per expert
-    }
-  }
-  if (tid == 0) {
-    big.meta[0] = min(nfull + npart, big.max_tiles);
-    small.meta[0] = min(nsmall, small.max_tiles);
-    big.meta[1] = small.meta[1] = meta[1];
-    big.meta[2] = small.meta[2] = meta[2];
-    big.meta[3] = bt;
-    small.meta[3] = st;
   }
 }
 
