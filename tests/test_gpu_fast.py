@@ -1,7 +1,7 @@
 """GPU parity of the drop-in ``enable_fast`` path, mirroring the reference's own tests
 (``tests/test_fast.py``, ``test_fast_lora.py``, ``test_fast_v4.py``,
-``test_fast_expertslora_delegation.py``, ``test_deterministic_scatter.py``) plus the BASELINE
-configurations at their real shapes.
+``test_fast_expertslora_delegation.py``, ``test_deterministic_scatter.py``) plus the benchmark
+configurations (OLMoE, Qwen3 double quant, gpt-oss) at their real shapes.
 
 Accuracy bars: against the fp32 oracle over the same dequantized weights, rel-Frobenius <= 1e-2
 and max-abs <= 2e-2 on oracle-RMS-normalised outputs, and no worse than
@@ -679,7 +679,7 @@ def test_gptoss_release_layout_matches_transformers(T):
     assert fro <= 1e-2 and maxabs <= max(2e-2, 2 * maxabs_l), (fro, maxabs, maxabs_l)
 
 
-# ---------------------------------------------------------- BASELINE-shaped parity
+# ---------------------------------------------------------- benchmark-shaped parity
 
 
 def _cfg_module(E, H, I, seed, dq):
