@@ -408,7 +408,8 @@ __global__ void __launch_bounds__(kRouteThreads) route_colscan_kernel(int64_t nc
 }
 
 // One workgroup: the expert totals route_colscan_kernel left in rt.offsets[0 .. E) (and the
-// dropped count in rt.offsets[E]) become the sorted offsets, tiles, active list and meta.
+// dropped count in rt.offsets[E]) become the sorted offsets, tiles, active list and meta, and
+// with sp.on the prefill's two tile lists.
 __global__ void __launch_bounds__(kRouteThreads) route_tables_kernel(int E, e4b_routing rt, SplitTiles sp) {
   __shared__ int wsum[kRouteWaves];
   const int tid = threadIdx.x;
