@@ -27,6 +27,8 @@
 // big tile would hold only a few rows.
 #pragma once
 
+#include <rocprim/warp/warp_scan.hpp>
+
 #include "common.h"
 #include "scale.h"
 
@@ -42,11 +44,13 @@ constexpr int kRouteChunk = 4 * kWave;     // ids per chunk (one workgroup) in t
 E4B_DEV int block_exclusive_scan(int v, int* total, int* wsum) {
   const int lane = threadIdx.x & (kWave - 1);
   const int wid = threadIdx.x / kWave;
-  int x = v;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int y = __shfl_up(x, o);
-    if (lane >= o) x += y;
+  // the wave's inclusive scan in registers (rocPRIM's cross-lane scan: DPP row shifts and
+  // broadcasts on gfx950, no LDS round trip per step)
+  int x;
+  {
+    using wave_scan = rocprim::warp_scan<int, kWave>;
+    typename wave_scan::storage_type st;
+    wave_scan().inclusive_scan(v, x, st);
   }
   if (lane == kWave - 1) wsum[wid] = x;
   __syncthreads();
