@@ -963,18 +963,27 @@ def test_weight_shift_matches_the_oracle_exponents(H, inter):
                 assert got[e] == 141 - max(E_, 20), (dq, i, e, got[e], E_)
 
 
-def test_out_of_range_ids_contribute_nothing():
-    _announce("dropped ids")
-    mod, hs, top_i, top_w = _make(E=8, tokens=6, k=2, seed=11)
+@pytest.mark.parametrize("tokens", [6, 512])
+def test_out_of_range_ids_contribute_nothing(tokens):
+    """Ids outside [0, E) drop their slots: at decode size, and at prefill size (256- and 32-row
+    tiles in the fp16 mode, fp16 down rows whose scales the combine looks up per slot)."""
+    _announce(f"dropped ids tokens={tokens}")
+    if tokens <= 8:
+        mod, hs, top_i, top_w = _make(E=8, tokens=tokens, k=2, seed=11)
+    else:
+        mod, hs, top_i, top_w = _make(E=8, H=512, inter=256, tokens=tokens, k=2, seed=12, scale=0.05)
     e4b.enable_fast(mod)
     bad = top_i.clone()
     bad[0, 1] = 99
     bad[3, 0] = -1
+    if tokens > 8:
+        bad[tokens - 1, 1] = -7
+        bad[tokens // 2, 0] = 8
     with torch.no_grad():
         got = mod(hs, bad, top_w)
     w_keep = top_w.clone()
-    w_keep[0, 1] = 0
-    w_keep[3, 0] = 0
+    w_keep[bad < 0] = 0
+    w_keep[bad > 7] = 0
     safe = bad.clamp(0, 7)
     with torch.no_grad():
         want = mod(hs, safe, w_keep)
