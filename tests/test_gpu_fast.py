@@ -15,6 +15,7 @@ import experts4bit_qlora_amd as e4b
 from experts4bit_qlora_amd import _native as N
 from experts4bit_qlora_amd import fast as F
 from experts4bit_qlora_amd import ops
+from experts4bit_qlora_amd import quant as Q
 from oracle import moe
 from oracle import quant as oq
 from oracle_weights import oracle_weights
@@ -897,6 +898,32 @@ def test_prefill_fp16_down_rows_keep_the_range(xscale, wscale, dq, outlier):
     print(f"[fidelity] prefill fp16 down rows x*{xscale} w*{wscale} dq={dq} outlier={outlier}: rel-fro {fro:.2e} "
           f"max-abs/row-rms {maxabs:.2e} max-abs/max {brel:.2e}", flush=True)
     assert fro <= 1e-2 and maxabs <= 2e-2, (fro, maxabs)
+
+
+@pytest.mark.parametrize("wdt", [torch.bfloat16, torch.float16, torch.float32])
+def test_prefill_combine_output_and_weight_dtypes(wdt):
+    """The combine of the prefill's fp16 down rows sums in fp32 and rounds once: the bf16 and fp16
+    outputs equal the fp32 output rounded, bit for bit, for router weights in bf16, fp16 and fp32
+    (the power of two each slot's weight takes on is exact in all three)."""
+    _announce(f"prefill combine dtypes wdt={wdt}")
+    g = torch.Generator().manual_seed(61)
+    E, H, I, k, T = 8, 512, 256, 2, 512
+    qw = []
+    for n, kk in ((2 * I, H), (H, I)):
+        packed, absmax = Q.quantize_4bit(torch.randn(E, n * kk, generator=g) * 0.05)
+        qw.append(ops.with_weight_shift(ops.nf4_qweight(packed.to(DEV), absmax.to(DEV),
+                                                        Q.code_4bit("nf4").to(DEV), n, kk, num_experts=E)))
+    w1, w2 = qw
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(DEV)
+    rank = torch.randperm(E, generator=g).float() + 1.0
+    val, idx = torch.topk(torch.randn(T, E, generator=g) - 1.1 * torch.log(rank), k, dim=-1)
+    w = torch.softmax(val, -1).to(wdt).to(DEV)
+    idx = idx.to(DEV)
+    ref = ops.moe_forward(x, idx, w, w1, w2, N.EPI_SWIGLU, torch.float32)
+    for odt in (torch.bfloat16, torch.float16):
+        got = ops.moe_forward(x, idx, w, w1, w2, N.EPI_SWIGLU, odt)
+        assert torch.equal(got, ref.to(odt)), (wdt, odt)
+    assert torch.isfinite(ref).all()
 
 
 @pytest.mark.parametrize("H,I,dq", [(1024, 192, False), (384, 256, True), (1280, 512, False), (1792, 640, True)])
