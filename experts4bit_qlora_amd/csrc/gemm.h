@@ -374,7 +374,10 @@ __global__ void __launch_bounds__(gemm_threads(BM)) gemm_mfma_kernel(GemmArgs p)
   const int ar = tid / TPR;
   const int aseg = (tid % TPR) * AV * 8;
   const int r = row0 + ar;
-  const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
+  // the row's source, loaded at a clamped index before row_end is known and dropped for rows
+  // past the expert's end (a load behind the row test waits for row_end first)
+  const int sfv = p.rt.sorted_flat[min(r, static_cast<int>(p.M) - 1)];
+  const int64_t src = (r < row_end) ? (p.gather_k > 0 ? sfv / p.gather_k : r) : 0;
   const uint16_t* aptr = p.a + src * k + aseg;
   // fp16 mode: the tile row's activation shift (for the epilogue) and the expert's weight shift
   int wsh = 0;

@@ -81,21 +81,29 @@ E4B_DEV void wide_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2
   // 32 i + t / 8, columns 8 (t % 8) .. + 7, so eight lanes read one row's 128 contiguous bytes
   // (one lane per row, 16 bytes from each of 64 rows per load, costs the load pipeline about
   // twice the issue time). aoff[i]: that piece of step 0, in 16-byte units of p.a.
+  // The rows' sources (and tile row t's, for the row shifts) are loaded together at clamped
+  // indices, before row_end is known, and dropped for rows past the expert's end: a load behind
+  // the row test, divided inside that branch, was waited on alone, one round trip per piece.
   const int apart = tid & 7;
+  const bool gather = p.gather_k > 0;
+  const int mlast = static_cast<int>(p.M) - 1;
+  int sf[AP + 1];
+#pragma unroll
+  for (int i = 0; i <= AP; ++i) {
+    const int r = min(row0 + (i < AP ? 32 * i + (tid >> 3) : tid), mlast);
+    const int v = p.rt.sorted_flat[r];
+    sf[i] = gather ? v : r;
+  }
+  auto row_src = [&](int r, int s) -> int64_t { return r < row_end ? (gather ? s / p.gather_k : s) : 0; };
   uint32_t aoff[AP];
 #pragma unroll
-  for (int i = 0; i < AP; ++i) {
-    const int r = row0 + 32 * i + (tid >> 3);
-    const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
-    aoff[i] = static_cast<uint32_t>((src * k) / 8 + apart);
-  }
+  for (int i = 0; i < AP; ++i)
+    aoff[i] = static_cast<uint32_t>((row_src(row0 + 32 * i + (tid >> 3), sf[i]) * k) / 8 + apart);
   int wsh = 0;
   if constexpr (F16C) {
     wsh = p.w.shift[e];
     // row_shift_s: the shift of tile row tid, for the epilogue
-    const int r = row0 + tid;
-    const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
-    row_shift_s[tid] = exp_shift(p.a_exp[src]);
+    row_shift_s[tid] = exp_shift(p.a_exp[row_src(row0 + tid, sf[AP])]);
   }
   // W: thread tid stages LDS weight row tid (for a gated epilogue rows 0..127 are the gate rows
   // of the tile's 128 output columns and rows 128..255 their up rows); rows past n_out read

@@ -32,9 +32,19 @@ namespace e4b {
 
 constexpr int kWide8Threads = 512;
 
+// A tile's record and its rows' sources, loaded by the kernel in the round trip after the tile's
+// (beside the code tables' loads): the expert, its first sorted row and the expert's row end, and
+// for thread t the sources of tile rows 64 i + t / 8 (i < 4: its activation pieces) and t % 256
+// (its row shift) -- sorted_flat at each row clamped to the last one with a gather, the row
+// itself without. Sources of rows past the expert's end are dropped where they are used.
+struct Wide8Rows {
+  int e, row0, end;
+  int sf[5];
+};
+
 // One tile. HALF: a tile of at most 128 rows as 128 rows x 256 weight rows (waves of 64 x 64).
 template <int DT, int FMT, bool F16C, bool HALF, bool LORA, bool H16>
-E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[2][kWideTileM * kTileK],
+E4B_DEV void wide8_tile(const GemmArgs& p, const Wide8Rows& tr, int n_tile, uint16_t (&As)[2][kWideTileM * kTileK],
                         uint16_t (&Ws)[2][kWideTileN * kTileK], const float* code2_s, int* row_shift_s,
                         const uint32_t* ptab) {
   constexpr int CT = F16C ? E4B_FP16 : DT;
@@ -51,9 +61,9 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
   const int wid = __builtin_amdgcn_readfirstlane(tid) / kWave;
   const int wave_m = wid & 1;
   const int wave_n = wid >> 1;
-  const int e = p.rt.tiles[2 * tile];
-  const int row0 = p.rt.tiles[2 * tile + 1];
-  const int row_end = min(row0 + BM, p.rt.offsets[e + 1]);
+  const int e = tr.e;
+  const int row0 = tr.row0;
+  const int row_end = min(row0 + BM, tr.end);
   const int64_t n = p.w.n;
   const int64_t k = p.w.k;
   const int64_t col0 = int64_t(n_tile) * cols;
@@ -62,19 +72,16 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
   // activation piece i of thread t: tile row 64 i + t / 8, columns 8 (t % 8) .. + 7 (eight lanes
   // read one row's 128 contiguous bytes); aoff[i]: that piece of step 0 in 16-byte units of p.a
   const int apart = tid & 7;
+  const bool gather = p.gather_k > 0;
+  auto row_src = [&](int r, int s) -> int64_t { return r < row_end ? (gather ? s / p.gather_k : s) : 0; };
   uint32_t aoff[AP];
 #pragma unroll
-  for (int i = 0; i < AP; ++i) {
-    const int r = row0 + 64 * i + (tid >> 3);
-    const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
-    aoff[i] = static_cast<uint32_t>((src * k) / 8 + apart);
-  }
+  for (int i = 0; i < AP; ++i)
+    aoff[i] = static_cast<uint32_t>((row_src(row0 + 64 * i + (tid >> 3), tr.sf[i]) * k) / 8 + apart);
   const int wsh = F16C ? p.w.shift[e] : 0;
-  if (F16C && tid < BM) {  // row_shift_s: the shift of tile row tid, for the epilogue
-    const int r = row0 + tid;
-    const int64_t src = (r < row_end) ? (p.gather_k > 0 ? p.rt.sorted_flat[r] / p.gather_k : r) : 0;
-    row_shift_s[tid] = exp_shift(p.a_exp[src]);
-  }
+  // the exponent of tile row t (t < BM), stored to row_shift_s (the epilogue's shifts) once the
+  // first steps' loads are out
+  const int a_exp_row = F16C ? p.a_exp[row_src(row0 + (tid & (kWideTileM - 1)), tr.sf[4])] : 0;
   // weights: thread t stages half wh = t % 2 of LDS weight row wr = t / 2 (for a gated epilogue
   // rows 0..127 are the gate rows of the tile's 128 output columns, 128..255 their up rows); rows
   // past n_out read weight row 0 and feed only columns that are never stored
@@ -174,6 +181,7 @@ E4B_DEV void wide8_tile(const GemmArgs& p, int tile, int n_tile, uint16_t (&As)[
   load_w(0, 0);
   load_a(1, min<int64_t>(1, klast));
   load_w(1, min<int64_t>(1, klast));
+  if (F16C && tid < BM) row_shift_s[tid] = exp_shift(a_exp_row);
   __syncthreads();  // code2 table, code-pair table, row shifts
   if constexpr (LORA) {
     // the accumulators start as the tile's LoRA delta, scaled like the products (lora_mfma.h):
@@ -336,7 +344,21 @@ __global__ void __launch_bounds__(kWide8Threads) gemm_wide8_kernel(GemmArgs p) {
   const int n_tiles = static_cast<int>((p.n_out + cols - 1) / cols);
   const TileItem item = tile_item(p.rt, n_tiles);
   if (!item.ok) return;
-  const int tile = item.tile, n_tile = item.n_tile;
+  const int n_tile = item.n_tile;
+  Wide8Rows tr;
+  tr.e = item.e;
+  tr.row0 = item.row0;
+  tr.end = p.rt.offsets[item.e + 1];
+  {
+    const int mlast = static_cast<int>(p.M) - 1;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+      const int r = min(item.row0 + (i < 4 ? 64 * i + (tid >> 3) : (tid & (kWideTileM - 1))), mlast);
+      const int v = p.rt.sorted_flat[r];
+      tr.sf[i] = p.gather_k > 0 ? v : r;
+    }
+  }
   if constexpr (F16C) {
     if (threadIdx.x < 256) {
       // the table of code pairs: pass j fills entries 16 j .. 16 j + 15, all copies; entry
@@ -348,9 +370,9 @@ __global__ void __launch_bounds__(kWide8Threads) gemm_wide8_kernel(GemmArgs p) {
       if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[threadIdx.x] = p.w.code2[threadIdx.x];
     }
   }
-  const int rows = p.rt.offsets[item.e + 1] - item.row0;  // the tile's rows, capped at BM below
-  if (rows <= BM / 2) wide8_tile<DT, FMT, F16C, true, LORA, H16>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
-  else wide8_tile<DT, FMT, F16C, false, LORA, H16>(p, tile, n_tile, As, Ws, code2_s, row_shift_s, ptab);
+  const int rows = tr.end - tr.row0;  // the tile's rows, capped at BM below
+  if (rows <= BM / 2) wide8_tile<DT, FMT, F16C, true, LORA, H16>(p, tr, n_tile, As, Ws, code2_s, row_shift_s, ptab);
+  else wide8_tile<DT, FMT, F16C, false, LORA, H16>(p, tr, n_tile, As, Ws, code2_s, row_shift_s, ptab);
 }
 
 }  // namespace e4b
