@@ -1076,30 +1076,41 @@ __global__ void __launch_bounds__(kDecThreads) decode_down_kernel(DecodeArgs p) 
       je[t] = ok ? r.act[job] : -1;
       jrows[t] = ok ? r.rows[job] : 0ull;
       jf[t] = ok ? __ffsll(static_cast<long long>(jrows[t])) - 1 : 0;
-      // a group without a job loads the first routed expert's chunks (which its group loads
-      // anyway): no branch around the loads, whose count each wait below depends on
-      const int e = ok ? je[t] : (nact > 0 ? r.act[0] : 0);
-      // the offset and the bias bits first: the row pass converts them before its first table
-      // lookup, which (loads counted in issue order) then waits for them and column 0's loads
-      // only; issued last, they made it wait for every column's weights and scales
-      joff[t] = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
+      // NF4 (split table): a group without a job loads the first routed expert's chunks (which
+      // its group loads anyway), so no branch sits around the loads whose count each wait below
+      // depends on; the offset and the bias bits go first (the row pass converts them before its
+      // first table lookup, which, loads being counted in issue order, then waits for them and
+      // column 0's loads only; issued last, they made it wait for every column's weights and
+      // scales). e2m1 keeps the branch and the bias last: the same order measured slower there
+      // (gpt-oss bs=1 21.6 -> 22.1 us).
+      const int e = ok ? je[t] : ((kSplit && nact > 0) ? r.act[0] : 0);
       // a spare load of x[0] when there is no bias: no branch on the loaded value
       const uint16_t* bp = has_bias ? bias + int64_t(e) * n : p.x;
+      if constexpr (kSplit) {
+        joff[t] = (FMT == E4B_FMT_NF4_DQ) ? w.offset[e] : 0.0f;
 #pragma unroll
-      for (int cl = 0; cl < C; ++cl) bb[t][cl] = bp[has_bias ? cols[cl] : 0];
+        for (int cl = 0; cl < C; ++cl) bb[t][cl] = bp[has_bias ? cols[cl] : 0];
+      }
 #pragma unroll
       for (int i = 0; i < CPL; ++i) {
         const int c = slot_chunk<G, FULL>(gl, i, nchunk, valid[i]);
-        load_chunk_x(p.x + int64_t(jf[t]) * k, c, xv[t][i]);
+        if (kSplit || ok) {
+          load_chunk_x(p.x + int64_t(jf[t]) * k, c, xv[t][i]);
 #pragma unroll
-        for (int cl = 0; cl < C; ++cl) {
-          q[t][i][cl] = load_chunk_w(w, e, cols[cl], c);
-          rs[t][i][cl] = load_scale<FMT>(w, e, cols[cl], c);
-          // each column's weights and scale issued together (left to itself the scheduler
-          // groups the weight loads ahead of the scale loads, and column 0's scale then
-          // arrives behind every column's weights)
-          __builtin_amdgcn_sched_barrier(0);
+          for (int cl = 0; cl < C; ++cl) {
+            q[t][i][cl] = load_chunk_w(w, e, cols[cl], c);
+            rs[t][i][cl] = load_scale<FMT>(w, e, cols[cl], c);
+            // NF4: each column's weights and scale issued together (left to itself the
+            // scheduler groups the weight loads ahead of the scale loads, and column 0's scale
+            // then arrives behind every column's weights)
+            if constexpr (kSplit) __builtin_amdgcn_sched_barrier(0);
+          }
         }
+      }
+      if constexpr (!kSplit) {
+        joff[t] = 0.0f;
+#pragma unroll
+        for (int cl = 0; cl < C; ++cl) bb[t][cl] = bp[has_bias ? cols[cl] : 0];
       }
       if constexpr (LORA) {
         if (ok) {
