@@ -149,6 +149,10 @@ gemm_narrow_kernel(GemmArgs p) {
   const int64_t src_any = p.gather_k > 0 ? p.rt.sorted_flat[rcl] / p.gather_k : rcl;
   const int64_t src = (r < row_end) ? src_any : 0;
   const uint16_t* aptr = p.a + src * k + 64 * (ac >> 1) + 16 * (ac & 1);
+  // the row's exponent, loaded ahead of the activation and weight loads: stored to row_shift_s
+  // before the first barrier, it was the last load of the prologue, and the wait for it was a
+  // wait for all of them (step 2's weights included)
+  const int a_exp_row = p.a_exp[src];
 
   // The tile's rows as MS 16-row MFMA sub-tiles: one when the tile holds at most 16 rows (a
   // mid-size batch's experts and most prefill tails hold a few rows each), halving the MFMAs and
@@ -212,7 +216,7 @@ gemm_narrow_kernel(GemmArgs p) {
       ptab[(w0 + 4 * i) * kNarrowCopies + lane] = cvt_pair<E4B_FP16>(hi[i >> 2], lo[i & 3]);
   }
   if constexpr (FMT == E4B_FMT_NF4_DQ) code2_s[tid] = p.w.code2[tid];
-  if ((tid & 7) == 0) row_shift_s[ar] = exp_shift(p.a_exp[src]);
+  if ((tid & 7) == 0) row_shift_s[ar] = exp_shift(a_exp_row);
   store_a(0);
   load_a(0, min(2, last));
   __syncthreads();
